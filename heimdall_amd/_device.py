@@ -1,0 +1,103 @@
+"""Device-side plumbing shared by the operator wrappers: dtype codes, workspace, stream, the GDN launcher."""
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import BifrostError, check
+
+SUPPORTED_D = (64, 128, 256)
+
+
+def require_device(*tensors) -> torch.device:
+    """All tensors must live on one HIP device: the operators have no CPU path."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise BifrostError("heimdall_amd operators run on the GPU only (got a tensor on "
+                               f"{t.device}); use the reference implementation for CPU tensors")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise BifrostError(f"tensors on different devices: {dev} and {t.device}")
+    if dev is None:
+        raise BifrostError("no tensor argument")
+    return dev
+
+
+def require_no_grad(*tensors) -> None:
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors):
+        raise BifrostError("heimdall_amd kernels are forward-only; call under torch.no_grad() or detach the inputs")
+
+
+def compute_dtype(*tensors) -> torch.dtype:
+    """bf16 if any input is a 16-bit float (bf16 MFMA operands, fp32 accumulation), else fp32."""
+    return torch.bfloat16 if any(t.dtype in (torch.bfloat16, torch.float16) for t in tensors) else torch.float32
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.bfloat16:
+        return _lib.DTYPE_BF16
+    if dt == torch.float32:
+        return _lib.DTYPE_F32
+    raise BifrostError(f"unsupported dtype {dt}")
+
+
+def stream_ptr(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def workspace(nbytes: int, dev: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+
+
+def gdn_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor, *,
+                num_seqs: int, cu_seqlens: Optional[torch.Tensor] = None, initial_state: Optional[torch.Tensor] = None,
+                scale: float = 1.0, out_dtype: torch.dtype = torch.float32, phases: int = _lib.PHASE_ALL,
+                out: Optional[torch.Tensor] = None, final_state: Optional[torch.Tensor] = None,
+                ws: Optional[torch.Tensor] = None):
+    """Packed GQA gated delta rule on the GPU.
+
+    q [N, G*R, D], k [N, G, D], v [N, G, D], g/beta [N, G]; cu_seqlens int32 [num_seqs + 1] on the device or None
+    (equal sequences). Returns (o [N, G*R, D] out_dtype, final_state [num_seqs, G, D, D] fp32).
+    """
+    dev = require_device(q, k, v, g, beta, cu_seqlens, initial_state)
+    N, H, D = q.shape
+    G = k.shape[1]
+    if H % G or k.shape != (N, G, D) or v.shape != (N, G, D) or g.shape != (N, G) or beta.shape != (N, G):
+        raise BifrostError(f"inconsistent shapes q{tuple(q.shape)} k{tuple(k.shape)} v{tuple(v.shape)} "
+                           f"g{tuple(g.shape)} beta{tuple(beta.shape)}")
+    if D not in SUPPORTED_D:
+        raise BifrostError(f"head dim {D} not supported (supported: {SUPPORTED_D})")
+    R = H // G
+    cdt = compute_dtype(q, k, v)
+    q, k, v = (t.to(cdt).contiguous() for t in (q, k, v))
+    g, beta = g.float().contiguous(), beta.float().contiguous()
+    if cu_seqlens is not None:
+        cu_seqlens = cu_seqlens.to(device=dev, dtype=torch.int32).contiguous()
+        if cu_seqlens.numel() != num_seqs + 1:
+            raise BifrostError("cu_seqlens must hold num_seqs + 1 offsets")
+    elif N % num_seqs:
+        raise BifrostError("token count is not a multiple of num_seqs")
+    s0 = None
+    if initial_state is not None:
+        s0 = initial_state.float().contiguous()
+        if s0.shape != (num_seqs, G, D, D):
+            raise BifrostError(f"initial_state must be [{num_seqs}, {G}, {D}, {D}], got {tuple(s0.shape)}")
+    lib = _lib.load()
+    nbytes = _lib.ctypes.c_size_t(0)
+    check(lib.bf_gdn_workspace_size(N, num_seqs, G, R, D, dtype_code(cdt), _lib.ctypes.byref(nbytes)),
+          "bf_gdn_workspace_size")
+    if ws is None or ws.numel() < nbytes.value:
+        ws = workspace(nbytes.value, dev)
+    o = out if out is not None else torch.empty(N, H, D, dtype=out_dtype, device=dev)
+    s_out = final_state if final_state is not None else torch.empty(num_seqs, G, D, D, dtype=torch.float32,
+                                                                     device=dev)
+    check(lib.bf_gdn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
+                         cu_seqlens.data_ptr() if cu_seqlens is not None else None, num_seqs, N, G, R, D,
+                         dtype_code(cdt), float(scale), s0.data_ptr() if s0 is not None else None, o.data_ptr(),
+                         dtype_code(o.dtype), s_out.data_ptr(), ws.data_ptr(), ws.numel(), phases, stream_ptr(dev)),
+          "bf_gdn_fwd")
+    return o, s_out

@@ -1,0 +1,48 @@
+"""ctypes binding of ``libbifrost_hip.so`` (the C ABI declared in ``include/bifrost.h``).
+
+There is no fallback: if the library is missing or does not load, every operator raises.
+"""
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libbifrost_hip.so"
+
+DTYPE_F32, DTYPE_BF16 = 0, 1
+PHASE_PREP, PHASE_SCAN, PHASE_ALL = 1, 2, 3
+
+_c_int, _c_i64, _c_sz, _vp, _fp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_float
+
+# name -> (restype, argtypes); every symbol declared in include/bifrost.h
+SIGNATURES = {
+    "bf_version": (_c_int, []),
+    "bf_status_string": (ctypes.c_char_p, [_c_int]),
+    "bf_gdn_workspace_size": (_c_int, [_c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_c_sz)]),
+    "bf_gdn_fwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_int, _fp, _vp,
+                            _vp, _c_int, _vp, _vp, _c_sz, _c_int, _vp]),
+}
+
+_LIB = None
+
+
+class BifrostError(RuntimeError):
+    pass
+
+
+def load():
+    """Load the library once; raise ``BifrostError`` if it is missing (build it with ``python -m heimdall_amd.build``)."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise BifrostError(f"{LIB_PATH} not found: build it with `python -m heimdall_amd.build`")
+        lib = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype, fn.argtypes = res, args
+        _LIB = lib
+    return _LIB
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = load().bf_status_string(status).decode()
+        raise BifrostError(f"{what} failed with status {status}: {msg}")

@@ -1,0 +1,173 @@
+// Shared device helpers for the Bifrost core kernels (gfx950 / CDNA4 only).
+//
+// Operand element types: bf16 (storage uint16_t, MFMA v_mfma_f32_16x16x32_bf16) and fp32 (MFMA
+// v_mfma_f32_16x16x4_f32). Every MFMA operand fragment is one 16-byte load per lane:
+//   - A fragment (M x K tile, 16 rows): lane l holds row (l % 16), elements k0 + VEC*(l/16) .. + VEC-1
+//   - B fragment (K x N tile, 16 cols): lane l holds col (l % 16), the same k range
+// so both operands are read from memory laid out with K contiguous. A bf16 fragment feeds one 16x16x32
+// MFMA; an fp32 fragment feeds four 16x16x4 MFMAs (step s uses k = k0 + 4*(l/16) + s on both operands,
+// a consistent permutation of the K index, which leaves the sum unchanged).
+// Accumulator (16x16 fp32): lane l holds column (l % 16), rows 4*(l/16) .. +3.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bf {
+
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+
+constexpr int WAVE = 64;
+
+__device__ __forceinline__ float bf2f(uint16_t x) { return __uint_as_float(((uint32_t)x) << 16); }
+__device__ __forceinline__ uint16_t f2bf(float f) {
+    __bf16 b = (__bf16)f;  // v_cvt_pk_bf16_f32: round to nearest even
+    return __builtin_bit_cast(uint16_t, b);
+}
+
+// Element-type traits. VEC = elements per 16-byte vector; KF = K covered by one fragment per MFMA group.
+struct BF16 {
+    using T = uint16_t;
+    static constexpr int VEC = 8;
+    static constexpr int KF = 32;
+    __device__ static __forceinline__ float to_f(T x) { return bf2f(x); }
+    __device__ static __forceinline__ T from_f(float f) { return f2bf(f); }
+};
+struct F32 {
+    using T = float;
+    static constexpr int VEC = 4;
+    static constexpr int KF = 16;
+    __device__ static __forceinline__ float to_f(T x) { return x; }
+    __device__ static __forceinline__ T from_f(float f) { return f; }
+};
+
+// acc += A(16 x KF) * B(KF x 16) for one fragment pair.
+template <class E>
+__device__ __forceinline__ void mma(f32x4& acc, const uint4& a, const uint4& b);
+
+template <>
+__device__ __forceinline__ void mma<BF16>(f32x4& acc, const uint4& a, const uint4& b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), acc,
+                                                   0, 0, 0);
+}
+template <>
+__device__ __forceinline__ void mma<F32>(f32x4& acc, const uint4& a, const uint4& b) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.x), __uint_as_float(b.x), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.y), __uint_as_float(b.y), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.z), __uint_as_float(b.z), acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.w), __uint_as_float(b.w), acc, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
+__device__ __forceinline__ void st16(void* p, const uint4& v) { *reinterpret_cast<uint4*>(p) = v; }
+__device__ __forceinline__ uint4 zero16() { return make_uint4(0u, 0u, 0u, 0u); }
+
+// Multiply the VEC elements of a 16-byte vector by s (through fp32), returning the same element type.
+template <class E>
+__device__ __forceinline__ uint4 scale16(const uint4& v, float s);
+template <>
+__device__ __forceinline__ uint4 scale16<F32>(const uint4& v, float s) {
+    return make_uint4(__float_as_uint(__uint_as_float(v.x) * s), __float_as_uint(__uint_as_float(v.y) * s),
+                      __float_as_uint(__uint_as_float(v.z) * s), __float_as_uint(__uint_as_float(v.w) * s));
+}
+__device__ __forceinline__ uint32_t scale_pair(uint32_t p, float s) {
+    float lo = __uint_as_float(p << 16) * s, hi = __uint_as_float(p & 0xffff0000u) * s;
+    return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+template <>
+__device__ __forceinline__ uint4 scale16<BF16>(const uint4& v, float s) {
+    return make_uint4(scale_pair(v.x, s), scale_pair(v.y, s), scale_pair(v.z, s), scale_pair(v.w, s));
+}
+
+// Store 4 consecutive fp32 values (an accumulator column segment) as element type E.
+template <class E>
+__device__ __forceinline__ void store4(typename E::T* p, float a, float b, float c, float d);
+template <>
+__device__ __forceinline__ void store4<F32>(float* p, float a, float b, float c, float d) {
+    *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+}
+template <>
+__device__ __forceinline__ void store4<BF16>(uint16_t* p, float a, float b, float c, float d) {
+    uint2 v;
+    v.x = (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+    v.y = (uint32_t)f2bf(c) | ((uint32_t)f2bf(d) << 16);
+    *reinterpret_cast<uint2*>(p) = v;
+}
+
+// Transpose a VEC x VEC block held as VEC 16-byte row vectors (rows[i] = row i) into column vectors.
+template <class E>
+__device__ __forceinline__ void transpose_block(uint4 (&r)[E::VEC]);
+template <>
+__device__ __forceinline__ void transpose_block<F32>(uint4 (&r)[4]) {
+    uint32_t m[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { m[i][0] = r[i].x; m[i][1] = r[i].y; m[i][2] = r[i].z; m[i][3] = r[i].w; }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[j] = make_uint4(m[0][j], m[1][j], m[2][j], m[3][j]);
+}
+template <>
+__device__ __forceinline__ void transpose_block<BF16>(uint4 (&r)[8]) {
+    uint16_t m[8][8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t w[4] = {r[i].x, r[i].y, r[i].z, r[i].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { m[i][2 * j] = (uint16_t)(w[j] & 0xffffu); m[i][2 * j + 1] = (uint16_t)(w[j] >> 16); }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = (uint32_t)m[2 * i][j] | ((uint32_t)m[2 * i + 1][j] << 16);
+        r[j] = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (WAVE - 1); }
+__device__ __forceinline__ int wave_id() { return threadIdx.x / WAVE; }
+
+// Sequence/chunk bookkeeping for packed variable-length input. cu (device, num_seqs + 1 entries) may be null, in
+// which case every sequence has length seq_len. Chunk ids enumerate the chunks of sequence 0, then 1, ...
+struct SeqInfo {
+    int seq;      // sequence index
+    int chunk;    // chunk index inside the sequence
+    long tok0;    // first token of the chunk (packed index)
+    int len;      // valid tokens in the chunk (1..C)
+};
+
+__device__ __forceinline__ bool locate_chunk(int cid, const int32_t* cu, int num_seqs, int seq_len, int C,
+                                             SeqInfo& out) {
+    int base = 0;
+    for (int n = 0; n < num_seqs; ++n) {
+        const long s0 = cu ? (long)cu[n] : (long)n * seq_len;
+        const long s1 = cu ? (long)cu[n + 1] : (long)(n + 1) * seq_len;
+        const int nc = (int)((s1 - s0 + C - 1) / C);
+        if (cid < base + nc) {
+            out.seq = n;
+            out.chunk = cid - base;
+            out.tok0 = s0 + (long)out.chunk * C;
+            const long rem = s1 - out.tok0;
+            out.len = rem < C ? (int)rem : C;
+            return true;
+        }
+        base += nc;
+    }
+    return false;
+}
+
+// First chunk id of sequence n and its chunk count.
+__device__ __forceinline__ void seq_chunks(int n, const int32_t* cu, int seq_len, int C, int& first, int& count,
+                                           long& tok0, long& tok1) {
+    int base = 0;
+    for (int m = 0; m < n; ++m) {
+        const long s0 = cu ? (long)cu[m] : (long)m * seq_len;
+        const long s1 = cu ? (long)cu[m + 1] : (long)(m + 1) * seq_len;
+        base += (int)((s1 - s0 + C - 1) / C);
+    }
+    tok0 = cu ? (long)cu[n] : (long)n * seq_len;
+    tok1 = cu ? (long)cu[n + 1] : (long)(n + 1) * seq_len;
+    first = base;
+    count = (int)((tok1 - tok0 + C - 1) / C);
+}
+
+}  // namespace bf

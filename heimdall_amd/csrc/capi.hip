@@ -1,0 +1,91 @@
+// C-ABI entry points of libbifrost_hip.so: argument checks, workspace carve-up, dispatch to the kernels.
+#include <hip/hip_runtime.h>
+
+#include "bf_internal.h"
+
+namespace {
+
+constexpr int kChunk = 64;
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+bool supported_dim(int D) { return D == 64 || D == 128 || D == 256; }
+bool supported_dtype(int dt) { return dt == BF_DTYPE_F32 || dt == BF_DTYPE_BF16; }
+size_t esize(int dt) { return dt == BF_DTYPE_BF16 ? 2 : 4; }
+
+struct GdnLayout {
+    size_t gcum, w, uT, kt, attn, total;
+    int max_chunks;
+};
+
+GdnLayout gdn_layout(int64_t total_tokens, int num_seqs, int G, int R, int D, int in_dtype) {
+    GdnLayout L;
+    // every sequence contributes ceil(len / C) chunks: at most total/C + num_seqs overall
+    L.max_chunks = (int)(total_tokens / kChunk) + num_seqs;
+    const size_t nc = (size_t)L.max_chunks, e = esize(in_dtype);
+    size_t off = 0;
+    L.gcum = off; off = align256(off + nc * G * kChunk * sizeof(float));
+    L.w = off;    off = align256(off + nc * G * kChunk * D * e);
+    L.uT = off;   off = align256(off + nc * G * D * kChunk * sizeof(float));
+    L.kt = off;   off = align256(off + nc * G * D * kChunk * e);
+    L.attn = off; off = align256(off + nc * G * R * kChunk * kChunk * e);
+    L.total = off;
+    return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+int bf_version(void) { return 100; }
+
+const char* bf_status_string(int status) {
+    switch (status) {
+        case BF_STATUS_OK: return "ok";
+        case BF_STATUS_INVALID: return "invalid argument (null pointer, bad size or inconsistent shape)";
+        case BF_STATUS_UNSUPPORTED: return "unsupported head dim, dtype or chunk size";
+        case BF_STATUS_WORKSPACE: return "workspace missing or too small";
+        default: break;
+    }
+    return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
+}
+
+int bf_gdn_workspace_size(int64_t total_tokens, int num_seqs, int G, int R, int D, int in_dtype, size_t* bytes) {
+    if (!bytes || total_tokens < 0 || num_seqs <= 0 || G <= 0 || R <= 0) return BF_STATUS_INVALID;
+    if (!supported_dim(D) || !supported_dtype(in_dtype)) return BF_STATUS_UNSUPPORTED;
+    *bytes = gdn_layout(total_tokens, num_seqs, G, R, D, in_dtype).total;
+    return BF_STATUS_OK;
+}
+
+int bf_gdn_fwd(const void* q, const void* k, const void* v, const float* g, const float* beta,
+               const int32_t* cu_seqlens, int num_seqs, int64_t total_tokens, int G, int R, int D, int in_dtype,
+               float scale, const float* initial_state, void* o, int o_dtype, float* final_state, void* workspace,
+               size_t workspace_bytes, int phases, void* stream) {
+    if (num_seqs <= 0 || total_tokens < 0 || G <= 0 || R <= 0 || (phases & ~BF_GDN_PHASE_ALL) || !phases)
+        return BF_STATUS_INVALID;
+    if (!supported_dim(D) || !supported_dtype(in_dtype) || !supported_dtype(o_dtype)) return BF_STATUS_UNSUPPORTED;
+    if (!cu_seqlens && total_tokens % num_seqs) return BF_STATUS_INVALID;
+    if (total_tokens > 0 && (!q || !k || !v || !g || !beta || !o)) return BF_STATUS_INVALID;
+    const GdnLayout L = gdn_layout(total_tokens, num_seqs, G, R, D, in_dtype);
+    if (!workspace || workspace_bytes < L.total) return BF_STATUS_WORKSPACE;
+    bf::GdnArgs a{};
+    a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta;
+    a.cu_seqlens = cu_seqlens;
+    a.num_seqs = num_seqs;
+    a.seq_len = cu_seqlens ? 0 : (int)(total_tokens / num_seqs);
+    a.total_tokens = total_tokens;
+    a.G = G; a.R = R; a.D = D;
+    a.in_dtype = in_dtype; a.o_dtype = o_dtype;
+    a.scale = scale;
+    a.s0 = initial_state; a.o = o; a.s_out = final_state;
+    a.max_chunks = L.max_chunks;
+    char* ws = static_cast<char*>(workspace);
+    a.ws_gcum = reinterpret_cast<float*>(ws + L.gcum);
+    a.ws_w = ws + L.w;
+    a.ws_uT = reinterpret_cast<float*>(ws + L.uT);
+    a.ws_kt = ws + L.kt;
+    a.ws_attn = ws + L.attn;
+    return bf::gdn_dispatch(a, phases, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

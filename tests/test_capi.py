@@ -1,0 +1,71 @@
+"""CPU checks of the C-ABI boundary: the library loads and exports every symbol declared in include/bifrost.h,
+argument errors come back as status codes without a GPU, and the ctypes signatures cover the header."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "bifrost.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(bf_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def cpu_lib():
+    from heimdall_amd import _lib
+    if not _lib.LIB_PATH.exists():                 # the build check builds it; a bare test run builds it here
+        from heimdall_amd.build import build_library
+        build_library()
+    return _lib.load()
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    assert "bf_gdn_fwd" in syms and "bf_gdn_workspace_size" in syms and len(syms) >= 4
+
+
+def test_library_exports_every_declared_symbol(cpu_lib):
+    missing = [s for s in declared_symbols() if not hasattr(cpu_lib, s)]
+    assert not missing, missing
+
+
+def test_ctypes_signatures_cover_header():
+    from heimdall_amd import _lib
+    assert sorted(_lib.SIGNATURES) == declared_symbols()
+
+
+def test_status_codes_without_gpu(cpu_lib):
+    assert cpu_lib.bf_version() >= 100
+    assert cpu_lib.bf_status_string(0) == b"ok"
+    n = ctypes.c_size_t(0)
+    assert cpu_lib.bf_gdn_workspace_size(4096, 1, 4, 1, 256, 1, ctypes.byref(n)) == 0 and n.value > 0
+    assert cpu_lib.bf_gdn_workspace_size(4096, 1, 4, 1, 96, 1, ctypes.byref(n)) == -2      # unsupported D
+    assert cpu_lib.bf_gdn_workspace_size(4096, 0, 4, 1, 256, 1, ctypes.byref(n)) == -1     # no sequences
+    # argument errors are reported before anything is launched (null workspace)
+    st = cpu_lib.bf_gdn_fwd(1, 1, 1, 1, 1, None, 1, 64, 4, 1, 256, 1, 1.0, None, 1, 0, None, None, 0, 3, None)
+    assert st == -3
+    st = cpu_lib.bf_gdn_fwd(1, 1, 1, 1, 1, None, 3, 64, 4, 1, 256, 1, 1.0, None, 1, 0, None, None, 0, 3, None)
+    assert st == -1                                                                          # 64 % 3 != 0
+
+
+def test_workspace_size_grows_with_tokens(cpu_lib):
+    a, b = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    cpu_lib.bf_gdn_workspace_size(4096, 1, 4, 1, 256, 1, ctypes.byref(a))
+    cpu_lib.bf_gdn_workspace_size(8192, 1, 4, 1, 256, 1, ctypes.byref(b))
+    assert b.value > a.value
+
+
+def test_product_has_no_cpu_path():
+    """The operators refuse CPU tensors instead of falling back."""
+    import torch
+    from heimdall_amd import kernels
+    from heimdall_amd._lib import BifrostError
+    q = torch.zeros(1, 4, 1, 64)
+    with pytest.raises(BifrostError):
+        kernels.delta_rule(q, q, q, torch.zeros(1, 4, 1), torch.zeros(1, 4, 1))

@@ -1,0 +1,190 @@
+#!/usr/bin/env python3
+"""Benchmark of the Bifrost core on one MI355X.
+
+Headline workload (one step = one pass of the hot path over one batch of synthetic input):
+  chunked gated delta-rule prefill, B=1, T=32768, H=4 (one state per head), D_k=D_v=256, chunk 64,
+  bf16 q/k/v (k L2-normalised, q unscaled, scale 1), beta = sigmoid(N(0,1)), g ~ U[-1e-3, 0], fp32 state and
+  accumulation, zero initial state; outputs o [1, T, 4, 256] fp32 and the final 4 x 256 x 256 fp32 state.
+  Inputs are resident in HBM before the timed region. value = tokens/s.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+Prints ONE JSON line. Only one GPU is supported (--gpus > 1 exits with a message).
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+import torch
+import torch.nn.functional as F
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "Bifrost-layer prefill tokens/s @32K; decode µs/step @B=64; % of MFMA/HBM roofline"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16 MFMA, TFLOP/s
+C = 64
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def make_inputs(T, H, D, dev, seed=0):
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    q = torch.randn(T, H, D, device=dev, generator=gen).bfloat16()
+    k = F.normalize(torch.randn(T, H, D, device=dev, generator=gen), dim=-1).bfloat16()
+    v = torch.randn(T, H, D, device=dev, generator=gen).bfloat16()
+    beta = torch.sigmoid(torch.randn(T, H, device=dev, generator=gen))
+    g = -torch.rand(T, H, device=dev, generator=gen) * 1e-3
+    return q, k, v, g, beta
+
+
+def gdn_flops(T, H, D):
+    """Algorithmic FLOPs per phase of the chunked form (per chunk and head): prep = KK^T, QK^T, Tm(beta v),
+    Tm(beta k e^g): 4 * 2C^2D; scan = wS, qS, k_tail^T v_new: 3 * 2CD^2, plus attn v_new: 2C^2D."""
+    chunks = (T + C - 1) // C
+    prep = 8 * C * C * D * chunks * H
+    scan = (6 * C * D * D + 2 * C * C * D) * chunks * H
+    return prep, scan
+
+
+def gdn_bytes(T, H, D):
+    """Algorithmic HBM bytes of the whole operator: bf16 q, k, v in; fp32 g, beta in; fp32 o and state out."""
+    return T * H * D * 2 * 3 + T * H * 4 * 2 + T * H * D * 4 + H * D * D * 4
+
+
+def traffic_from_profile(kernel: str):
+    """HBM bytes per launch of `kernel` measured by the rocprofv3 FETCH_SIZE / WRITE_SIZE runs (profiles/)."""
+    p = ROOT / "profiles" / "traffic.json"
+    try:
+        return json.loads(p.read_text()).get(kernel)
+    except (OSError, ValueError):
+        return None
+
+
+def run_gdn(steps, warmup, dev):
+    from heimdall_amd import _lib
+    from heimdall_amd._device import gdn_forward, workspace
+
+    T, H, D = 32768, 4, 256
+    q, k, v, g, beta = make_inputs(T, H, D, dev)
+    o = torch.empty(T, H, D, dtype=torch.float32, device=dev)
+    s = torch.empty(1, H, D, D, dtype=torch.float32, device=dev)
+    nbytes = _lib.ctypes.c_size_t(0)
+    _lib.check(_lib.load().bf_gdn_workspace_size(T, 1, H, 1, D, _lib.DTYPE_BF16, _lib.ctypes.byref(nbytes)),
+               "bf_gdn_workspace_size")
+    ws = workspace(nbytes.value, dev)
+
+    def phase(p):
+        gdn_forward(q, k, v, g, beta, num_seqs=1, out=o, final_state=s, ws=ws, phases=p)
+
+    for _ in range(warmup):
+        phase(_lib.PHASE_PREP)
+        phase(_lib.PHASE_SCAN)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record(stream)
+        phase(_lib.PHASE_PREP)
+        ev[i][1].record(stream)
+        phase(_lib.PHASE_SCAN)
+        ev[i][2].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    prep_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
+    scan_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / steps
+    return dict(T=T, H=H, D=D, wall=wall, prep_ms=prep_ms, scan_ms=scan_ms, inputs=(q, k, v, g, beta))
+
+
+def cpu_baseline(inputs, budget_s=30.0):
+    """The oracle (fp32 PyTorch restatement of the reference's chunked delta rule) on the host cores, on the same
+    workload (full T=32768) as long as one run fits the budget, else on a prefix."""
+    from oracle import gdn
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    q, k, v, g, beta = (z.detach().float().cpu()[None] for z in inputs)
+    T = q.shape[1]
+    t = time.perf_counter()
+    gdn.delta_rule_chunked(q[:, :4096], k[:, :4096], v[:, :4096], g[:, :4096], beta[:, :4096], 64)   # warm-up
+    per_4k = (time.perf_counter() - t) * 1.5          # cost grows slightly faster than linearly in T
+    n = T
+    while n > 4096 and per_4k * n / 4096 > budget_s / 2:
+        n //= 2
+    times = []
+    for _ in range(3):
+        t = time.perf_counter()
+        gdn.delta_rule_chunked(q[:, :n], k[:, :n], v[:, :n], g[:, :n], beta[:, :n], 64)
+        times.append(time.perf_counter() - t)
+        if sum(times) > budget_s:
+            break
+    best = sorted(times)[len(times) // 2]
+    return {"value": n / best, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle delta_rule_chunked fp32, T={n} H=4 D=256 (same synthetic inputs), median of "
+                      f"{len(times)} run(s), {cpu_model()}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the Bifrost core needs no inter-GPU exchange; "
+              "see the sharding notes in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    r = run_gdn(args.steps, args.warmup, dev)
+    T, H, D = r["T"], r["H"], r["D"]
+    ms = r["wall"] * 1e3 / args.steps
+    prep_f, scan_f = gdn_flops(T, H, D)
+    dom = "scan" if r["scan_ms"] >= r["prep_ms"] else "prep"
+    dom_ms = r[dom + "_ms"]
+    dom_f = scan_f if dom == "scan" else prep_f
+    achieved = dom_f / (dom_ms * 1e-3) / 1e12
+    line = {
+        "metric": METRIC,
+        "value": T / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "gdn_prefill", "B": 1, "T": T, "H": H, "G": H, "D": D, "chunk": C,
+                   "inputs": "bf16 q/k/v, fp32 g/beta/state/output", "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": f"gdn_{dom}_kernel", "achieved": achieved, "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS,
+                     "traffic": traffic_from_profile(f"gdn_{dom}_kernel")},
+        "phases_ms": {"prep": r["prep_ms"], "scan": r["scan_ms"]},
+        "hbm": {"algorithmic_bytes": gdn_bytes(T, H, D),
+                "achieved_GBs": gdn_bytes(T, H, D) / (ms * 1e-3) / 1e9, "peak_GBs": HBM_PEAK_GBS},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(r["inputs"])
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

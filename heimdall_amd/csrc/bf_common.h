@@ -123,6 +123,10 @@ __device__ __forceinline__ void transpose_block<BF16>(uint4 (&r)[8]) {
     }
 }
 
+// s_waitcnt vmcnt(0): all outstanding vector-memory operations of the wave have completed. Used before a loop whose
+// first iteration consumes loads issued ahead of it, so the compiler's wait analysis at the loop header starts clean.
+__device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (WAVE - 1); }
 __device__ __forceinline__ int wave_id() { return threadIdx.x / WAVE; }
 
@@ -168,6 +172,46 @@ __device__ __forceinline__ void seq_chunks(int n, const int32_t* cu, int seq_len
     tok1 = cu ? (long)cu[n + 1] : (long)(n + 1) * seq_len;
     first = base;
     count = (int)((tok1 - tok0 + C - 1) / C);
+}
+
+}  // namespace bf
+
+namespace bf {
+
+// Buffer-resource memory access: the (uniform) base address and byte range live in an SGPR descriptor, each lane
+// supplies a 32-bit byte offset. Loads outside [0, nbytes) return 0 and stores outside are dropped, which the
+// kernels use for rows past the end of a sequence.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;   // raw (untyped) 32-bit buffer, gfx9-family layout
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t nbytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)nbytes, kRsrcWord3);
+}
+__device__ __forceinline__ uint4 buf_ld16(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ float4 buf_ldf4(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+__device__ __forceinline__ float buf_ldf(rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+}
+__device__ __forceinline__ void buf_stf(rsrc_t r, uint32_t off, float v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, 0);
+}
+__device__ __forceinline__ void buf_sth(rsrc_t r, uint32_t off, uint16_t v) {
+    __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, 0);
+}
+__device__ __forceinline__ void buf_st16(rsrc_t r, uint32_t off, const uint4& v) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, v), r,
+                                           off, 0, 0);
+}
+
+// Store one fp32 value as the output element type (fp32 or bf16) through a buffer descriptor.
+template <bool BF16OUT>
+__device__ __forceinline__ void buf_st_out(rsrc_t r, uint32_t elem, float v) {
+    if constexpr (BF16OUT) buf_sth(r, elem * 2u, f2bf(v));
+    else buf_stf(r, elem * 4u, v);
 }
 
 }  // namespace bf

@@ -207,6 +207,18 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(GdnArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------------ sequential scan
+// 8 waves per workgroup, specialised:
+//   row waves   (0-3): wave w owns chunk rows 16w..16w+15: v_new = u - w S (step 1); the outputs
+//                      o = scale e^{gc} q S_old + attn v_new (step 3).
+//   state waves (4-7): wave w owns state row tiles (w-4) + 4i: S = e^{gc_last} S + kt v_new (step 2), reading
+//                      each v_new fragment once for all of its row tiles.
+// Per chunk: step 1 | barrier | step 2 || step 3 | barrier.
+// Prefetch: each wave issues the loads of its next-chunk operand fragments at the start of the current chunk and
+// copies them into its current set after the chunk's work, so the only memory wait sits at the end of the chunk.
+// Chunk operands are read through buffer descriptors (uniform base in SGPRs, 32-bit lane offsets); rows past the end
+// of a sequence read as zero and their output stores are dropped by the descriptor's range.
+constexpr int NT_SCAN = 512;
+
 template <class E, int D, int BV>
 struct ScanShared {
     typename E::T sT[2][BV][D + E::VEC];   // S^T slab (double buffered): [column j][row d]
@@ -214,31 +226,269 @@ struct ScanShared {
 };
 
 template <class E, int D, int BV>
-__global__ __launch_bounds__(NT) void gdn_scan_kernel(GdnArgs a) {
-    using T = typename E::T;
-    constexpr int VEC = E::VEC, KF = E::KF;
-    constexpr int NCT = BV / 16;          // column tiles of the slab
-    constexpr int NRT = D / 16;           // row tiles of S
-    constexpr int RPW = (NRT + 3) / 4;    // S row tiles per wave
-    constexpr int NKD = D / KF;           // fragments along D
-    constexpr int NKC = CH / KF;          // fragments along the chunk
+struct RowFrags {                         // row-wave operands of one chunk
+    static constexpr int NKD = D / E::KF, NKC = CH / E::KF, NCT = BV / 16;
+    uint4 w[NKD];          // w rows (A operand of w S)
+    uint4 at[NKC];         // attn rows of query head r = 0
+    float4 u[NCT];         // u^T[j][t..t+3]
+    float4 gq;             // gc of accumulator rows 16w + 4lg .. +3
+};
+
+template <class E, int D, int BV>
+struct StateFrags {                       // state-wave operands of one chunk
+    static constexpr int NKC = CH / E::KF, RPW = (D / 16 + 3) / 4;
+    uint4 kt[RPW][NKC];    // kt rows of this wave's state row tiles
+    float gc;              // gc of row `lane` (vector load; a scalar load would be waited on at every barrier)
+};
+
+struct ChunkPos {
+    long cid, t0;
+    int len;
+};
+
+__device__ __forceinline__ ChunkPos chunk_pos(int c, int first, long tok0, long tok1) {
+    ChunkPos p;
+    p.cid = first + c;
+    p.t0 = tok0 + (long)c * CH;
+    p.len = (int)((tok1 - p.t0) < CH ? (tok1 - p.t0) : CH);
+    return p;
+}
+
+template <class E, int D>
+__device__ __forceinline__ rsrc_t q_rsrc(const GdnArgs& a, const ChunkPos& p, int h) {
+    const long H = (long)a.G * a.R, es = sizeof(typename E::T);
+    return make_rsrc(reinterpret_cast<const char*>(a.q) + (p.t0 * H + h) * D * es, (uint32_t)(p.len * H * D * es));
+}
+
+template <class E>
+__device__ __forceinline__ rsrc_t attn_rsrc(const GdnArgs& a, const ChunkPos& p, int h) {
+    constexpr int ES = sizeof(typename E::T);
+    const long H = (long)a.G * a.R;
+    return make_rsrc(reinterpret_cast<const char*>(a.ws_attn) + (p.cid * H + h) * CH * CH * ES, CH * CH * ES);
+}
+
+template <class E, int D, int BV>
+__device__ __forceinline__ void load_rows(RowFrags<E, D, BV>& f, const GdnArgs& a, const ChunkPos& p, int g, int j0,
+                                          int wv, int l16, int lg) {
+    using F = RowFrags<E, D, BV>;
+    constexpr int VEC = E::VEC, KF = E::KF, ES = sizeof(typename E::T);
+    const int G = a.G, H = G * a.R, h = g * a.R;
+    const int t = 16 * wv + l16;
+    const rsrc_t rw = make_rsrc(reinterpret_cast<const char*>(a.ws_w) + (p.cid * G + g) * CH * D * ES, CH * D * ES);
+#pragma unroll
+    for (int kf = 0; kf < F::NKD; ++kf) f.w[kf] = buf_ld16(rw, (t * D + VEC * lg + kf * KF) * ES);
+    const rsrc_t ra = attn_rsrc<E>(a, p, h);
+#pragma unroll
+    for (int kf = 0; kf < F::NKC; ++kf) f.at[kf] = buf_ld16(ra, (t * CH + VEC * lg + kf * KF) * ES);
+    const rsrc_t ru = make_rsrc(a.ws_uT + (p.cid * G + g) * D * CH, D * CH * 4);
+#pragma unroll
+    for (int ct = 0; ct < F::NCT; ++ct) f.u[ct] = buf_ldf4(ru, ((j0 + 16 * ct + l16) * CH + 16 * wv + 4 * lg) * 4);
+    const rsrc_t rg = make_rsrc(a.ws_gcum + (p.cid * G + g) * CH, CH * 4);
+    f.gq = buf_ldf4(rg, (16 * wv + 4 * lg) * 4);
+}
+
+template <class E, int D, int BV>
+__device__ __forceinline__ void load_state(StateFrags<E, D, BV>& f, const GdnArgs& a, const ChunkPos& p, int g,
+                                           int ws, int l16, int lg) {
+    using F = StateFrags<E, D, BV>;
+    constexpr int VEC = E::VEC, KF = E::KF, ES = sizeof(typename E::T);
+    const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.ws_kt) + (p.cid * a.G + g) * D * CH * ES,
+                                D * CH * ES);
+#pragma unroll
+    for (int ri = 0; ri < F::RPW; ++ri) {
+        const int rt = ws + 4 * ri < D / 16 ? ws + 4 * ri : 0;
+#pragma unroll
+        for (int kf = 0; kf < F::NKC; ++kf) f.kt[ri][kf] = buf_ld16(rk, ((16 * rt + l16) * CH + VEC * lg + kf * KF) * ES);
+    }
+    const rsrc_t rg = make_rsrc(a.ws_gcum + (p.cid * a.G + g) * CH, CH * 4);
+    f.gc = buf_ldf(rg, lane_id() * 4);
+}
+
+// acc(rows 16*wv.., BV columns) += A(rows, D) S_old.
+template <class E, int D, int BV>
+__device__ __forceinline__ void times_state(const ScanShared<E, D, BV>& sm, int buf, const uint4 (&a0)[D / E::KF],
+                                            f32x4 (&c0)[BV / 16], int l16, int lg) {
+    constexpr int VEC = E::VEC, KF = E::KF, NCT = BV / 16, NKD = D / E::KF;
+#pragma unroll
+    for (int kf = 0; kf < NKD; ++kf)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) mma<E>(c0[ct], a0[kf], ld16(&sm.sT[buf][16 * ct + l16][kf * KF + VEC * lg]));
+}
+
+// acc += attn_rows(16 x C) v_new(C x BV), then store the rows (row i of acc scaled by rs[i] before the add).
+template <class E, int D, int BV, bool BO>
+__device__ __forceinline__ void finish_output(const ScanShared<E, D, BV>& sm, const uint4 (&fa)[CH / E::KF],
+                                              f32x4 (&acc)[BV / 16], const float4& rs, const GdnArgs& a,
+                                              const ChunkPos& p, int h, int j0, int wv, int l16, int lg) {
+    constexpr int VEC = E::VEC, KF = E::KF, NCT = BV / 16, NKC = CH / E::KF;
+    constexpr int OS = BO ? 2 : 4;
+    const int H = a.G * a.R;
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+        acc[ct][0] *= rs.x;
+        acc[ct][1] *= rs.y;
+        acc[ct][2] *= rs.z;
+        acc[ct][3] *= rs.w;
+    }
+#pragma unroll
+    for (int kf = 0; kf < NKC; ++kf)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) mma<E>(acc[ct], fa[kf], ld16(&sm.vnT[16 * ct + l16][kf * KF + VEC * lg]));
+    const rsrc_t ro = make_rsrc(reinterpret_cast<char*>(a.o) + (p.t0 * H + h) * (long)D * OS,
+                                (uint32_t)((long)p.len * H * D * OS));
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) buf_st_out<BO>(ro, (16 * wv + 4 * lg + i) * H * D + j0 + 16 * ct + l16, acc[ct][i]);
+}
+
+template <class E, int D, int BV, bool BO>
+__device__ __forceinline__ void rows_loop(ScanShared<E, D, BV>& sm, const GdnArgs& a, int count, int first, long tok0,
+                                          long tok1, int g, int j0, int wv, int lane) {
+    using F = RowFrags<E, D, BV>;
+    constexpr int VEC = E::VEC, KF = E::KF, NCT = F::NCT, NKD = F::NKD, NKC = F::NKC, ES = sizeof(typename E::T);
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int t = 16 * wv + l16;
+    const int G = a.G, R = a.R, H = G * R;
+    F cur;
+    if (count > 0) load_rows<E, D, BV>(cur, a, chunk_pos(0, first, tok0, tok1), g, j0, wv, l16, lg);
+    wait_vmem_all();
+    __syncthreads();                                      // initial S^T written by the state waves
+    for (int c = 0; c < count; ++c) {
+        const int buf = c & 1;
+        const ChunkPos p = chunk_pos(c, first, tok0, tok1);
+        // the next-chunk prefetch is unconditional (the last chunk re-reads itself): a conditional prefetch makes the
+        // compiler's wait counts cover both paths and drain the prefetch early
+        const int cn = c + 1 < count ? c + 1 : c;
+        // q rows of query head 0 for this chunk (used in step 3), issued ahead of the next-chunk prefetch
+        uint4 fq0[NKD];
+        {
+            const rsrc_t rq = q_rsrc<E, D>(a, p, g * R);
+#pragma unroll
+            for (int kf = 0; kf < NKD; ++kf) fq0[kf] = buf_ld16(rq, (t * H * D + VEC * lg + kf * KF) * ES);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        F nxt;
+        load_rows<E, D, BV>(nxt, a, chunk_pos(cn, first, tok0, tok1), g, j0, wv, l16, lg);
+
+        // step 1: v_new = u - w S
+        f32x4 av[NCT], ao[NCT];
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) av[ct] = ao[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+        times_state<E, D, BV>(sm, buf, cur.w, av, l16, lg);
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) {
+            const float4 u = cur.u[ct];
+            store4<E>(&sm.vnT[16 * ct + l16][16 * wv + 4 * lg], u.x - av[ct][0], u.y - av[ct][1], u.z - av[ct][2],
+                      u.w - av[ct][3]);
+        }
+        // row factors scale * e^{gc} of the accumulator rows
+        const float4 rs = make_float4(a.scale * __expf(cur.gq.x), a.scale * __expf(cur.gq.y),
+                                      a.scale * __expf(cur.gq.z), a.scale * __expf(cur.gq.w));
+        __syncthreads();
+
+        // step 3: o_0 = q_0 S_old (row-scaled) + attn_0 v_new; further query heads of the group (R > 1) likewise
+        times_state<E, D, BV>(sm, buf, fq0, ao, l16, lg);
+        finish_output<E, D, BV, BO>(sm, cur.at, ao, rs, a, p, g * R, j0, wv, l16, lg);
+        for (int r = 1; r < R; ++r) {
+            const int h = g * R + r;
+            uint4 fq[NKD], fa[NKC];
+            const rsrc_t rq = q_rsrc<E, D>(a, p, h);
+#pragma unroll
+            for (int kf = 0; kf < NKD; ++kf) fq[kf] = buf_ld16(rq, (t * H * D + VEC * lg + kf * KF) * ES);
+            const rsrc_t ra = attn_rsrc<E>(a, p, h);
+#pragma unroll
+            for (int kf = 0; kf < NKC; ++kf) fa[kf] = buf_ld16(ra, (t * CH + VEC * lg + kf * KF) * ES);
+            f32x4 o2[NCT];
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) o2[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+            times_state<E, D, BV>(sm, buf, fq, o2, l16, lg);
+            finish_output<E, D, BV, BO>(sm, fa, o2, rs, a, p, h, j0, wv, l16, lg);
+        }
+        __syncthreads();
+        cur = nxt;
+    }
+}
+
+template <class E, int D, int BV>
+__device__ __forceinline__ void state_loop(ScanShared<E, D, BV>& sm, f32x4 (&S)[StateFrags<E, D, BV>::RPW][BV / 16],
+                                           const GdnArgs& a, int count, int first, long tok0, long tok1, int g, int ws,
+                                           int lane) {
+    using F = StateFrags<E, D, BV>;
+    constexpr int VEC = E::VEC, KF = E::KF, NCT = BV / 16, NKC = F::NKC, RPW = F::RPW;
+    const int l16 = lane & 15, lg = lane >> 4;
+    F cur;
+    if (count > 0) load_state<E, D, BV>(cur, a, chunk_pos(0, first, tok0, tok1), g, ws, l16, lg);
+    wait_vmem_all();
+    __syncthreads();
+    for (int c = 0; c < count; ++c) {
+        const int buf = c & 1;
+        const int cn = c + 1 < count ? c + 1 : c;
+        F nxt;
+        load_state<E, D, BV>(nxt, a, chunk_pos(cn, first, tok0, tok1), g, ws, l16, lg);
+        const float decay = __expf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(cur.gc), CH - 1)));
+        __syncthreads();
+        // step 2: S = e^{gc_last} S + kt v_new, each v_new fragment read once for all row tiles
+        f32x4 acc[RPW][NCT];
+#pragma unroll
+        for (int ri = 0; ri < RPW; ++ri)
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) acc[ri][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kf = 0; kf < NKC; ++kf)
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) {
+                const uint4 b = ld16(&sm.vnT[16 * ct + l16][kf * KF + VEC * lg]);
+#pragma unroll
+                for (int ri = 0; ri < RPW; ++ri)
+                    if (ws + 4 * ri < D / 16) mma<E>(acc[ri][ct], cur.kt[ri][kf], b);
+            }
+#pragma unroll
+        for (int ri = 0; ri < RPW; ++ri) {
+            const int rt = ws + 4 * ri;
+            if (rt < D / 16) {
+#pragma unroll
+                for (int ct = 0; ct < NCT; ++ct) {
+                    f32x4 s = S[ri][ct];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) s[i] = decay * s[i] + acc[ri][ct][i];
+                    S[ri][ct] = s;
+                    store4<E>(&sm.sT[buf ^ 1][16 * ct + l16][16 * rt + 4 * lg], s[0], s[1], s[2], s[3]);
+                }
+            }
+        }
+        __syncthreads();
+        cur = nxt;
+    }
+}
+
+template <class E, int D, int BV, bool BO>
+__global__ __launch_bounds__(NT_SCAN) void gdn_scan_kernel(GdnArgs a) {
+    using SF = StateFrags<E, D, BV>;
+    constexpr int NCT = BV / 16, NRT = D / 16, RPW = SF::RPW;
     __shared__ ScanShared<E, D, BV> sm;
 
     const int jb = blockIdx.x, g = blockIdx.y, n = blockIdx.z;
-    const int G = a.G, R = a.R, H = G * R;
-    const int lane = lane_id(), wv = wave_id(), l16 = lane & 15, lg = lane >> 4;
+    const int G = a.G;
+    const int lane = lane_id(), wv = wave_id(), lg = lane >> 4, l16 = lane & 15;
     const int j0 = jb * BV;
     int first, count;
     long tok0, tok1;
     seq_chunks(n, a.cu_seqlens, a.seq_len, CH, first, count, tok0, tok1);
 
-    // state slab in registers: tile (rt = wv + 4*ri, ct) holds S[16rt + 4lg + i][j0 + 16ct + l16]
+    if (wv < 4) {
+        rows_loop<E, D, BV, BO>(sm, a, count, first, tok0, tok1, g, j0, wv, lane);
+        return;
+    }
+
+    // state waves: the slab of S in registers, tile (rt = ws + 4*ri, ct) holds S[16rt + 4lg + i][j0 + 16ct + l16]
+    const int ws = wv - 4;
     f32x4 S[RPW][NCT];
 #pragma unroll
     for (int ri = 0; ri < RPW; ++ri)
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct) {
-            const int rt = wv + 4 * ri;
+            const int rt = ws + 4 * ri;
             f32x4 v = {0.f, 0.f, 0.f, 0.f};
             if (a.s0 && rt < NRT) {
                 const float* p = a.s0 + (((long)n * G + g) * D + 16 * rt + 4 * lg) * D + j0 + 16 * ct + l16;
@@ -248,107 +498,13 @@ __global__ __launch_bounds__(NT) void gdn_scan_kernel(GdnArgs a) {
             S[ri][ct] = v;
             if (rt < NRT) store4<E>(&sm.sT[0][16 * ct + l16][16 * rt + 4 * lg], v[0], v[1], v[2], v[3]);
         }
-    __syncthreads();
-
-    const T* Wb = reinterpret_cast<const T*>(a.ws_w);
-    const T* KTb = reinterpret_cast<const T*>(a.ws_kt);
-    const T* ATb = reinterpret_cast<const T*>(a.ws_attn);
-    const T* Qb = reinterpret_cast<const T*>(a.q);
-
-    for (int c = 0; c < count; ++c) {
-        const int cur = c & 1;
-        const long cid = first + c;
-        const long t0 = tok0 + (long)c * CH;
-        const int len = (int)((tok1 - t0) < CH ? (tok1 - t0) : CH);
-        const float* gcum = a.ws_gcum + (cid * G + g) * CH;
-
-        // ---- step 1: v_new rows 16*wv.. = u - w S   (A = w rows, B = S^T)
-        {
-            const T* W = Wb + (cid * G + g) * CH * D + (long)(16 * wv + l16) * D;
-            uint4 fw[NKD];
-#pragma unroll
-            for (int kf = 0; kf < NKD; ++kf) fw[kf] = ld16(W + kf * KF + VEC * lg);
-            const float* UT = a.ws_uT + (cid * G + g) * D * CH;
-#pragma unroll
-            for (int ct = 0; ct < NCT; ++ct) {
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int kf = 0; kf < NKD; ++kf) mma<E>(acc, fw[kf], ld16(&sm.sT[cur][16 * ct + l16][kf * KF + VEC * lg]));
-                const float4 u = *reinterpret_cast<const float4*>(UT + (long)(j0 + 16 * ct + l16) * CH + 16 * wv + 4 * lg);
-                store4<E>(&sm.vnT[16 * ct + l16][16 * wv + 4 * lg], u.x - acc[0], u.y - acc[1], u.z - acc[2],
-                          u.w - acc[3]);
-            }
-        }
-        __syncthreads();
-
-        // ---- step 2: S = e^{gc_last} S + kt v_new   (A = kt rows d, B = v_new^T) -> next S^T buffer
-        {
-            const float decay = __expf(gcum[CH - 1]);
-            const T* KT = KTb + (cid * G + g) * D * CH;
-#pragma unroll
-            for (int ri = 0; ri < RPW; ++ri) {
-                const int rt = wv + 4 * ri;
-                if (rt >= NRT) break;
-                uint4 fk[NKC];
-#pragma unroll
-                for (int kf = 0; kf < NKC; ++kf) fk[kf] = ld16(KT + (long)(16 * rt + l16) * CH + kf * KF + VEC * lg);
-#pragma unroll
-                for (int ct = 0; ct < NCT; ++ct) {
-                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int kf = 0; kf < NKC; ++kf) mma<E>(acc, fk[kf], ld16(&sm.vnT[16 * ct + l16][kf * KF + VEC * lg]));
-                    f32x4 s = S[ri][ct];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) s[i] = decay * s[i] + acc[i];
-                    S[ri][ct] = s;
-                    store4<E>(&sm.sT[cur ^ 1][16 * ct + l16][16 * rt + 4 * lg], s[0], s[1], s[2], s[3]);
-                }
-            }
-        }
-
-        // ---- step 3: outputs rows 16*wv..: o_r = scale e^{gc} q_r S_old + attn_r v_new
-        {
-            const int t = 16 * wv + l16;                 // A-fragment row of this lane
-            const float qs = a.scale * __expf(gcum[t]);
-            for (int r = 0; r < R; ++r) {
-                const int h = g * R + r;
-                const T* Q = Qb + (t0 + t) * (long)H * D + (long)h * D;
-                uint4 fq[NKD];
-#pragma unroll
-                for (int kf = 0; kf < NKD; ++kf) fq[kf] = t < len ? scale16<E>(ld16(Q + kf * KF + VEC * lg), qs) : zero16();
-                const T* AT = ATb + ((cid * H + h) * CH + t) * CH;
-                uint4 fa[NKC];
-#pragma unroll
-                for (int kf = 0; kf < NKC; ++kf) fa[kf] = ld16(AT + kf * KF + VEC * lg);
-#pragma unroll
-                for (int ct = 0; ct < NCT; ++ct) {
-                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                    for (int kf = 0; kf < NKD; ++kf) mma<E>(acc, fq[kf], ld16(&sm.sT[cur][16 * ct + l16][kf * KF + VEC * lg]));
-#pragma unroll
-                    for (int kf = 0; kf < NKC; ++kf) mma<E>(acc, fa[kf], ld16(&sm.vnT[16 * ct + l16][kf * KF + VEC * lg]));
-                    const int j = j0 + 16 * ct + l16;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int tr = 16 * wv + 4 * lg + i;
-                        if (tr < len) {
-                            const long off = (t0 + tr) * (long)H * D + (long)h * D + j;
-                            if (a.o_dtype == DT_F32) reinterpret_cast<float*>(a.o)[off] = acc[i];
-                            else reinterpret_cast<uint16_t*>(a.o)[off] = f2bf(acc[i]);
-                        }
-                    }
-                }
-            }
-        }
-        __syncthreads();
-    }
-
+    state_loop<E, D, BV>(sm, S, a, count, first, tok0, tok1, g, ws, lane);
     if (a.s_out) {
 #pragma unroll
         for (int ri = 0; ri < RPW; ++ri)
 #pragma unroll
             for (int ct = 0; ct < NCT; ++ct) {
-                const int rt = wv + 4 * ri;
+                const int rt = ws + 4 * ri;
                 if (rt >= NRT) continue;
                 float* p = a.s_out + (((long)n * G + g) * D + 16 * rt + 4 * lg) * D + j0 + 16 * ct + l16;
 #pragma unroll
@@ -366,7 +522,9 @@ static int launch_gdn(const GdnArgs& a, int phases, hipStream_t stream) {
         if (e != hipSuccess) return (int)e;
     }
     if (phases & GDN_PHASE_SCAN) {
-        hipLaunchKernelGGL((gdn_scan_kernel<E, D, BV>), dim3(D / BV, a.G, a.num_seqs), dim3(NT), 0, stream, a);
+        const dim3 grid(D / BV, a.G, a.num_seqs);
+        if (a.o_dtype == DT_BF16) hipLaunchKernelGGL((gdn_scan_kernel<E, D, BV, true>), grid, dim3(NT_SCAN), 0, stream, a);
+        else hipLaunchKernelGGL((gdn_scan_kernel<E, D, BV, false>), grid, dim3(NT_SCAN), 0, stream, a);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return (int)e;
     }

@@ -19,6 +19,9 @@ SIGNATURES = {
     "bf_gdn_workspace_size": (_c_int, [_c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, ctypes.POINTER(_c_sz)]),
     "bf_gdn_fwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_int, _fp, _vp,
                             _vp, _c_int, _vp, _vp, _c_sz, _c_int, _vp]),
+    "bf_gdn_step": (_c_int, [_vp] * 8 + [_c_int] * 4 + [_vp]),
+    "bf_decode_workspace_size": (_c_int, [_c_int] * 5 + [ctypes.POINTER(_c_sz)]),
+    "bf_decode_fwd": (_c_int, [_c_int] * 6 + [_c_i64] + [_c_int] * 3 + [_vp] * 12 + [_c_int] + [_vp] * 10 + [_c_sz, _vp]),
 }
 
 _LIB = None

@@ -41,4 +41,52 @@ struct GdnArgs {
 
 int gdn_dispatch(const GdnArgs& a, int phases, hipStream_t stream);
 
+struct DecodeArgs {
+    int B, G, R, D, W, sinks;
+    long pos;                 // absolute position of the new token (same for all sequences)
+    int mem_on;               // memory branch active: pos >= W and memory enabled
+    int kv_dtype, q_dtype;
+    const void* qr;           // [B][H][D] q_dtype
+    const float* qm;          // [B][H][D]
+    const void* kr;           // [B][G][D] kv_dtype
+    const void* v;            // [B][G][D] kv_dtype
+    const float* km;          // [B][G][D]
+    const float* g_new;       // [B][G]
+    const float* beta_new;    // [B][G]
+    const float* z;           // [B][H] mix logits
+    const float* mix_lse;     // [H]
+    const float* mem_scale;   // [H]
+    const void* sink_k;       // [B][G][n_sinks][D] kv_dtype
+    const void* sink_v;
+    int n_sinks;
+    void* ring_k;             // [B][G][W][D] kv_dtype
+    void* ring_v;
+    float* ring_km;           // [B][W][G][D]
+    float* ring_g;            // [B][W][G]
+    float* ring_beta;         // [B][W][G]
+    int64_t* ring_pos;        // [W]
+    float* state;             // [B][G][D][D]
+    float* o;                 // [B][H][D]
+    float* lse;               // [B][H] or null
+    int nsplit;               // window splits of 256 ring slots
+    float* ws_om;             // [B][H][D] memory read
+    float* ws_part;           // [B][G][nsplit][R][D + 2] window partials
+};
+
+int decode_dispatch(const DecodeArgs& a, hipStream_t stream);
+
+struct StepArgs {
+    int B, G, R, D;
+    const float* q;           // [B][G*R][D]
+    const float* k;           // [B][G][D]
+    const float* v;           // [B][G][D]
+    const float* g;           // [B][G]
+    const float* beta;        // [B][G]
+    const float* s_in;        // [B][G][D][D]
+    float* s_out;             // [B][G][D][D] (may equal s_in)
+    float* o;                 // [B][G*R][D]
+};
+
+int step_dispatch(const StepArgs& a, hipStream_t stream);
+
 }  // namespace bf

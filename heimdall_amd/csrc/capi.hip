@@ -88,4 +88,60 @@ int bf_gdn_fwd(const void* q, const void* k, const void* v, const float* g, cons
     return bf::gdn_dispatch(a, phases, static_cast<hipStream_t>(stream));
 }
 
+int bf_gdn_step(const float* q, const float* k, const float* v, const float* g, const float* beta,
+                const float* state_in, float* state_out, float* o, int B, int G, int R, int D, void* stream) {
+    if (B <= 0 || G <= 0 || R <= 0 || R > 8) return BF_STATUS_INVALID;
+    if (!supported_dim(D)) return BF_STATUS_UNSUPPORTED;
+    if (!q || !k || !v || !g || !beta || !state_in || !state_out || !o) return BF_STATUS_INVALID;
+    bf::StepArgs a{};
+    a.B = B; a.G = G; a.R = R; a.D = D;
+    a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta;
+    a.s_in = state_in; a.s_out = state_out; a.o = o;
+    return bf::step_dispatch(a, static_cast<hipStream_t>(stream));
+}
+
+int bf_decode_workspace_size(int B, int G, int R, int D, int W, size_t* bytes) {
+    if (!bytes || B <= 0 || G <= 0 || R <= 0 || W <= 0) return BF_STATUS_INVALID;
+    if (!supported_dim(D) || R > 8) return BF_STATUS_UNSUPPORTED;
+    const size_t nsplit = (size_t)(W + 255) / 256;
+    *bytes = align256((size_t)B * G * R * D * sizeof(float)) +
+             align256((size_t)B * G * nsplit * R * (D + 2) * sizeof(float));
+    return BF_STATUS_OK;
+}
+
+int bf_decode_fwd(int B, int G, int R, int D, int W, int sinks, int64_t pos, int memory, int kv_dtype, int q_dtype,
+                  const void* qr, const float* qm, const void* kr, const void* v, const float* km, const float* g_new,
+                  const float* beta_new, const float* z, const float* mix_lse, const float* mem_scale,
+                  const void* sink_k, const void* sink_v, int n_sinks, void* ring_k, void* ring_v, float* ring_km,
+                  float* ring_g, float* ring_beta, int64_t* ring_pos, float* state, float* o, float* lse,
+                  void* workspace, size_t workspace_bytes, void* stream) {
+    if (B <= 0 || G <= 0 || R <= 0 || W <= 0 || sinks < 0 || pos < 0) return BF_STATUS_INVALID;
+    if (!supported_dim(D) || R > 8 || !supported_dtype(kv_dtype) || !supported_dtype(q_dtype))
+        return BF_STATUS_UNSUPPORTED;
+    if (n_sinks < 0 || n_sinks > 63 || n_sinks > sinks || (n_sinks > 0 && (!sink_k || !sink_v)))
+        return BF_STATUS_INVALID;
+    if (!qr || !kr || !v || !km || !g_new || !beta_new || !ring_k || !ring_v || !ring_km || !ring_g || !ring_beta ||
+        !ring_pos || !o)
+        return BF_STATUS_INVALID;
+    const int mem_on = memory && pos >= W;
+    if (mem_on && (!qm || !z || !mix_lse || !mem_scale || !state)) return BF_STATUS_INVALID;
+    size_t need = 0;
+    const int st = bf_decode_workspace_size(B, G, R, D, W, &need);
+    if (st) return st;
+    if (!workspace || workspace_bytes < need) return BF_STATUS_WORKSPACE;
+    bf::DecodeArgs a{};
+    a.B = B; a.G = G; a.R = R; a.D = D; a.W = W; a.sinks = sinks; a.pos = pos; a.mem_on = mem_on;
+    a.kv_dtype = kv_dtype; a.q_dtype = q_dtype;
+    a.qr = qr; a.qm = qm; a.kr = kr; a.v = v; a.km = km; a.g_new = g_new; a.beta_new = beta_new;
+    a.z = z; a.mix_lse = mix_lse; a.mem_scale = mem_scale;
+    a.sink_k = sink_k; a.sink_v = sink_v; a.n_sinks = n_sinks;
+    a.ring_k = ring_k; a.ring_v = ring_v; a.ring_km = ring_km; a.ring_g = ring_g; a.ring_beta = ring_beta;
+    a.ring_pos = ring_pos; a.state = state; a.o = o; a.lse = lse;
+    a.nsplit = (W + 255) / 256;
+    char* ws = static_cast<char*>(workspace);
+    a.ws_om = reinterpret_cast<float*>(ws);
+    a.ws_part = reinterpret_cast<float*>(ws + align256((size_t)B * G * R * D * sizeof(float)));
+    return bf::decode_dispatch(a, static_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"

@@ -1,0 +1,412 @@
+// K3: one decode step of the converted layer for B sequences (one new token each, all at absolute position p), and
+// the single-token gated delta-rule step.
+//
+// Reference semantics (Heimdall/heimdall/hibrit.py:363-424 with t == 1; kernels.py:132-138):
+//   window  : keys = sinks (j < ns) + ring entries with max(S, p-W+1) <= pos <= p-1 + the new token (if p >= S);
+//             s = qr.k / sqrt(D), lse = log sum exp s, o_win = softmax(s) V
+//   memory  : (p >= W) the ring row leaving the window (position p - W, slot p mod W) is written into the state:
+//             S <- e^g S;  delta = beta (v - S^T km);  S <- S + km delta^T;   then o_mem = S^T qm per query head
+//   mix     : gamma = sigmoid(z + mix_lse (lse - ln W)) [p >= W];  o = o_win + gamma (mem_scale o_mem - o_win)
+//   cache   : slot p mod W <- (kr, v, km, g, beta, p)
+//
+// Layout (row-major): state [B][G][D][D] f32; ring_k, ring_v [B][G][W][D]; ring_km [B][W][G][D] f32;
+// ring_g, ring_beta [B][W][G] f32; ring_pos [W] int64; sinks [B][G][ns][D]; qr, qm, o [B][H][D]; kr, v, km [B][G][D].
+//
+// Kernels:
+//   decode_main    grid (max(D/32, W/256 splits), G, B): state slab x (32 columns) and window split x (256 slots)
+//   decode_combine grid (G, B): merge the window splits, gamma mix, ring write
+//   gdn_step       grid (D/32, G, B): the state slab pass alone (delta_rule_step)
+#include "bf_common.h"
+#include "bf_internal.h"
+
+namespace bf {
+
+constexpr int NT_DEC = 256;
+constexpr int SLOTS = 256;       // ring slots per window split
+constexpr int SCOL = 32;         // state columns per slab
+constexpr int RMAX = 8;          // query heads per KV head supported by the decode kernels
+
+template <class KV>
+__device__ __forceinline__ float kv_ld(const typename KV::T* p) { return KV::to_f(*p); }
+
+// Load 16 consecutive elements (as fp32) starting at p (16-byte aligned).
+template <class KV>
+__device__ __forceinline__ void ld16f(const typename KV::T* p, float (&out)[16]);
+template <>
+__device__ __forceinline__ void ld16f<BF16>(const uint16_t* p, float (&out)[16]) {
+    const uint4 a = ld16(p), b = ld16(p + 8);
+    const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        out[2 * i] = __uint_as_float(w[i] << 16);
+        out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+}
+template <>
+__device__ __forceinline__ void ld16f<F32>(const float* p, float (&out)[16]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 v = *reinterpret_cast<const float4*>(p + 4 * i);
+        out[4 * i] = v.x; out[4 * i + 1] = v.y; out[4 * i + 2] = v.z; out[4 * i + 3] = v.w;
+    }
+}
+
+// Sum over the 32 threads of a block that share (tid % 8): lanes l, l+8, .., l+56 of each wave, then the 4 waves.
+// red: shared scratch of 4 * 8 * NV floats. Returns the total in every thread of the group (tid % 8).
+template <int NV>
+__device__ __forceinline__ void reduce_colgroups(float (&v)[NV], float* red) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        float x = v[i];
+        x += __shfl_xor(x, 8);
+        x += __shfl_xor(x, 16);
+        x += __shfl_xor(x, 32);
+        v[i] = x;
+    }
+    if (lane < 8) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) red[(wv * 8 + lane) * NV + i] = v[i];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = tid & 7;
+        v[i] = red[(0 * 8 + c) * NV + i] + red[(1 * 8 + c) * NV + i] + red[(2 * 8 + c) * NV + i] +
+               red[(3 * 8 + c) * NV + i];
+    }
+    __syncthreads();
+}
+
+// State slab pass for one (b, g): columns [j0, j0 + 32). Thread tid owns columns j0 + 4 (tid % 8) .. +3 of rows
+// tid / 8 + 32 i. Applies S <- e^{wg} S; delta = wb (wv - S^T wk); S <- S + wk delta^T (skipped when !write), then
+// writes o[r][j] = sum_d qm_r[d] S[d][j] for the R query heads. S is updated in place (s_in == s_out allowed).
+template <int D, int RMAX>
+__device__ __forceinline__ void state_slab(const float* s_in, float* s_out, const float* wk, const float* wv,
+                                           float wg, float wb, bool write, const float* qm, int R, long q_stride,
+                                           float* om, long o_stride, int j0, float* red) {
+    constexpr int RPT = D / 32;                      // rows per thread
+    const int tid = threadIdx.x, cg = tid & 7, r0 = tid >> 3;
+    const int jc = j0 + 4 * cg;
+    float4 s[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) s[i] = *reinterpret_cast<const float4*>(s_in + (long)(r0 + 32 * i) * D + jc);
+    if (write) {
+        const float a = __expf(wg);
+        float rc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) {
+            const float k = wk[r0 + 32 * i];
+            rc[0] += k * s[i].x; rc[1] += k * s[i].y; rc[2] += k * s[i].z; rc[3] += k * s[i].w;
+        }
+        reduce_colgroups<4>(rc, red);
+        const float4 v4 = *reinterpret_cast<const float4*>(wv + jc);
+        const float dl[4] = {wb * (v4.x - a * rc[0]), wb * (v4.y - a * rc[1]), wb * (v4.z - a * rc[2]),
+                             wb * (v4.w - a * rc[3])};
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) {
+            const float k = wk[r0 + 32 * i];
+            s[i].x = a * s[i].x + k * dl[0];
+            s[i].y = a * s[i].y + k * dl[1];
+            s[i].z = a * s[i].z + k * dl[2];
+            s[i].w = a * s[i].w + k * dl[3];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) *reinterpret_cast<float4*>(s_out + (long)(r0 + 32 * i) * D + jc) = s[i];
+    if (!om) return;
+    float acc[RMAX * 4];
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) {
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+        if (r < R) {
+#pragma unroll
+            for (int i = 0; i < RPT; ++i) {
+                const float qv = qm[r * q_stride + r0 + 32 * i];
+                a0 += qv * s[i].x; a1 += qv * s[i].y; a2 += qv * s[i].z; a3 += qv * s[i].w;
+            }
+        }
+        acc[4 * r] = a0; acc[4 * r + 1] = a1; acc[4 * r + 2] = a2; acc[4 * r + 3] = a3;
+    }
+    reduce_colgroups<RMAX * 4>(acc, red);
+    if (r0 == 0) {
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r)
+            if (r < R) *reinterpret_cast<float4*>(om + r * o_stride + jc) =
+                make_float4(acc[4 * r], acc[4 * r + 1], acc[4 * r + 2], acc[4 * r + 3]);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------- decode
+template <class KV, int D, int RM>
+__global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
+    using T = typename KV::T;
+    constexpr int RMAX = RM;                    // query heads per KV head this instance supports (R <= RM)
+    constexpr int LPS = D / 16;                 // lanes per key slot (16 dims each)
+    constexpr int SPW = 64 / LPS;               // slots per wave per iteration
+    __shared__ float red[4 * 8 * RMAX * 4];
+    __shared__ float sc[RMAX][SLOTS + 64];      // scores, then probabilities (ring slots + sinks + new token)
+    __shared__ float part[4][RMAX][D];          // per-wave PV partials
+    __shared__ float mx[RMAX], sm[RMAX];
+
+    const int x = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    const int G = a.G, R = a.R, H = G * R, W = a.W;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const long bg = (long)b * G + g;
+
+    // ---- state slab x (memory branch)
+    if (a.mem_on && x < D / SCOL) {
+        const int slot = (int)(a.pos % W);
+        const long pe = a.pos - W;
+        const bool valid = pe >= 0 && a.ring_pos[slot] == pe;
+        const float* wk = a.ring_km + (((long)b * W + slot) * G + g) * D;
+        // evicted value row (kv dtype) -> fp32 in shared scratch
+        __shared__ float vrow[D];
+        const T* rv = reinterpret_cast<const T*>(a.ring_v) + (bg * W + slot) * D;
+        for (int d = tid; d < D; d += NT_DEC) vrow[d] = KV::to_f(rv[d]);
+        __syncthreads();
+        const float wg = valid ? a.ring_g[((long)b * W + slot) * G + g] : 0.f;
+        const float wb = valid ? a.ring_beta[((long)b * W + slot) * G + g] : 0.f;
+        float* S = a.state + bg * D * D;
+        state_slab<D, RM>(S, S, wk, vrow, wg, wb, valid, a.qm + ((long)b * H + g * R) * D, R, D,
+                      a.ws_om + ((long)b * H + g * R) * D, D, x * SCOL, red);
+    }
+
+    // ---- window split x
+    const int nsplit = (W + SLOTS - 1) / SLOTS;
+    if (x >= nsplit) return;
+    const int s0 = x * SLOTS, s1 = min(W, s0 + SLOTS);
+    const int nring = s1 - s0;
+    const int nextra = x == 0 ? a.n_sinks + 1 : 0;      // sinks and the new token ride on split 0
+    const int nkeys = nring + nextra;
+    const float scale = rsqrtf((float)D);
+    const long lo = max((long)a.sinks, a.pos - W + 1);  // oldest visible window position
+
+    const int sl = lane / LPS, dl = (lane % LPS) * 16;  // slot within the wave step, dims dl..dl+15
+    float q[RMAX][16];
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r) {
+        if (r < R) {
+            if (a.q_dtype == DT_BF16) ld16f<BF16>(reinterpret_cast<const uint16_t*>(a.qr) + ((long)b * H + g * R + r) * D + dl, q[r]);
+            else ld16f<F32>(reinterpret_cast<const float*>(a.qr) + ((long)b * H + g * R + r) * D + dl, q[r]);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) q[r][i] *= scale;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) q[r][i] = 0.f;
+        }
+    }
+    const T* RK = reinterpret_cast<const T*>(a.ring_k) + bg * W * D;
+    const T* RV = reinterpret_cast<const T*>(a.ring_v) + bg * W * D;
+    const T* SK = reinterpret_cast<const T*>(a.sink_k) + bg * a.n_sinks * D;
+    const T* SV = reinterpret_cast<const T*>(a.sink_v) + bg * a.n_sinks * D;
+    const T* NK = reinterpret_cast<const T*>(a.kr) + bg * D;
+    const T* NV = reinterpret_cast<const T*>(a.v) + bg * D;
+
+    // key index k in [0, nkeys): ring slot s0 + k, then sinks, then the new token
+    auto key_row = [&](int k, const T* ring, const T* sink, const T* nw) -> const T* {
+        if (k < nring) return ring + (long)(s0 + k) * D;
+        if (k < nring + a.n_sinks) return sink + (long)(k - nring) * D;
+        return nw;
+    };
+    auto visible = [&](int k) -> bool {
+        if (k < nring) {
+            const long p = a.ring_pos[s0 + k];
+            return p >= lo && p <= a.pos - 1;
+        }
+        if (k < nring + a.n_sinks) return true;
+        return a.pos >= a.sinks;
+    };
+
+    // scores
+    for (int k0 = wv * SPW; k0 < nkeys; k0 += 4 * SPW) {
+        const int k = k0 + sl;
+        float d[RMAX];
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r) d[r] = 0.f;
+        if (k < nkeys) {
+            float kv[16];
+            ld16f<KV>(key_row(k, RK, SK, NK) + dl, kv);
+#pragma unroll
+            for (int r = 0; r < RMAX; ++r)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) d[r] += q[r][i] * kv[i];
+        }
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r)
+#pragma unroll
+            for (int off = 1; off < LPS; off <<= 1) d[r] += __shfl_xor(d[r], off);
+        if (k < nkeys && (lane % LPS) == 0) {
+            const bool vis = visible(k);
+#pragma unroll
+            for (int r = 0; r < RMAX; ++r)
+                if (r < R) sc[r][k] = vis ? d[r] : -INFINITY;
+        }
+    }
+    __syncthreads();
+    // max and exp-sum per head (wave r handles head r, r + 4, ...)
+    for (int r = wv; r < R; r += 4) {
+        float m = -INFINITY;
+        for (int k = lane; k < nkeys; k += 64) m = fmaxf(m, sc[r][k]);
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+        float l = 0.f;
+        for (int k = lane; k < nkeys; k += 64) {
+            const float p = m == -INFINITY ? 0.f : __expf(sc[r][k] - m);
+            sc[r][k] = p;
+            l += p;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) l += __shfl_xor(l, off);
+        if (lane == 0) { mx[r] = m; sm[r] = l; }
+    }
+    __syncthreads();
+    // P V
+    float acc[RMAX][16];
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[r][i] = 0.f;
+    for (int k0 = wv * SPW; k0 < nkeys; k0 += 4 * SPW) {
+        const int k = k0 + sl;
+        if (k < nkeys) {
+            float vv[16];
+            ld16f<KV>(key_row(k, RV, SV, NV) + dl, vv);
+#pragma unroll
+            for (int r = 0; r < RMAX; ++r) {
+                const float p = r < R ? sc[r][k] : 0.f;
+#pragma unroll
+                for (int i = 0; i < 16; ++i) acc[r][i] += p * vv[i];
+            }
+        }
+    }
+    // reduce over the SPW slot groups of the wave (lanes with equal lane % LPS), then over the 4 waves
+#pragma unroll
+    for (int r = 0; r < RMAX; ++r)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+#pragma unroll
+            for (int off = LPS; off < 64; off <<= 1) acc[r][i] += __shfl_xor(acc[r][i], off);
+    if (lane < LPS) {
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r)
+            if (r < R) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) part[wv][r][dl + i] = acc[r][i];
+            }
+    }
+    __syncthreads();
+    // partial record for this split: [m, l, o[0..D)] per head
+    float* out = a.ws_part + ((bg * a.nsplit + x) * R) * (D + 2);
+    for (int idx = tid; idx < R * D; idx += NT_DEC) {
+        const int r = idx / D, dd = idx % D;
+        out[r * (D + 2) + 2 + dd] = part[0][r][dd] + part[1][r][dd] + part[2][r][dd] + part[3][r][dd];
+    }
+    if (tid < R) {
+        out[tid * (D + 2)] = mx[tid];
+        out[tid * (D + 2) + 1] = sm[tid];
+    }
+}
+
+template <class KV, int D>
+__global__ __launch_bounds__(NT_DEC) void decode_combine_kernel(DecodeArgs a) {
+    using T = typename KV::T;
+    const int g = blockIdx.x, b = blockIdx.y;
+    const int G = a.G, R = a.R, H = G * R, W = a.W, NS = a.nsplit;
+    const int tid = threadIdx.x;
+    const long bg = (long)b * G + g;
+    const float* part = a.ws_part + bg * NS * R * (D + 2);
+    const float lnW = logf((float)W);
+    for (int idx = tid; idx < R * D; idx += NT_DEC) {
+        const int r = idx / D, d = idx % D;
+        float M = -INFINITY;
+        for (int s = 0; s < NS; ++s) M = fmaxf(M, part[(s * R + r) * (D + 2)]);
+        float L = 0.f, ow = 0.f;
+        for (int s = 0; s < NS; ++s) {
+            const float* p = part + (s * R + r) * (D + 2);
+            const float f = p[0] == -INFINITY ? 0.f : __expf(p[0] - M);
+            L += f * p[1];
+            ow += f * p[2 + d];
+        }
+        ow /= L;
+        const float lse = M + logf(L);
+        const int h = g * R + r;
+        float o = ow;
+        if (a.mem_on) {
+            const float gam = 1.f / (1.f + __expf(-(a.z[(long)b * H + h] + a.mix_lse[h] * (lse - lnW))));
+            const float om = a.ws_om[((long)b * H + h) * D + d];
+            o = ow + gam * (a.mem_scale[h] * om - ow);
+        }
+        a.o[((long)b * H + h) * D + d] = o;
+        if (d == 0 && a.lse) a.lse[(long)b * H + h] = lse;
+    }
+    // cache write: slot pos mod W <- (kr, v, km, g, beta, pos)
+    const int slot = (int)(a.pos % W);
+    T* RK = reinterpret_cast<T*>(a.ring_k) + (bg * W + slot) * D;
+    T* RV = reinterpret_cast<T*>(a.ring_v) + (bg * W + slot) * D;
+    const T* NK = reinterpret_cast<const T*>(a.kr) + bg * D;
+    const T* NV = reinterpret_cast<const T*>(a.v) + bg * D;
+    float* KM = a.ring_km + (((long)b * W + slot) * G + g) * D;
+    for (int d = tid; d < D; d += NT_DEC) {
+        RK[d] = NK[d];
+        RV[d] = NV[d];
+        KM[d] = a.km[bg * D + d];
+    }
+    if (tid == 0) {
+        a.ring_g[((long)b * W + slot) * G + g] = a.g_new[bg];
+        a.ring_beta[((long)b * W + slot) * G + g] = a.beta_new[bg];
+        if (b == 0 && g == 0) a.ring_pos[slot] = a.pos;
+    }
+}
+
+// ----------------------------------------------------------------------------------------------- single-token GDN
+template <int D>
+__global__ __launch_bounds__(NT_DEC) void gdn_step_kernel(StepArgs a) {
+    __shared__ float red[4 * 8 * RMAX * 4];
+    const int x = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    const int G = a.G, R = a.R, H = G * R;
+    const long bg = (long)b * G + g;
+    state_slab<D, RMAX>(a.s_in + bg * D * D, a.s_out + bg * D * D, a.k + bg * D, a.v + bg * D, a.g[bg], a.beta[bg], true,
+                  a.q + ((long)b * H + g * R) * D, R, D, a.o + ((long)b * H + g * R) * D, D, x * SCOL, red);
+}
+
+// ------------------------------------------------------------------------------------------------ host launchers
+template <class KV, int D>
+static int launch_decode(const DecodeArgs& a, hipStream_t stream) {
+    const int nx = max(D / SCOL, a.nsplit);
+    if (a.R <= 4) hipLaunchKernelGGL((decode_main_kernel<KV, D, 4>), dim3(nx, a.G, a.B), dim3(NT_DEC), 0, stream, a);
+    else hipLaunchKernelGGL((decode_main_kernel<KV, D, 8>), dim3(nx, a.G, a.B), dim3(NT_DEC), 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    hipLaunchKernelGGL((decode_combine_kernel<KV, D>), dim3(a.G, a.B), dim3(NT_DEC), 0, stream, a);
+    e = hipGetLastError();
+    return e == hipSuccess ? 0 : (int)e;
+}
+
+int decode_dispatch(const DecodeArgs& a, hipStream_t stream) {
+    const bool bf = a.kv_dtype == DT_BF16;
+    switch (a.D) {
+        case 64: return bf ? launch_decode<BF16, 64>(a, stream) : launch_decode<F32, 64>(a, stream);
+        case 128: return bf ? launch_decode<BF16, 128>(a, stream) : launch_decode<F32, 128>(a, stream);
+        case 256: return bf ? launch_decode<BF16, 256>(a, stream) : launch_decode<F32, 256>(a, stream);
+        default: return BF_ERR_UNSUPPORTED;
+    }
+}
+
+template <int D>
+static int launch_step(const StepArgs& a, hipStream_t stream) {
+    hipLaunchKernelGGL((gdn_step_kernel<D>), dim3(D / SCOL, a.G, a.B), dim3(NT_DEC), 0, stream, a);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : (int)e;
+}
+
+int step_dispatch(const StepArgs& a, hipStream_t stream) {
+    switch (a.D) {
+        case 64: return launch_step<64>(a, stream);
+        case 128: return launch_step<128>(a, stream);
+        case 256: return launch_step<256>(a, stream);
+        default: return BF_ERR_UNSUPPORTED;
+    }
+}
+
+}  // namespace bf

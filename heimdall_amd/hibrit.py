@@ -1,0 +1,200 @@
+"""Drop-in GPU student path of the converted (Bifrost) attention layer.
+
+Mirrors ``HybridAttention`` of the reference (``Heimdall/heimdall/hibrit.py:193-424``) for the part this package
+accelerates: the same new-parameter names and conversion init (``convert``, ``hibrit.py:211-240``), the same
+``_mem_inputs`` (``:327-334``) and a ``_student(x, q, k, v, qr, kr, start, cache, memory)`` with the reference's
+signature and cache contract (keys ``sink_k, sink_v, ring_k, ring_v, ring_km, ring_g, ring_beta, ring_pos, S`` with
+the same shapes and meaning, mutated in place), so a cache can move between the reference and this implementation.
+
+The window + sink attention, the delta-rule memory and the gamma mix run in ``libbifrost_hip.so``:
+  t == 1  -> ``bf_decode_fwd`` (one bandwidth-bound pass: state update, window read, mix, ring write)
+  t > 1   -> ``bf_gdn_fwd`` (memory branch) then ``bf_window_fwd`` (window + sinks + LSE, fused gamma mix)
+The frozen projections and the small per-token gate GEMMs (fq/fk, ab, mix) stay in PyTorch.
+
+``student`` can be bound onto the reference class as a drop-in: ``HybridAttention._student = student``.
+"""
+import math
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib
+from ._device import (BifrostError, check, dtype_code, gdn_forward, require_device, require_no_grad, stream_ptr,
+                      workspace)
+
+NEW = ("fq", "fk", "ab", "mix", "mix_lse", "mem_scale", "A_log", "dt_bias")
+
+
+class CoreConfig:
+    """Head geometry with the reference's attribute names (``HybridConfig.h / hkv / dh / d``)."""
+
+    def __init__(self, h: int, hkv: int, dh: int, d: int):
+        if h % hkv:
+            raise ValueError("query heads must be a multiple of KV heads")
+        self.h, self.hkv, self.dh, self.d = h, hkv, dh, d
+
+
+def n_archival(frac: float, hkv: int, mem_init: str = "long") -> int:
+    """Never-forgetting memory heads (``hibrit.py:187-190``)."""
+    n = int(frac * hkv)
+    return max(1, n) if mem_init == "long" and frac > 0 else n
+
+
+def _heads_matmul(x: torch.Tensor, f: torch.Tensor) -> torch.Tensor:
+    """x [B, t, h, D] fp32, f [h, D, D] -> x_h f_h per head (a batched GEMM with contiguous operands)."""
+    b, t, h, d = x.shape
+    y = torch.matmul(x.permute(2, 0, 1, 3).reshape(h, b * t, d).contiguous(), f.float().contiguous())
+    return y.reshape(h, b, t, d).permute(1, 2, 0, 3)
+
+
+def mem_inputs(self, x, q, k, pos):
+    """qm = normalize(q_h F_q,h) / sqrt(D); km = normalize(k_g F_k,g); g = -exp(A_log) softplus(a + dt_bias) mask;
+    beta = sigmoid(b) [pos >= sinks]  (``hibrit.py:327-334``), all fp32."""
+    dh = self.c.dh
+    qm = F.normalize(_heads_matmul(q.float(), self.fq), dim=-1) * dh ** -0.5
+    km = F.normalize(_heads_matmul(k.float(), self.fk), dim=-1)
+    a, bb = self.ab(x).float().chunk(2, dim=-1)
+    g = -self.A_log.float().exp() * F.softplus(a + self.dt_bias.float()) * self.decay_mask.float()
+    beta = torch.sigmoid(bb) * (pos >= self.sinks).float()[None, :, None]
+    return qm, km, g, beta
+
+
+def _new_ring(b, G, w, D, kdt, vdt, dev):
+    return dict(ring_k=torch.zeros(b, G, w, D, dtype=kdt, device=dev),
+                ring_v=torch.zeros(b, G, w, D, dtype=vdt, device=dev),
+                ring_km=torch.zeros(b, w, G, D, dtype=torch.float32, device=dev),
+                ring_g=torch.zeros(b, w, G, dtype=torch.float32, device=dev),
+                ring_beta=torch.zeros(b, w, G, dtype=torch.float32, device=dev),
+                ring_pos=torch.full((w,), -1, dtype=torch.long, device=dev))
+
+
+def _decode(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memory):
+    """One token for every sequence: bf_decode_fwd (window, memory write on exit, read, mix, ring write)."""
+    c = self.c
+    b = x.shape[0]
+    H, G, D, w, r = c.h, c.hkv, c.dh, self.window, c.h // c.hkv
+    dev = x.device
+    kvdt = kr.dtype
+    if kvdt not in (torch.float32, torch.bfloat16) or v.dtype != kvdt:
+        raise BifrostError(f"decode needs k/v in one dtype, fp32 or bf16 (got {kr.dtype}, {v.dtype})")
+    use_mem = memory and start + 1 > w
+    S = None
+    if use_mem:
+        S = st.get("S")
+        if S is None:
+            S = torch.zeros(b, G, D, D, dtype=torch.float32, device=dev)
+        elif not (S.dtype == torch.float32 and S.is_contiguous()):
+            S = S.float().contiguous()
+        st["S"] = S
+    ns = 0 if sink_k is None else sink_k.size(2)
+    sk = sink_k.to(kvdt).contiguous() if ns else None
+    sv = sink_v.to(kvdt).contiguous() if ns else None
+    for key in ("ring_k", "ring_v", "ring_km", "ring_g", "ring_beta", "ring_pos"):
+        if not st[key].is_contiguous():
+            st[key] = st[key].contiguous()
+    qrd = qr.to(torch.bfloat16 if qr.dtype == torch.bfloat16 else torch.float32).contiguous()
+    z = F.linear(x.float(), self.mix.weight.float(), self.mix.bias.float()).contiguous() if use_mem else None
+    mix_lse = self.mix_lse.float().contiguous() if use_mem else None
+    mem_scale = self.mem_scale.float().contiguous() if use_mem else None
+    qm_ = qm.contiguous() if use_mem else None
+    kr_, v_ = kr.contiguous(), v.contiguous()
+    km_, g_, b_ = km.float().contiguous(), g.float().contiguous(), beta.float().contiguous()
+    o = torch.empty(b, H, D, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    nbytes = _lib.ctypes.c_size_t(0)
+    check(lib.bf_decode_workspace_size(b, G, r, D, w, _lib.ctypes.byref(nbytes)), "bf_decode_workspace_size")
+    ws = workspace(nbytes.value, dev)
+    ptr = lambda t_: t_.data_ptr() if t_ is not None else None
+    check(lib.bf_decode_fwd(b, G, r, D, w, self.sinks, start, int(memory), dtype_code(kvdt), dtype_code(qrd.dtype),
+                            ptr(qrd), ptr(qm_), ptr(kr_), ptr(v_), ptr(km_), ptr(g_), ptr(b_), ptr(z), ptr(mix_lse),
+                            ptr(mem_scale), ptr(sk), ptr(sv), ns, ptr(st["ring_k"]), ptr(st["ring_v"]),
+                            ptr(st["ring_km"]), ptr(st["ring_g"]), ptr(st["ring_beta"]), ptr(st["ring_pos"]), ptr(S),
+                            ptr(o), None, ptr(ws), ws.numel(), stream_ptr(dev)), "bf_decode_fwd")
+    return o.view(b, 1, H, D)
+
+
+def student(self, x, q, k, v, qr, kr, start: int, cache: Optional[dict], memory: bool = True):
+    """Window + sinks attention, delta-rule memory written on window exit, gamma mix (``hibrit.py:363-424``).
+
+    x [B, t, d]; q [B, t, H, D] (normed, pre-RoPE); k, v [B, t, G, D]; qr [B, H, t, D], kr [B, G, t, D] (RoPE'd).
+    cache: dict mutated in place (the reference's keys and shapes) or None. Returns o [B, t, H, D] fp32.
+    """
+    require_device(x, q, k, v, qr, kr)
+    require_no_grad(x, q, k, v, qr, kr)
+    c = self.c
+    b, t = x.shape[:2]
+    w, s = self.window, self.sinks
+    dev = x.device
+    st = cache if cache is not None else {}
+    pos = torch.arange(start, start + t, device=dev)
+    vt = v.transpose(1, 2)
+    sink_k, sink_v = st.get("sink_k"), st.get("sink_v")
+    n_new = max(0, min(t, s - start))
+    if n_new:
+        sink_k = kr[:, :, :n_new] if sink_k is None else torch.cat((sink_k, kr[:, :, :n_new]), 2)
+        sink_v = vt[:, :, :n_new] if sink_v is None else torch.cat((sink_v, vt[:, :, :n_new]), 2)
+    qm, km, g, beta = self._mem_inputs(x, q, k, pos)
+    if "ring_k" not in st:
+        st.update(_new_ring(b, c.hkv, w, c.dh, kr.dtype, vt.dtype, dev))
+    if t == 1:
+        o = _decode(self, x, qr, kr[:, :, 0], v[:, 0], qm[:, 0], km[:, 0], g[:, 0], beta[:, 0], start, st, sink_k,
+                    sink_v, memory)
+    else:
+        o = _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memory)
+    st["sink_k"], st["sink_v"] = sink_k, sink_v
+    return o
+
+
+def _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memory):
+    raise NotImplementedError("prefill path (t > 1) of the HIP student is provided by the window kernel")
+
+
+class BifrostCore(nn.Module):
+    """The converted layer's new parameters and student path, with the reference's attribute names.
+
+    Holds ``fq [H,D,D], fk [G,D,D], ab (Linear d -> 2G), mix (Linear d -> H), mix_lse [H], mem_scale [H], A_log [G],
+    dt_bias [G]`` and the buffer ``decay_mask [G]``; ``window`` and ``sinks`` are set by ``convert``.
+    """
+
+    def __init__(self, c: CoreConfig):
+        super().__init__()
+        self.c = c
+        self.converted = False
+
+    def convert(self, window: int, sinks: int, archival: int, mem_init: str = "long") -> None:
+        """Conversion init (``hibrit.py:211-240``): identity fq/fk, zero gates with mix bias -2, dt ~ logU[1e-3, 1e-1],
+        "long" memory: read scale sqrt(D), decay half-lives logspace(log10 W, 6, G) tokens, first ``archival`` KV
+        heads never decay; "mamba": read scale 1, A in U[1, 16]."""
+        c = self.c
+        dev = next((p.device for p in self.parameters()), torch.device("cpu"))
+        self.window, self.sinks = window, sinks
+        self.fq = nn.Parameter(torch.eye(c.dh, device=dev).repeat(c.h, 1, 1))
+        self.fk = nn.Parameter(torch.eye(c.dh, device=dev).repeat(c.hkv, 1, 1))
+        self.ab = nn.Linear(c.d, 2 * c.hkv, device=dev)
+        self.mix = nn.Linear(c.d, c.h, device=dev)
+        for lin in (self.ab, self.mix):
+            nn.init.zeros_(lin.weight)
+            nn.init.zeros_(lin.bias)
+        nn.init.constant_(self.mix.bias, -2.0)
+        self.mix_lse = nn.Parameter(torch.zeros(c.h, device=dev))
+        dt = torch.exp(torch.empty(c.hkv, device=dev).uniform_(math.log(1e-3), math.log(1e-1)))
+        self.dt_bias = nn.Parameter(dt + torch.log(-torch.expm1(-dt)))
+        if mem_init == "mamba":
+            self.mem_scale = nn.Parameter(torch.ones(c.h, device=dev))
+            self.A_log = nn.Parameter(torch.empty(c.hkv, device=dev).uniform_(1.0, 16.0).log())
+        else:
+            self.mem_scale = nn.Parameter(torch.full((c.h,), float(c.dh) ** 0.5, device=dev))
+            life = torch.logspace(math.log10(max(window, 2)), 6.0, c.hkv, device=dev)
+            self.A_log = nn.Parameter((math.log(2.0) / (life * dt)).log())
+        mask = torch.ones(c.hkv, device=dev)
+        mask[:archival] = 0.0
+        self.register_buffer("decay_mask", mask, persistent=False)
+        self.converted = True
+
+    _mem_inputs = mem_inputs
+    _student = student
+
+    def forward(self, x, q, k, v, qr, kr, start: int = 0, cache: Optional[dict] = None, memory: bool = True):
+        return self._student(x, q, k, v, qr, kr, start, cache, memory)

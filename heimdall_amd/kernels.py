@@ -7,7 +7,8 @@ from typing import Optional, Tuple
 
 import torch
 
-from ._device import gdn_forward, require_device, require_no_grad
+from . import _lib
+from ._device import BifrostError, check, gdn_forward, require_device, require_no_grad, stream_ptr
 
 
 def delta_rule(q, k, v, g, beta, chunk_size: int = 64, initial_state: Optional[torch.Tensor] = None,
@@ -32,11 +33,27 @@ def delta_rule(q, k, v, g, beta, chunk_size: int = 64, initial_state: Optional[t
 def delta_rule_step(q, k, v, g, beta, state) -> Tuple[torch.Tensor, torch.Tensor]:
     """One token (``Heimdall/heimdall/kernels.py:132-138``). q, k [B, H, Dk], v [B, H, Dv], g, beta [B, H],
     state [B, H, Dk, Dv] fp32. Returns (o [B, H, Dv] fp32, new state)."""
-    require_device(q, k, v, g, beta, state)
+    return gdn_step(q, k, v, g, beta, state)
+
+
+def gdn_step(q, k, v, g, beta, state, out_state: Optional[torch.Tensor] = None):
+    """GQA single-token step on ``bf_gdn_step``: q [B, G*R, Dk], k [B, G, Dk], v [B, G, Dv], g, beta [B, G],
+    state [B, G, Dk, Dv]. Returns (o [B, G*R, Dv] fp32, new state fp32; ``out_state`` may be ``state`` for an
+    in-place update)."""
+    dev = require_device(q, k, v, g, beta, state)
     require_no_grad(q, k, v, g, beta, state)
     B, H, D = q.shape
-    o, s = gdn_forward(q, k, v, g, beta, num_seqs=B, initial_state=state)
-    return o, s
+    G = k.shape[1]
+    if H % G or k.shape != (B, G, D) or v.shape != (B, G, D) or state.shape != (B, G, D, D):
+        raise BifrostError("inconsistent shapes for the single-token step")
+    q, k, v, g, beta = (z.float().contiguous() for z in (q, k, v, g, beta))
+    s_in = state.float().contiguous()
+    s_out = out_state if out_state is not None else torch.empty_like(s_in)
+    o = torch.empty(B, H, D, dtype=torch.float32, device=dev)
+    check(_lib.load().bf_gdn_step(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
+                                  s_in.data_ptr(), s_out.data_ptr(), o.data_ptr(), B, G, H // G, D, stream_ptr(dev)),
+          "bf_gdn_step")
+    return o, s_out
 
 
 def delta_rule_varlen(q, k, v, g, beta, cu_seqlens, initial_state: Optional[torch.Tensor] = None,

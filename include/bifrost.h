@@ -73,6 +73,42 @@ int bf_gdn_fwd(const void* q, const void* k, const void* v, const float* g, cons
                float scale, const float* initial_state, void* o, int o_dtype, float* final_state, void* workspace,
                size_t workspace_bytes, int phases, void* stream);
 
+/*
+ * Single-token gated delta rule (GQA): kernels.delta_rule_step(q, k, v, g, beta, state)
+ * (Heimdall/heimdall/kernels.py:132-138) and the inline rank-1 decode update of Heimdall/heimdall/hibrit.py:398-403.
+ *   S' = e^g S + k (beta (v - e^g S^T k))^T,   o_h = S'^T q_h for the R query heads of each KV head.
+ *   q [B][G*R][D], k, v [B][G][D], g, beta [B][G], state_in, state_out [B][G][D][D], o [B][G*R][D]; all fp32.
+ *   state_out may equal state_in (in-place update). R <= 8.
+ */
+int bf_gdn_step(const float* q, const float* k, const float* v, const float* g, const float* beta,
+                const float* state_in, float* state_out, float* o, int B, int G, int R, int D, void* stream);
+
+/*
+ * One decode step of the converted layer for B sequences, all at absolute position `pos`: the core of
+ * HybridAttention._student with t == 1 (Heimdall/heimdall/hibrit.py:363-424) and of the llama.cpp decode graph
+ * build_layer_bifrost (Heimdall/llamacpp/bifrost.patch:1039-1054,1118-1166), as one bandwidth-bound pass.
+ *   window: softmax over the sinks, the ring entries with max(sinks, pos-W+1) <= position <= pos-1 and the new token
+ *           (if pos >= sinks), scores qr.k / sqrt(D); lse written to `lse` (if non-null).
+ *   memory (memory != 0 and pos >= W): the ring row of position pos - W (slot pos mod W; ignored unless
+ *           ring_pos[slot] == pos - W) is written into the per-KV-head state (decay, delta rule), then read with qm.
+ *   mix:    gamma = sigmoid(z + mix_lse (lse - ln W)) when the memory is active; o = o_win + gamma (mem_scale o_mem - o_win).
+ *   cache:  ring slot pos mod W receives (kr, v, km, g_new, beta_new) and ring_pos[slot] = pos. Sinks are passed in
+ *           already holding the new token when pos < sinks (the caller appends it, as the reference does).
+ * Layouts: qr [B][H][D] (q_dtype), qm [B][H][D] f32 (normalised, scaled by 1/sqrt(D)), kr, v [B][G][D] (kv_dtype),
+ * km [B][G][D] f32, g_new, beta_new [B][G] f32, z [B][H] f32, mix_lse, mem_scale [H] f32, sink_k/sink_v
+ * [B][G][n_sinks][D] (kv_dtype), ring_k/ring_v [B][G][W][D] (kv_dtype), ring_km [B][W][G][D] f32,
+ * ring_g/ring_beta [B][W][G] f32, ring_pos [W] int64, state [B][G][D][D] f32 (updated in place), o [B][H][D] f32,
+ * lse [B][H] f32 or null. H = G*R, R <= 8, n_sinks <= 63.
+ */
+int bf_decode_workspace_size(int B, int G, int R, int D, int W, size_t* bytes);
+
+int bf_decode_fwd(int B, int G, int R, int D, int W, int sinks, int64_t pos, int memory, int kv_dtype, int q_dtype,
+                  const void* qr, const float* qm, const void* kr, const void* v, const float* km, const float* g_new,
+                  const float* beta_new, const float* z, const float* mix_lse, const float* mem_scale,
+                  const void* sink_k, const void* sink_v, int n_sinks, void* ring_k, void* ring_v, float* ring_km,
+                  float* ring_g, float* ring_beta, int64_t* ring_pos, float* state, float* o, float* lse,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

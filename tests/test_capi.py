@@ -40,6 +40,23 @@ def test_ctypes_signatures_cover_header():
     assert sorted(_lib.SIGNATURES) == declared_symbols()
 
 
+def declared_arity():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for name, args in re.findall(r"\b(bf_[a-z0-9_]+)\s*\(([^)]*)\)\s*;", text):
+        args = args.strip()
+        out[name] = 0 if args in ("", "void") else args.count(",") + 1
+    return out
+
+
+def test_ctypes_arity_matches_header():
+    from heimdall_amd import _lib
+    ar = declared_arity()
+    assert sorted(ar) == declared_symbols()
+    for name, (_, argtypes) in _lib.SIGNATURES.items():
+        assert len(argtypes) == ar[name], (name, len(argtypes), ar[name])
+
+
 def test_status_codes_without_gpu(cpu_lib):
     assert cpu_lib.bf_version() >= 100
     assert cpu_lib.bf_status_string(0) == b"ok"

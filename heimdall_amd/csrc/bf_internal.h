@@ -89,4 +89,31 @@ struct StepArgs {
 
 int step_dispatch(const StepArgs& a, hipStream_t stream);
 
+struct WinArgs {
+    int B, G, R, D, T, W, sinks;
+    long start;               // absolute position of the chunk's first token
+    int in_dtype, o_dtype;
+    const void* q;            // queries, element strides (batch, head, token), D contiguous
+    long q_sb, q_sh, q_st;
+    const void* k;            // chunk keys
+    long k_sb, k_sh, k_st;
+    const void* v;            // chunk values
+    long v_sb, v_sh, v_st;
+    const void* ring_k;       // [B][G][W][D] or null
+    const void* ring_v;
+    const int64_t* ring_pos;  // [W]
+    const void* sink_k;       // [B][G][n_sinks][D]
+    const void* sink_v;
+    int n_sinks;
+    int mix_on;
+    const float* o_mem;       // [B][T][H][D]
+    const float* z;           // [B][T][H]
+    const float* mix_lse;     // [H]
+    const float* mem_scale;   // [H]
+    void* o;                  // [B][T][H][D] o_dtype
+    float* lse;               // [B][H][T] or null
+};
+
+int window_dispatch(const WinArgs& a, hipStream_t stream);
+
 }  // namespace bf

@@ -55,7 +55,7 @@ def mem_inputs(self, x, q, k, pos):
     dh = self.c.dh
     qm = F.normalize(_heads_matmul(q.float(), self.fq), dim=-1) * dh ** -0.5
     km = F.normalize(_heads_matmul(k.float(), self.fk), dim=-1)
-    a, bb = self.ab(x).float().chunk(2, dim=-1)
+    a, bb = F.linear(x.float(), self.ab.weight.float(), self.ab.bias.float()).chunk(2, dim=-1)
     g = -self.A_log.float().exp() * F.softplus(a + self.dt_bias.float()) * self.decay_mask.float()
     beta = torch.sigmoid(bb) * (pos >= self.sinks).float()[None, :, None]
     return qm, km, g, beta
@@ -147,8 +147,71 @@ def student(self, x, q, k, v, qr, kr, start: int, cache: Optional[dict], memory:
     return o
 
 
+def _strides(t: torch.Tensor, dims):
+    return tuple(int(t.stride(d)) for d in dims)
+
+
 def _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memory):
-    raise NotImplementedError("prefill path (t > 1) of the HIP student is provided by the window kernel")
+    """A chunk of t > 1 tokens: memory branch on bf_gdn_fwd (write stream = ring rows leaving the window, then the
+    chunk's own rows, hibrit.py:391-408), then bf_window_fwd with the gamma mix fused (hibrit.py:385-411), then the
+    ring / sink / state write-back (hibrit.py:412-423)."""
+    c = self.c
+    b, t = x.shape[:2]
+    H, G, D, w, r = c.h, c.hkv, c.dh, self.window, c.h // c.hkv
+    dev = x.device
+    cdt = torch.bfloat16 if qr.dtype in (torch.bfloat16, torch.float16) else torch.float32
+    lib = _lib.load()
+    pos = torch.arange(start, start + t, device=dev)
+    use_mem = memory and start + t > w
+    o_mem = z = None
+    if use_mem:
+        # write stream: token i - W is written before the query at position i reads (ext[:t] of the reference)
+        pp = torch.arange(start - w, start, device=dev)
+        idx = pp % w
+        vf = (st["ring_pos"][idx] == pp).float()[None, :, None]
+        wk = torch.cat((st["ring_km"][:, idx].float(), km), 1)[:, :t]
+        wv = torch.cat((st["ring_v"][:, :, idx].transpose(1, 2).float(), v.float()), 1)[:, :t]
+        wg = torch.cat((st["ring_g"][:, idx] * vf, g), 1)[:, :t]
+        wb = torch.cat((st["ring_beta"][:, idx] * vf, beta), 1)[:, :t]
+        s0 = st.get("S")
+        o_mem, s_new = gdn_forward(qm.to(cdt).reshape(b * t, H, D), wk.to(cdt).reshape(b * t, G, D),
+                                   wv.to(cdt).reshape(b * t, G, D), wg.reshape(b * t, G), wb.reshape(b * t, G),
+                                   num_seqs=b, initial_state=None if s0 is None else s0.float())
+        o_mem = o_mem.view(b, t, H, D)
+        z = F.linear(x.float(), self.mix.weight.float(), self.mix.bias.float()).contiguous()
+    # window + sinks + LSE (+ mix)
+    q_ = qr.to(cdt)
+    q_ = q_ if q_.stride(-1) == 1 else q_.contiguous()
+    k_ = kr.to(cdt)
+    k_ = k_ if k_.stride(-1) == 1 else k_.contiguous()
+    v_ = v.to(cdt)
+    v_ = v_ if v_.stride(-1) == 1 else v_.contiguous()
+    rk, rv = st["ring_k"].to(cdt).contiguous(), st["ring_v"].to(cdt).contiguous()
+    ns = 0 if sink_k is None else sink_k.size(2)
+    sk = sink_k.to(cdt).contiguous() if ns else None
+    sv = sink_v.to(cdt).contiguous() if ns else None
+    o = torch.empty(b, t, H, D, dtype=torch.float32, device=dev)
+    lse = torch.empty(b, H, t, dtype=torch.float32, device=dev)
+    mix_lse = self.mix_lse.float().contiguous() if use_mem else None
+    mem_scale = self.mem_scale.float().contiguous() if use_mem else None
+    ptr = lambda t_: t_.data_ptr() if t_ is not None else None
+    check(lib.bf_window_fwd(b, G, r, D, t, w, self.sinks, start, dtype_code(cdt),
+                            ptr(q_), *_strides(q_, (0, 1, 2)), ptr(k_), *_strides(k_, (0, 1, 2)),
+                            ptr(v_), *_strides(v_, (0, 2, 1)), ptr(rk), ptr(rv), ptr(st["ring_pos"]), ptr(sk),
+                            ptr(sv), ns, int(use_mem), ptr(o_mem), ptr(z), ptr(mix_lse), ptr(mem_scale), ptr(o),
+                            dtype_code(torch.float32), ptr(lse), stream_ptr(dev)), "bf_window_fwd")
+    # cache write-back: the last min(t, W) tokens take their ring slots
+    n = min(t, w)
+    slot = pos[-n:] % w
+    st["ring_k"][:, :, slot] = kr[:, :, -n:].to(st["ring_k"].dtype)
+    st["ring_v"][:, :, slot] = v.transpose(1, 2)[:, :, -n:].to(st["ring_v"].dtype)
+    st["ring_km"][:, slot] = km[:, -n:].float()
+    st["ring_g"][:, slot] = g[:, -n:].float()
+    st["ring_beta"][:, slot] = beta[:, -n:].float()
+    st["ring_pos"][slot] = pos[-n:]
+    if use_mem:
+        st["S"] = s_new
+    return o
 
 
 class BifrostCore(nn.Module):

@@ -137,12 +137,117 @@ def cpu_baseline(inputs, budget_s=30.0):
                       f"{len(times)} run(s), {cpu_model()}"}
 
 
+def run_decode(steps, warmup, dev):
+    """Decode step, B=64, H=16, G=4, D=256, W=2048 + 4 sinks, bf16 ring, fp32 state ~ N(0, 0.02), at position
+    100000 (ring full, memory active): the bf_decode_fwd pass alone, inputs resident."""
+    from heimdall_amd import _lib
+    from heimdall_amd._device import stream_ptr, workspace
+
+    B, H, G, D, W, S = 64, 16, 4, 256, 2048, 4
+    R, p = H // G, 100000
+    gen = torch.Generator(device=dev).manual_seed(1)
+    rn = lambda *shape: torch.randn(*shape, device=dev, generator=gen)
+    ring_k, ring_v = rn(B, G, W, D).bfloat16(), rn(B, G, W, D).bfloat16()
+    sink_k, sink_v = rn(B, G, S, D).bfloat16(), rn(B, G, S, D).bfloat16()
+    ring_km = F.normalize(rn(B, W, G, D), dim=-1)
+    ring_g = -torch.rand(B, W, G, device=dev, generator=gen) * 1e-3
+    ring_beta = torch.sigmoid(rn(B, W, G))
+    ring_pos = torch.tensor([pp for pp in range(p - W, p)], device=dev, dtype=torch.long)
+    ring_pos = ring_pos[torch.argsort(ring_pos % W)].contiguous()
+    state = rn(B, G, D, D) * 0.02
+    qr = F.normalize(rn(B, H, D), dim=-1).bfloat16()
+    qm = F.normalize(rn(B, H, D), dim=-1) * D ** -0.5
+    kr, v = F.normalize(rn(B, G, D), dim=-1).bfloat16(), rn(B, G, D).bfloat16()
+    km = F.normalize(rn(B, G, D), dim=-1)
+    g_new = -torch.rand(B, G, device=dev, generator=gen) * 1e-3
+    b_new = torch.sigmoid(rn(B, G))
+    z = rn(B, H)
+    mix_lse, mem_scale = torch.zeros(H, device=dev), torch.full((H,), D ** 0.5, device=dev)
+    o = torch.empty(B, H, D, device=dev)
+    lib = _lib.load()
+    nb = _lib.ctypes.c_size_t(0)
+    _lib.check(lib.bf_decode_workspace_size(B, G, R, D, W, _lib.ctypes.byref(nb)), "bf_decode_workspace_size")
+    ws = workspace(nb.value, dev)
+    st = stream_ptr(dev)
+    args = (B, G, R, D, W, S, p, 1, _lib.DTYPE_BF16, _lib.DTYPE_BF16, qr.data_ptr(), qm.data_ptr(), kr.data_ptr(),
+            v.data_ptr(), km.data_ptr(), g_new.data_ptr(), b_new.data_ptr(), z.data_ptr(), mix_lse.data_ptr(),
+            mem_scale.data_ptr(), sink_k.data_ptr(), sink_v.data_ptr(), S, ring_k.data_ptr(), ring_v.data_ptr(),
+            ring_km.data_ptr(), ring_g.data_ptr(), ring_beta.data_ptr(), ring_pos.data_ptr(), state.data_ptr(),
+            o.data_ptr(), None, ws.data_ptr(), ws.numel(), st)
+    for _ in range(warmup):
+        _lib.check(lib.bf_decode_fwd(*args), "bf_decode_fwd")
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(torch.cuda.current_stream(dev))
+    for _ in range(steps):
+        lib.bf_decode_fwd(*args)
+    e1.record(torch.cuda.current_stream(dev))
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    # algorithmic bytes: state read + write, full ring K and V read (W slots) + sinks + new row, queries, outputs
+    nbytes = (B * G * D * D * 4 * 2 + B * G * (W + S + 1) * D * 2 * 2 + B * H * D * (2 + 4 + 4)
+              + B * G * D * (4 + 2 + 2 + 4))
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"workload": "decode B=64 H=16 G=4 D=256 W=2048+4 bf16 ring, fp32 state", "us_per_step": us,
+            "steps": steps, "roofline": {"bound": "hbm", "kernel": "decode_main_kernel+decode_combine_kernel",
+                                         "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                         "frac": gbs / HBM_PEAK_GBS, "bytes_per_step": nbytes}}
+
+
+def window_pairs(T, W, S):
+    """Visible (query, key) pairs per head over positions 0..T-1: min(p + 1, W + S) each."""
+    return sum(min(p + 1, W + S) for p in range(T))
+
+
+def run_layer(steps, warmup, dev):
+    """Full converted-layer prefill at 32K: B=1, T=32768, H=24, G=4, D=256, W=2048 + 4 sinks, bf16 activations,
+    fp32 state; x/q/k/v/qr/kr synthetic (q, k L2-normalised), init-time gates (fq = fk = I). One step =
+    heimdall_amd.hibrit.student over the whole chunk from an empty cache (memory branch, window, mix, cache)."""
+    from heimdall_amd import hibrit
+
+    B, T, H, G, D, W, S, d = 1, 32768, 24, 4, 256, 2048, 4, 1024
+    torch.manual_seed(0)
+    m = hibrit.BifrostCore(hibrit.CoreConfig(H, G, D, d))
+    m.convert(W, S, 1)
+    m = m.to(dev)
+    gen = torch.Generator(device=dev).manual_seed(2)
+    rn = lambda *shape: torch.randn(*shape, device=dev, generator=gen)
+    x = rn(B, T, d).bfloat16()
+    q = F.normalize(rn(B, T, H, D), dim=-1).bfloat16()
+    k = F.normalize(rn(B, T, G, D), dim=-1).bfloat16()
+    v = rn(B, T, G, D).bfloat16()
+    qr, kr = q.transpose(1, 2).contiguous(), k.transpose(1, 2).contiguous()
+
+    def step():
+        return hibrit.student(m, x, q, k, v, qr, kr, 0, {})
+
+    with torch.no_grad():
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    pairs = window_pairs(T, W, S)
+    win_flops = 4 * D * pairs * H
+    chunks = T // C
+    mem_flops = chunks * G * (8 * C * C * D + 6 * C * D * D + 2 * C * C * D) + chunks * (H - G) * (
+        4 * C * D * D + 4 * C * C * D)
+    return {"workload": "layer prefill B=1 T=32768 H=24 G=4 D=256 W=2048+4 bf16", "ms_per_step": ms,
+            "tokens_per_s": T / (ms * 1e-3), "steps": steps, "flops": {"window": win_flops, "memory": mem_flops},
+            "tflops": (win_flops + mem_flops) / (ms * 1e-3) / 1e12}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="skip the decode and layer-prefill legs")
+    ap.add_argument("--copy-probe", action="store_true", help="run one 256 MiB device copy first (counter scaling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the Bifrost core needs no inter-GPU exchange; "
@@ -150,6 +255,13 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_probe:
+        # a plain copy of known size, so HBM byte counters of a profiling run can be scaled (read and write 256 MiB)
+        src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     r = run_gdn(args.steps, args.warmup, dev)
     T, H, D = r["T"], r["H"], r["D"]
@@ -181,6 +293,9 @@ def main():
         "hbm": {"algorithmic_bytes": gdn_bytes(T, H, D),
                 "achieved_GBs": gdn_bytes(T, H, D) / (ms * 1e-3) / 1e9, "peak_GBs": HBM_PEAK_GBS},
     }
+    if not args.no_extra:
+        line["decode"] = run_decode(100, 10, dev)
+        line["layer_prefill_32k"] = run_layer(3, 1, dev)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(r["inputs"])
     print(json.dumps(line), flush=True)

@@ -9,7 +9,7 @@
 //
 // Two kernels:
 //   gdn_prep  grid (chunks, G): everything that does not depend on S, fully parallel.
-//   gdn_scan  grid (Dv / BV, G, sequences): the sequential pass. Columns of S are independent, so each workgroup
+//   gdn_scan  one workgroup per (sequence, KV head, Dv / BV slab), XCD-grouped: the sequential pass. Columns of S are independent, so each workgroup
 //             owns a BV-column slab of one KV head's state, keeps it in registers (fp32) for the whole sequence and
 //             a bf16/fp32 copy in LDS as the MFMA B operand.
 //
@@ -21,6 +21,7 @@
 namespace bf {
 
 constexpr int CH = 64;     // chunk length
+constexpr int kXcds = 8;   // XCDs of an MI355X (gfx950); workgroups are dispatched round-robin across them
 constexpr int NT = 256;    // threads per workgroup (4 waves)
 
 template <class E, int D>
@@ -468,8 +469,14 @@ __global__ __launch_bounds__(NT_SCAN) void gdn_scan_kernel(GdnArgs a) {
     constexpr int NCT = BV / 16, NRT = D / 16, RPW = SF::RPW;
     __shared__ ScanShared<E, D, BV> sm;
 
-    const int jb = blockIdx.x, g = blockIdx.y, n = blockIdx.z;
+    // XCD-aware mapping: workgroups are dispatched round-robin over the XCDs by linear id, and every column slab of
+    // one (sequence, KV head) reads the same chunk operands, so all slabs of a group go to one XCD (one L2).
+    const int xcd = blockIdx.x % kXcds, local = blockIdx.x / kXcds;
+    const int nslab = D / BV;
+    const int grp = xcd + kXcds * (local / nslab), jb = local % nslab;
     const int G = a.G;
+    if (grp >= a.num_seqs * G) return;
+    const int g = grp % G, n = grp / G;
     const int lane = lane_id(), wv = wave_id(), lg = lane >> 4, l16 = lane & 15;
     const int j0 = jb * BV;
     int first, count;
@@ -522,7 +529,8 @@ static int launch_gdn(const GdnArgs& a, int phases, hipStream_t stream) {
         if (e != hipSuccess) return (int)e;
     }
     if (phases & GDN_PHASE_SCAN) {
-        const dim3 grid(D / BV, a.G, a.num_seqs);
+        const int groups = a.num_seqs * a.G;
+        const dim3 grid(kXcds * ((groups + kXcds - 1) / kXcds) * (D / BV));
         if (a.o_dtype == DT_BF16) hipLaunchKernelGGL((gdn_scan_kernel<E, D, BV, true>), grid, dim3(NT_SCAN), 0, stream, a);
         else hipLaunchKernelGGL((gdn_scan_kernel<E, D, BV, false>), grid, dim3(NT_SCAN), 0, stream, a);
         const hipError_t e = hipGetLastError();

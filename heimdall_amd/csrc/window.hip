@@ -32,19 +32,8 @@ struct WinShared {
     typename E::T ks[KB][D + E::VEC];        // key rows of the block
     typename E::T vt[D][KB + E::VEC];        // value rows of the block, transposed [d][key]
     int valid[KB];                           // key row holds a real key (else its scores are masked)
-    long kpos[KB];                           // absolute position of the key row
+    int krel[KB];                            // key position minus the workgroup's first query position
 };
-
-// Source row of key position kp (or null when the position has no key): ring for kp < start, chunk for kp >= start.
-template <class T>
-__device__ __forceinline__ const T* key_src(const WinArgs& a, const T* ring, const T* chunk, long cs_tok, long kp) {
-    if (kp < a.start) {
-        if (!ring) return nullptr;
-        const int slot = (int)(kp % a.W);
-        return a.ring_pos[slot] == kp ? ring + (long)slot * a.D : nullptr;
-    }
-    return chunk + (kp - a.start) * cs_tok;
-}
 
 template <class E, int D>
 struct WinPrefetch {
@@ -55,44 +44,50 @@ struct WinPrefetch {
     static constexpr int VPT = (VBT * VBD + NT_WIN - 1) / NT_WIN;      // V blocks per thread
     uint4 k[KCH];
     uint4 v[VPT][E::VEC];
+    uint2 rp;          // ring_pos of row (thread % KB) for ring blocks, read with the rows
 };
 
-// Block `blk` of key rows: blk < 0 is the sink block (rows = sinks), else positions kb0 .. kb0 + KB - 1.
+// The keys of a workgroup are split into segments that each come from one contiguous source: the sinks, the ring
+// up to its wrap point, the ring after it, and the chunk. A key block never straddles two segments, so the address
+// of every row is base + min(row, last) * stride with no per-row branching.
+template <class T>
+struct KeySeg {
+    const T* kb;       // first key row of the segment
+    const T* vb;       // first value row
+    long ks, vs;       // row strides (elements)
+    long pos0;         // position of the first row (sinks: 0)
+    int count;         // rows
+    int slot0;         // ring slot of the first row, or -1 outside the ring
+    int sink;          // sink rows: visible to every query at or after their position, no window limit
+};
+
+// Load the rows of one key block into registers. Rows past the segment's end re-read its last row; their scores are
+// masked to -inf so they add nothing (exec-masked loads would make the compiler wait for the whole prefetch early).
 template <class E, int D>
-__device__ __forceinline__ void win_fetch(WinPrefetch<E, D>& f, const WinArgs& a, bool sink_block, long kb0, long kp_hi,
-                                          const typename E::T* rk, const typename E::T* rv, const typename E::T* ck,
-                                          const typename E::T* cv, const typename E::T* sk, const typename E::T* sv) {
-    using T = typename E::T;
+__device__ __forceinline__ void win_fetch(WinPrefetch<E, D>& f, const KeySeg<typename E::T>& br, rsrc_t rpos) {
     using P = WinPrefetch<E, D>;
-    constexpr int VEC = E::VEC, KB = P::KB;
+    constexpr int VEC = E::VEC;
     const int tid = threadIdx.x;
-    auto src = [&](int row, bool val) -> const T* {
-        if (sink_block) return row < a.n_sinks ? (val ? sv : sk) + (long)row * D : nullptr;
-        const long kp = kb0 + row;
-        if (kp > kp_hi) return nullptr;
-        return key_src<T>(a, val ? rv : rk, val ? cv : ck, val ? a.v_st : a.k_st, kp);
-    };
+    const int last = min(br.count, P::KB) - 1;
+    // out-of-range offset (outside the ring) reads 0
+    f.rp = buf_ld8(rpos, br.slot0 >= 0 ? (uint32_t)(br.slot0 + min(tid % P::KB, last)) * 8u : 0xFFFFFFF0u);
 #pragma unroll
     for (int j = 0; j < P::KCH; ++j) {
         const int c = tid + NT_WIN * j, row = c / P::CPR, col = (c % P::CPR) * VEC;
-        const T* p = src(row, false);
-        f.k[j] = p ? ld16(p + col) : zero16();
+        f.k[j] = ld16(br.kb + min(row, last) * br.ks + col);
     }
 #pragma unroll
     for (int j = 0; j < P::VPT; ++j) {
         const int blk = tid + NT_WIN * j;
-        const int bt = blk % P::VBT, bd = blk / P::VBT;
+        const int bt = blk % P::VBT, bd = (blk / P::VBT) % P::VBD;
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) {
-            const T* p = blk < P::VBT * P::VBD ? src(bt * VEC + i, true) : nullptr;
-            f.v[j][i] = p ? ld16(p + bd * VEC) : zero16();
-        }
+        for (int i = 0; i < VEC; ++i) f.v[j][i] = ld16(br.vb + min(bt * VEC + i, last) * br.vs + bd * VEC);
     }
 }
 
 template <class E, int D>
-__device__ __forceinline__ void win_park(WinShared<E, D>& sm, WinPrefetch<E, D>& f, const WinArgs& a, bool sink_block,
-                                         long kb0, long kp_hi) {
+__device__ __forceinline__ void win_park(WinShared<E, D>& sm, WinPrefetch<E, D>& f, const WinArgs& a,
+                                         const KeySeg<typename E::T>& br, long p_first) {
     using P = WinPrefetch<E, D>;
     constexpr int VEC = E::VEC, KB = P::KB;
     const int tid = threadIdx.x;
@@ -112,17 +107,12 @@ __device__ __forceinline__ void win_park(WinShared<E, D>& sm, WinPrefetch<E, D>&
         }
     }
     if (tid < KB) {
-        bool val;
-        long kp;
-        if (sink_block) {
-            kp = tid;
-            val = tid < a.n_sinks;
-        } else {
-            kp = kb0 + tid;
-            val = kp <= kp_hi && (kp >= a.start || (a.ring_k && a.ring_pos[(int)(kp % a.W)] == kp));
-        }
+        const long kp = br.pos0 + tid;
+        bool val = tid < br.count;
+        if (br.slot0 >= 0) val = val && (long)(((uint64_t)f.rp.y << 32) | f.rp.x) == kp;
         sm.valid[tid] = val;
-        sm.kpos[tid] = kp;
+        const long rel = kp - p_first;                      // sinks far behind the chunk clamp (always visible)
+        sm.krel[tid] = (int)max(rel, -(1L << 30));
     }
 }
 
@@ -162,46 +152,82 @@ __global__ __launch_bounds__(NT_WIN) void window_kernel(WinArgs a) {
 #pragma unroll
         for (int kf = 0; kf < NKD; ++kf) fq[qt][kf] = qi < nq ? ld16(qrow + kf * KF + VEC * lg) : zero16();
     }
-    long qpos[NQT];
+    int qrel[NQT];                                        // query position minus p_first
     f32x4 o[NDT][NQT];
     float m[NQT], l[NQT];
 #pragma unroll
     for (int qt = 0; qt < NQT; ++qt) {
-        qpos[qt] = p_first + QW * wv + 16 * qt + l16;
+        qrel[qt] = QW * wv + 16 * qt + l16;
         m[qt] = -INFINITY;
         l[qt] = 0.f;
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) o[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    // key blocks: the sink block (if any), then window positions [kp_lo, p_last] in blocks of KB
+    // key segments (sinks, ring before its wrap point, ring after it, chunk), consumed in blocks of KB rows
+    using Seg = KeySeg<T>;
     const long kp_lo = max((long)a.sinks, p_first - a.W + 1);
-    const int nwin = p_last >= kp_lo ? (int)((p_last - kp_lo) / KB + 1) : 0;
-    const int nblk = (a.n_sinks ? 1 : 0) + nwin;
-    auto blk_info = [&](int i, bool& sink, long& kb0) {
-        sink = a.n_sinks && i == 0;
-        kb0 = kp_lo + (long)(i - (a.n_sinks ? 1 : 0)) * KB;
+    Seg sg[4];
+    int nb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        sg[j] = Seg{ck, cv, 0, 0, 0, 0, -1, 0};
+        nb[j] = 0;
+    }
+    if (a.n_sinks) sg[0] = Seg{sk, sv, D, D, 0, a.n_sinks, -1, 1};
+    const long rhi = min(p_last, a.start - 1);
+    if (rk && kp_lo <= rhi) {
+        const int sa = (int)(kp_lo % a.W);                  // one division per workgroup
+        const long n = rhi - kp_lo + 1;
+        const long n1 = min(n, (long)(a.W - sa));
+        sg[1] = Seg{rk + (long)sa * D, rv + (long)sa * D, D, D, kp_lo, (int)n1, sa, 0};
+        if (n > n1) sg[2] = Seg{rk, rv, D, D, kp_lo + n1, (int)(n - n1), 0, 0};
+    }
+    const long clo = max(kp_lo, a.start);
+    if (clo <= p_last)
+        sg[3] = Seg{ck + (clo - a.start) * a.k_st, cv + (clo - a.start) * a.v_st, a.k_st, a.v_st, clo,
+                    (int)(p_last - clo + 1), -1, 0};
+    int nblk = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        nb[j] = (sg[j].count + KB - 1) / KB;
+        nblk += nb[j];
+    }
+    // block i as a segment of its own: the KB rows starting at row KB * (i - first block of its segment)
+    auto block_ref = [&](int i) {
+        Seg r = sg[3];
+        int base = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (i >= base && i < base + nb[j]) {
+                const int off = (i - base) * KB;
+                r = sg[j];
+                r.kb += off * sg[j].ks;
+                r.vb += off * sg[j].vs;
+                r.pos0 += off;
+                r.count -= off;
+                if (r.slot0 >= 0) r.slot0 += off;
+            }
+            base += nb[j];
+        }
+        return r;
     };
 
+    const rsrc_t rpos = make_rsrc(a.ring_pos, a.ring_pos ? (uint32_t)a.W * 8u : 0u);
     P pf;
+    Seg br;
     if (nblk > 0) {
-        bool sb;
-        long kb0;
-        blk_info(0, sb, kb0);
-        win_fetch<E, D>(pf, a, sb, kb0, p_last, rk, rv, ck, cv, sk, sv);
+        br = block_ref(0);
+        win_fetch<E, D>(pf, br, rpos);
     }
     for (int i = 0; i < nblk; ++i) {
-        bool sb;
-        long kb0;
-        blk_info(i, sb, kb0);
+        const bool sb = br.sink;
         __syncthreads();                                   // previous block fully consumed
-        win_park<E, D>(sm, pf, a, sb, kb0, p_last);
+        win_park<E, D>(sm, pf, a, br, p_first);
         __syncthreads();
-        if (i + 1 < nblk) {
-            bool sb2;
-            long kb2;
-            blk_info(i + 1, sb2, kb2);
-            win_fetch<E, D>(pf, a, sb2, kb2, p_last, rk, rv, ck, cv, sk, sv);
+        if (i + 1 < nblk) {                                // uniform: the next block's loads fly during this one
+            br = block_ref(i + 1);
+            win_fetch<E, D>(pf, br, rpos);
         }
         // S^T = K Q^T for this block
         f32x4 s[NKT][NQT];
@@ -220,14 +246,14 @@ __global__ __launch_bounds__(NT_WIN) void window_kernel(WinArgs a) {
         // mask, online softmax per query column
 #pragma unroll
         for (int qt = 0; qt < NQT; ++qt) {
-            const long qp = qpos[qt];
+            const int qp = qrel[qt];
             float bm = -INFINITY;
 #pragma unroll
             for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int kr = 16 * kt + 4 * lg + e;
-                    const long kp = sm.kpos[kr];
+                    const int kp = sm.krel[kr];
                     const bool vis = sm.valid[kr] && kp <= qp && (sb || qp - kp < a.W);
                     const float x = vis ? s[kt][qt][e] * scale : -INFINITY;
                     s[kt][qt][e] = x;
@@ -300,7 +326,7 @@ __global__ __launch_bounds__(NT_WIN) void window_kernel(WinArgs a) {
         const float lse = m[qt] + logf(l[qt]);
         if (a.lse && lg == 0) a.lse[((long)b * H + h) * a.T + tq] = lse;
         float gam = 0.f;
-        if (a.mix_on && qpos[qt] >= a.W)
+        if (a.mix_on && p_first + qrel[qt] >= a.W)
             gam = 1.f / (1.f + __expf(-(a.z[((long)b * a.T + tq) * H + h] + a.mix_lse[h] * (lse - lnW))));
         const float ms = a.mix_on ? a.mem_scale[h] : 0.f;
         const long orow = (((long)b * a.T + tq) * H + h) * D;

@@ -57,11 +57,12 @@ def gdn_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tens
                 num_seqs: int, cu_seqlens: Optional[torch.Tensor] = None, initial_state: Optional[torch.Tensor] = None,
                 scale: float = 1.0, out_dtype: torch.dtype = torch.float32, phases: int = _lib.PHASE_ALL,
                 out: Optional[torch.Tensor] = None, final_state: Optional[torch.Tensor] = None,
-                ws: Optional[torch.Tensor] = None):
+                ws: Optional[torch.Tensor] = None, segment_chunks: int = 0):
     """Packed GQA gated delta rule on the GPU.
 
     q [N, G*R, D], k [N, G, D], v [N, G, D], g/beta [N, G]; cu_seqlens int32 [num_seqs + 1] on the device or None
-    (equal sequences). Returns (o [N, G*R, D] out_dtype, final_state [num_seqs, G, D, D] fp32).
+    (equal sequences). ``segment_chunks``: 64-token chunks per independently scanned segment (0 = chosen from the
+    problem size). Returns (o [N, G*R, D] out_dtype, final_state [num_seqs, G, D, D] fp32).
     """
     dev = require_device(q, k, v, g, beta, cu_seqlens, initial_state)
     N, H, D = q.shape
@@ -88,8 +89,8 @@ def gdn_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tens
             raise BifrostError(f"initial_state must be [{num_seqs}, {G}, {D}, {D}], got {tuple(s0.shape)}")
     lib = _lib.load()
     nbytes = _lib.ctypes.c_size_t(0)
-    check(lib.bf_gdn_workspace_size(N, num_seqs, G, R, D, dtype_code(cdt), _lib.ctypes.byref(nbytes)),
-          "bf_gdn_workspace_size")
+    check(lib.bf_gdn_workspace_size(N, num_seqs, G, R, D, dtype_code(cdt), int(segment_chunks),
+                                    _lib.ctypes.byref(nbytes)), "bf_gdn_workspace_size")
     if ws is None or ws.numel() < nbytes.value:
         ws = workspace(nbytes.value, dev)
     o = out if out is not None else torch.empty(N, H, D, dtype=out_dtype, device=dev)
@@ -98,6 +99,7 @@ def gdn_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tens
     check(lib.bf_gdn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
                          cu_seqlens.data_ptr() if cu_seqlens is not None else None, num_seqs, N, G, R, D,
                          dtype_code(cdt), float(scale), s0.data_ptr() if s0 is not None else None, o.data_ptr(),
-                         dtype_code(o.dtype), s_out.data_ptr(), ws.data_ptr(), ws.numel(), phases, stream_ptr(dev)),
+                         dtype_code(o.dtype), s_out.data_ptr(), int(segment_chunks), ws.data_ptr(), ws.numel(), phases,
+                         stream_ptr(dev)),
           "bf_gdn_fwd")
     return o, s_out

@@ -24,6 +24,12 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
     __bf16 b = (__bf16)f;  // v_cvt_pk_bf16_f32: round to nearest even
     return __builtin_bit_cast(uint16_t, b);
 }
+// Two floats to packed bf16 (x in the low half) with one v_cvt_pk_bf16_f32, round to nearest even.
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+__device__ __forceinline__ uint32_t pack_bf16x2(float x, float y) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{x, y}, bf16x2));
+}
 
 // Element-type traits. VEC = elements per 16-byte vector; KF = K covered by one fragment per MFMA group.
 struct BF16 {
@@ -128,7 +134,10 @@ __device__ __forceinline__ void transpose_block<BF16>(uint4 (&r)[8]) {
 __device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (WAVE - 1); }
-__device__ __forceinline__ int wave_id() { return threadIdx.x / WAVE; }
+// Wave index inside the workgroup, marked wave-uniform (readfirstlane) so that values derived from it (buffer
+// descriptors, LDS bases, loop bounds) live in SGPRs; plain threadIdx.x / 64 is treated as divergent and descriptors
+// built from it are executed in a waterfall loop.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x / WAVE); }
 
 // Sequence/chunk bookkeeping for packed variable-length input. cu (device, num_seqs + 1 entries) may be null, in
 // which case every sequence has length seq_len. Chunk ids enumerate the chunks of sequence 0, then 1, ...
@@ -184,8 +193,14 @@ namespace bf {
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 constexpr int kRsrcWord3 = 0x00020000;   // raw (untyped) 32-bit buffer, gfx9-family layout
 
+// The base and range must be wave-uniform: they are moved to SGPRs with readfirstlane (a descriptor the compiler
+// cannot prove uniform is otherwise used through a waterfall loop, one iteration per distinct lane value).
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t nbytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)nbytes, kRsrcWord3);
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    void* ub = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(ub, (short)0, (int)__builtin_amdgcn_readfirstlane(nbytes), kRsrcWord3);
 }
 __device__ __forceinline__ uint4 buf_ld16(rsrc_t r, uint32_t off) {
     return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));

@@ -12,7 +12,8 @@ constexpr int DT_F32 = BF_DTYPE_F32;
 constexpr int DT_BF16 = BF_DTYPE_BF16;
 constexpr int BF_ERR_UNSUPPORTED = BF_STATUS_UNSUPPORTED;
 constexpr int GDN_PHASE_PREP = BF_GDN_PHASE_PREP;
-constexpr int GDN_PHASE_SCAN = BF_GDN_PHASE_SCAN;
+constexpr int GDN_PHASE_STATES = BF_GDN_PHASE_STATES;
+constexpr int GDN_PHASE_OUTPUT = BF_GDN_PHASE_OUTPUT;
 
 struct GdnArgs {
     const void* q;           // [N_tok][G*R][D]  in_dtype
@@ -31,15 +32,23 @@ struct GdnArgs {
     void* o;                 // [N_tok][G*R][D]  o_dtype
     float* s_out;            // [num_seqs][G][D][D] or null
     int max_chunks;          // grid bound for the per-chunk kernel
-    // workspace carve-up
-    float* ws_gcum;
-    void* ws_w;
-    float* ws_uT;
-    void* ws_kt;
-    void* ws_attn;
+    int seg_chunks;          // chunks per segment (L)
+    int max_segs;            // grid bound on segments over all sequences
+    int multi_seg;           // some sequence may span more than one segment (STATES phase needed)
+    // workspace carve-up (cid = chunk id, sid = segment id; C = 64)
+    float* ws_gcum;          // [cid][G][C]        in-chunk cumulative log-decay
+    void* ws_T;              // [cid][G][C][C]     (I + A)^-1 diag(beta), in_dtype
+    void* ws_attn;           // [cid][H][C][C]     scale * (q k^T masked, decayed), in_dtype
+    void* ws_phi;            // [sid][G][D][D]     Psi = Phi - c I of each segment map (in_dtype)
+    float* ws_c;             // [sid][G]           c = e^{sum of g over the segment}
+    float* ws_n;             // [sid][G][D][D]     segment state from a zero entry state (fp32)
+    float* ws_sin;           // [sid][G][D][D]     entry state of each segment (fp32; written for segments > 0)
 };
 
-int gdn_dispatch(const GdnArgs& a, int phases, hipStream_t stream);
+int gdn_prep(const GdnArgs& a, hipStream_t stream);
+int gdn_states(const GdnArgs& a, hipStream_t stream);
+int gdn_output(const GdnArgs& a, hipStream_t stream);
+
 
 struct DecodeArgs {
     int B, G, R, D, W, sinks;

@@ -14,21 +14,39 @@ bool supported_dtype(int dt) { return dt == BF_DTYPE_F32 || dt == BF_DTYPE_BF16;
 size_t esize(int dt) { return dt == BF_DTYPE_BF16 ? 2 : 4; }
 
 struct GdnLayout {
-    size_t gcum, w, uT, kt, attn, total;
-    int max_chunks;
+    size_t gcum, T, attn, phi, c, n, sin, total;
+    int max_chunks, seg_chunks, max_segs;
 };
 
-GdnLayout gdn_layout(int64_t total_tokens, int num_seqs, int G, int R, int D, int in_dtype) {
+// Segment length (chunks) when the caller passes 0: enough segments that the output scan has about
+// kSegTargetWgs workgroups in flight (each (segment, KV head) pair runs D/128 column groups per query head),
+// and at least kSegMinChunks chunks per segment so the per-segment summary and combine stay small.
+constexpr int kSegTargetWgs = 256;
+constexpr int kSegMinChunks = 8;
+
+int auto_segment_chunks(int max_chunks, int G, int R, int D) {
+    const long per_seg = (long)G * R * (D >= 128 ? D / 128 : 1);
+    const long want_segs = kSegTargetWgs / per_seg > 1 ? kSegTargetWgs / per_seg : 1;
+    const long L = (max_chunks + want_segs - 1) / want_segs;
+    return (int)(L > kSegMinChunks ? L : kSegMinChunks);
+}
+
+GdnLayout gdn_layout(int64_t total_tokens, int num_seqs, int G, int R, int D, int in_dtype, int segment_chunks) {
     GdnLayout L;
     // every sequence contributes ceil(len / C) chunks: at most total/C + num_seqs overall
     L.max_chunks = (int)(total_tokens / kChunk) + num_seqs;
-    const size_t nc = (size_t)L.max_chunks, e = esize(in_dtype);
+    L.seg_chunks = segment_chunks > 0 ? segment_chunks : auto_segment_chunks(L.max_chunks, G, R, D);
+    // every sequence contributes max(1, ceil(chunks / L)) segments
+    L.max_segs = (L.max_chunks + L.seg_chunks - 1) / L.seg_chunks + num_seqs;
+    const size_t nc = (size_t)L.max_chunks, ns = (size_t)L.max_segs, e = esize(in_dtype);
     size_t off = 0;
     L.gcum = off; off = align256(off + nc * G * kChunk * sizeof(float));
-    L.w = off;    off = align256(off + nc * G * kChunk * D * e);
-    L.uT = off;   off = align256(off + nc * G * D * kChunk * sizeof(float));
-    L.kt = off;   off = align256(off + nc * G * D * kChunk * e);
+    L.T = off;    off = align256(off + nc * G * kChunk * kChunk * e);
     L.attn = off; off = align256(off + nc * G * R * kChunk * kChunk * e);
+    L.phi = off;  off = align256(off + ns * G * D * D * e);
+    L.c = off;    off = align256(off + ns * G * sizeof(float));
+    L.n = off;    off = align256(off + ns * G * D * D * sizeof(float));
+    L.sin = off;  off = align256(off + ns * G * D * D * sizeof(float));
     L.total = off;
     return L;
 }
@@ -50,23 +68,26 @@ const char* bf_status_string(int status) {
     return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
 }
 
-int bf_gdn_workspace_size(int64_t total_tokens, int num_seqs, int G, int R, int D, int in_dtype, size_t* bytes) {
-    if (!bytes || total_tokens < 0 || num_seqs <= 0 || G <= 0 || R <= 0) return BF_STATUS_INVALID;
+int bf_gdn_workspace_size(int64_t total_tokens, int num_seqs, int G, int R, int D, int in_dtype,
+                          int segment_chunks, size_t* bytes) {
+    if (!bytes || total_tokens < 0 || num_seqs <= 0 || G <= 0 || R <= 0 || segment_chunks < 0)
+        return BF_STATUS_INVALID;
     if (!supported_dim(D) || !supported_dtype(in_dtype)) return BF_STATUS_UNSUPPORTED;
-    *bytes = gdn_layout(total_tokens, num_seqs, G, R, D, in_dtype).total;
+    *bytes = gdn_layout(total_tokens, num_seqs, G, R, D, in_dtype, segment_chunks).total;
     return BF_STATUS_OK;
 }
 
 int bf_gdn_fwd(const void* q, const void* k, const void* v, const float* g, const float* beta,
                const int32_t* cu_seqlens, int num_seqs, int64_t total_tokens, int G, int R, int D, int in_dtype,
-               float scale, const float* initial_state, void* o, int o_dtype, float* final_state, void* workspace,
-               size_t workspace_bytes, int phases, void* stream) {
-    if (num_seqs <= 0 || total_tokens < 0 || G <= 0 || R <= 0 || (phases & ~BF_GDN_PHASE_ALL) || !phases)
+               float scale, const float* initial_state, void* o, int o_dtype, float* final_state,
+               int segment_chunks, void* workspace, size_t workspace_bytes, int phases, void* stream) {
+    if (num_seqs <= 0 || total_tokens < 0 || G <= 0 || R <= 0 || segment_chunks < 0 ||
+        (phases & ~BF_GDN_PHASE_ALL) || !phases)
         return BF_STATUS_INVALID;
     if (!supported_dim(D) || !supported_dtype(in_dtype) || !supported_dtype(o_dtype)) return BF_STATUS_UNSUPPORTED;
     if (!cu_seqlens && total_tokens % num_seqs) return BF_STATUS_INVALID;
     if (total_tokens > 0 && (!q || !k || !v || !g || !beta || !o)) return BF_STATUS_INVALID;
-    const GdnLayout L = gdn_layout(total_tokens, num_seqs, G, R, D, in_dtype);
+    const GdnLayout L = gdn_layout(total_tokens, num_seqs, G, R, D, in_dtype, segment_chunks);
     if (!workspace || workspace_bytes < L.total) return BF_STATUS_WORKSPACE;
     bf::GdnArgs a{};
     a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta;
@@ -79,13 +100,26 @@ int bf_gdn_fwd(const void* q, const void* k, const void* v, const float* g, cons
     a.scale = scale;
     a.s0 = initial_state; a.o = o; a.s_out = final_state;
     a.max_chunks = L.max_chunks;
+    a.seg_chunks = L.seg_chunks;
+    a.max_segs = L.max_segs;
+    // equal sequences: known segment count; packed sequences: any of them may be long
+    a.multi_seg = cu_seqlens ? (L.max_chunks > L.seg_chunks)
+                             : ((total_tokens / num_seqs + kChunk - 1) / kChunk > L.seg_chunks);
     char* ws = static_cast<char*>(workspace);
     a.ws_gcum = reinterpret_cast<float*>(ws + L.gcum);
-    a.ws_w = ws + L.w;
-    a.ws_uT = reinterpret_cast<float*>(ws + L.uT);
-    a.ws_kt = ws + L.kt;
+    a.ws_T = ws + L.T;
     a.ws_attn = ws + L.attn;
-    return bf::gdn_dispatch(a, phases, static_cast<hipStream_t>(stream));
+    a.ws_phi = ws + L.phi;
+    a.ws_c = reinterpret_cast<float*>(ws + L.c);
+    a.ws_n = reinterpret_cast<float*>(ws + L.n);
+    a.ws_sin = reinterpret_cast<float*>(ws + L.sin);
+    if (total_tokens == 0 && !final_state) return BF_STATUS_OK;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    int rc = 0;
+    if ((phases & BF_GDN_PHASE_PREP) && total_tokens > 0 && (rc = bf::gdn_prep(a, st))) return rc;
+    if ((phases & BF_GDN_PHASE_STATES) && (rc = bf::gdn_states(a, st))) return rc;
+    if (phases & BF_GDN_PHASE_OUTPUT) return bf::gdn_output(a, st);
+    return BF_STATUS_OK;
 }
 
 int bf_gdn_step(const float* q, const float* k, const float* v, const float* g, const float* beta,

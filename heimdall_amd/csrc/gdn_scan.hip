@@ -1,0 +1,838 @@
+// K1 part 2: the sequential part of the chunked gated delta rule, cut into segments that are scanned in parallel.
+//
+// With T' = (I + A)^-1 diag(beta), gc and attn from gdn_prefill.hip, one chunk of KV head g maps the state S
+// (D x D, fp32) as (reference: Heimdall/heimdall/kernels.py:112-127, motor.py:86-100)
+//   Y = K S,   v_new = T' (V - e^{gc} Y),   o_r = scale e^{gc} q_r S + attn_r v_new,
+//   S' = e^{gc_last} S + K^T (e^{gc_last - gc} v_new).
+// S' is affine in S, so each sequence is cut into segments of L chunks and three kernels run in turn:
+//   gdn_summary_kernel  per (segment, KV head, column group): the chunk map applied to the 2D columns [N | Phi]
+//                       from [0 | I], with V for the N columns and zero for the Phi columns, gives the segment's
+//                       map S_end = Phi S_start + N (the last segment of a sequence is skipped).
+//   gdn_combine_kernel  per (sequence, KV head, 16-column strip): X_0 = S0, X_{p+1} = Phi_p X_p + N_p in fp32
+//                       (bf16 runs: three split-bf16 MFMAs per product), the entry state of every segment.
+//   gdn_output_kernel   per (segment, KV head, column group, query head): the chunk map with outputs from the
+//                       segment's entry state; the last segment of a sequence writes the final state.
+//
+// Inside a workgroup each wave owns 32 state columns (two 16-column MFMA tiles) for all D rows, held in registers as
+// MFMA accumulators, so the per-chunk chain runs inside the wave with no exchange between waves:
+//   K S, q S      A = K / q rows (LDS),     B = S packed from the accumulators
+//   T' y          A = T' rows (LDS),        B = the Y accumulators after y = V - e^{gc} Y
+//   attn v_new    A = attn rows (global, prefetched one chunk ahead), B = the v_new accumulators
+//   K^T v'        A = K^T gathered from the K tile in LDS,  B = the v_new accumulators scaled by e^{gc_last - gc}
+// An accumulator tile holds rows 4g..4g+3 of its 16 rows in lane group g, while an MFMA operand fragment holds VEC
+// consecutive K indices per lane group. Tiles over the token and state-row dimensions therefore use the row
+// permutation prow(tile, m): rows 4g..4g+3 of the HP = VEC/4 tiles of one K fragment are that fragment's VEC values
+// of group g, so accumulators feed the next product directly. A rows are read through the same permutation.
+//
+// The chunk operands all waves share (K, q of the workgroup's query head, T', gc) are staged in LDS with
+// buffer_load ... lds (no registers, out-of-range rows read as zero); bf16 runs double-buffer the stage so chunk c+1
+// is in flight while chunk c is computed. LDS rows are swizzled by 16-byte blocks (swz) so that the fragment reads
+// of 16 rows hit distinct banks.
+#include <type_traits>
+
+#include "bf_common.h"
+#include "bf_internal.h"
+
+namespace bf {
+
+namespace {
+
+constexpr int SC = 64;       // chunk length
+constexpr int NXCD = 8;      // XCDs of an MI355X: workgroups are dispatched round-robin over them by linear id
+constexpr int WCOLS = 32;    // state columns per wave
+
+template <class E>
+__device__ __forceinline__ int prow(int tile, int m) {
+    constexpr int VEC = E::VEC, KF = E::KF, HP = VEC / 4;
+    return KF * (tile / HP) + VEC * (m >> 2) + 4 * (tile % HP) + (m & 3);
+}
+
+// 16-byte block permutation of LDS row `row` (rows have >= 8 blocks; the value is < 8). Requirements:
+//  - the 8 rows that one 8-lane phase of an MFMA fragment read touches (prow of m = 0..7) get distinct values, so a
+//    16-byte-per-lane read hits 8 distinct bank groups;
+//  - bf16: the 4 rows that a 16-lane group of a transposing K^T read touches (4 consecutive rows from a multiple of
+//    4) alternate bit 2, so those 8-byte reads are at most 2-way conflicted;
+//  - the value depends on the lane only (fragment reads) or on the lane and the row within a group of 4 (transposing
+//    reads), so addresses are a per-lane base plus an instruction immediate.
+template <class E>
+__device__ __forceinline__ int swz(int row) {
+    if constexpr (E::VEC == 8) return (row & 3) | ((((row >> 3) ^ row) & 1) << 2);
+    else return (row & 3) | (((row >> 2) & 1) << 2);
+}
+
+// 16-byte block permutation of the V tile rows (rows of VROWB >= 128 bytes): the 4 consecutive rows (from a multiple
+// of 4) that a 16-lane group of a transposing V read touches land 32 bytes apart, and bit 3 separates the two 16-lane
+// groups of a 32-lane half, so those 8-byte reads do not share banks.
+__device__ __forceinline__ int swz_v(int row, int nblk) { return ((2 * (row & 3)) | (((row >> 3) & 1) << 3)) & (nblk - 1); }
+
+// Per-chunk operands, double-buffered for bf16: K (C x D), T' and attn (C x C), gc.
+template <class E, int D, bool OUT>
+struct __align__(16) ChunkLds {
+    typename E::T K[SC * D];
+    typename E::T Tp[SC * SC];
+    typename E::T At[OUT ? SC * SC : 8];
+    float gc[SC];
+};
+// Single-buffered operands: q of the workgroup's query head (bf16 output scan) and the V columns of the workgroup;
+// each is reloaded for the next chunk as soon as the current chunk has consumed it.
+template <class E, int D, bool QL, int VW>
+struct __align__(16) OnceLds {
+    typename E::T Q[QL ? SC * D : 8];
+    typename E::T V[SC * VW];
+};
+struct __align__(16) NoLds {
+    float pad[4];
+};
+
+__device__ __forceinline__ uint4 lds16(const void* base, int byte_off) {
+    return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base) + byte_off);
+}
+
+// Copy a tile of SC rows into LDS with buffer_load ... lds: LDS row r (rowb bytes) holds global row r (pitch bytes)
+// with its 16-byte blocks permuted by sw(r). One instruction moves 64 x 16 bytes; `nbytes` = SC * rowb is a multiple
+// of 1 KB. Blocks at or beyond `valid_blk` of a row read as zero, as do rows past the descriptor's range.
+template <class Swz>
+__device__ __forceinline__ void stage_tile(rsrc_t src, uint32_t pitch, int rowb, void* lds, int nbytes, int wv,
+                                           int nw, int lane, Swz sw, int valid_blk) {
+    const int nblk = rowb / 16;
+    for (int i = wv; i < nbytes / 1024; i += nw) {
+        const int s = i * 64 + lane;
+        const int r = s / nblk, pb = s % nblk;
+        const int lb = pb ^ sw(r);
+        const uint32_t off = lb < valid_blk ? (uint32_t)r * pitch + (uint32_t)(lb * 16) : 0xFFFFFFF0u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            src, (__attribute__((address_space(3))) void*)(reinterpret_cast<char*>(lds) + i * 1024), 16, off, 0, 0,
+            0);
+    }
+}
+
+// B operand (K index = accumulator rows) from the HP accumulator tiles of one fragment.
+template <class E>
+__device__ __forceinline__ uint4 pack_b(const f32x4& a, const f32x4& b);
+template <>
+__device__ __forceinline__ uint4 pack_b<F32>(const f32x4& a, const f32x4&) {
+    return make_uint4(__float_as_uint(a[0]), __float_as_uint(a[1]), __float_as_uint(a[2]), __float_as_uint(a[3]));
+}
+template <>
+__device__ __forceinline__ uint4 pack_b<BF16>(const f32x4& a, const f32x4& b) {
+    return make_uint4(pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]), pack_bf16x2(b[2], b[3]));
+}
+
+struct SegInfo {
+    int n;        // sequence
+    int p;        // segment index inside the sequence
+    int nseg;     // segments of the sequence
+    int cid0;     // chunk id of the segment's first chunk
+    int count;    // chunks in the segment (0 only for an empty sequence)
+    long tok0;    // first token of the segment
+    long tok1;    // end of the sequence (exclusive)
+};
+
+__device__ __forceinline__ void seq_bounds(const GdnArgs& a, int n, long& s0, long& s1) {
+    s0 = a.cu_seqlens ? (long)a.cu_seqlens[n] : (long)n * a.seq_len;
+    s1 = a.cu_seqlens ? (long)a.cu_seqlens[n + 1] : (long)(n + 1) * a.seq_len;
+}
+
+// Segments enumerate sequence 0's segments, then sequence 1's, ...; an empty sequence has one empty segment.
+__device__ __forceinline__ bool locate_segment(const GdnArgs& a, int sid, SegInfo& s) {
+    const int L = a.seg_chunks;
+    int base_seg = 0, base_cid = 0;
+    for (int n = 0; n < a.num_seqs; ++n) {
+        long s0, s1;
+        seq_bounds(a, n, s0, s1);
+        const int nc = (int)((s1 - s0 + SC - 1) / SC);
+        const int ns = nc > 0 ? (nc + L - 1) / L : 1;
+        if (sid < base_seg + ns) {
+            const int p = sid - base_seg;
+            s.n = n;
+            s.p = p;
+            s.nseg = ns;
+            s.cid0 = base_cid + p * L;
+            s.count = nc - p * L < L ? nc - p * L : L;
+            s.tok0 = s0 + (long)p * L * SC;
+            s.tok1 = s1;
+            return true;
+        }
+        base_seg += ns;
+        base_cid += nc;
+    }
+    return false;
+}
+
+__device__ __forceinline__ void seq_segments(const GdnArgs& a, int n, int& first_sid, int& nseg) {
+    const int L = a.seg_chunks;
+    int base = 0;
+    for (int m = 0; m <= n; ++m) {
+        long s0, s1;
+        seq_bounds(a, m, s0, s1);
+        const int nc = (int)((s1 - s0 + SC - 1) / SC);
+        const int ns = nc > 0 ? (nc + L - 1) / L : 1;
+        if (m == n) {
+            first_sid = base;
+            nseg = ns;
+        }
+        base += ns;
+    }
+}
+
+template <class E, int D, bool OUT>
+struct SegCfg {
+    static constexpr int COLS = OUT ? D : 2 * D;                    // state columns per (segment, KV head)
+    static constexpr int NW = COLS / WCOLS < 4 ? COLS / WCOLS : 4;  // waves per workgroup
+    static constexpr int NCG = COLS / (NW * WCOLS);                 // column groups (workgroups per head)
+    static constexpr bool DBUF = E::VEC == 8;                       // bf16: double-buffered stage
+};
+
+}  // namespace
+
+// ------------------------------------------------------------------------------------------------ segment scan
+// Addressing. With tp(tile) = KF*(tile/HP) + 4*(tile%HP) and lt = VEC*(l16/4) + l16%4, a fragment row is
+// prow(tile, l16) = tp(tile) + lt and an accumulator row is prow(tile, 4lg + i) = tp(tile) + VEC*lg + i. Every LDS and
+// global offset below is split into a per-lane part (computed once) and a part that depends only on unrolled loop
+// indices (an instruction immediate or a scalar offset), so the chunk loop keeps a handful of address registers.
+template <class E>
+__device__ __forceinline__ constexpr int tpart(int tile) {
+    return E::KF * (tile / (E::VEC / 4)) + 4 * (tile % (E::VEC / 4));
+}
+
+typedef short v4s __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16: in each 16-lane group, output lane 4q + r receives element r of the 8-byte chunks that lanes
+// 4e + q (e = 0..3) address.
+__device__ __forceinline__ uint2 lds_tr16(const char* p) {
+    const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(p));
+    return make_uint2((uint16_t)v[0] | ((uint32_t)(uint16_t)v[1] << 16),
+                      (uint16_t)v[2] | ((uint32_t)(uint16_t)v[3] << 16));
+}
+
+template <class E, int D, bool OUT, bool BO>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gdn_seg_kernel(GdnArgs a) {
+    using T = typename E::T;
+    using Cfg = SegCfg<E, D, OUT>;
+    constexpr int VEC = E::VEC, KF = E::KF, ES = (int)sizeof(T), HP = VEC / 4;
+    constexpr int NTD = D / 16, NTC = SC / 16, NKD = D / KF, NKC = SC / KF;
+    constexpr int ROWB = D * ES, TROWB = SC * ES;
+    constexpr int NW = Cfg::NW, NCG = Cfg::NCG;
+    constexpr bool DBUF = Cfg::DBUF;
+    constexpr bool QL = OUT && ES == 2;                  // q staged in LDS (bf16); fp32 reads it from global
+    constexpr int VW = NW * WCOLS, VROWB = VW * ES;      // V tile: the workgroup's columns
+    using CL = ChunkLds<E, D, OUT>;
+    using OL = OnceLds<E, D, QL, VW>;
+    __shared__ CL cl0;
+    __shared__ typename std::conditional<DBUF, CL, NoLds>::type cl1;
+    __shared__ OL ol;
+
+    const int G = a.G, R = a.R, H = G * R;
+    const int per = NCG * (OUT ? R : 1);
+    const int xcd = blockIdx.x % NXCD, local = blockIdx.x / NXCD;
+    const int grp = xcd + NXCD * (local / per), sub = local % per;
+    if (grp >= a.max_segs * G) return;
+    const int g = grp % G, sid = grp / G;
+    const int cg = sub % NCG, r = sub / NCG;
+    SegInfo sg;
+    if (!locate_segment(a, sid, sg)) return;
+    if (!OUT && sg.p == sg.nseg - 1) return;
+
+    const int lane = lane_id(), wv = wave_id(), l16 = lane & 15, lg = lane >> 4;
+    const int cb = cg * VW;                              // first column of the workgroup in [0, COLS)
+    const int j0 = cb + wv * WCOLS;                      // first of this wave's columns
+    const bool phi_part = !OUT && j0 >= D;
+    const int jc = phi_part ? j0 - D : j0;               // column inside the D x D block
+    const int h = g * R + r;
+    const int n = sg.n;
+    const int v_blk = OUT ? VROWB / 16 : (cb < D ? ((D - cb < VW ? D - cb : VW) * ES) / 16 : 0);  // loaded V blocks
+
+    // per-lane address parts
+    const int lt = VEC * (l16 >> 2) + (l16 & 3);         // fragment row offset inside a tile
+    const int sl = swz<E>(lt);                           // swizzle of fragment rows (depends on the lane only)
+    int xb[2];                                           // swizzled 16-byte block of K index group (ks, lg), per ks&1
+#pragma unroll
+    for (int par = 0; par < 2; ++par) xb[par] = 4 * (par ^ (sl >> 2)) + (lg ^ (sl & 3));
+    // K^T A fragments (rows tp(td) + lt, K index = tokens KF*ks + VEC*lg + e).
+    // bf16: two transposing reads per fragment; lane (e, q) = (l16/4, l16%4) of group lg reads the 4 state rows
+    // tp(td) + 8q .. +3 of token 32ks + 8lg + 4h + e, so lane 4q + r collects tokens 8lg + 4h + 0..3 of row
+    // prow(td, 4q + r). With s = (lg ^ e) & 1 that chunk lies at trb[(td/2) & 1] + (32ks + 4h)*ROWB + 64*(td/2) + 8*(td&1).
+    // fp32: one 4-byte read per element, at ktb[td & 1][e] + (16ks + e)*ROWB + 64*td.
+    int trb[2], ktb[2][4];
+    if constexpr (ES == 2) {
+        const int e_ = l16 >> 2, q_ = l16 & 3, s_ = (lg ^ e_) & 1;
+#pragma unroll
+        for (int par = 0; par < 2; ++par) trb[par] = (8 * lg + e_) * ROWB + 16 * (q_ ^ e_) + (par ? -64 : 64) * s_;
+    } else {
+#pragma unroll
+        for (int par = 0; par < 2; ++par)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+                ktb[par][c] = VEC * lg * ROWB + (par ? -64 : 64) * (lg & 1) + 16 * ((l16 >> 2) ^ c) + (l16 & 3) * ES;
+    }
+    // V B fragments (K index = tokens KF*ks + VEC*lg + e, column wv*32 + 16jt + l16 of the V tile).
+    // bf16: lane (e, q) of group lg reads columns 16jt + 4q .. +3 of token 32ks + 8lg + 4h + e: at
+    // vtb[jt] + (32ks + 4h)*VROWB. fp32: element (token, column) read directly.
+    int vtb[2];
+    if constexpr (ES == 2) {
+        const int e_ = l16 >> 2, q_ = l16 & 3;
+        const int sv = swz_v(8 * lg + e_, VROWB / 16);
+#pragma unroll
+        for (int jt = 0; jt < 2; ++jt)
+            vtb[jt] = (8 * lg + e_) * VROWB + 16 * ((4 * wv + 2 * jt + (q_ >> 1)) ^ sv) + 8 * (q_ & 1);
+    } else {
+        vtb[0] = vtb[1] = 0;
+    }
+
+    // state strip: S[tile over rows][column tile], rows prow(tile, 4lg + i), column jc + 16 jt + l16
+    f32x4 S[NTD][2];
+#pragma unroll
+    for (int td = 0; td < NTD; ++td)
+#pragma unroll
+        for (int jt = 0; jt < 2; ++jt) {
+            const int j = jc + 16 * jt + l16;
+            f32x4 v = {0.f, 0.f, 0.f, 0.f};
+            if constexpr (OUT) {
+                const float* src = sg.p > 0 ? a.ws_sin + ((long)sid * G + g) * D * D
+                                            : (a.s0 ? a.s0 + ((long)n * G + g) * D * D : nullptr);
+                if (src) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[i] = src[(long)prow<E>(td, 4 * lg + i) * D + j];
+                }
+            } else if (phi_part) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) v[i] = prow<E>(td, 4 * lg + i) == j ? 1.f : 0.f;
+            }
+            S[td][jt] = v;
+        }
+
+    const int count = sg.count;
+    // The state is kept as S_stored with S = sc * S_stored for a wave-uniform scale sc, so the per-chunk decay
+    // multiplies one scalar instead of the whole strip; sc is folded into the row factors of Y, o and the update, and
+    // the strip is rescaled only when sc leaves [2^-32, 2^32]. cum_g is the segment's summed log-decay.
+    float sc = 1.f, cum_g = 0.f;
+
+    auto chunk_tok0 = [&](int c) { return sg.tok0 + (long)c * SC; };
+    auto chunk_len = [&](int c) {
+        const long rem = sg.tok1 - chunk_tok0(c);
+        return (int)(rem < SC ? rem : SC);
+    };
+    const auto sw_row = [](int row) { return swz<E>(row); };
+    const auto sw_v = [](int row) { return swz_v(row, VROWB / 16); };
+    auto load_chunk = [&](auto& cl, int c) {
+        const long t0 = chunk_tok0(c);
+        const int len = chunk_len(c);
+        const long cid = sg.cid0 + c;
+        const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.k) + (t0 * G + g) * D * ES,
+                                    (uint32_t)((long)len * G * D * ES));
+        stage_tile(rk, (uint32_t)(G * D * ES), ROWB, cl.K, SC * ROWB, wv, NW, lane, sw_row, 1 << 30);
+        const rsrc_t rt = make_rsrc(reinterpret_cast<const char*>(a.ws_T) + (cid * G + g) * SC * SC * ES,
+                                    (uint32_t)(SC * SC * ES));
+        stage_tile(rt, (uint32_t)TROWB, TROWB, cl.Tp, SC * TROWB, wv, NW, lane, sw_row, 1 << 30);
+        if constexpr (OUT) {
+            const rsrc_t ra = make_rsrc(reinterpret_cast<const char*>(a.ws_attn) + (cid * H + h) * SC * SC * ES,
+                                        (uint32_t)(SC * SC * ES));
+            stage_tile(ra, (uint32_t)TROWB, TROWB, cl.At, SC * TROWB, wv, NW, lane, sw_row, 1 << 30);
+        }
+        if (wv == 0 && lane < SC / 4) {
+            const rsrc_t rg = make_rsrc(a.ws_gcum + (cid * G + g) * SC, SC * 4);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rg, (__attribute__((address_space(3))) void*)cl.gc, 16,
+                                                     lane * 16, 0, 0, 0);
+        }
+    };
+    auto load_q = [&](int c) {
+        if constexpr (QL) {
+            const long t0 = chunk_tok0(c);
+            const rsrc_t rq = make_rsrc(reinterpret_cast<const char*>(a.q) + (t0 * H + h) * D * ES,
+                                        (uint32_t)((long)chunk_len(c) * H * D * ES));
+            stage_tile(rq, (uint32_t)(H * D * ES), ROWB, ol.Q, SC * ROWB, wv, NW, lane, sw_row, 1 << 30);
+        }
+    };
+    auto load_v = [&](int c) {
+        if (v_blk > 0) {
+            const long t0 = chunk_tok0(c);
+            const rsrc_t rv = make_rsrc(reinterpret_cast<const char*>(a.v) + ((t0 * G + g) * D + cb) * ES,
+                                        (uint32_t)((long)chunk_len(c) * G * D * ES - (long)cb * ES));
+            stage_tile(rv, (uint32_t)(G * D * ES), VROWB, ol.V, SC * VROWB, wv, NW, lane, sw_v, v_blk);
+        }
+    };
+
+    auto compute = [&](const CL& cl, int c, bool prefetch) {
+        const int cn = c + 1 < count ? c + 1 : c;
+        const char* Kb = reinterpret_cast<const char*>(cl.K);
+        const char* Tb = reinterpret_cast<const char*>(cl.Tp);
+        const char* Ab = reinterpret_cast<const char*>(cl.At);
+        const char* Qb = reinterpret_cast<const char*>(ol.Q);
+        const char* Vb = reinterpret_cast<const char*>(ol.V);
+        const float glast = cl.gc[SC - 1];
+        const float decay = __expf(glast);
+        float egc[NTC][4];                        // sc e^{gc} of the accumulator rows
+#pragma unroll
+        for (int tt = 0; tt < NTC; ++tt) {
+            const float4 gq = *reinterpret_cast<const float4*>(&cl.gc[tpart<E>(tt) + VEC * lg]);
+            egc[tt][0] = sc * __expf(gq.x);
+            egc[tt][1] = sc * __expf(gq.y);
+            egc[tt][2] = sc * __expf(gq.z);
+            egc[tt][3] = sc * __expf(gq.w);
+        }
+
+        // phase 1: Y = K S_stored, O = q S_stored. A fragments of step ks + 1 are read while step ks multiplies; the
+        // scheduling barrier keeps the compiler from hoisting every step's reads (and their registers) to the front.
+        f32x4 Y[NTC][2], O[OUT ? NTC : 1][2];
+#pragma unroll
+        for (int tt = 0; tt < NTC; ++tt)
+#pragma unroll
+            for (int jt = 0; jt < 2; ++jt) {
+                Y[tt][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                if constexpr (OUT) O[tt][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        const int kq_base[2] = {lt * ROWB + 16 * xb[0], lt * ROWB + 16 * xb[1]};
+        // fp32 output scan: q fragments straight from global memory (rows past the end read as zero)
+        const rsrc_t rqg = make_rsrc(reinterpret_cast<const char*>(a.q) + (chunk_tok0(c) * H + h) * D * ES,
+                                     (uint32_t)(OUT && !QL ? (long)chunk_len(c) * H * D * ES : 0));
+        auto read_kq = [&](int ks, uint4 (&ak)[NTC], uint4 (&aq)[NTC]) {
+#pragma unroll
+            for (int tt = 0; tt < NTC; ++tt) {
+                const int off = kq_base[ks & 1] + tpart<E>(tt) * ROWB + 128 * (ks >> 1);
+                ak[tt] = lds16(Kb, off);
+                if constexpr (QL) aq[tt] = lds16(Qb, off);
+                else if constexpr (OUT)
+                    aq[tt] = buf_ld16(rqg, (uint32_t)(((tpart<E>(tt) + lt) * H * D + KF * ks + VEC * lg) * ES));
+            }
+        };
+        uint4 ak[NTC], aq[NTC];
+        read_kq(0, ak, aq);
+#pragma unroll
+        for (int ks = 0; ks < NKD; ++ks) {
+            uint4 nk[NTC], nq[NTC];
+            if (ks + 1 < NKD) read_kq(ks + 1, nk, nq);
+            uint4 sb[2];
+#pragma unroll
+            for (int jt = 0; jt < 2; ++jt) sb[jt] = pack_b<E>(S[ks * HP][jt], S[ks * HP + HP - 1][jt]);
+#pragma unroll
+            for (int tt = 0; tt < NTC; ++tt) {
+#pragma unroll
+                for (int jt = 0; jt < 2; ++jt) mma<E>(Y[tt][jt], ak[tt], sb[jt]);
+                if constexpr (OUT) {
+#pragma unroll
+                    for (int jt = 0; jt < 2; ++jt) mma<E>(O[tt][jt], aq[tt], sb[jt]);
+                }
+            }
+            if (ks + 1 < NKD) {
+#pragma unroll
+                for (int tt = 0; tt < NTC; ++tt) {
+                    ak[tt] = nk[tt];
+                    aq[tt] = nq[tt];
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (QL) {
+            if (prefetch) {
+                __syncthreads();                   // every wave is done with q of this chunk
+                load_q(cn);
+            }
+        }
+
+        // phase 2: v_new = T' (V - e^{gc} K S) = T' V + T' (-sc e^{gc} Y)
+        f32x4 Vn[NTC][2];
+#pragma unroll
+        for (int tt = 0; tt < NTC; ++tt)
+#pragma unroll
+            for (int jt = 0; jt < 2; ++jt) {
+                Vn[tt][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) Y[tt][jt][i] *= -egc[tt][i];
+            }
+        const int t_base[2] = {lt * TROWB + 16 * xb[0], lt * TROWB + 16 * xb[1]};
+#pragma unroll
+        for (int ks = 0; ks < NKC; ++ks) {
+            uint4 yb[2], vb[2];
+#pragma unroll
+            for (int jt = 0; jt < 2; ++jt) {
+                yb[jt] = pack_b<E>(Y[ks * HP][jt], Y[ks * HP + HP - 1][jt]);
+                if constexpr (ES == 2) {
+                    const uint2 lo = lds_tr16(Vb + vtb[jt] + 32 * ks * VROWB);
+                    const uint2 hi = lds_tr16(Vb + vtb[jt] + (32 * ks + 4) * VROWB);
+                    vb[jt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                } else {
+                    // element (token t, tile column cv) of the swizzled V tile
+                    const int cv = wv * WCOLS + 16 * jt + l16;
+                    uint32_t w[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int t = KF * ks + VEC * lg + e;
+                        w[e] = *reinterpret_cast<const uint32_t*>(
+                            Vb + t * VROWB + (((cv >> 2) ^ swz_v(t, VROWB / 16)) << 4) + (cv & 3) * 4);
+                    }
+                    vb[jt] = make_uint4(w[0], w[1], w[2], w[3]);
+                }
+            }
+#pragma unroll
+            for (int tt = 0; tt < NTC; ++tt) {
+                const uint4 at = lds16(Tb, t_base[ks & 1] + tpart<E>(tt) * TROWB + 128 * (ks >> 1));
+#pragma unroll
+                for (int jt = 0; jt < 2; ++jt) {
+                    mma<E>(Vn[tt][jt], at, yb[jt]);
+                    if (!phi_part) mma<E>(Vn[tt][jt], at, vb[jt]);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (prefetch) {
+            __syncthreads();                       // every wave is done with V of this chunk
+            load_v(cn);
+        }
+
+        // phase 3: o = scale e^{gc} (q S) + attn v_new
+        if constexpr (OUT) {
+#pragma unroll
+            for (int tt = 0; tt < NTC; ++tt)
+#pragma unroll
+                for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) O[tt][jt][i] *= a.scale * egc[tt][i];   // egc carries sc
+#pragma unroll
+            for (int ks = 0; ks < NKC; ++ks) {
+                uint4 vb[2];
+#pragma unroll
+                for (int jt = 0; jt < 2; ++jt) vb[jt] = pack_b<E>(Vn[ks * HP][jt], Vn[ks * HP + HP - 1][jt]);
+#pragma unroll
+                for (int tt = 0; tt < NTC; ++tt) {
+                    const uint4 aa = lds16(Ab, t_base[ks & 1] + tpart<E>(tt) * TROWB + 128 * (ks >> 1));
+#pragma unroll
+                    for (int jt = 0; jt < 2; ++jt) mma<E>(O[tt][jt], aa, vb[jt]);
+                }
+            }
+            constexpr int OS = BO ? 2 : 4;
+            const long t0 = chunk_tok0(c);
+            const int len = chunk_len(c);
+            const uint32_t o_lane = (uint32_t)((VEC * lg * H * D + l16) * OS);
+            auto put = [&](rsrc_t ro, uint32_t voff, uint32_t soff, float x) {
+                if constexpr (BO) __builtin_amdgcn_raw_buffer_store_b16(f2bf(x), ro, voff, soff, 0);
+                else __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), ro, voff, soff, 0);
+            };
+            if (len == SC) {
+                // whole chunk: one descriptor, the row and column parts go to the scalar offset
+                const rsrc_t ro = make_rsrc(reinterpret_cast<char*>(a.o) + (t0 * H + h) * (long)D * OS,
+                                            (uint32_t)((long)SC * H * D * OS));
+#pragma unroll
+                for (int tt = 0; tt < NTC; ++tt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (int jt = 0; jt < 2; ++jt)
+                            put(ro, o_lane, (uint32_t)(((tpart<E>(tt) + i) * H * D + jc + 16 * jt) * OS),
+                                O[tt][jt][i]);
+            } else {
+                // last chunk of a sequence: one descriptor per row offset, so rows past the end are dropped
+#pragma unroll
+                for (int tt = 0; tt < NTC; ++tt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int row = tpart<E>(tt) + i;
+                        const int nrow = len > row ? len - row : 0;
+                        const rsrc_t ro = make_rsrc(
+                            reinterpret_cast<char*>(a.o) + ((t0 + row) * H + h) * (long)D * OS,
+                            (uint32_t)(nrow * H * D * OS));
+#pragma unroll
+                        for (int jt = 0; jt < 2; ++jt)
+                            put(ro, o_lane + (uint32_t)((jc + 16 * jt) * OS), 0u, O[tt][jt][i]);
+                    }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+
+        // phase 4: S = e^{gc_last} S + K^T (e^{gc_last - gc} v_new), as S_stored += K^T (e^{gc_last - gc} v_new / sc')
+        // row factor e^{gc_last - gc} / sc' = (sc e^{gc_last} / sc') / (sc e^{gc}) = ratio / egc
+        const float scn = sc * decay;
+        cum_g += glast;
+        float ratio = 1.f;
+        if (scn >= 0x1p-32f && scn <= 0x1p32f) {
+            sc = scn;
+        } else {
+#pragma unroll
+            for (int td = 0; td < NTD; ++td)
+#pragma unroll
+                for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) S[td][jt][i] *= scn;
+            ratio = scn;
+            sc = 1.f;
+        }
+#pragma unroll
+        for (int tt = 0; tt < NTC; ++tt) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float f = ratio * __builtin_amdgcn_rcpf(egc[tt][i]);
+#pragma unroll
+                for (int jt = 0; jt < 2; ++jt) Vn[tt][jt][i] *= f;
+            }
+        }
+        auto frag_kt = [&](int td, int ks) {
+            if constexpr (ES == 2) {
+                const int at = td >> 1;
+                const char* p = Kb + trb[at & 1] + 32 * ks * ROWB + 64 * at + 8 * (td & 1);
+                const uint2 lo = lds_tr16(p), hi = lds_tr16(p + 4 * ROWB);
+                return make_uint4(lo.x, lo.y, hi.x, hi.y);
+            } else {
+                uint32_t w[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    w[e] = *reinterpret_cast<const uint32_t*>(Kb + ktb[td & 1][e] + (KF * ks + e) * ROWB + 64 * td);
+                return make_uint4(w[0], w[1], w[2], w[3]);
+            }
+        };
+#pragma unroll
+        for (int ks = 0; ks < NKC; ++ks) {
+            uint4 vb[2];
+#pragma unroll
+            for (int jt = 0; jt < 2; ++jt) vb[jt] = pack_b<E>(Vn[ks * HP][jt], Vn[ks * HP + HP - 1][jt]);
+            uint4 akt = frag_kt(0, ks);
+#pragma unroll
+            for (int td = 0; td < NTD; ++td) {
+                uint4 nxt = akt;
+                if (td + 1 < NTD) nxt = frag_kt(td + 1, ks);
+#pragma unroll
+                for (int jt = 0; jt < 2; ++jt) mma<E>(S[td][jt], akt, vb[jt]);
+                akt = nxt;
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+
+    if (count > 0) {
+        if constexpr (DBUF) {
+            load_chunk(cl0, 0);
+            load_q(0);
+            load_v(0);
+            wait_vmem_all();
+            __syncthreads();
+            for (int c = 0;;) {
+                // the next chunk's stage is loaded unconditionally (the last chunk re-loads itself into the idle
+                // buffer): a conditional load would make the wait counts drain it before the current chunk
+                load_chunk(cl1, c + 1 < count ? c + 1 : c);
+                compute(cl0, c, true);
+                wait_vmem_all();
+                __syncthreads();
+                if (++c >= count) break;
+                load_chunk(cl0, c + 1 < count ? c + 1 : c);
+                compute(cl1, c, true);
+                wait_vmem_all();
+                __syncthreads();
+                if (++c >= count) break;
+            }
+        } else {
+            for (int c = 0; c < count; ++c) {
+                load_chunk(cl0, c);
+                load_v(c);
+                wait_vmem_all();
+                __syncthreads();
+                compute(cl0, c, false);
+                __syncthreads();
+            }
+        }
+    }
+
+    if constexpr (OUT) {
+        if (sg.p == sg.nseg - 1 && r == 0 && a.s_out) {
+            float* dst = a.s_out + ((long)n * G + g) * D * D;
+#pragma unroll
+            for (int td = 0; td < NTD; ++td)
+#pragma unroll
+                for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        dst[(long)prow<E>(td, 4 * lg + i) * D + jc + 16 * jt + l16] = sc * S[td][jt][i];
+        }
+    } else {
+        // segment map S_end = Phi S_start + N, stored as N (fp32), Psi = Phi - c I (in_dtype) and c = e^{sum of g}
+        const float c = __expf(cum_g);
+        const long off = ((long)sid * G + g) * D * D;
+#pragma unroll
+        for (int td = 0; td < NTD; ++td)
+#pragma unroll
+            for (int jt = 0; jt < 2; ++jt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int d = prow<E>(td, 4 * lg + i), j = jc + 16 * jt + l16;
+                    const float x = sc * S[td][jt][i];
+                    if (phi_part) reinterpret_cast<T*>(a.ws_phi)[off + (long)d * D + j] = E::from_f(x - (d == j ? c : 0.f));
+                    else a.ws_n[off + (long)d * D + j] = x;
+                }
+        if (cg == 0 && wv == 0 && lane == 0) a.ws_c[(long)sid * G + g] = c;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ segment combine
+// One workgroup per (sequence, KV head, 16-column strip), 4 waves; wave w produces row tiles w*NTD/4 ..
+// (w+1)*NTD/4 - 1 of X_{p+1} = c_p X_p + Psi_p X_p + N_p (Psi_p = Phi_p - c_p I). The pure-decay part c_p X_p is exact
+// fp32; Psi_p X_p is an MFMA with Psi_p in in_dtype and, for bf16, X split into bf16 high and low parts. X^T is shared
+// through LDS between steps. bf16 prefetches the next step's Psi fragments, N and c while a step computes.
+template <class E, int D>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gdn_combine_kernel(GdnArgs a) {
+    using T = typename E::T;
+    constexpr int VEC = E::VEC, KF = E::KF, NTD = D / 16, NKD = D / KF, TPW = NTD / 4;
+    constexpr bool DBUF = E::VEC == 8;
+    __shared__ __align__(16) float XT[16][D + 4];
+    const int strips = D / 16, G = a.G;
+    const int n = blockIdx.x / (G * strips), g = (blockIdx.x / strips) % G, jb = blockIdx.x % strips;
+    if (n >= a.num_seqs) return;
+    int first, nseg;
+    seq_segments(a, n, first, nseg);
+    if (nseg <= 1) return;
+    const int lane = lane_id(), wv = wave_id(), l16 = lane & 15, lg = lane >> 4;
+    const int j0 = 16 * jb;
+    const float* s0 = a.s0 ? a.s0 + ((long)n * G + g) * D * D : nullptr;
+    for (int idx = threadIdx.x; idx < 16 * D; idx += blockDim.x) {
+        const int j = idx & 15, d = idx >> 4;
+        XT[j][d] = s0 ? s0[(long)d * D + j0 + j] : 0.f;
+    }
+
+    struct Pre {
+        uint4 A[TPW][NKD];     // Psi rows 16*(wv*TPW + u) + l16, K index KF*ks + VEC*lg
+        float N[TPW][4];       // N at the accumulator rows
+        float c;
+    };
+    auto load = [&](Pre& P, int p) {
+        const long sid = first + p;
+        const T* Psi = reinterpret_cast<const T*>(a.ws_phi) + (sid * G + g) * D * D;
+        const float* Nm = a.ws_n + (sid * G + g) * D * D;
+#pragma unroll
+        for (int u = 0; u < TPW; ++u) {
+            const int tr = wv * TPW + u;
+#pragma unroll
+            for (int ks = 0; ks < NKD; ++ks) P.A[u][ks] = ld16(Psi + (long)(16 * tr + l16) * D + KF * ks + VEC * lg);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) P.N[u][i] = Nm[(long)(16 * tr + 4 * lg + i) * D + j0 + l16];
+        }
+        P.c = a.ws_c[sid * G + g];
+    };
+    auto step = [&](const Pre& P, int p) {
+        const long sid = first + p;
+        f32x4 acc[TPW];
+#pragma unroll
+        for (int u = 0; u < TPW; ++u) {
+            const int tr = wv * TPW + u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[u][i] = P.N[u][i] + P.c * XT[l16][16 * tr + 4 * lg + i];
+        }
+#pragma unroll
+        for (int ks = 0; ks < NKD; ++ks) {
+            float bv[VEC];
+#pragma unroll
+            for (int e = 0; e < VEC; e += 4) {
+                const float4 x = *reinterpret_cast<const float4*>(&XT[l16][KF * ks + VEC * lg + e]);
+                bv[e] = x.x; bv[e + 1] = x.y; bv[e + 2] = x.z; bv[e + 3] = x.w;
+            }
+            if constexpr (VEC == 8) {
+                uint32_t hw[4], lw[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    hw[e] = pack_bf16x2(bv[2 * e], bv[2 * e + 1]);
+                    lw[e] = pack_bf16x2(bv[2 * e] - __uint_as_float(hw[e] << 16),
+                                        bv[2 * e + 1] - __uint_as_float(hw[e] & 0xffff0000u));
+                }
+                const uint4 BH = make_uint4(hw[0], hw[1], hw[2], hw[3]), BL = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+#pragma unroll
+                for (int u = 0; u < TPW; ++u) {
+                    mma<E>(acc[u], P.A[u][ks], BL);
+                    mma<E>(acc[u], P.A[u][ks], BH);
+                }
+            } else {
+                const uint4 B = make_uint4(__float_as_uint(bv[0]), __float_as_uint(bv[1]), __float_as_uint(bv[2]),
+                                           __float_as_uint(bv[3]));
+#pragma unroll
+                for (int u = 0; u < TPW; ++u) mma<E>(acc[u], P.A[u][ks], B);
+            }
+        }
+        __syncthreads();
+        float* dst = a.ws_sin + ((sid + 1) * G + g) * D * D;
+#pragma unroll
+        for (int u = 0; u < TPW; ++u) {
+            const int tr = wv * TPW + u;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = 16 * tr + 4 * lg + i;
+                XT[l16][d] = acc[u][i];
+                dst[(long)d * D + j0 + l16] = acc[u][i];
+            }
+        }
+        __syncthreads();
+    };
+
+    const int steps = nseg - 1;
+    if constexpr (DBUF) {
+        Pre P0, P1;
+        load(P0, 0);
+        wait_vmem_all();
+        __syncthreads();
+        for (int p = 0;;) {
+            // unconditional prefetch (the last step re-loads itself), as in the segment scan
+            load(P1, p + 1 < steps ? p + 1 : p);
+            step(P0, p);
+            if (++p >= steps) break;
+            load(P0, p + 1 < steps ? p + 1 : p);
+            step(P1, p);
+            if (++p >= steps) break;
+        }
+        wait_vmem_all();
+    } else {
+        __syncthreads();
+        for (int p = 0; p < steps; ++p) {
+            Pre P;
+            load(P, p);
+            step(P, p);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ host launchers
+namespace {
+
+template <class E, int D, bool OUT>
+dim3 seg_grid(const GdnArgs& a) {
+    using Cfg = SegCfg<E, D, OUT>;
+    const int per = Cfg::NCG * (OUT ? a.R : 1);
+    const int groups = a.max_segs * a.G;
+    return dim3(NXCD * ((groups + NXCD - 1) / NXCD) * per);
+}
+
+template <class E, int D>
+int launch_states(const GdnArgs& a, hipStream_t stream) {
+    const dim3 grid = seg_grid<E, D, false>(a), block(SegCfg<E, D, false>::NW * 64);
+    hipLaunchKernelGGL((gdn_seg_kernel<E, D, false, false>), grid, block, 0, stream, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    hipLaunchKernelGGL((gdn_combine_kernel<E, D>), dim3(a.num_seqs * a.G * (D / 16)), dim3(256), 0, stream, a);
+    return (int)hipGetLastError();
+}
+
+template <class E, int D>
+int launch_output(const GdnArgs& a, hipStream_t stream) {
+    const dim3 grid = seg_grid<E, D, true>(a), block(SegCfg<E, D, true>::NW * 64);
+    if (a.o_dtype == DT_BF16)
+        hipLaunchKernelGGL((gdn_seg_kernel<E, D, true, true>), grid, block, 0, stream, a);
+    else
+        hipLaunchKernelGGL((gdn_seg_kernel<E, D, true, false>), grid, block, 0, stream, a);
+    return (int)hipGetLastError();
+}
+
+}  // namespace
+
+int gdn_states(const GdnArgs& a, hipStream_t stream) {
+    if (!a.multi_seg) return 0;
+    const bool bf = a.in_dtype == DT_BF16;
+    switch (a.D) {
+        case 64: return bf ? launch_states<BF16, 64>(a, stream) : launch_states<F32, 64>(a, stream);
+        case 128: return bf ? launch_states<BF16, 128>(a, stream) : launch_states<F32, 128>(a, stream);
+        case 256: return bf ? launch_states<BF16, 256>(a, stream) : launch_states<F32, 256>(a, stream);
+        default: return BF_ERR_UNSUPPORTED;
+    }
+}
+
+int gdn_output(const GdnArgs& a, hipStream_t stream) {
+    const bool bf = a.in_dtype == DT_BF16;
+    switch (a.D) {
+        case 64: return bf ? launch_output<BF16, 64>(a, stream) : launch_output<F32, 64>(a, stream);
+        case 128: return bf ? launch_output<BF16, 128>(a, stream) : launch_output<F32, 128>(a, stream);
+        case 256: return bf ? launch_output<BF16, 256>(a, stream) : launch_output<F32, 256>(a, stream);
+        default: return BF_ERR_UNSUPPORTED;
+    }
+}
+
+}  // namespace bf

@@ -33,10 +33,15 @@ extern "C" {
 #define BF_STATUS_UNSUPPORTED (-2) /* head dim, dtype or chunk size outside the supported set */
 #define BF_STATUS_WORKSPACE (-3)   /* workspace missing or smaller than the size query returned */
 
-/* Phases of bf_gdn_fwd (bit mask); BF_GDN_PHASE_ALL runs the whole operator. */
+/* Phases of bf_gdn_fwd (bit mask), run in this order; BF_GDN_PHASE_ALL runs the whole operator.
+ *   PREP    per-chunk quantities that do not depend on the state (decay, (I + A)^-1, masked q.k^T)
+ *   STATES  state entering every segment: per-segment affine summaries S_end = Phi S_start + N, then their
+ *           sequential composition per sequence (skipped when every sequence is a single segment)
+ *   OUTPUT  per-segment scan from the segment's entry state: outputs and the final state */
 #define BF_GDN_PHASE_PREP 1
-#define BF_GDN_PHASE_SCAN 2
-#define BF_GDN_PHASE_ALL 3
+#define BF_GDN_PHASE_STATES 2
+#define BF_GDN_PHASE_OUTPUT 4
+#define BF_GDN_PHASE_ALL 7
 
 /* Library version (major * 10000 + minor * 100 + patch). */
 int bf_version(void);
@@ -62,16 +67,20 @@ const char* bf_status_string(int status);
  *   cu_seqlens [num_seqs + 1] int32 (device), or null for num_seqs equal sequences of N_tok / num_seqs tokens
  *   initial_state [num_seqs][G][D][D] fp32 or null;  final_state [num_seqs][G][D][D] fp32 or null
  *   o [N_tok][G*R][D] in o_dtype (fp32 or bf16)
- *   phases: BF_GDN_PHASE_ALL, or PREP then SCAN in two calls with the same arguments and workspace.
+ *   segment_chunks: each sequence is cut into segments of this many 64-token chunks that are scanned in parallel
+ *     (their entry states come from the STATES phase); 0 picks a length from the problem size. The result does not
+ *     depend on it beyond rounding.
+ *   phases: BF_GDN_PHASE_ALL, or PREP, STATES, OUTPUT in separate calls with the same arguments and workspace.
  * Chunk length is 64. Arithmetic: MFMA in in_dtype with fp32 accumulation; state, decay and the triangular
- * inverse in fp32.
+ * inverse in fp32; segment entry states composed in fp32 (split-bf16 MFMA for bf16 runs).
  */
-int bf_gdn_workspace_size(int64_t total_tokens, int num_seqs, int G, int R, int D, int in_dtype, size_t* bytes);
+int bf_gdn_workspace_size(int64_t total_tokens, int num_seqs, int G, int R, int D, int in_dtype,
+                          int segment_chunks, size_t* bytes);
 
 int bf_gdn_fwd(const void* q, const void* k, const void* v, const float* g, const float* beta,
                const int32_t* cu_seqlens, int num_seqs, int64_t total_tokens, int G, int R, int D, int in_dtype,
-               float scale, const float* initial_state, void* o, int o_dtype, float* final_state, void* workspace,
-               size_t workspace_bytes, int phases, void* stream);
+               float scale, const float* initial_state, void* o, int o_dtype, float* final_state,
+               int segment_chunks, void* workspace, size_t workspace_bytes, int phases, void* stream);
 
 /*
  * Single-token gated delta rule (GQA): kernels.delta_rule_step(q, k, v, g, beta, state)

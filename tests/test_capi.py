@@ -61,21 +61,28 @@ def test_status_codes_without_gpu(cpu_lib):
     assert cpu_lib.bf_version() >= 100
     assert cpu_lib.bf_status_string(0) == b"ok"
     n = ctypes.c_size_t(0)
-    assert cpu_lib.bf_gdn_workspace_size(4096, 1, 4, 1, 256, 1, ctypes.byref(n)) == 0 and n.value > 0
-    assert cpu_lib.bf_gdn_workspace_size(4096, 1, 4, 1, 96, 1, ctypes.byref(n)) == -2      # unsupported D
-    assert cpu_lib.bf_gdn_workspace_size(4096, 0, 4, 1, 256, 1, ctypes.byref(n)) == -1     # no sequences
+    assert cpu_lib.bf_gdn_workspace_size(4096, 1, 4, 1, 256, 1, 0, ctypes.byref(n)) == 0 and n.value > 0
+    assert cpu_lib.bf_gdn_workspace_size(4096, 1, 4, 1, 96, 1, 0, ctypes.byref(n)) == -2      # unsupported D
+    assert cpu_lib.bf_gdn_workspace_size(4096, 0, 4, 1, 256, 1, 0, ctypes.byref(n)) == -1     # no sequences
+    assert cpu_lib.bf_gdn_workspace_size(4096, 1, 4, 1, 256, 1, -1, ctypes.byref(n)) == -1    # bad segment length
     # argument errors are reported before anything is launched (null workspace)
-    st = cpu_lib.bf_gdn_fwd(1, 1, 1, 1, 1, None, 1, 64, 4, 1, 256, 1, 1.0, None, 1, 0, None, None, 0, 3, None)
+    st = cpu_lib.bf_gdn_fwd(1, 1, 1, 1, 1, None, 1, 64, 4, 1, 256, 1, 1.0, None, 1, 0, None, 0, None, 0, 7, None)
     assert st == -3
-    st = cpu_lib.bf_gdn_fwd(1, 1, 1, 1, 1, None, 3, 64, 4, 1, 256, 1, 1.0, None, 1, 0, None, None, 0, 3, None)
-    assert st == -1                                                                          # 64 % 3 != 0
+    st = cpu_lib.bf_gdn_fwd(1, 1, 1, 1, 1, None, 3, 64, 4, 1, 256, 1, 1.0, None, 1, 0, None, 0, None, 0, 7, None)
+    assert st == -1                                                                            # 64 % 3 != 0
+    st = cpu_lib.bf_gdn_fwd(1, 1, 1, 1, 1, None, 1, 64, 4, 1, 256, 1, 1.0, None, 1, 0, None, 0, None, 0, 8, None)
+    assert st == -1                                                                            # unknown phase bit
 
 
 def test_workspace_size_grows_with_tokens(cpu_lib):
     a, b = ctypes.c_size_t(0), ctypes.c_size_t(0)
-    cpu_lib.bf_gdn_workspace_size(4096, 1, 4, 1, 256, 1, ctypes.byref(a))
-    cpu_lib.bf_gdn_workspace_size(8192, 1, 4, 1, 256, 1, ctypes.byref(b))
+    cpu_lib.bf_gdn_workspace_size(4096, 1, 4, 1, 256, 1, 0, ctypes.byref(a))
+    cpu_lib.bf_gdn_workspace_size(8192, 1, 4, 1, 256, 1, 0, ctypes.byref(b))
     assert b.value > a.value
+    # shorter segments need more per-segment summaries
+    cpu_lib.bf_gdn_workspace_size(8192, 1, 4, 1, 256, 1, 2, ctypes.byref(a))
+    cpu_lib.bf_gdn_workspace_size(8192, 1, 4, 1, 256, 1, 64, ctypes.byref(b))
+    assert a.value > b.value
 
 
 def test_product_has_no_cpu_path():

@@ -128,3 +128,64 @@ def test_full_size_split_and_linearity(dev):
         o12, s12 = kernels.delta_rule(q, k, vs, g, beta)
         assert rel(o + o2, o12) < 2e-2 and rel(s + s2, s12) < 2e-2
         assert torch.isfinite(o).all() and torch.isfinite(s).all()
+
+
+# Multi-segment scans: sequences cut into segments of `seg` chunks whose entry states come from the per-segment
+# summaries (Phi, N) and their composition; the result must equal the single sequential scan of the oracle.
+@pytest.mark.parametrize("d,seg", [(64, 1), (128, 2), (256, 1), (256, 3)])
+def test_segments_fp32(dev, d, seg):
+    from heimdall_amd._device import gdn_forward
+    print(f"gdn segments fp32 B=2 T=700 H=2 D={d} segment_chunks={seg}", flush=True)
+    q, k, v, g, beta, s0 = make(2, 700, 2, d, seed=30 + d + seg)
+    N = 2 * 700
+    with torch.no_grad():
+        o, s = gdn_forward(*(z.to(dev).reshape(N, *z.shape[2:]) for z in (q, k, v)),
+                           g.to(dev).reshape(N, 2), beta.to(dev).reshape(N, 2), num_seqs=2,
+                           initial_state=s0.to(dev), segment_chunks=seg)
+    o_ref, s_ref = gdn.delta_rule_chunked(*(z.double() for z in (q, k, v, g, beta)), 64, s0.double())
+    eo, es = rel(o.view(2, 700, 2, d), o_ref), rel(s, s_ref)
+    assert eo < TOL_F32 and es < TOL_F32, (eo, es)
+
+
+@pytest.mark.parametrize("seg", [1, 2, 5])
+def test_segments_bf16(dev, seg):
+    from heimdall_amd._device import gdn_forward
+    print(f"gdn segments bf16 B=1 T=1000 H=4 D=256 segment_chunks={seg}", flush=True)
+    q, k, v, g, beta, s0 = make(1, 1000, 4, 256, seed=40 + seg, g_lo=-1e-2, dtype=torch.bfloat16)
+    with torch.no_grad():
+        o, s = gdn_forward(*(z.to(dev)[0] for z in (q, k, v, g, beta)), num_seqs=1, initial_state=s0.to(dev),
+                           segment_chunks=seg)
+    o_ref, s_ref = gdn.delta_rule_chunked(*(z.float() for z in (q, k, v, g, beta)), 64, s0)
+    eo, es = rel(o[None], o_ref), rel(s, s_ref)
+    assert eo < TOL_BF16 and es < TOL_BF16, (eo, es)
+
+
+def test_segments_gqa_varlen_fp32(dev):
+    """GQA (R = 3) over packed sequences with empty and one-token members, two-chunk segments."""
+    from heimdall_amd._device import gdn_forward
+    lens = [300, 0, 1, 130, 64, 257]
+    print(f"gdn segments gqa varlen fp32 lens={lens} G=2 R=3 D=64 segment_chunks=2", flush=True)
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    N, G, R, D = cu[-1], 2, 3, 64
+    gen = torch.Generator().manual_seed(50)
+    q = torch.randn(N, G * R, D, generator=gen) * D ** -0.5
+    k = F.normalize(torch.randn(N, G, D, generator=gen), dim=-1)
+    v = torch.randn(N, G, D, generator=gen)
+    g = -torch.rand(N, G, generator=gen) * 0.05
+    beta = torch.rand(N, G, generator=gen)
+    s0 = torch.randn(len(lens), G, D, D, generator=gen) * 0.1
+    with torch.no_grad():
+        o, s = gdn_forward(q.to(dev), k.to(dev), v.to(dev), g.to(dev), beta.to(dev), num_seqs=len(lens),
+                           cu_seqlens=torch.tensor(cu, dtype=torch.int32, device=dev), initial_state=s0.to(dev),
+                           segment_chunks=2)
+    for n in range(len(lens)):
+        a, b = cu[n], cu[n + 1]
+        qq = q[a:b].view(1, b - a, G, R, D)
+        o_ref, s_ref = gdn.delta_rule_gqa(qq.double(), k[a:b][None].double(), v[a:b][None].double(),
+                                          g[a:b][None].double(), beta[a:b][None].double(), 64,
+                                          s0[n:n + 1].double())
+        if b > a:
+            assert rel(o[a:b].view(1, b - a, G, R, D), o_ref) < TOL_F32, n
+        assert rel(s[n:n + 1], s_ref) < TOL_F32, n

@@ -232,4 +232,51 @@ __device__ __forceinline__ void buf_st_out(rsrc_t r, uint32_t elem, float v) {
     else buf_stf(r, elem * 4u, v);
 }
 
+// ------------------------------------------------------------------------------------------------ LDS staging
+// 16-byte block permutation of LDS row `row` of a tile with nblk >= 8 blocks per row, chosen by measurement on gfx950
+// with 4 and 8 waves reading the same tile concurrently (the case in the scan kernels):
+//  - bf16 rows of >= 16 blocks: every 16-lane phase of an MFMA fragment read (the 16 rows prow(tile, 0..15) at one
+//    block) and of a transposing K^T read (rows 4 consecutive tokens from a multiple of 4, 4 lanes each) spreads over
+//    16 distinct blocks, at the same speed as a linear read;
+//  - bf16 rows of 8 blocks and fp32: 3-bit form (8 distinct blocks per fragment phase).
+// The value depends on the row only through row & 3, (row >> 3) & 3 and bit 1 or bit 2, so fragment addresses are a
+// per-lane base plus an instruction immediate.
+template <class E>
+__device__ __forceinline__ int swz(int row, int nblk) {
+    if constexpr (E::VEC == 8) {
+        if (nblk >= 16) return (row & 3) | ((((row >> 3) & 3) ^ (row & 2)) << 2);
+        return (row & 3) | ((((row >> 3) ^ row) & 1) << 2);
+    } else {
+        return (row & 3) | (((row >> 2) & 1) << 2);
+    }
+}
+
+// 16-byte block permutation of the V tile rows (rows of VROWB >= 128 bytes): the 4 consecutive rows (from a multiple
+// of 4) that a 16-lane group of a transposing V read touches land 32 bytes apart, and bit 3 separates the two 16-lane
+// groups of a 32-lane half, so those 8-byte reads do not share banks.
+__device__ __forceinline__ int swz_v(int row, int nblk) { return ((2 * (row & 3)) | (((row >> 3) & 1) << 3)) & (nblk - 1); }
+
+// Per-chunk operands, double-buffered for bf16: K (C x D), T' and attn (C x C), gc.
+__device__ __forceinline__ uint4 lds16(const void* base, int byte_off) {
+    return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base) + byte_off);
+}
+
+// Copy a tile of SC rows into LDS with buffer_load ... lds: LDS row r (rowb bytes) holds global row r (pitch bytes)
+// with its 16-byte blocks permuted by sw(r). One instruction moves 64 x 16 bytes; `nbytes` = SC * rowb is a multiple
+// of 1 KB. Blocks at or beyond `valid_blk` of a row read as zero, as do rows past the descriptor's range.
+template <class Swz>
+__device__ __forceinline__ void stage_tile(rsrc_t src, uint32_t pitch, int rowb, void* lds, int nbytes, int wv,
+                                           int nw, int lane, Swz sw, int valid_blk) {
+    const int nblk = rowb / 16;
+    for (int i = wv; i < nbytes / 1024; i += nw) {
+        const int s = i * 64 + lane;
+        const int r = s / nblk, pb = s % nblk;
+        const int lb = pb ^ sw(r);
+        const uint32_t off = lb < valid_blk ? (uint32_t)r * pitch + (uint32_t)(lb * 16) : 0xFFFFFFF0u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            src, (__attribute__((address_space(3))) void*)(reinterpret_cast<char*>(lds) + i * 1024), 16, off, 0, 0,
+            0);
+    }
+}
+
 }  // namespace bf

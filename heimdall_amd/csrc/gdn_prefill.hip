@@ -7,8 +7,9 @@
 // so that the reference's u - w S equals T' (V - e^{gc} K S): the scan (gdn_scan.hip) needs only T', attn and gc
 // next to the inputs q, k, v, and nothing of size C x D is written back here.
 //
-// gdn_prep_kernel, grid (chunks, G), 4 waves: wave 0 forms gc, then everybody computes A by MFMA; wave 0 inverts
-// (I + A) by forward substitution (one column per lane, fp32) while waves 1-3 compute the R attn tiles.
+// gdn_prep_kernel, grid (chunks, G), 4 waves: K and q tiles are staged in LDS (buffer_load ... lds); the waves compute
+// the attn tiles of the R query heads, then A, by MFMA; one wave inverts (I + A) by forward substitution (one column
+// per lane, fp32).
 //
 // Workspace written (chunk id cid, KV head g, query head h):
 //   gcum [cid][g][C] f32 | T [cid][g][C][C] in_dtype | attn [cid][h][C][C] in_dtype
@@ -20,8 +21,15 @@ namespace bf {
 constexpr int CH = 64;     // chunk length
 constexpr int NT = 256;    // threads per workgroup (4 waves)
 
-struct PrepShared {
-    float A[CH][CH + 4];   // strictly lower A (fp32)
+// LDS: the chunk's K tile and one query head's q tile (swizzled rows, staged by buffer_load ... lds); after the attn
+// tiles are done the q region holds A.
+template <class E, int D>
+struct __align__(16) PrepLds {
+    typename E::T K[CH * D];
+    union {
+        typename E::T Q[CH * D];
+        float A[CH][CH + 4];
+    };
     float gc[CH];
     float beta[CH];
 };
@@ -29,16 +37,25 @@ struct PrepShared {
 template <class E, int D>
 __global__ __launch_bounds__(NT) void gdn_prep_kernel(GdnArgs a) {
     using T = typename E::T;
-    constexpr int VEC = E::VEC, KF = E::KF;
-    __shared__ PrepShared sm;
+    constexpr int VEC = E::VEC, KF = E::KF, ES = (int)sizeof(T), ROWB = D * ES, NKD = D / KF;
+    __shared__ PrepLds<E, D> sm;
     SeqInfo si;
     if (!locate_chunk(blockIdx.x, a.cu_seqlens, a.num_seqs, a.seq_len, CH, si)) return;
     const int g = blockIdx.y, G = a.G, R = a.R, H = G * R;
     const long cid = blockIdx.x;
     const int lane = lane_id(), wv = wave_id(), l16 = lane & 15, lg = lane >> 4;
-    const T* K = reinterpret_cast<const T*>(a.k) + si.tok0 * G * D + (long)g * D;
-    const long ldk = (long)G * D;
+    const auto sw_row = [](int row) { return swz<E>(row, ROWB / 16); };
+    const int nw = NT / WAVE;
 
+    const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.k) + (si.tok0 * G + g) * D * ES,
+                                (uint32_t)((long)si.len * G * D * ES));
+    stage_tile(rk, (uint32_t)(G * D * ES), ROWB, sm.K, CH * ROWB, wv, nw, lane, sw_row, 1 << 30);
+    auto stage_q = [&](int r) {
+        const rsrc_t rq = make_rsrc(reinterpret_cast<const char*>(a.q) + (si.tok0 * H + (long)g * R + r) * D * ES,
+                                    (uint32_t)((long)si.len * H * D * ES));
+        stage_tile(rq, (uint32_t)(H * D * ES), ROWB, sm.Q, CH * ROWB, wv, nw, lane, sw_row, 1 << 30);
+    };
+    stage_q(0);
     if (wv == 0) {
         float gv = 0.f, bv = 0.f;
         if (lane < si.len) {
@@ -54,21 +71,55 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(GdnArgs a) {
         sm.beta[lane] = bv;
         a.ws_gcum[(cid * G + g) * CH + lane] = gv;
     }
+    wait_vmem_all();
     __syncthreads();
+
+    // fragment of rows 16*tile + l16 of a swizzled tile, K index KF*ks + VEC*lg .. (16 bytes)
+    auto frag = [&](const T* base, int tile, int ks) {
+        const int row = 16 * tile + l16;
+        return lds16(base, row * ROWB + (((4 * ks + lg) ^ swz<E>(row, ROWB / 16)) << 4));
+    };
+
+    // attn_r^T = K q_r^T (rows t' = key, cols t = query), masked to t' <= t, decayed and scaled; the 6 tiles above
+    // the diagonal are zero.
+    for (int r = 0; r < R; ++r) {
+        if (r > 0) {
+            __syncthreads();
+            stage_q(r);
+            wait_vmem_all();
+            __syncthreads();
+        }
+        for (int tile = wv; tile < 16; tile += nw) {
+            const int at = tile >> 2, bt = tile & 3;     // at: key tile (rows), bt: query tile (cols)
+            const int t = 16 * bt + l16;
+            T* dst = reinterpret_cast<T*>(a.ws_attn) + ((cid * H + (long)g * R + r) * CH + t) * CH + 16 * at + 4 * lg;
+            if (at > bt) {
+                store4<E>(dst, 0.f, 0.f, 0.f, 0.f);
+                continue;
+            }
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < NKD; ++ks) mma<E>(acc, frag(sm.K, at, ks), frag(sm.Q, bt, ks));
+            float o[4];
+            const float gt = sm.gc[t];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tk = 16 * at + 4 * lg + i;
+                o[i] = tk <= t ? a.scale * __expf(gt - sm.gc[tk]) * acc[i] : 0.f;
+            }
+            store4<E>(dst, o[0], o[1], o[2], o[3]);
+        }
+    }
+    __syncthreads();                                     // the q region becomes A
 
     // A = strict_lower(beta_r e^{gc_r - gc_c} (K K^T)_{rc}). K K^T is symmetric: tile (rt, ct) with rt <= ct read
     // in transposed form fills rows 16ct.., columns 16rt.. of A.
-    for (int tix = wv; tix < 10; tix += 4) {
+    for (int tix = wv; tix < 10; tix += nw) {
         const int rt = tix < 4 ? 0 : tix < 7 ? 1 : tix < 9 ? 2 : 3;
         const int ct = rt + (tix - (rt == 0 ? 0 : rt == 1 ? 4 : rt == 2 ? 7 : 9));
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        const int ra = 16 * rt + l16, rb = 16 * ct + l16;
 #pragma unroll
-        for (int kk = 0; kk < D; kk += KF) {
-            const uint4 fa = ra < si.len ? ld16(K + (long)ra * ldk + kk + VEC * lg) : zero16();
-            const uint4 fb = rb < si.len ? ld16(K + (long)rb * ldk + kk + VEC * lg) : zero16();
-            mma<E>(acc, fa, fb);
-        }
+        for (int ks = 0; ks < NKD; ++ks) mma<E>(acc, frag(sm.K, rt, ks), frag(sm.K, ct, ks));
         const int r = 16 * ct + l16;
         const float br = sm.beta[r], gr = sm.gc[r];
         float o[4];
@@ -81,9 +132,10 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(GdnArgs a) {
     }
     __syncthreads();
 
-    if (wv == 0) {
-        // (I + A)^-1 by forward substitution, one column per lane: x_i = [i == j] - sum_{m < i} A[i][m] x_m;
-        // T'[i][j] = x_i beta_j (rows of tokens past the end are zero because their A rows and beta are).
+    // (I + A)^-1 by forward substitution, one column per lane: x_i = [i == j] - sum_{m < i} A[i][m] x_m;
+    // T'[i][j] = x_i beta_j (rows of tokens past the end are zero because their A rows and beta are). The wave doing
+    // it rotates with the chunk so that workgroups sharing a CU use different SIMDs.
+    if (wv == (int)(blockIdx.x % nw)) {
         const int j = lane;
         float x[CH];
 #pragma unroll
@@ -97,36 +149,6 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(GdnArgs a) {
         T* Tp = reinterpret_cast<T*>(a.ws_T) + (cid * G + g) * CH * CH + j;
 #pragma unroll
         for (int i = 0; i < CH; ++i) Tp[i * CH] = E::from_f(x[i] * bj);
-    } else {
-        // attn_r^T = K q_r^T (rows t' = key, cols t = query), masked to t' <= t, decayed and scaled.
-        const T* Q = reinterpret_cast<const T*>(a.q) + si.tok0 * H * D + (long)g * R * D;
-        const long ldq = (long)H * D;
-        for (int item = wv - 1; item < R * 16; item += 3) {
-            const int r = item >> 4, tile = item & 15;
-            const int at = tile >> 2, bt = tile & 3;     // at: key tile (rows), bt: query tile (cols)
-            const int t = 16 * bt + l16;
-            T* dst = reinterpret_cast<T*>(a.ws_attn) + ((cid * H + (long)g * R + r) * CH + t) * CH + 16 * at + 4 * lg;
-            if (at > bt) {
-                store4<E>(dst, 0.f, 0.f, 0.f, 0.f);
-                continue;
-            }
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-            const int ka = 16 * at + l16;
-#pragma unroll
-            for (int kk = 0; kk < D; kk += KF) {
-                const uint4 fa = ka < si.len ? ld16(K + (long)ka * ldk + kk + VEC * lg) : zero16();
-                const uint4 fb = t < si.len ? ld16(Q + (long)t * ldq + (long)r * D + kk + VEC * lg) : zero16();
-                mma<E>(acc, fa, fb);
-            }
-            float o[4];
-            const float gt = sm.gc[t];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int tk = 16 * at + 4 * lg + i;
-                o[i] = tk <= t ? a.scale * __expf(gt - sm.gc[tk]) * acc[i] : 0.f;
-            }
-            store4<E>(dst, o[0], o[1], o[2], o[3]);
-        }
     }
 }
 

@@ -39,7 +39,13 @@ namespace {
 
 constexpr int SC = 64;       // chunk length
 constexpr int NXCD = 8;      // XCDs of an MI355X: workgroups are dispatched round-robin over them by linear id
-constexpr int WCOLS = 32;    // state columns per wave
+// State columns per wave (one or two 16-column MFMA tiles) and columns per workgroup. 16 columns per wave keep a
+// wave under 256 registers, so two waves share a SIMD and one's MFMA work overlaps the other's VALU and LDS work.
+constexpr int WCOLS = 16;
+constexpr int NJ = WCOLS / 16;
+constexpr int WG_COLS = 128;
+constexpr int SEG_THREADS = WG_COLS / WCOLS * 64;
+constexpr int SEG_WAVES_PER_EU = SEG_THREADS / 256;
 
 template <class E>
 __device__ __forceinline__ int prow(int tile, int m) {
@@ -47,25 +53,6 @@ __device__ __forceinline__ int prow(int tile, int m) {
     return KF * (tile / HP) + VEC * (m >> 2) + 4 * (tile % HP) + (m & 3);
 }
 
-// 16-byte block permutation of LDS row `row` (rows have >= 8 blocks; the value is < 8). Requirements:
-//  - the 8 rows that one 8-lane phase of an MFMA fragment read touches (prow of m = 0..7) get distinct values, so a
-//    16-byte-per-lane read hits 8 distinct bank groups;
-//  - bf16: the 4 rows that a 16-lane group of a transposing K^T read touches (4 consecutive rows from a multiple of
-//    4) alternate bit 2, so those 8-byte reads are at most 2-way conflicted;
-//  - the value depends on the lane only (fragment reads) or on the lane and the row within a group of 4 (transposing
-//    reads), so addresses are a per-lane base plus an instruction immediate.
-template <class E>
-__device__ __forceinline__ int swz(int row) {
-    if constexpr (E::VEC == 8) return (row & 3) | ((((row >> 3) ^ row) & 1) << 2);
-    else return (row & 3) | (((row >> 2) & 1) << 2);
-}
-
-// 16-byte block permutation of the V tile rows (rows of VROWB >= 128 bytes): the 4 consecutive rows (from a multiple
-// of 4) that a 16-lane group of a transposing V read touches land 32 bytes apart, and bit 3 separates the two 16-lane
-// groups of a 32-lane half, so those 8-byte reads do not share banks.
-__device__ __forceinline__ int swz_v(int row, int nblk) { return ((2 * (row & 3)) | (((row >> 3) & 1) << 3)) & (nblk - 1); }
-
-// Per-chunk operands, double-buffered for bf16: K (C x D), T' and attn (C x C), gc.
 template <class E, int D, bool OUT>
 struct __align__(16) ChunkLds {
     typename E::T K[SC * D];
@@ -83,28 +70,6 @@ struct __align__(16) OnceLds {
 struct __align__(16) NoLds {
     float pad[4];
 };
-
-__device__ __forceinline__ uint4 lds16(const void* base, int byte_off) {
-    return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base) + byte_off);
-}
-
-// Copy a tile of SC rows into LDS with buffer_load ... lds: LDS row r (rowb bytes) holds global row r (pitch bytes)
-// with its 16-byte blocks permuted by sw(r). One instruction moves 64 x 16 bytes; `nbytes` = SC * rowb is a multiple
-// of 1 KB. Blocks at or beyond `valid_blk` of a row read as zero, as do rows past the descriptor's range.
-template <class Swz>
-__device__ __forceinline__ void stage_tile(rsrc_t src, uint32_t pitch, int rowb, void* lds, int nbytes, int wv,
-                                           int nw, int lane, Swz sw, int valid_blk) {
-    const int nblk = rowb / 16;
-    for (int i = wv; i < nbytes / 1024; i += nw) {
-        const int s = i * 64 + lane;
-        const int r = s / nblk, pb = s % nblk;
-        const int lb = pb ^ sw(r);
-        const uint32_t off = lb < valid_blk ? (uint32_t)r * pitch + (uint32_t)(lb * 16) : 0xFFFFFFF0u;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            src, (__attribute__((address_space(3))) void*)(reinterpret_cast<char*>(lds) + i * 1024), 16, off, 0, 0,
-            0);
-    }
-}
 
 // B operand (K index = accumulator rows) from the HP accumulator tiles of one fragment.
 template <class E>
@@ -178,7 +143,7 @@ __device__ __forceinline__ void seq_segments(const GdnArgs& a, int n, int& first
 template <class E, int D, bool OUT>
 struct SegCfg {
     static constexpr int COLS = OUT ? D : 2 * D;                    // state columns per (segment, KV head)
-    static constexpr int NW = COLS / WCOLS < 4 ? COLS / WCOLS : 4;  // waves per workgroup
+    static constexpr int NW = (COLS < WG_COLS ? COLS : WG_COLS) / WCOLS;  // waves per workgroup
     static constexpr int NCG = COLS / (NW * WCOLS);                 // column groups (workgroups per head)
     static constexpr bool DBUF = E::VEC == 8;                       // bf16: double-buffered stage
 };
@@ -205,7 +170,7 @@ __device__ __forceinline__ uint2 lds_tr16(const char* p) {
 }
 
 template <class E, int D, bool OUT, bool BO>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gdn_seg_kernel(GdnArgs a) {
+__global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(GdnArgs a) {
     using T = typename E::T;
     using Cfg = SegCfg<E, D, OUT>;
     constexpr int VEC = E::VEC, KF = E::KF, ES = (int)sizeof(T), HP = VEC / 4;
@@ -242,21 +207,31 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int v_blk = OUT ? VROWB / 16 : (cb < D ? ((D - cb < VW ? D - cb : VW) * ES) / 16 : 0);  // loaded V blocks
 
     // per-lane address parts
+    constexpr int NBLK = ROWB / 16, TNBLK = TROWB / 16;
+    constexpr bool FAST = ES == 2 && NBLK >= 16;           // 4-bit swizzle of the K / q tiles
+    constexpr int NX = FAST ? 4 : 2;
     const int lt = VEC * (l16 >> 2) + (l16 & 3);         // fragment row offset inside a tile
-    const int sl = swz<E>(lt);                           // swizzle of fragment rows (depends on the lane only)
-    int xb[2];                                           // swizzled 16-byte block of K index group (ks, lg), per ks&1
+    // K / q fragment of K index group (ks, lg) at row tp(tile) + lt: block (4ks + lg) ^ swz(row), and the swizzle of
+    // those rows depends on the lane only, so the block is 4*NX*(ks / NX) + xb[ks % NX]
+    const int sl = swz<E>(lt, NBLK), tsl = swz<E>(lt, TNBLK);
+    int kq_base[NX], t_base[2];
 #pragma unroll
-    for (int par = 0; par < 2; ++par) xb[par] = 4 * (par ^ (sl >> 2)) + (lg ^ (sl & 3));
+    for (int c = 0; c < NX; ++c) kq_base[c] = lt * ROWB + 16 * (4 * (c ^ (sl >> 2)) + (lg ^ (sl & 3)));
+#pragma unroll
+    for (int c = 0; c < 2; ++c) t_base[c] = lt * TROWB + 16 * (4 * (c ^ (tsl >> 2)) + (lg ^ (tsl & 3)));
     // K^T A fragments (rows tp(td) + lt, K index = tokens KF*ks + VEC*lg + e).
     // bf16: two transposing reads per fragment; lane (e, q) = (l16/4, l16%4) of group lg reads the 4 state rows
     // tp(td) + 8q .. +3 of token 32ks + 8lg + 4h + e, so lane 4q + r collects tokens 8lg + 4h + 0..3 of row
-    // prow(td, 4q + r). With s = (lg ^ e) & 1 that chunk lies at trb[(td/2) & 1] + (32ks + 4h)*ROWB + 64*(td/2) + 8*(td&1).
+    // prow(td, 4q + r). That chunk's block is (4A + q) ^ swz(token) with A = td/2, i.e. 4(A ^ s) + (q ^ e) for the lane
+    // constant s, so it lies at trb[A % NTR] + (32ks + 4h)*ROWB + 64*A + 8*(td&1).
     // fp32: one 4-byte read per element, at ktb[td & 1][e] + (16ks + e)*ROWB + 64*td.
-    int trb[2], ktb[2][4];
+    constexpr int NTR = FAST ? 4 : 2;
+    int trb[NTR], ktb[2][4];
     if constexpr (ES == 2) {
-        const int e_ = l16 >> 2, q_ = l16 & 3, s_ = (lg ^ e_) & 1;
+        const int e_ = l16 >> 2, q_ = l16 & 3;
+        const int s_ = FAST ? (lg ^ (e_ & 2)) : ((lg ^ e_) & 1);
 #pragma unroll
-        for (int par = 0; par < 2; ++par) trb[par] = (8 * lg + e_) * ROWB + 16 * (q_ ^ e_) + (par ? -64 : 64) * s_;
+        for (int c = 0; c < NTR; ++c) trb[c] = (8 * lg + e_) * ROWB + 64 * ((c ^ s_) - c) + 16 * (q_ ^ e_);
     } else {
 #pragma unroll
         for (int par = 0; par < 2; ++par)
@@ -267,23 +242,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     // V B fragments (K index = tokens KF*ks + VEC*lg + e, column wv*32 + 16jt + l16 of the V tile).
     // bf16: lane (e, q) of group lg reads columns 16jt + 4q .. +3 of token 32ks + 8lg + 4h + e: at
     // vtb[jt] + (32ks + 4h)*VROWB. fp32: element (token, column) read directly.
-    int vtb[2];
+    int vtb[NJ];
     if constexpr (ES == 2) {
         const int e_ = l16 >> 2, q_ = l16 & 3;
         const int sv = swz_v(8 * lg + e_, VROWB / 16);
 #pragma unroll
-        for (int jt = 0; jt < 2; ++jt)
-            vtb[jt] = (8 * lg + e_) * VROWB + 16 * ((4 * wv + 2 * jt + (q_ >> 1)) ^ sv) + 8 * (q_ & 1);
+        for (int jt = 0; jt < NJ; ++jt)
+            vtb[jt] = (8 * lg + e_) * VROWB + 16 * ((wv * WCOLS / 8 + 2 * jt + (q_ >> 1)) ^ sv) + 8 * (q_ & 1);
     } else {
         vtb[0] = vtb[1] = 0;
     }
 
     // state strip: S[tile over rows][column tile], rows prow(tile, 4lg + i), column jc + 16 jt + l16
-    f32x4 S[NTD][2];
+    f32x4 S[NTD][NJ];
 #pragma unroll
     for (int td = 0; td < NTD; ++td)
 #pragma unroll
-        for (int jt = 0; jt < 2; ++jt) {
+        for (int jt = 0; jt < NJ; ++jt) {
             const int j = jc + 16 * jt + l16;
             f32x4 v = {0.f, 0.f, 0.f, 0.f};
             if constexpr (OUT) {
@@ -311,7 +286,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         const long rem = sg.tok1 - chunk_tok0(c);
         return (int)(rem < SC ? rem : SC);
     };
-    const auto sw_row = [](int row) { return swz<E>(row); };
+    const auto sw_row = [](int row) { return swz<E>(row, ROWB / 16); };
+    const auto sw_t = [](int row) { return swz<E>(row, TROWB / 16); };
     const auto sw_v = [](int row) { return swz_v(row, VROWB / 16); };
     auto load_chunk = [&](auto& cl, int c) {
         const long t0 = chunk_tok0(c);
@@ -322,11 +298,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         stage_tile(rk, (uint32_t)(G * D * ES), ROWB, cl.K, SC * ROWB, wv, NW, lane, sw_row, 1 << 30);
         const rsrc_t rt = make_rsrc(reinterpret_cast<const char*>(a.ws_T) + (cid * G + g) * SC * SC * ES,
                                     (uint32_t)(SC * SC * ES));
-        stage_tile(rt, (uint32_t)TROWB, TROWB, cl.Tp, SC * TROWB, wv, NW, lane, sw_row, 1 << 30);
+        stage_tile(rt, (uint32_t)TROWB, TROWB, cl.Tp, SC * TROWB, wv, NW, lane, sw_t, 1 << 30);
         if constexpr (OUT) {
             const rsrc_t ra = make_rsrc(reinterpret_cast<const char*>(a.ws_attn) + (cid * H + h) * SC * SC * ES,
                                         (uint32_t)(SC * SC * ES));
-            stage_tile(ra, (uint32_t)TROWB, TROWB, cl.At, SC * TROWB, wv, NW, lane, sw_row, 1 << 30);
+            stage_tile(ra, (uint32_t)TROWB, TROWB, cl.At, SC * TROWB, wv, NW, lane, sw_t, 1 << 30);
         }
         if (wv == 0 && lane < SC / 4) {
             const rsrc_t rg = make_rsrc(a.ws_gcum + (cid * G + g) * SC, SC * 4);
@@ -372,22 +348,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
         // phase 1: Y = K S_stored, O = q S_stored. A fragments of step ks + 1 are read while step ks multiplies; the
         // scheduling barrier keeps the compiler from hoisting every step's reads (and their registers) to the front.
-        f32x4 Y[NTC][2], O[OUT ? NTC : 1][2];
+        f32x4 Y[NTC][NJ], O[OUT ? NTC : 1][NJ];
 #pragma unroll
         for (int tt = 0; tt < NTC; ++tt)
 #pragma unroll
-            for (int jt = 0; jt < 2; ++jt) {
+            for (int jt = 0; jt < NJ; ++jt) {
                 Y[tt][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
                 if constexpr (OUT) O[tt][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
             }
-        const int kq_base[2] = {lt * ROWB + 16 * xb[0], lt * ROWB + 16 * xb[1]};
         // fp32 output scan: q fragments straight from global memory (rows past the end read as zero)
         const rsrc_t rqg = make_rsrc(reinterpret_cast<const char*>(a.q) + (chunk_tok0(c) * H + h) * D * ES,
                                      (uint32_t)(OUT && !QL ? (long)chunk_len(c) * H * D * ES : 0));
         auto read_kq = [&](int ks, uint4 (&ak)[NTC], uint4 (&aq)[NTC]) {
 #pragma unroll
             for (int tt = 0; tt < NTC; ++tt) {
-                const int off = kq_base[ks & 1] + tpart<E>(tt) * ROWB + 128 * (ks >> 1);
+                const int off = kq_base[ks % NX] + tpart<E>(tt) * ROWB + 64 * NX * (ks / NX);
                 ak[tt] = lds16(Kb, off);
                 if constexpr (QL) aq[tt] = lds16(Qb, off);
                 else if constexpr (OUT)
@@ -400,16 +375,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         for (int ks = 0; ks < NKD; ++ks) {
             uint4 nk[NTC], nq[NTC];
             if (ks + 1 < NKD) read_kq(ks + 1, nk, nq);
-            uint4 sb[2];
+            uint4 sb[NJ];
 #pragma unroll
-            for (int jt = 0; jt < 2; ++jt) sb[jt] = pack_b<E>(S[ks * HP][jt], S[ks * HP + HP - 1][jt]);
+            for (int jt = 0; jt < NJ; ++jt) sb[jt] = pack_b<E>(S[ks * HP][jt], S[ks * HP + HP - 1][jt]);
 #pragma unroll
             for (int tt = 0; tt < NTC; ++tt) {
 #pragma unroll
-                for (int jt = 0; jt < 2; ++jt) mma<E>(Y[tt][jt], ak[tt], sb[jt]);
+                for (int jt = 0; jt < NJ; ++jt) mma<E>(Y[tt][jt], ak[tt], sb[jt]);
                 if constexpr (OUT) {
 #pragma unroll
-                    for (int jt = 0; jt < 2; ++jt) mma<E>(O[tt][jt], aq[tt], sb[jt]);
+                    for (int jt = 0; jt < NJ; ++jt) mma<E>(O[tt][jt], aq[tt], sb[jt]);
                 }
             }
             if (ks + 1 < NKD) {
@@ -428,27 +403,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             }
         }
 
-        // phase 2: v_new = T' (V - e^{gc} K S) = T' V + T' (-sc e^{gc} Y)
-        f32x4 Vn[NTC][2];
-#pragma unroll
-        for (int tt = 0; tt < NTC; ++tt)
-#pragma unroll
-            for (int jt = 0; jt < 2; ++jt) {
-                Vn[tt][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) Y[tt][jt][i] *= -egc[tt][i];
-            }
-        const int t_base[2] = {lt * TROWB + 16 * xb[0], lt * TROWB + 16 * xb[1]};
+        // phase 2: v_new = T' (V - e^{gc} K S) = T' V + T' (-sc e^{gc} Y). All T' and V fragments of the chunk are read
+        // first, so their LDS latency is covered by the scaling of Y.
+        uint4 tf[NKC][NTC], vf[NKC][NJ];
 #pragma unroll
         for (int ks = 0; ks < NKC; ++ks) {
-            uint4 yb[2], vb[2];
 #pragma unroll
-            for (int jt = 0; jt < 2; ++jt) {
-                yb[jt] = pack_b<E>(Y[ks * HP][jt], Y[ks * HP + HP - 1][jt]);
+            for (int tt = 0; tt < NTC; ++tt) tf[ks][tt] = lds16(Tb, t_base[ks & 1] + tpart<E>(tt) * TROWB + 128 * (ks >> 1));
+#pragma unroll
+            for (int jt = 0; jt < NJ; ++jt) {
                 if constexpr (ES == 2) {
                     const uint2 lo = lds_tr16(Vb + vtb[jt] + 32 * ks * VROWB);
                     const uint2 hi = lds_tr16(Vb + vtb[jt] + (32 * ks + 4) * VROWB);
-                    vb[jt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                    vf[ks][jt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
                 } else {
                     // element (token t, tile column cv) of the swizzled V tile
                     const int cv = wv * WCOLS + 16 * jt + l16;
@@ -459,16 +426,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                         w[e] = *reinterpret_cast<const uint32_t*>(
                             Vb + t * VROWB + (((cv >> 2) ^ swz_v(t, VROWB / 16)) << 4) + (cv & 3) * 4);
                     }
-                    vb[jt] = make_uint4(w[0], w[1], w[2], w[3]);
+                    vf[ks][jt] = make_uint4(w[0], w[1], w[2], w[3]);
                 }
             }
+        }
+        f32x4 Vn[NTC][NJ];
+#pragma unroll
+        for (int tt = 0; tt < NTC; ++tt)
+#pragma unroll
+            for (int jt = 0; jt < NJ; ++jt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) Y[tt][jt][i] *= -egc[tt][i];
+#pragma unroll
+        for (int ks = 0; ks < NKC; ++ks) {
+            uint4 yb[NJ];
+#pragma unroll
+            for (int jt = 0; jt < NJ; ++jt) yb[jt] = pack_b<E>(Y[ks * HP][jt], Y[ks * HP + HP - 1][jt]);
 #pragma unroll
             for (int tt = 0; tt < NTC; ++tt) {
-                const uint4 at = lds16(Tb, t_base[ks & 1] + tpart<E>(tt) * TROWB + 128 * (ks >> 1));
 #pragma unroll
-                for (int jt = 0; jt < 2; ++jt) {
-                    mma<E>(Vn[tt][jt], at, yb[jt]);
-                    if (!phi_part) mma<E>(Vn[tt][jt], at, vb[jt]);
+                for (int jt = 0; jt < NJ; ++jt) {
+                    if (ks == 0) Vn[tt][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    mma<E>(Vn[tt][jt], tf[ks][tt], yb[jt]);
+                    if (!phi_part) mma<E>(Vn[tt][jt], tf[ks][tt], vf[ks][jt]);
                 }
             }
         }
@@ -478,25 +458,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             load_v(cn);
         }
 
-        // phase 3: o = scale e^{gc} (q S) + attn v_new
+        // phase 3: o = scale e^{gc} (q S) + attn v_new (attn fragments read before the scaling of O)
         if constexpr (OUT) {
+            uint4 af[NKC][NTC];
+#pragma unroll
+            for (int ks = 0; ks < NKC; ++ks)
+#pragma unroll
+                for (int tt = 0; tt < NTC; ++tt)
+                    af[ks][tt] = lds16(Ab, t_base[ks & 1] + tpart<E>(tt) * TROWB + 128 * (ks >> 1));
 #pragma unroll
             for (int tt = 0; tt < NTC; ++tt)
 #pragma unroll
-                for (int jt = 0; jt < 2; ++jt)
+                for (int jt = 0; jt < NJ; ++jt)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) O[tt][jt][i] *= a.scale * egc[tt][i];   // egc carries sc
 #pragma unroll
             for (int ks = 0; ks < NKC; ++ks) {
-                uint4 vb[2];
+                uint4 vb[NJ];
 #pragma unroll
-                for (int jt = 0; jt < 2; ++jt) vb[jt] = pack_b<E>(Vn[ks * HP][jt], Vn[ks * HP + HP - 1][jt]);
+                for (int jt = 0; jt < NJ; ++jt) vb[jt] = pack_b<E>(Vn[ks * HP][jt], Vn[ks * HP + HP - 1][jt]);
 #pragma unroll
-                for (int tt = 0; tt < NTC; ++tt) {
-                    const uint4 aa = lds16(Ab, t_base[ks & 1] + tpart<E>(tt) * TROWB + 128 * (ks >> 1));
+                for (int tt = 0; tt < NTC; ++tt)
 #pragma unroll
-                    for (int jt = 0; jt < 2; ++jt) mma<E>(O[tt][jt], aa, vb[jt]);
-                }
+                    for (int jt = 0; jt < NJ; ++jt) mma<E>(O[tt][jt], af[ks][tt], vb[jt]);
             }
             constexpr int OS = BO ? 2 : 4;
             const long t0 = chunk_tok0(c);
@@ -515,7 +499,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
 #pragma unroll
-                        for (int jt = 0; jt < 2; ++jt)
+                        for (int jt = 0; jt < NJ; ++jt)
                             put(ro, o_lane, (uint32_t)(((tpart<E>(tt) + i) * H * D + jc + 16 * jt) * OS),
                                 O[tt][jt][i]);
             } else {
@@ -530,7 +514,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                             reinterpret_cast<char*>(a.o) + ((t0 + row) * H + h) * (long)D * OS,
                             (uint32_t)(nrow * H * D * OS));
 #pragma unroll
-                        for (int jt = 0; jt < 2; ++jt)
+                        for (int jt = 0; jt < NJ; ++jt)
                             put(ro, o_lane + (uint32_t)((jc + 16 * jt) * OS), 0u, O[tt][jt][i]);
                     }
             }
@@ -548,7 +532,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
             for (int td = 0; td < NTD; ++td)
 #pragma unroll
-                for (int jt = 0; jt < 2; ++jt)
+                for (int jt = 0; jt < NJ; ++jt)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) S[td][jt][i] *= scn;
             ratio = scn;
@@ -560,13 +544,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             for (int i = 0; i < 4; ++i) {
                 const float f = ratio * __builtin_amdgcn_rcpf(egc[tt][i]);
 #pragma unroll
-                for (int jt = 0; jt < 2; ++jt) Vn[tt][jt][i] *= f;
+                for (int jt = 0; jt < NJ; ++jt) Vn[tt][jt][i] *= f;
             }
         }
         auto frag_kt = [&](int td, int ks) {
             if constexpr (ES == 2) {
                 const int at = td >> 1;
-                const char* p = Kb + trb[at & 1] + 32 * ks * ROWB + 64 * at + 8 * (td & 1);
+                const char* p = Kb + trb[at % NTR] + 32 * ks * ROWB + 64 * at + 8 * (td & 1);
                 const uint2 lo = lds_tr16(p), hi = lds_tr16(p + 4 * ROWB);
                 return make_uint4(lo.x, lo.y, hi.x, hi.y);
             } else {
@@ -577,21 +561,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 return make_uint4(w[0], w[1], w[2], w[3]);
             }
         };
+        // K^T fragments are read PF4 tiles ahead of their MFMAs (a ring of PF4 + 1 fragments over the
+        // NKC * NTD (ks, td) steps), so the LDS latency of the transposing reads stays covered
+        constexpr int NST = NKC * NTD, PF4 = 3;
+        uint4 ring[PF4 + 1];
 #pragma unroll
-        for (int ks = 0; ks < NKC; ++ks) {
-            uint4 vb[2];
+        for (int q = 0; q < PF4; ++q) ring[q] = frag_kt(q % NTD, q / NTD);
+        uint4 vb[NKC][NJ];
 #pragma unroll
-            for (int jt = 0; jt < 2; ++jt) vb[jt] = pack_b<E>(Vn[ks * HP][jt], Vn[ks * HP + HP - 1][jt]);
-            uint4 akt = frag_kt(0, ks);
+        for (int ks = 0; ks < NKC; ++ks)
 #pragma unroll
-            for (int td = 0; td < NTD; ++td) {
-                uint4 nxt = akt;
-                if (td + 1 < NTD) nxt = frag_kt(td + 1, ks);
+            for (int jt = 0; jt < NJ; ++jt) vb[ks][jt] = pack_b<E>(Vn[ks * HP][jt], Vn[ks * HP + HP - 1][jt]);
 #pragma unroll
-                for (int jt = 0; jt < 2; ++jt) mma<E>(S[td][jt], akt, vb[jt]);
-                akt = nxt;
-                __builtin_amdgcn_sched_barrier(0);
-            }
+        for (int st = 0; st < NST; ++st) {
+            const int ks = st / NTD, td = st % NTD;
+            if (st + PF4 < NST) ring[(st + PF4) % (PF4 + 1)] = frag_kt((st + PF4) % NTD, (st + PF4) / NTD);
+#pragma unroll
+            for (int jt = 0; jt < NJ; ++jt) mma<E>(S[td][jt], ring[st % (PF4 + 1)], vb[ks][jt]);
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
 
@@ -634,7 +621,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
             for (int td = 0; td < NTD; ++td)
 #pragma unroll
-                for (int jt = 0; jt < 2; ++jt)
+                for (int jt = 0; jt < NJ; ++jt)
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
                         dst[(long)prow<E>(td, 4 * lg + i) * D + jc + 16 * jt + l16] = sc * S[td][jt][i];
@@ -646,7 +633,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int td = 0; td < NTD; ++td)
 #pragma unroll
-            for (int jt = 0; jt < 2; ++jt)
+            for (int jt = 0; jt < NJ; ++jt)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int d = prow<E>(td, 4 * lg + i), j = jc + 16 * jt + l16;
@@ -704,12 +691,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     };
     auto step = [&](const Pre& P, int p) {
         const long sid = first + p;
-        f32x4 acc[TPW];
+        // acc collects Psi X_hi (bf16) or Psi X (fp32); accl collects Psi X_lo, in separate accumulators so that no
+        // MFMA waits for the one before it
+        f32x4 acc[TPW], accl[TPW];
 #pragma unroll
         for (int u = 0; u < TPW; ++u) {
             const int tr = wv * TPW + u;
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[u][i] = P.N[u][i] + P.c * XT[l16][16 * tr + 4 * lg + i];
+            accl[u] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
         for (int ks = 0; ks < NKD; ++ks) {
@@ -729,17 +719,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                 }
                 const uint4 BH = make_uint4(hw[0], hw[1], hw[2], hw[3]), BL = make_uint4(lw[0], lw[1], lw[2], lw[3]);
 #pragma unroll
-                for (int u = 0; u < TPW; ++u) {
-                    mma<E>(acc[u], P.A[u][ks], BL);
-                    mma<E>(acc[u], P.A[u][ks], BH);
-                }
+                for (int u = 0; u < TPW; ++u) mma<E>(accl[u], P.A[u][ks], BL);
+#pragma unroll
+                for (int u = 0; u < TPW; ++u) mma<E>(acc[u], P.A[u][ks], BH);
             } else {
                 const uint4 B = make_uint4(__float_as_uint(bv[0]), __float_as_uint(bv[1]), __float_as_uint(bv[2]),
                                            __float_as_uint(bv[3]));
 #pragma unroll
-                for (int u = 0; u < TPW; ++u) mma<E>(acc[u], P.A[u][ks], B);
+                for (int u = 0; u < TPW; ++u) mma<E>((ks & 1) ? accl[u] : acc[u], P.A[u][ks], B);
             }
         }
+#pragma unroll
+        for (int u = 0; u < TPW; ++u)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[u][i] += accl[u][i];
         __syncthreads();
         float* dst = a.ws_sin + ((sid + 1) * G + g) * D * D;
 #pragma unroll

@@ -656,8 +656,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     constexpr int VEC = E::VEC, KF = E::KF, NTD = D / 16, NKD = D / KF, TPW = NTD / 4;
     constexpr bool DBUF = E::VEC == 8;
     __shared__ __align__(16) float XT[16][D + 4];
+    // XCD-aware mapping: all strips of one (sequence, KV head) read the same Psi, so they go to one XCD (one L2)
     const int strips = D / 16, G = a.G;
-    const int n = blockIdx.x / (G * strips), g = (blockIdx.x / strips) % G, jb = blockIdx.x % strips;
+    const int xcd = blockIdx.x % NXCD, local = blockIdx.x / NXCD;
+    const int grp = xcd + NXCD * (local / strips), jb = local % strips;
+    const int n = grp / G, g = grp % G;
     if (n >= a.num_seqs) return;
     int first, nseg;
     seq_segments(a, n, first, nseg);
@@ -733,6 +736,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         for (int u = 0; u < TPW; ++u)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[u][i] += accl[u][i];
+        // every load of the step (this Psi / N / c, issued a step ago, and the next one, issued before the MFMAs)
+        // has had the MFMA time to land; draining here keeps the compiler from interleaving waits for late current-step
+        // data with the next prefetch, and also retires the previous step's stores
+        wait_vmem_all();
         __syncthreads();
         float* dst = a.ws_sin + ((sid + 1) * G + g) * D * D;
 #pragma unroll
@@ -752,18 +759,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     if constexpr (DBUF) {
         Pre P0, P1;
         load(P0, 0);
-        wait_vmem_all();
         __syncthreads();
         for (int p = 0;;) {
-            // unconditional prefetch (the last step re-loads itself), as in the segment scan
-            load(P1, p + 1 < steps ? p + 1 : p);
+            if (p + 1 < steps) load(P1, p + 1);
+            __builtin_amdgcn_sched_barrier(0);
             step(P0, p);
             if (++p >= steps) break;
-            load(P0, p + 1 < steps ? p + 1 : p);
+            if (p + 1 < steps) load(P0, p + 1);
+            __builtin_amdgcn_sched_barrier(0);
             step(P1, p);
             if (++p >= steps) break;
         }
-        wait_vmem_all();
     } else {
         __syncthreads();
         for (int p = 0; p < steps; ++p) {
@@ -791,7 +797,9 @@ int launch_states(const GdnArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL((gdn_seg_kernel<E, D, false, false>), grid, block, 0, stream, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL((gdn_combine_kernel<E, D>), dim3(a.num_seqs * a.G * (D / 16)), dim3(256), 0, stream, a);
+    const int groups = a.num_seqs * a.G;
+    hipLaunchKernelGGL((gdn_combine_kernel<E, D>), dim3(NXCD * ((groups + NXCD - 1) / NXCD) * (D / 16)), dim3(256), 0,
+                       stream, a);
     return (int)hipGetLastError();
 }
 

@@ -205,13 +205,13 @@ def window_pairs(T, W, S):
     return sum(min(p + 1, W + S) for p in range(T))
 
 
-def run_layer(steps, warmup, dev):
+def run_layer(steps, warmup, dev, T=32768):
     """Full converted-layer prefill at 32K: B=1, T=32768, H=24, G=4, D=256, W=2048 + 4 sinks, bf16 activations,
     fp32 state; x/q/k/v/qr/kr synthetic (q, k L2-normalised), init-time gates (fq = fk = I). One step =
     heimdall_amd.hibrit.student over the whole chunk from an empty cache (memory branch, window, mix, cache)."""
     from heimdall_amd import hibrit
 
-    B, T, H, G, D, W, S, d = 1, 32768, 24, 4, 256, 2048, 4, 1024
+    B, H, G, D, W, S, d = 1, 24, 4, 256, 2048, 4, 1024
     torch.manual_seed(0)
     m = hibrit.BifrostCore(hibrit.CoreConfig(H, G, D, d))
     m.convert(W, S, 1)
@@ -241,7 +241,7 @@ def run_layer(steps, warmup, dev):
     chunks = T // C
     mem_flops = chunks * G * (8 * C * C * D + 6 * C * D * D + 2 * C * C * D) + chunks * (H - G) * (
         4 * C * D * D + 4 * C * C * D)
-    return {"workload": "layer prefill B=1 T=32768 H=24 G=4 D=256 W=2048+4 bf16", "ms_per_step": ms,
+    return {"workload": f"layer prefill B=1 T={T} H=24 G=4 D=256 W=2048+4 bf16", "ms_per_step": ms,
             "tokens_per_s": T / (ms * 1e-3), "steps": steps, "flops": {"window": win_flops, "memory": mem_flops},
             "tflops": (win_flops + mem_flops) / (ms * 1e-3) / 1e12}
 
@@ -255,6 +255,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the decode and layer-prefill legs")
     ap.add_argument("--copy-probe", action="store_true", help="run one 256 MiB device copy first (counter scaling)")
     ap.add_argument("--segment-chunks", type=int, default=0, help="chunks per scan segment (0 = library default)")
+    ap.add_argument("--only", choices=("decode", "layer", "layer131k"), default=None,
+                    help="run one secondary leg alone and print its JSON object (for per-workload profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the Bifrost core needs no inter-GPU exchange; "
@@ -269,6 +271,13 @@ def main():
         dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+
+    if args.only:
+        leg = {"decode": lambda: run_decode(args.steps, args.warmup, dev),
+               "layer": lambda: run_layer(args.steps, args.warmup, dev),
+               "layer131k": lambda: run_layer(args.steps, args.warmup, dev, T=131072)}[args.only]
+        print(json.dumps(leg()), flush=True)
+        return
 
     r = run_gdn(args.steps, args.warmup, dev, args.segment_chunks)
     T, H, D = r["T"], r["H"], r["D"]

@@ -250,7 +250,8 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
         for (int jt = 0; jt < NJ; ++jt)
             vtb[jt] = (8 * lg + e_) * VROWB + 16 * ((wv * WCOLS / 8 + 2 * jt + (q_ >> 1)) ^ sv) + 8 * (q_ & 1);
     } else {
-        vtb[0] = vtb[1] = 0;
+#pragma unroll
+        for (int jt = 0; jt < NJ; ++jt) vtb[jt] = 0;
     }
 
     // state strip: S[tile over rows][column tile], rows prow(tile, 4lg + i), column jc + 16 jt + l16

@@ -124,5 +124,6 @@ struct WinArgs {
 };
 
 int window_dispatch(const WinArgs& a, hipStream_t stream);
+int window_fa_dispatch(const WinArgs& a, hipStream_t stream);   // bf16 operands
 
 }  // namespace bf

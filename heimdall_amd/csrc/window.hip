@@ -359,11 +359,11 @@ static int launch_window(const WinArgs& a, hipStream_t stream) {
 }
 
 int window_dispatch(const WinArgs& a, hipStream_t stream) {
-    const bool bf = a.in_dtype == DT_BF16;
+    if (a.in_dtype == DT_BF16) return window_fa_dispatch(a, stream);
     switch (a.D) {
-        case 64: return bf ? launch_window<BF16, 64>(a, stream) : launch_window<F32, 64>(a, stream);
-        case 128: return bf ? launch_window<BF16, 128>(a, stream) : launch_window<F32, 128>(a, stream);
-        case 256: return bf ? launch_window<BF16, 256>(a, stream) : launch_window<F32, 256>(a, stream);
+        case 64: return launch_window<F32, 64>(a, stream);
+        case 128: return launch_window<F32, 128>(a, stream);
+        case 256: return launch_window<F32, 256>(a, stream);
         default: return BF_ERR_UNSUPPORTED;
     }
 }

@@ -1,0 +1,424 @@
+// K2, bf16 operands: exact sliding-window + sink attention over a prefill chunk with per-row log-sum-exp and the
+// fused gamma mix (reference: HybridAttention._window_fp32, Heimdall/heimdall/hibrit.py:341-361, mix :409-411).
+//
+// Semantics are those of window.hip (which serves fp32 operands): query i of the chunk sits at position
+// p = start + i and sees the sinks j < n_sinks with j <= p and the keys kp with S <= kp <= p, p - kp < W (the ring
+// for kp < start, slot kp mod W valid iff ring_pos[slot] == kp; the chunk for kp >= start).
+//
+// Work split. One workgroup = 128 consecutive queries of one query head, 4 waves x 32 queries. A wave holds its 32
+// queries as two 16-query MFMA tiles, so every K / V fragment it reads from LDS feeds two v_mfma_f32_16x16x32_bf16:
+// 32 FLOP per LDS byte, above the ~21 FLOP/B at which gfx950's LDS read rate (~165 B/clk/CU) and MFMA rate meet.
+//   S^T = K Q^T      A = K rows (LDS),             B = Q (registers, loaded once)
+//   O^T += V^T P^T   A = V^T via ds_read_b64_tr_b16 of the row-major V tile,  B = P straight from the S registers
+// Scores are transposed so that a query's softmax statistics live in its own lane column (max: two cross-lane
+// steps per block; sum: per-lane partials reduced once at the end). The running max is raised only when a block's
+// max exceeds it by more than 8 (log2 units), so O is rescaled rarely and P stays <= 2^8.
+//
+// Keys come in blocks of 64 rows from one contiguous source (sinks, ring before / after its wrap point, chunk). A
+// block's K and V tiles are copied global -> LDS with buffer_load ... lds (no registers), double-buffered: block i+1
+// is in flight while block i is computed. Per wave, blocks no query of the wave can see are skipped and blocks every
+// query sees skip the mask. Workgroups are mapped XCD-aware: consecutive workgroups of one XCD take the R query
+// heads of one query block, then the next query block of the same KV head, so one L2 serves their K / V re-reads.
+#include "bf_common.h"
+#include "bf_internal.h"
+
+namespace bf {
+
+namespace {
+
+constexpr int FA_BQ = 128;                  // queries per workgroup
+constexpr int FA_KB = 64;                   // keys per block
+constexpr int FA_NXCD = 8;
+constexpr float FA_LOG2E = 1.4426950408889634f;
+constexpr float FA_LN2 = 0.6931471805599453f;
+constexpr float FA_SLACK = 8.f;             // lazy max: rescale only when a block max exceeds the running max by this
+
+// Waves per workgroup and 16-query MFMA tiles per wave: D <= 128 holds 32 queries per wave (two tiles share each
+// K / V fragment read), D = 256 holds 16 queries in each of 8 waves so that two waves fit one SIMD's registers.
+template <int D>
+struct FaShape {
+    static constexpr int QT = D <= 128 ? 2 : 1;
+    static constexpr int NW = FA_BQ / (16 * QT);
+    static constexpr int NT = 64 * NW;
+};
+
+template <int D>
+struct __align__(16) FaTile {
+    uint16_t k[FA_KB * D];     // key rows, 16-byte blocks permuted by fa_swk(row)
+    uint16_t v[FA_KB * D];     // value rows, 16-byte blocks permuted by fa_swv(row)
+};
+
+// LDS block permutations (NBLK = 16-byte blocks per row). K: the 16 rows of an A fragment read (one block each) hit
+// 16 distinct 16-byte bank groups. V: the 8 consecutive rows x 32 bytes of a 32-lane transposing read do too.
+template <int NBLK>
+__device__ __forceinline__ int fa_swk(int row) { return NBLK >= 16 ? (row & 15) : ((row >> 1) & 7); }
+template <int NBLK>
+__device__ __forceinline__ int fa_swv(int row) { return NBLK >= 16 ? 2 * (row & 7) : 2 * ((row >> 1) & 3); }
+
+typedef short fa_v4s __attribute__((ext_vector_type(4)));
+// ds_read_b64_tr_b16: in each 16-lane group, lane 4q + r receives element r of the 8-byte chunks that lanes 4e + q
+// (e = 0..3) address, in order of e.
+__device__ __forceinline__ uint2 fa_tr16(const char* p) {
+    const fa_v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) fa_v4s*)(p));
+    return make_uint2((uint16_t)v[0] | ((uint32_t)(uint16_t)v[1] << 16), (uint16_t)v[2] | ((uint32_t)(uint16_t)v[3] << 16));
+}
+
+// global_load_lds_dwordx4: 16 bytes from each lane's own address into LDS at dst + 16 * lane (dst wave-uniform).
+__device__ __forceinline__ void fa_g2l(const void* src, void* dst) {
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
+}
+
+}  // namespace
+
+template <int D, bool BO>
+__global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a) {
+    constexpr int QT = FaShape<D>::QT, NW = FaShape<D>::NW, QW = 16 * QT;
+    constexpr int ROWB = D * 2, NBLK = ROWB / 16;
+    constexpr int NKD = D / 32;                 // K fragments along D (S product)
+    constexpr int NDT = D / 16;                 // output d tiles (PV product)
+    constexpr int NKB = NKD < 4 ? NKD : 4;      // distinct per-lane K fragment bases
+    constexpr int NVB = NDT < 8 ? NDT : 8;      // distinct per-lane V fragment bases
+    constexpr int NLD = FA_KB * ROWB / 1024 / NW;   // global -> LDS copies per wave per tile (64 x 16 bytes each)
+    static_assert(NLD * NW * 1024 == FA_KB * ROWB, "tile copy split");
+    __shared__ FaTile<D> t0;
+    __shared__ FaTile<D> t1;
+
+    // ---- work item (XCD-aware)
+    const int R = a.R, G = a.G, H = G * R;
+    const int nqb = (a.T + FA_BQ - 1) / FA_BQ;
+    const long nwork = (long)a.B * G * nqb * R;
+    const long per = (nwork + FA_NXCD - 1) / FA_NXCD;
+    const long wi = (long)(blockIdx.x % FA_NXCD) * per + blockIdx.x / FA_NXCD;
+    if (wi >= nwork) return;
+    const int r = (int)(wi % R);
+    long rest = wi / R;
+    const int qb = (int)(rest % nqb);
+    rest /= nqb;
+    const int g = (int)(rest % G), b = (int)(rest / G);
+    const int h = g * R + r;
+
+    const int lane = lane_id(), wv = wave_id(), l16 = lane & 15, lg = lane >> 4;
+    const long qi0 = (long)qb * FA_BQ;
+    const int nq = (int)min((long)FA_BQ, (long)a.T - qi0);
+    const long p_first = a.start + qi0, p_last = p_first + nq - 1;
+    const int nqw = max(0, min(QW, nq - QW * wv));                // queries of this wave
+    const long qw0 = p_first + QW * wv, qw1 = qw0 + nqw - 1;
+
+    // ---- Q fragments (B operand of S^T = K Q^T): query tile qt, column l16, d range 32 kf + 8 lg
+    const uint16_t* Qb = reinterpret_cast<const uint16_t*>(a.q) + b * a.q_sb + h * a.q_sh;
+    uint4 fq[QT][NKD];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        const int qi = QW * wv + 16 * qt + l16;
+        const uint16_t* qrow = Qb + (qi0 + qi) * a.q_st;
+#pragma unroll
+        for (int kf = 0; kf < NKD; ++kf) fq[qt][kf] = qi < nq ? ld16(qrow + 32 * kf + 8 * lg) : zero16();
+    }
+
+    // ---- key blocks: [the sink block] then 64 consecutive positions each from kp_lo (window start of the first
+    // query) to p_last. A window key at kp < start is ring slot kp mod W (valid iff ring_pos[slot] == kp), at
+    // kp >= start chunk row kp - start. Rows outside [kp_lo, p_last] (or past the sinks) are masked.
+    const uint16_t* ck = reinterpret_cast<const uint16_t*>(a.k) + b * a.k_sb + g * a.k_sh;
+    const uint16_t* cv = reinterpret_cast<const uint16_t*>(a.v) + b * a.v_sb + g * a.v_sh;
+    const long gbase = ((long)b * G + g);
+    const uint16_t* rk = a.ring_k ? reinterpret_cast<const uint16_t*>(a.ring_k) + gbase * a.W * D : nullptr;
+    const uint16_t* rv = a.ring_v ? reinterpret_cast<const uint16_t*>(a.ring_v) + gbase * a.W * D : nullptr;
+    const int ns = a.n_sinks;
+    const uint16_t* sk = ns ? reinterpret_cast<const uint16_t*>(a.sink_k) + gbase * ns * D : nullptr;
+    const uint16_t* sv = ns ? reinterpret_cast<const uint16_t*>(a.sink_v) + gbase * ns * D : nullptr;
+    const long kp_lo = max((long)a.sinks, p_first - a.W + 1);
+    const int has_sink = ns > 0 ? 1 : 0;
+    const int nwin = kp_lo <= p_last ? (int)((p_last - kp_lo) / FA_KB) + 1 : 0;
+    const int nblk = has_sink + nwin;
+    const int slot_lo = rk ? (int)(kp_lo % a.W) : 0;               // ring slot of kp_lo (one division)
+    const long start = a.start;
+
+    // row `row` of block i: key and value source addresses (an invalid row reads a valid dummy row)
+    auto row_src = [&](int i, int row, const uint16_t*& kr_, const uint16_t*& vr_) {
+        if (has_sink && i == 0) {
+            const int rr = row < ns ? row : 0;
+            kr_ = sk + (long)rr * D;
+            vr_ = sv + (long)rr * D;
+            return;
+        }
+        long kp = kp_lo + (long)(i - has_sink) * FA_KB + row;
+        kp = kp <= p_last ? kp : p_last;
+        if (kp >= start || !rk) {                      // no ring: rows before the chunk read chunk row 0 (masked)
+            const long cr = kp >= start ? kp - start : 0;
+            kr_ = ck + cr * a.k_st;
+            vr_ = cv + cr * a.v_st;
+        } else {
+            int slot = slot_lo + (int)(kp - kp_lo);
+            slot = slot >= a.W ? slot - a.W : slot;
+            kr_ = rk + (long)slot * D;
+            vr_ = rv + (long)slot * D;
+        }
+    };
+    // copy block i's K and V rows into tile t (row r's 16-byte block pb holds the row's block pb ^ sw(r))
+    auto stage = [&](FaTile<D>& t, int i) {
+#pragma unroll
+        for (int j = 0; j < NLD; ++j) {
+            const int c = (wv + NW * j) * 64 + lane;                   // 16-byte slot of the tile
+            const int row = c / NBLK, pb = c % NBLK;
+            const uint16_t *kr_, *vr_;
+            row_src(i, row, kr_, vr_);
+            fa_g2l(kr_ + 8 * (pb ^ fa_swk<NBLK>(row)), reinterpret_cast<char*>(t.k) + (wv + NW * j) * 1024);
+            fa_g2l(vr_ + 8 * (pb ^ fa_swv<NBLK>(row)), reinterpret_cast<char*>(t.v) + (wv + NW * j) * 1024);
+        }
+    };
+    // ring_pos of row `lane` of block i (0 when the row is not a ring row)
+    const rsrc_t rpos = make_rsrc(a.ring_pos, a.ring_pos ? (uint32_t)a.W * 8u : 0u);
+    auto load_rp = [&](int i) {
+        const long kp = kp_lo + (long)(i - has_sink) * FA_KB + lane;
+        int slot = slot_lo + (int)(kp - kp_lo);
+        slot = slot >= a.W ? slot - a.W : slot;
+        const bool ring = rk && !(has_sink && i == 0) && kp < start && kp <= p_last;
+        return buf_ld8(rpos, ring ? (uint32_t)slot * 8u : 0xFFFFFFF0u);
+    };
+    auto valid_row = [&](int i, uint2 rp) {
+        if (has_sink && i == 0) return lane < ns;
+        const long kp = kp_lo + (long)(i - has_sink) * FA_KB + lane;
+        if (kp > p_last) return false;
+        return kp >= start || (rk && (long)(((uint64_t)rp.y << 32) | rp.x) == kp);
+    };
+
+    // ---- per-lane LDS fragment offsets
+    int kbase[NKB];
+    {
+        const int skz = fa_swk<NBLK>(l16);
+#pragma unroll
+        for (int c = 0; c < NKB; ++c) kbase[c] = l16 * ROWB + 64 * (c ^ (skz >> 2)) + 16 * (lg ^ (skz & 3));
+    }
+    int vbase[NVB];
+    {
+        const int e = l16 >> 2, rowl = 4 * lg + e;            // row inside a 16-row group of the tile
+        const int rho = fa_swv<NBLK>(rowl) >> 1;
+#pragma unroll
+        for (int c = 0; c < NVB; ++c)
+            vbase[c] = rowl * ROWB + 32 * (c ^ rho) + 16 * ((l16 & 3) >> 1) + 8 * (l16 & 1);
+    }
+
+    f32x4 o[NDT][QT];
+    float m[QT], l[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        m[qt] = -INFINITY;
+        l[qt] = 0.f;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) o[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const float cs = FA_LOG2E * rsqrtf((float)D);             // score scale in log2 units
+
+    auto compute = [&](const FaTile<D>& t, int i, uint64_t vmask) {
+        const bool sink = has_sink && i == 0;
+        const long kp0 = sink ? 0 : kp_lo + (long)(i - has_sink) * FA_KB;
+        const int cnt = 64 - __builtin_clzll(vmask | 1ull);   // rows up to the last valid one
+        const long kp1 = kp0 + cnt - 1;
+        // this wave's queries see nothing of the block: skip; every row visible to every query: no mask
+        const bool none = nqw == 0 || vmask == 0 || kp0 > qw1 || (!sink && qw0 - kp1 >= a.W);
+        if (none) return;
+        const bool full = vmask == ~0ull && kp1 <= qw0 && (sink || qw1 - kp0 < a.W);
+        const char* Kb = reinterpret_cast<const char*>(t.k);
+        const char* Vb = reinterpret_cast<const char*>(t.v);
+
+        // S^T = K Q^T. K fragments of step kf + 1 are read while step kf multiplies; the scheduling barrier keeps the
+        // compiler from hoisting every step's reads (and their registers) to the front.
+        f32x4 s[4][QT];
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) s[kt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        auto read_k = [&](int kf, uint4 (&ak)[4]) {
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) ak[kt] = lds16(Kb, kbase[kf % NKB] + 16 * kt * ROWB + 256 * (kf / NKB));
+        };
+        uint4 ak[4];
+        read_k(0, ak);
+#pragma unroll
+        for (int kf = 0; kf < NKD; ++kf) {
+            uint4 an[4];
+            if (kf + 1 < NKD) read_k(kf + 1, an);
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) mma<BF16>(s[kt][qt], ak[kt], fq[qt][kf]);
+            if (kf + 1 < NKD) {
+#pragma unroll
+                for (int kt = 0; kt < 4; ++kt) ak[kt] = an[kt];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+
+        // scale (+ mask): element (kt, qt, e) is key row 16 kt + 4 lg + e, query 16 qt + l16 of the wave
+        if (full) {
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) s[kt][qt][e] *= cs;
+        } else {
+            const long dq = qw0 - kp0;
+            const int base = (int)max(min(dq, (long)(1 << 30)), -(long)(1 << 30)) + l16 - 4 * lg;
+            const uint64_t vm = vmask >> (4 * lg);
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int rel = base + 16 * (qt - kt) - e;
+                        const bool vis = ((vm >> (16 * kt + e)) & 1ull) && rel >= 0 && (sink || rel < a.W);
+                        s[kt][qt][e] = vis ? s[kt][qt][e] * cs : -INFINITY;
+                    }
+        }
+
+        // online softmax (lazy max)
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            float bm = s[0][qt][0];
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) bm = fmaxf(bm, s[kt][qt][e]);
+            bm = fmaxf(bm, __shfl_xor(bm, 16));
+            bm = fmaxf(bm, __shfl_xor(bm, 32));
+            const bool up = bm > m[qt] + FA_SLACK;
+            if (__builtin_amdgcn_ballot_w64(up)) {
+                const float mn = up ? bm : m[qt];
+                const float corr = __builtin_amdgcn_exp2f(m[qt] - mn);   // 0 when m was -inf, 1 without update
+                m[qt] = mn;
+                l[qt] *= corr;
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+                    o[dt][qt][0] *= corr; o[dt][qt][1] *= corr; o[dt][qt][2] *= corr; o[dt][qt][3] *= corr;
+                }
+            }
+            const float msub = m[qt] == -INFINITY ? 0.f : m[qt];
+            float ls = 0.f;
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float p = __builtin_amdgcn_exp2f(s[kt][qt][e] - msub);
+                    s[kt][qt][e] = p;
+                    ls += p;
+                }
+            l[qt] += ls;
+        }
+
+        // O^T += V^T P^T; P fragment f holds keys {32 f + 4 lg + e} (tile 2f) and {32 f + 16 + 4 lg + e} (tile 2f+1)
+#pragma unroll
+        for (int f = 0; f < 2; ++f) {
+            uint4 pb[QT];
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+                const f32x4 x0 = s[2 * f][qt], x1 = s[2 * f + 1][qt];
+                pb[qt] = make_uint4(pack_bf16x2(x0[0], x0[1]), pack_bf16x2(x0[2], x0[3]), pack_bf16x2(x1[0], x1[1]),
+                                    pack_bf16x2(x1[2], x1[3]));
+            }
+            // V^T fragments are read VPF tiles ahead of their MFMAs
+            constexpr int VPF = 4;
+            auto read_v = [&](int dt) {
+                const char* p = Vb + vbase[dt % NVB] + 32 * f * ROWB + 256 * (dt / NVB);
+                const uint2 lo = fa_tr16(p), hi = fa_tr16(p + 16 * ROWB);
+                return make_uint4(lo.x, lo.y, hi.x, hi.y);
+            };
+            uint4 vr[VPF];
+#pragma unroll
+            for (int q = 0; q < VPF - 1; ++q) vr[q] = read_v(q);
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                if (dt + VPF - 1 < NDT) vr[(dt + VPF - 1) % VPF] = read_v(dt + VPF - 1);
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) mma<BF16>(o[dt][qt], vr[dt % VPF], pb[qt]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
+
+    // ---- main loop over key blocks, two tiles in turn. The next block is staged unconditionally (the last block
+    // re-stages itself into the idle tile), so the compiler's wait counts never drain it before the current compute.
+    uint2 rp = load_rp(0);
+    stage(t0, 0);
+    auto step = [&](FaTile<D>& tc, FaTile<D>& tn, int i) {
+        wait_vmem_all();
+        __syncthreads();                                   // block i is in tc; every wave is done with tn
+        const uint64_t vmask = __builtin_amdgcn_ballot_w64(valid_row(i, rp));
+        const int inext = i + 1 < nblk ? i + 1 : i;
+        rp = load_rp(inext);
+        stage(tn, inext);
+        compute(tc, i, vmask);
+    };
+    for (int i = 0;;) {
+        step(t0, t1, i);
+        if (++i >= nblk) break;
+        step(t1, t0, i);
+        if (++i >= nblk) break;
+    }
+    wait_vmem_all();                                       // the last (redundant) stage has landed before exit
+
+    // ---- epilogue: row sums, normalise, lse (natural log), gamma mix, store o [B][T][H][D]
+    const float lnW = logf((float)a.W);
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+        float lt = l[qt];
+        lt += __shfl_xor(lt, 16);
+        lt += __shfl_xor(lt, 32);
+        const int qi = QW * wv + 16 * qt + l16;
+        if (qi >= nq) continue;
+        const long tq = qi0 + qi;
+        const float inv = 1.f / lt;
+        const float lse = (m[qt] + __log2f(lt)) * FA_LN2;
+        if (a.lse && lg == 0) a.lse[((long)b * H + h) * a.T + tq] = lse;
+        float gam = 0.f;
+        if (a.mix_on && p_first + qi >= a.W)
+            gam = 1.f / (1.f + __expf(-(a.z[((long)b * a.T + tq) * H + h] + a.mix_lse[h] * (lse - lnW))));
+        const float ms = a.mix_on ? a.mem_scale[h] : 0.f;
+        const long orow = (((long)b * a.T + tq) * H + h) * D;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+            const int d0 = 16 * dt + 4 * lg;
+            float r4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r4[e] = o[dt][qt][e] * inv;
+            if (gam != 0.f) {
+                const float4 om = *reinterpret_cast<const float4*>(a.o_mem + orow + d0);
+                r4[0] += gam * (ms * om.x - r4[0]);
+                r4[1] += gam * (ms * om.y - r4[1]);
+                r4[2] += gam * (ms * om.z - r4[2]);
+                r4[3] += gam * (ms * om.w - r4[3]);
+            }
+            if constexpr (BO) store4<BF16>(reinterpret_cast<uint16_t*>(a.o) + orow + d0, r4[0], r4[1], r4[2], r4[3]);
+            else store4<F32>(reinterpret_cast<float*>(a.o) + orow + d0, r4[0], r4[1], r4[2], r4[3]);
+        }
+    }
+}
+
+namespace {
+
+template <int D>
+int launch_window_fa(const WinArgs& a, hipStream_t stream) {
+    const long nqb = (a.T + FA_BQ - 1) / FA_BQ;
+    const long nwork = (long)a.B * a.G * nqb * a.R;
+    const long per = (nwork + FA_NXCD - 1) / FA_NXCD;
+    if (FA_NXCD * per > 0x7fffffffL) return BF_STATUS_INVALID;
+    const dim3 grid((unsigned)(FA_NXCD * per)), block(FaShape<D>::NT);
+    if (a.o_dtype == DT_BF16) hipLaunchKernelGGL((window_fa_kernel<D, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((window_fa_kernel<D, false>), grid, block, 0, stream, a);
+    const hipError_t e = hipGetLastError();
+    return e == hipSuccess ? 0 : (int)e;
+}
+
+}  // namespace
+
+int window_fa_dispatch(const WinArgs& a, hipStream_t stream) {
+    switch (a.D) {
+        case 64: return launch_window_fa<64>(a, stream);
+        case 128: return launch_window_fa<128>(a, stream);
+        case 256: return launch_window_fa<256>(a, stream);
+        default: return BF_ERR_UNSUPPORTED;
+    }
+}
+
+}  // namespace bf

@@ -124,6 +124,18 @@ struct WinArgs {
 };
 
 int window_dispatch(const WinArgs& a, hipStream_t stream);
+
+struct MemProjArgs {
+    const void* x;            // bf16 rows: token t, head h at x + t * x_st + h * x_sh (elements), D contiguous
+    long n_tok;
+    int nh, D;
+    long x_st, x_sh;
+    const void* ft;           // [nh][D][D] bf16, F_h transposed: ft[h][j][i] = F_h[i][j]
+    float scale;
+    void* out;                // [n_tok][nh][D] bf16
+};
+
+int mem_project_dispatch(const MemProjArgs& a, hipStream_t stream);
 int window_fa_dispatch(const WinArgs& a, hipStream_t stream);   // bf16 operands
 
 }  // namespace bf

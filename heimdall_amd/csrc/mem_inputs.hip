@@ -1,0 +1,117 @@
+// Memory-branch read/write keys of the converted layer (reference: HybridAttention._mem_inputs,
+// Heimdall/heimdall/hibrit.py:327-334):
+//   y_{t,h} = scale * normalize(x_{t,h} F_h),   normalize(u) = u / max(||u||_2, 1e-12)
+// used for qm (x = q, F = fq, scale = D^-1/2) and km (x = k, F = fk, scale = 1), for bf16 activations.
+//
+// One workgroup owns one head h and a strided set of 64-token tiles. F_h^T (D x D bf16, 128 KB at D = 256) is staged
+// in LDS once; each of the 4 waves computes 16 tokens x D outputs per tile as Y^T = F_h^T X^T with
+// v_mfma_f32_16x16x32_bf16 (A = rows of F_h^T from LDS, B = the token rows of x from global memory, loaded one tile
+// ahead), so every lane holds 4 consecutive outputs of one token: the row norm is a sum over the lane's values and
+// two cross-lane steps, and the bf16 result is stored 8 bytes at a time.
+#include "bf_common.h"
+#include "bf_internal.h"
+
+namespace bf {
+
+namespace {
+
+constexpr int MP_WAVES = 4;
+constexpr int MP_TILE = 16 * MP_WAVES;       // tokens per tile
+
+template <int NBLK>
+__device__ __forceinline__ int mp_sw(int row) { return NBLK >= 16 ? (row & 15) : ((row >> 1) & 7); }
+
+}  // namespace
+
+template <int D>
+__global__ __launch_bounds__(64 * MP_WAVES, 1) void mem_project_kernel(MemProjArgs a) {
+    constexpr int ROWB = D * 2, NBLK = ROWB / 16;
+    constexpr int NKD = D / 32, NDT = D / 16;
+    constexpr int NKB = NKD < 4 ? NKD : 4;
+    __shared__ __align__(16) uint16_t ft[D * D];
+
+    const int h = blockIdx.x % a.nh, tg = blockIdx.x / a.nh, ntg = gridDim.x / a.nh;
+    const int lane = lane_id(), wv = wave_id(), l16 = lane & 15, lg = lane >> 4;
+
+    // stage F_h^T: LDS row j holds row j of F_h^T with its 16-byte blocks permuted by mp_sw(j)
+    const rsrc_t rf = make_rsrc(reinterpret_cast<const uint16_t*>(a.ft) + (long)h * D * D, (uint32_t)(D * ROWB));
+    stage_tile(rf, (uint32_t)ROWB, ROWB, ft, D * ROWB, wv, MP_WAVES, lane, [](int row) { return mp_sw<NBLK>(row); },
+               NBLK);
+
+    int abase[NKB];
+    {
+        const int s = mp_sw<NBLK>(l16);
+#pragma unroll
+        for (int c = 0; c < NKB; ++c) abase[c] = l16 * ROWB + 64 * (c ^ (s >> 2)) + 16 * (lg ^ (s & 3));
+    }
+    const char* Fb = reinterpret_cast<const char*>(ft);
+    const uint16_t* X = reinterpret_cast<const uint16_t*>(a.x) + (long)h * a.x_sh;
+    uint16_t* Out = reinterpret_cast<uint16_t*>(a.out);
+
+    const long ntiles = (a.n_tok + MP_TILE - 1) / MP_TILE;
+    // B fragments of token 16 wv + l16 of tile t: x[token][32 ks + 8 lg .. +7]
+    auto load_x = [&](long t, uint4 (&xf)[NKD]) {
+        const rsrc_t rx = make_rsrc(X + (t * MP_TILE + 16 * wv) * a.x_st,
+                                    t < ntiles ? (uint32_t)(max(0L, min((long)16, a.n_tok - (t * MP_TILE + 16 * wv))) *
+                                                            a.x_st * 2) : 0u);
+#pragma unroll
+        for (int ks = 0; ks < NKD; ++ks)
+            xf[ks] = buf_ld16(rx, (uint32_t)((l16 * a.x_st + 32 * ks + 8 * lg) * 2));
+    };
+    uint4 xf[NKD];
+    load_x(tg, xf);
+    wait_vmem_all();
+    __syncthreads();
+
+    for (long t = tg; t < ntiles; t += ntg) {
+        uint4 xn[NKD];
+        load_x(t + ntg, xn);                        // next tile (out of range: reads zero)
+        f32x4 acc[NDT];
+#pragma unroll
+        for (int jt = 0; jt < NDT; ++jt) acc[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < NKD; ++ks) {
+#pragma unroll
+            for (int jt = 0; jt < NDT; ++jt)
+                mma<BF16>(acc[jt], lds16(Fb, abase[ks % NKB] + 16 * jt * ROWB + 256 * (ks / NKB)), xf[ks]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int jt = 0; jt < NDT; ++jt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) ss += acc[jt][i] * acc[jt][i];
+        ss += __shfl_xor(ss, 16);
+        ss += __shfl_xor(ss, 32);
+        const float inv = a.scale / fmaxf(sqrtf(ss), 1e-12f);
+        const long tok = t * MP_TILE + 16 * wv + l16;
+        if (tok < a.n_tok) {
+            uint16_t* orow = Out + (tok * a.nh + h) * D;
+#pragma unroll
+            for (int jt = 0; jt < NDT; ++jt) {
+                uint2 v;
+                v.x = pack_bf16x2(acc[jt][0] * inv, acc[jt][1] * inv);
+                v.y = pack_bf16x2(acc[jt][2] * inv, acc[jt][3] * inv);
+                *reinterpret_cast<uint2*>(orow + 16 * jt + 4 * lg) = v;
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < NKD; ++ks) xf[ks] = xn[ks];
+    }
+}
+
+int mem_project_dispatch(const MemProjArgs& a, hipStream_t stream) {
+    const long ntiles = (a.n_tok + MP_TILE - 1) / MP_TILE;
+    const long want = (512 + a.nh - 1) / a.nh;                  // ~512 workgroups over all heads
+    const int ntg = (int)(ntiles < want ? ntiles : want);
+    const dim3 grid((unsigned)(a.nh * (ntg > 0 ? ntg : 1))), block(64 * MP_WAVES);
+    switch (a.D) {
+        case 64: hipLaunchKernelGGL(mem_project_kernel<64>, grid, block, 0, stream, a); break;
+        case 128: hipLaunchKernelGGL(mem_project_kernel<128>, grid, block, 0, stream, a); break;
+        case 256: hipLaunchKernelGGL(mem_project_kernel<256>, grid, block, 0, stream, a); break;
+        default: return BF_ERR_UNSUPPORTED;
+    }
+    return (int)hipGetLastError();
+}
+
+}  // namespace bf

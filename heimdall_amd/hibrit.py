@@ -61,6 +61,30 @@ def mem_inputs(self, x, q, k, pos):
     return qm, km, g, beta
 
 
+def _project_bf16(x: torch.Tensor, f: torch.Tensor, scale: float) -> torch.Tensor:
+    """bf16 x [B, t, nh, D] -> scale * normalize(x_h f_h) as bf16 [B, t, nh, D] on bf_mem_project."""
+    b, t, nh, d = x.shape
+    if x.stride(-1) != 1 or (b > 1 and x.stride(0) != t * x.stride(1)):
+        x = x.contiguous()
+    ft = f.detach().transpose(1, 2).to(torch.bfloat16).contiguous()
+    out = torch.empty(b, t, nh, d, dtype=torch.bfloat16, device=x.device)
+    check(_lib.load().bf_mem_project(x.data_ptr(), b * t, nh, d, x.stride(1), x.stride(2), ft.data_ptr(), float(scale),
+                                     out.data_ptr(), _lib.DTYPE_BF16, stream_ptr(x.device)), "bf_mem_project")
+    return out
+
+
+def _mem_inputs_bf16(self, xf, q, k, pos):
+    """mem_inputs for bf16 activations: qm, km from the fused projection kernel (bf16 out, fp32 accumulation and
+    norm), the gates g, beta in fp32 from xf = x in fp32 (``hibrit.py:327-334``)."""
+    dh = self.c.dh
+    qm = _project_bf16(q, self.fq, dh ** -0.5)
+    km = _project_bf16(k, self.fk, 1.0)
+    a, bb = F.linear(xf, self.ab.weight.float(), self.ab.bias.float()).chunk(2, dim=-1)
+    g = -self.A_log.float().exp() * F.softplus(a + self.dt_bias.float()) * self.decay_mask.float()
+    beta = torch.sigmoid(bb) * (pos >= self.sinks).float()[None, :, None]
+    return qm, km, g, beta
+
+
 def _new_ring(b, G, w, D, kdt, vdt, dev):
     return dict(ring_k=torch.zeros(b, G, w, D, dtype=kdt, device=dev),
                 ring_v=torch.zeros(b, G, w, D, dtype=vdt, device=dev),
@@ -135,14 +159,19 @@ def student(self, x, q, k, v, qr, kr, start: int, cache: Optional[dict], memory:
     if n_new:
         sink_k = kr[:, :, :n_new] if sink_k is None else torch.cat((sink_k, kr[:, :, :n_new]), 2)
         sink_v = vt[:, :, :n_new] if sink_v is None else torch.cat((sink_v, vt[:, :, :n_new]), 2)
-    qm, km, g, beta = self._mem_inputs(x, q, k, pos)
+    xf = None
+    if t > 1 and all(z.dtype == torch.bfloat16 for z in (q, k, qr, kr)):
+        xf = x.float()
+        qm, km, g, beta = _mem_inputs_bf16(self, xf, q, k, pos)
+    else:
+        qm, km, g, beta = self._mem_inputs(x, q, k, pos)
     if "ring_k" not in st:
         st.update(_new_ring(b, c.hkv, w, c.dh, kr.dtype, vt.dtype, dev))
     if t == 1:
         o = _decode(self, x, qr, kr[:, :, 0], v[:, 0], qm[:, 0], km[:, 0], g[:, 0], beta[:, 0], start, st, sink_k,
                     sink_v, memory)
     else:
-        o = _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memory)
+        o = _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memory, xf)
     st["sink_k"], st["sink_v"] = sink_k, sink_v
     return o
 
@@ -151,10 +180,14 @@ def _strides(t: torch.Tensor, dims):
     return tuple(int(t.stride(d)) for d in dims)
 
 
-def _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memory):
+def _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memory, xf=None):
     """A chunk of t > 1 tokens: memory branch on bf_gdn_fwd (write stream = ring rows leaving the window, then the
     chunk's own rows, hibrit.py:391-408), then bf_window_fwd with the gamma mix fused (hibrit.py:385-411), then the
-    ring / sink / state write-back (hibrit.py:412-423)."""
+    ring / sink / state write-back (hibrit.py:412-423).
+
+    From an empty cache (start 0, no state) the write stream of query i is token i - W of the chunk itself and the
+    queries before W never read the memory (gamma is 0 there), so the memory branch runs on views: queries W..t-1
+    against the writes of tokens 0..t-W-1."""
     c = self.c
     b, t = x.shape[:2]
     H, G, D, w, r = c.h, c.hkv, c.dh, self.window, c.h // c.hkv
@@ -164,7 +197,17 @@ def _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, mem
     pos = torch.arange(start, start + t, device=dev)
     use_mem = memory and start + t > w
     o_mem = z = None
-    if use_mem:
+    s0 = st.get("S") if use_mem else None
+    if use_mem and start == 0 and s0 is None:
+        n = t - w
+        sl = lambda z, a_, e_: z[:, a_:e_].reshape(b * (e_ - a_), *z.shape[2:])
+        o_mem = torch.empty(b, t, H, D, dtype=torch.float32, device=dev)      # rows < W are never read
+        om, s_new = gdn_forward(sl(qm, w, t).to(cdt), sl(km, 0, n).to(cdt), sl(v, 0, n).to(cdt), sl(g, 0, n),
+                                sl(beta, 0, n), num_seqs=b, out=o_mem[0, w:] if b == 1 else None)
+        if b > 1:
+            o_mem[:, w:] = om.view(b, n, H, D)
+        z = F.linear(xf if xf is not None else x.float(), self.mix.weight.float(), self.mix.bias.float()).contiguous()
+    elif use_mem:
         # write stream: token i - W is written before the query at position i reads (ext[:t] of the reference)
         pp = torch.arange(start - w, start, device=dev)
         idx = pp % w
@@ -173,12 +216,11 @@ def _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, mem
         wv = torch.cat((st["ring_v"][:, :, idx].transpose(1, 2).float(), v.float()), 1)[:, :t]
         wg = torch.cat((st["ring_g"][:, idx] * vf, g), 1)[:, :t]
         wb = torch.cat((st["ring_beta"][:, idx] * vf, beta), 1)[:, :t]
-        s0 = st.get("S")
         o_mem, s_new = gdn_forward(qm.to(cdt).reshape(b * t, H, D), wk.to(cdt).reshape(b * t, G, D),
                                    wv.to(cdt).reshape(b * t, G, D), wg.reshape(b * t, G), wb.reshape(b * t, G),
                                    num_seqs=b, initial_state=None if s0 is None else s0.float())
         o_mem = o_mem.view(b, t, H, D)
-        z = F.linear(x.float(), self.mix.weight.float(), self.mix.bias.float()).contiguous()
+        z = F.linear(xf if xf is not None else x.float(), self.mix.weight.float(), self.mix.bias.float()).contiguous()
     # window + sinks + LSE (+ mix)
     q_ = qr.to(cdt)
     q_ = q_ if q_.stride(-1) == 1 else q_.contiguous()

@@ -67,3 +67,31 @@ def test_production_geometry_bf16(dev):
             print(f"  chunk {a}:{e} rel err {rel(o, o_ref):.2e}", flush=True)
             assert rel(o, o_ref) < TOL_BF16
     assert rel(c_gpu["S"], c_ref["S"]) < TOL_BF16
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+def test_mem_inputs_bf16_fused_projection(dev, d):
+    """bf_mem_project (qm, km of _mem_inputs for bf16 activations) against the oracle's fp32 mem_inputs with trained-
+    like projections (identity + noise) on the same bf16 values; strided q (a [B, T, H, D] view of a wider tensor),
+    B = 2, a token count that is not a multiple of the 64-token tile."""
+    from heimdall_amd import hibrit
+    print(f"mem_inputs bf16 fused projection D={d}", flush=True)
+    m = make_core(6, 2, d, 32, window=16, sinks=2)
+    mg = make_core(6, 2, d, 32, window=16, sinks=2).to(dev)
+    b, t = 2, 157
+    gen = torch.Generator().manual_seed(21)
+    x = torch.randn(b, t, 32, generator=gen)
+    qw = torch.randn(b, t, 8, d, generator=gen).bfloat16()
+    q = qw[:, :, 1:7]                                      # strided head view
+    k = torch.randn(b, t, 2, d, generator=gen).bfloat16()
+    pos = torch.arange(t)
+    qm_ref, km_ref, g_ref, b_ref = olayer.mem_inputs(m, x, q.float(), k.float(), pos)
+    with torch.no_grad():
+        qm, km, g, beta = hibrit._mem_inputs_bf16(mg, x.to(dev), q.to(dev), k.to(dev), pos.to(dev))
+    assert qm.dtype == km.dtype == torch.bfloat16
+    for got, ref in ((qm, qm_ref), (km, km_ref), (g, g_ref), (beta, b_ref)):
+        assert rel(got, ref) < TOL_BF16, rel(got, ref)
+    print(f"  rel qm={rel(qm, qm_ref):.2e} km={rel(km, km_ref):.2e}", flush=True)
+    # rows are unit vectors times the scale
+    nq = qm.float().norm(dim=-1).cpu()
+    assert torch.allclose(nq, torch.full_like(nq, d ** -0.5), rtol=1e-2)

@@ -13,8 +13,11 @@
 // ring_g, ring_beta [B][W][G] f32; ring_pos [W] int64; sinks [B][G][ns][D]; qr, qm, o [B][H][D]; kr, v, km [B][G][D].
 //
 // Kernels:
-//   decode_main    grid (max(D/32, W/256 splits), G, B): state slab x (32 columns) and window split x (256 slots)
-//   decode_combine grid (G, B): merge the window splits, gamma mix, ring write
+//   decode_slab    grid (D/32, G, B): state slab x (32 columns): memory write of the evicted row, memory read
+//   decode_main    grid (W/256, G, B): window split x (256 ring slots; split 0 also takes the sinks and new token)
+//   decode_combine grid (R, G, B): merge the window splits, gamma mix, ring write
+// The slab and window kernels are launched one after the other: run as one grid, their mixed workgroups took
+// longer than the two launches together.
 //   gdn_step       grid (D/32, G, B): the state slab pass alone (delta_rule_step)
 #include "bf_common.h"
 #include "bf_internal.h"
@@ -144,7 +147,6 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
     constexpr int RMAX = RM;                    // query heads per KV head this instance supports (R <= RM)
     constexpr int LPS = D / 16;                 // lanes per key slot (16 dims each)
     constexpr int SPW = 64 / LPS;               // slots per wave per iteration
-    __shared__ float red[4 * 8 * RMAX * 4];
     __shared__ float sc[RMAX][SLOTS + 64];      // scores, then probabilities (ring slots + sinks + new token)
     __shared__ float part[4][RMAX][D];          // per-wave PV partials
     __shared__ float mx[RMAX], sm[RMAX];
@@ -154,27 +156,7 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const long bg = (long)b * G + g;
 
-    // ---- state slab x (memory branch)
-    if (a.mem_on && x < D / SCOL) {
-        const int slot = (int)(a.pos % W);
-        const long pe = a.pos - W;
-        const bool valid = pe >= 0 && a.ring_pos[slot] == pe;
-        const float* wk = a.ring_km + (((long)b * W + slot) * G + g) * D;
-        // evicted value row (kv dtype) -> fp32 in shared scratch
-        __shared__ float vrow[D];
-        const T* rv = reinterpret_cast<const T*>(a.ring_v) + (bg * W + slot) * D;
-        for (int d = tid; d < D; d += NT_DEC) vrow[d] = KV::to_f(rv[d]);
-        __syncthreads();
-        const float wg = valid ? a.ring_g[((long)b * W + slot) * G + g] : 0.f;
-        const float wb = valid ? a.ring_beta[((long)b * W + slot) * G + g] : 0.f;
-        float* S = a.state + bg * D * D;
-        state_slab<D, RM>(S, S, wk, vrow, wg, wb, valid, a.qm + ((long)b * H + g * R) * D, R, D,
-                      a.ws_om + ((long)b * H + g * R) * D, D, x * SCOL, red);
-    }
-
     // ---- window split x
-    const int nsplit = (W + SLOTS - 1) / SLOTS;
-    if (x >= nsplit) return;
     const int s0 = x * SLOTS, s1 = min(W, s0 + SLOTS);
     const int nring = s1 - s0;
     const int nextra = x == 0 ? a.n_sinks + 1 : 0;      // sinks and the new token ride on split 0
@@ -183,19 +165,6 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
     const long lo = max((long)a.sinks, a.pos - W + 1);  // oldest visible window position
 
     const int sl = lane / LPS, dl = (lane % LPS) * 16;  // slot within the wave step, dims dl..dl+15
-    float q[RMAX][16];
-#pragma unroll
-    for (int r = 0; r < RMAX; ++r) {
-        if (r < R) {
-            if (a.q_dtype == DT_BF16) ld16f<BF16>(reinterpret_cast<const uint16_t*>(a.qr) + ((long)b * H + g * R + r) * D + dl, q[r]);
-            else ld16f<F32>(reinterpret_cast<const float*>(a.qr) + ((long)b * H + g * R + r) * D + dl, q[r]);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) q[r][i] *= scale;
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) q[r][i] = 0.f;
-        }
-    }
     const T* RK = reinterpret_cast<const T*>(a.ring_k) + bg * W * D;
     const T* RV = reinterpret_cast<const T*>(a.ring_v) + bg * W * D;
     const T* SK = reinterpret_cast<const T*>(a.sink_k) + bg * a.n_sinks * D;
@@ -218,29 +187,112 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
         return a.pos >= a.sinks;
     };
 
-    // scores
-    for (int k0 = wv * SPW; k0 < nkeys; k0 += 4 * SPW) {
-        const int k = k0 + sl;
-        float d[RMAX];
+    // Scores. bf16: MFMA, S^T = K Q^T with 16-key groups of K rows straight from global memory as A fragments and the
+    // R query heads as the first R columns of the B fragment (no cross-lane reduction). fp32: a lane-parallel dot
+    // product over the LPS lanes of a slot.
+    if constexpr (sizeof(T) == 2) {
+        constexpr int NKD = D / 32;
+        const int l16 = lane & 15, lg = lane >> 4;
+        uint4 qf[NKD];
+        {
+            const int r = l16 < R ? l16 : 0;
+            const long qrow = ((long)b * H + g * R + r) * D;
 #pragma unroll
-        for (int r = 0; r < RMAX; ++r) d[r] = 0.f;
-        if (k < nkeys) {
+            for (int ks = 0; ks < NKD; ++ks) {
+                uint4 v = zero16();
+                if (l16 < R) {
+                    if (a.q_dtype == DT_BF16) {
+                        v = ld16(reinterpret_cast<const uint16_t*>(a.qr) + qrow + 32 * ks + 8 * lg);
+                    } else {
+                        const float* qp = reinterpret_cast<const float*>(a.qr) + qrow + 32 * ks + 8 * lg;
+                        v = make_uint4(pack_bf16x2(qp[0], qp[1]), pack_bf16x2(qp[2], qp[3]),
+                                       pack_bf16x2(qp[4], qp[5]), pack_bf16x2(qp[6], qp[7]));
+                    }
+                }
+                qf[ks] = v;
+            }
+        }
+        // ring keys: two 16-key groups per wave iteration (addresses past the last ring key clamped to it)
+        const int ngrp = (nring + 15) / 16;
+        const uint16_t* rk16 = reinterpret_cast<const uint16_t*>(RK) + (long)s0 * D + 8 * lg;
+        for (int t0 = wv; t0 < ngrp; t0 += 8) {
+            uint4 ka[2][NKD];
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int key = min(16 * (t0 + 4 * u) + l16, nring - 1);
+#pragma unroll
+                for (int ks = 0; ks < NKD; ++ks) ka[u][ks] = ld16(rk16 + (long)key * D + 32 * ks);
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int t = t0 + 4 * u;
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < NKD; ++ks) mma<BF16>(acc, ka[u][ks], qf[ks]);
+                if (t < ngrp && l16 < R) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int k = 16 * t + 4 * lg + i;
+                        if (k < nring) sc[l16][k] = visible(k) ? acc[i] * scale : -INFINITY;
+                    }
+                }
+            }
+        }
+        // extra keys of split 0 (sinks, new token), wave 0, 16 at a time
+        if (nextra > 0 && wv == 0) {
+            for (int e0 = 0; e0 < nextra; e0 += 16) {
+                const int k = nring + min(e0 + l16, nextra - 1);
+                const uint16_t* row = reinterpret_cast<const uint16_t*>(key_row(k, RK, SK, NK)) + 8 * lg;
+                uint4 kx[NKD];
+#pragma unroll
+                for (int ks = 0; ks < NKD; ++ks) kx[ks] = ld16(row + 32 * ks);
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int ks = 0; ks < NKD; ++ks) mma<BF16>(acc, kx[ks], qf[ks]);
+                if (l16 < R) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int ke = nring + e0 + 4 * lg + i;
+                        if (ke < nkeys) sc[l16][ke] = visible(ke) ? acc[i] * scale : -INFINITY;
+                    }
+                }
+            }
+        }
+    } else {
+        float q[RMAX][16];
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r) {
+            if (r < R) {
+                if (a.q_dtype == DT_BF16) ld16f<BF16>(reinterpret_cast<const uint16_t*>(a.qr) + ((long)b * H + g * R + r) * D + dl, q[r]);
+                else ld16f<F32>(reinterpret_cast<const float*>(a.qr) + ((long)b * H + g * R + r) * D + dl, q[r]);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) q[r][i] *= scale;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) q[r][i] = 0.f;
+            }
+        }
+        for (int k0 = wv * SPW; k0 < nkeys; k0 += 4 * SPW) {
+            const int k = k0 + sl;
             float kv[16];
-            ld16f<KV>(key_row(k, RK, SK, NK) + dl, kv);
+            ld16f<KV>(key_row(min(k, nkeys - 1), RK, SK, NK) + dl, kv);
+            float d[RMAX];
 #pragma unroll
-            for (int r = 0; r < RMAX; ++r)
+            for (int r = 0; r < RMAX; ++r) {
+                d[r] = 0.f;
 #pragma unroll
                 for (int i = 0; i < 16; ++i) d[r] += q[r][i] * kv[i];
-        }
-#pragma unroll
-        for (int r = 0; r < RMAX; ++r)
-#pragma unroll
-            for (int off = 1; off < LPS; off <<= 1) d[r] += __shfl_xor(d[r], off);
-        if (k < nkeys && (lane % LPS) == 0) {
-            const bool vis = visible(k);
+            }
 #pragma unroll
             for (int r = 0; r < RMAX; ++r)
-                if (r < R) sc[r][k] = vis ? d[r] : -INFINITY;
+#pragma unroll
+                for (int off = 1; off < LPS; off <<= 1) d[r] += __shfl_xor(d[r], off);
+            if (k < nkeys && (lane % LPS) == 0) {
+                const bool vis = visible(k);
+#pragma unroll
+                for (int r = 0; r < RMAX; ++r)
+                    if (r < R) sc[r][k] = vis ? d[r] : -INFINITY;
+            }
         }
     }
     __syncthreads();
@@ -267,17 +319,37 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
     for (int r = 0; r < RMAX; ++r)
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[r][i] = 0.f;
-    for (int k0 = wv * SPW; k0 < nkeys; k0 += 4 * SPW) {
-        const int k = k0 + sl;
-        if (k < nkeys) {
-            float vv[16];
-            ld16f<KV>(key_row(k, RV, SV, NV) + dl, vv);
+    // ring keys: U slot steps per wave iteration, every lane's U rows loaded before use (addresses past the last
+    // ring key are clamped to it and their probabilities taken as zero)
+    constexpr int U = RM <= 4 ? 4 : 2;
+    for (int k0 = wv * SPW * U; k0 < nring; k0 += 4 * SPW * U) {
+        float vv[U][16];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int k = min(k0 + u * SPW + sl, nring - 1);
+            ld16f<KV>(RV + (long)(s0 + k) * D + dl, vv[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int k = k0 + u * SPW + sl;
 #pragma unroll
             for (int r = 0; r < RMAX; ++r) {
-                const float p = r < R ? sc[r][k] : 0.f;
+                const float p = (r < R && k < nring) ? sc[r][k < nring ? k : 0] : 0.f;
 #pragma unroll
-                for (int i = 0; i < 16; ++i) acc[r][i] += p * vv[i];
+                for (int i = 0; i < 16; ++i) acc[r][i] += p * vv[u][i];
             }
+        }
+    }
+    // extra keys of split 0 (sinks, new token)
+    for (int k0 = nring + wv * SPW; k0 < nkeys; k0 += 4 * SPW) {
+        const int k = k0 + sl;
+        float vv[16];
+        ld16f<KV>(key_row(min(k, nkeys - 1), RV, SV, NV) + dl, vv);
+#pragma unroll
+        for (int r = 0; r < RMAX; ++r) {
+            const float p = (r < R && k < nkeys) ? sc[r][k < nkeys ? k : 0] : 0.f;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[r][i] += p * vv[i];
         }
     }
     // reduce over the SPW slot groups of the wave (lanes with equal lane % LPS), then over the 4 waves
@@ -308,29 +380,68 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
     }
 }
 
+// State slab x (32 columns) of (b, g): the write of the ring row leaving the window, then the memory read of the
+// R query heads into ws_om.
+template <class KV, int D, int RM>
+__global__ __launch_bounds__(NT_DEC) void decode_slab_kernel(DecodeArgs a) {
+    using T = typename KV::T;
+    __shared__ float red[4 * 8 * RM * 4];
+    __shared__ float vrow[D];
+    const int x = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+    const int G = a.G, R = a.R, H = G * R, W = a.W;
+    const int tid = threadIdx.x;
+    const long bg = (long)b * G + g;
+    const int slot = (int)(a.pos % W);
+    const long pe = a.pos - W;
+    const bool valid = pe >= 0 && a.ring_pos[slot] == pe;
+    const float* wk = a.ring_km + (((long)b * W + slot) * G + g) * D;
+    // evicted value row (kv dtype) -> fp32 in shared scratch
+    const T* rv = reinterpret_cast<const T*>(a.ring_v) + (bg * W + slot) * D;
+    for (int d = tid; d < D; d += NT_DEC) vrow[d] = KV::to_f(rv[d]);
+    __syncthreads();
+    const float wg = valid ? a.ring_g[((long)b * W + slot) * G + g] : 0.f;
+    const float wb = valid ? a.ring_beta[((long)b * W + slot) * G + g] : 0.f;
+    float* S = a.state + bg * D * D;
+    state_slab<D, RM>(S, S, wk, vrow, wg, wb, valid, a.qm + ((long)b * H + g * R) * D, R, D,
+                      a.ws_om + ((long)b * H + g * R) * D, D, x * SCOL, red);
+}
+
+// Merge of the window splits for query head r of (b, g): one output dimension per thread; the split statistics are
+// read once into LDS. Then the gamma mix and, by the r == 0 block, the ring write of the new token.
 template <class KV, int D>
 __global__ __launch_bounds__(NT_DEC) void decode_combine_kernel(DecodeArgs a) {
     using T = typename KV::T;
-    const int g = blockIdx.x, b = blockIdx.y;
+    constexpr int MAXS = 64;                            // window splits held in LDS (W <= 16384)
+    __shared__ float fs[MAXS];
+    __shared__ float stat[2];
+    const int r = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
     const int G = a.G, R = a.R, H = G * R, W = a.W, NS = a.nsplit;
     const int tid = threadIdx.x;
     const long bg = (long)b * G + g;
+    const int h = g * R + r;
     const float* part = a.ws_part + bg * NS * R * (D + 2);
+    if (tid < 64) {
+        // wave 0: M = max over splits, f_s = e^{m_s - M}, L = sum f_s l_s
+        const float ms = tid < NS ? part[(tid * R + r) * (D + 2)] : -INFINITY;
+        const float ls = tid < NS ? part[(tid * R + r) * (D + 2) + 1] : 0.f;
+        float M = ms;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
+        const float f = ms == -INFINITY ? 0.f : __expf(ms - M);
+        float L = f * ls;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
+        if (tid < NS) fs[tid] = f;
+        if (tid == 0) { stat[0] = M; stat[1] = L; }
+    }
+    __syncthreads();
+    const float M = stat[0], L = stat[1];
+    const float lse = M + logf(L);
     const float lnW = logf((float)W);
-    for (int idx = tid; idx < R * D; idx += NT_DEC) {
-        const int r = idx / D, d = idx % D;
-        float M = -INFINITY;
-        for (int s = 0; s < NS; ++s) M = fmaxf(M, part[(s * R + r) * (D + 2)]);
-        float L = 0.f, ow = 0.f;
-        for (int s = 0; s < NS; ++s) {
-            const float* p = part + (s * R + r) * (D + 2);
-            const float f = p[0] == -INFINITY ? 0.f : __expf(p[0] - M);
-            L += f * p[1];
-            ow += f * p[2 + d];
-        }
+    for (int d = tid; d < D; d += NT_DEC) {
+        float ow = 0.f;
+        for (int s_ = 0; s_ < NS; ++s_) ow += fs[s_] * part[(s_ * R + r) * (D + 2) + 2 + d];
         ow /= L;
-        const float lse = M + logf(L);
-        const int h = g * R + r;
         float o = ow;
         if (a.mem_on) {
             const float gam = 1.f / (1.f + __expf(-(a.z[(long)b * H + h] + a.mix_lse[h] * (lse - lnW))));
@@ -338,8 +449,9 @@ __global__ __launch_bounds__(NT_DEC) void decode_combine_kernel(DecodeArgs a) {
             o = ow + gam * (a.mem_scale[h] * om - ow);
         }
         a.o[((long)b * H + h) * D + d] = o;
-        if (d == 0 && a.lse) a.lse[(long)b * H + h] = lse;
     }
+    if (tid == 0 && a.lse) a.lse[(long)b * H + h] = lse;
+    if (r != 0) return;
     // cache write: slot pos mod W <- (kr, v, km, g, beta, pos)
     const int slot = (int)(a.pos % W);
     T* RK = reinterpret_cast<T*>(a.ring_k) + (bg * W + slot) * D;
@@ -373,12 +485,17 @@ __global__ __launch_bounds__(NT_DEC) void gdn_step_kernel(StepArgs a) {
 // ------------------------------------------------------------------------------------------------ host launchers
 template <class KV, int D>
 static int launch_decode(const DecodeArgs& a, hipStream_t stream) {
-    const int nx = max(D / SCOL, a.nsplit);
-    if (a.R <= 4) hipLaunchKernelGGL((decode_main_kernel<KV, D, 4>), dim3(nx, a.G, a.B), dim3(NT_DEC), 0, stream, a);
-    else hipLaunchKernelGGL((decode_main_kernel<KV, D, 8>), dim3(nx, a.G, a.B), dim3(NT_DEC), 0, stream, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return (int)e;
-    hipLaunchKernelGGL((decode_combine_kernel<KV, D>), dim3(a.G, a.B), dim3(NT_DEC), 0, stream, a);
+    if (a.nsplit > 64) return BF_STATUS_UNSUPPORTED;
+    hipError_t e;
+    if (a.mem_on) {
+        if (a.R <= 4) hipLaunchKernelGGL((decode_slab_kernel<KV, D, 4>), dim3(D / SCOL, a.G, a.B), dim3(NT_DEC), 0, stream, a);
+        else hipLaunchKernelGGL((decode_slab_kernel<KV, D, 8>), dim3(D / SCOL, a.G, a.B), dim3(NT_DEC), 0, stream, a);
+        if ((e = hipGetLastError()) != hipSuccess) return (int)e;
+    }
+    if (a.R <= 4) hipLaunchKernelGGL((decode_main_kernel<KV, D, 4>), dim3(a.nsplit, a.G, a.B), dim3(NT_DEC), 0, stream, a);
+    else hipLaunchKernelGGL((decode_main_kernel<KV, D, 8>), dim3(a.nsplit, a.G, a.B), dim3(NT_DEC), 0, stream, a);
+    if ((e = hipGetLastError()) != hipSuccess) return (int)e;
+    hipLaunchKernelGGL((decode_combine_kernel<KV, D>), dim3(a.R, a.G, a.B), dim3(NT_DEC), 0, stream, a);
     e = hipGetLastError();
     return e == hipSuccess ? 0 : (int)e;
 }

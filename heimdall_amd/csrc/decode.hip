@@ -148,6 +148,7 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
     constexpr int LPS = D / 16;                 // lanes per key slot (16 dims each)
     constexpr int SPW = 64 / LPS;               // slots per wave per iteration
     __shared__ float sc[RMAX][SLOTS + 64];      // scores, then probabilities (ring slots + sinks + new token)
+    __shared__ int vis[SLOTS + 64];             // key visible to the query (ring validity and window range)
     __shared__ float part[4][RMAX][D];          // per-wave PV partials
     __shared__ float mx[RMAX], sm[RMAX];
 
@@ -178,14 +179,19 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
         if (k < nring + a.n_sinks) return sink + (long)(k - nring) * D;
         return nw;
     };
-    auto visible = [&](int k) -> bool {
+    // visibility of every key of the split, read once into LDS (its ring_pos loads overlap the first K loads)
+    for (int k = tid; k < nkeys; k += NT_DEC) {
+        bool v_;
         if (k < nring) {
             const long p = a.ring_pos[s0 + k];
-            return p >= lo && p <= a.pos - 1;
+            v_ = p >= lo && p <= a.pos - 1;
+        } else {
+            v_ = k < nring + a.n_sinks ? true : a.pos >= a.sinks;
         }
-        if (k < nring + a.n_sinks) return true;
-        return a.pos >= a.sinks;
-    };
+        vis[k] = v_;
+    }
+    __syncthreads();
+    auto visible = [&](int k) -> bool { return vis[k] != 0; };
 
     // Scores. bf16: MFMA, S^T = K Q^T with 16-key groups of K rows straight from global memory as A fragments and the
     // R query heads as the first R columns of the B fragment (no cross-lane reduction). fp32: a lane-parallel dot
@@ -215,16 +221,17 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
         // ring keys: two 16-key groups per wave iteration (addresses past the last ring key clamped to it)
         const int ngrp = (nring + 15) / 16;
         const uint16_t* rk16 = reinterpret_cast<const uint16_t*>(RK) + (long)s0 * D + 8 * lg;
-        for (int t0 = wv; t0 < ngrp; t0 += 8) {
-            uint4 ka[2][NKD];
+        constexpr int KG = D <= 128 ? 8 : 4;              // 16-key groups per wave iteration, loaded together
+        for (int t0 = wv; t0 < ngrp; t0 += 4 * KG) {
+            uint4 ka[KG][NKD];
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
+            for (int u = 0; u < KG; ++u) {
                 const int key = min(16 * (t0 + 4 * u) + l16, nring - 1);
 #pragma unroll
                 for (int ks = 0; ks < NKD; ++ks) ka[u][ks] = ld16(rk16 + (long)key * D + 32 * ks);
             }
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
+            for (int u = 0; u < KG; ++u) {
                 const int t = t0 + 4 * u;
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -320,8 +327,44 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[r][i] = 0.f;
     // ring keys: U slot steps per wave iteration, every lane's U rows loaded before use (addresses past the last
-    // ring key are clamped to it and their probabilities taken as zero)
+    // ring key are clamped to it and their probabilities taken as zero). bf16: the rows stay packed in registers and
+    // the next iteration's rows are loaded while the current ones are accumulated.
     constexpr int U = RM <= 4 ? 4 : 2;
+    if constexpr (sizeof(T) == 2) {
+        const uint16_t* rv16 = reinterpret_cast<const uint16_t*>(RV) + (long)s0 * D + dl;
+        auto ldv = [&](int k0, uint4 (&vr)[U][2]) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int k = min(k0 + u * SPW + sl, nring - 1);
+                vr[u][0] = ld16(rv16 + (long)k * D);
+                vr[u][1] = ld16(rv16 + (long)k * D + 8);
+            }
+        };
+        uint4 cur[U][2];
+        int k0 = wv * SPW * U;
+        ldv(k0, cur);
+        for (; k0 < nring; k0 += 4 * SPW * U) {
+            uint4 nxt[U][2];
+            ldv(min(k0 + 4 * SPW * U, nring - 1), nxt);
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int k = k0 + u * SPW + sl;
+                const uint32_t w[8] = {cur[u][0].x, cur[u][0].y, cur[u][0].z, cur[u][0].w,
+                                       cur[u][1].x, cur[u][1].y, cur[u][1].z, cur[u][1].w};
+#pragma unroll
+                for (int r = 0; r < RMAX; ++r) {
+                    const float p = (r < R && k < nring) ? sc[r][k < nring ? k : 0] : 0.f;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        acc[r][2 * i] += p * __uint_as_float(w[i] << 16);
+                        acc[r][2 * i + 1] += p * __uint_as_float(w[i] & 0xffff0000u);
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) { cur[u][0] = nxt[u][0]; cur[u][1] = nxt[u][1]; }
+        }
+    } else
     for (int k0 = wv * SPW * U; k0 < nring; k0 += 4 * SPW * U) {
         float vv[U][16];
 #pragma unroll

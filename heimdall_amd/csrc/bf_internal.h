@@ -39,10 +39,10 @@ struct GdnArgs {
     float* ws_gcum;          // [cid][G][C]        in-chunk cumulative log-decay
     void* ws_T;              // [cid][G][C][C]     (I + A)^-1 diag(beta), in_dtype
     void* ws_attn;           // [cid][H][C][C]     scale * (q k^T masked, decayed), in_dtype
-    void* ws_phi;            // [sid][G][D][D]     Psi = Phi - c I of each segment map (in_dtype)
+    void* ws_phi;            // [sid][G][D*D]      Psi = Phi - c I of each segment map (in_dtype, fragment order)
     float* ws_c;             // [sid][G]           c = e^{sum of g over the segment}
-    float* ws_n;             // [sid][G][D][D]     segment state from a zero entry state (fp32)
-    float* ws_sin;           // [sid][G][D][D]     entry state of each segment (fp32; written for segments > 0)
+    float* ws_n;             // [sid][G][D*D]      segment state from a zero entry state (fp32, accumulator-fragment order)
+    float* ws_sin;           // [sid][G][D*D]      entry state of each segment (fp32, accumulator-fragment order; segments > 0)
 };
 
 int gdn_prep(const GdnArgs& a, hipStream_t stream);

@@ -83,6 +83,26 @@ __device__ __forceinline__ uint4 pack_b<BF16>(const f32x4& a, const f32x4& b) {
     return make_uint4(pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]), pack_bf16x2(b[2], b[3]));
 }
 
+// Psi = Phi - cI of a segment map is stored in MFMA fragment order, so that the combine kernel's A-fragment loads are
+// contiguous 1 KB pieces (an A fragment read straight from a row-major matrix touches 16 rows x 64 bytes per
+// instruction, about 4x slower from L2). Element (d, j) sits in fragment (tile d / 16, k step j / KF) at lane
+// 16 * ((j % KF) / VEC) + d % 16, element j % VEC.
+template <class E, int D>
+__device__ __forceinline__ long psi_frag_index(int d, int j) {
+    constexpr int VEC = E::VEC, KF = E::KF, NKD = D / KF;
+    const int lane = 16 * ((j % KF) / VEC) + (d & 15);
+    return ((long)((d >> 4) * NKD + j / KF) * 64 + lane) * VEC + j % VEC;
+}
+
+// N and the segment entry states (fp32 D x D) are stored in accumulator-fragment order: element (d, j) sits in the
+// 16 x 16 tile (d / 16, j / 16) at lane 16 * ((d % 16) / 4) + j % 16, element d % 4, so the combine kernel reads and
+// writes each tile of a 16-column strip as one contiguous float4 per lane.
+template <int D>
+__device__ __forceinline__ long acc_frag_index(int d, int j) {
+    const int lane = 16 * ((d & 15) >> 2) + (j & 15);
+    return ((long)((d >> 4) * (D / 16) + (j >> 4)) * 64 + lane) * 4 + (d & 3);
+}
+
 struct SegInfo {
     int n;        // sequence
     int p;        // segment index inside the sequence
@@ -263,9 +283,12 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
             const int j = jc + 16 * jt + l16;
             f32x4 v = {0.f, 0.f, 0.f, 0.f};
             if constexpr (OUT) {
-                const float* src = sg.p > 0 ? a.ws_sin + ((long)sid * G + g) * D * D
-                                            : (a.s0 ? a.s0 + ((long)n * G + g) * D * D : nullptr);
-                if (src) {
+                if (sg.p > 0) {                          // entry state from the combine (fragment order)
+                    const float* src = a.ws_sin + ((long)sid * G + g) * D * D;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) v[i] = src[acc_frag_index<D>(prow<E>(td, 4 * lg + i), j)];
+                } else if (a.s0) {                       // the caller's initial state (row-major)
+                    const float* src = a.s0 + ((long)n * G + g) * D * D;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) v[i] = src[(long)prow<E>(td, 4 * lg + i) * D + j];
                 }
@@ -634,14 +657,18 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
 #pragma unroll
         for (int td = 0; td < NTD; ++td)
 #pragma unroll
-            for (int jt = 0; jt < NJ; ++jt)
+            for (int jt = 0; jt < NJ; ++jt) {
+                const int d0 = prow<E>(td, 4 * lg), j = jc + 16 * jt + l16;   // the lane's rows d0 .. d0 + 3
+                if (phi_part) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int d = prow<E>(td, 4 * lg + i), j = jc + 16 * jt + l16;
-                    const float x = sc * S[td][jt][i];
-                    if (phi_part) reinterpret_cast<T*>(a.ws_phi)[off + (long)d * D + j] = E::from_f(x - (d == j ? c : 0.f));
-                    else a.ws_n[off + (long)d * D + j] = x;
+                    for (int i = 0; i < 4; ++i)
+                        reinterpret_cast<T*>(a.ws_phi)[off + psi_frag_index<E, D>(d0 + i, j)] =
+                            E::from_f(sc * S[td][jt][i] - (d0 + i == j ? c : 0.f));
+                } else {                                  // one float4 of the accumulator-fragment layout
+                    *reinterpret_cast<float4*>(a.ws_n + off + acc_frag_index<D>(d0, j)) =
+                        make_float4(sc * S[td][jt][0], sc * S[td][jt][1], sc * S[td][jt][2], sc * S[td][jt][3]);
                 }
+            }
         if (cg == 0 && wv == 0 && lane == 0) a.ws_c[(long)sid * G + g] = c;
     }
 }
@@ -679,17 +706,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         float N[TPW][4];       // N at the accumulator rows
         float c;
     };
+    // Each strip walks the row tiles starting at its own index (tile (wv * TPW + u + jb) mod NTD).
     auto load = [&](Pre& P, int p) {
         const long sid = first + p;
         const T* Psi = reinterpret_cast<const T*>(a.ws_phi) + (sid * G + g) * D * D;
         const float* Nm = a.ws_n + (sid * G + g) * D * D;
 #pragma unroll
         for (int u = 0; u < TPW; ++u) {
-            const int tr = wv * TPW + u;
+            const int tr = (wv * TPW + u + jb) & (NTD - 1);   // rotated by the strip: see load()
 #pragma unroll
-            for (int ks = 0; ks < NKD; ++ks) P.A[u][ks] = ld16(Psi + (long)(16 * tr + l16) * D + KF * ks + VEC * lg);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) P.N[u][i] = Nm[(long)(16 * tr + 4 * lg + i) * D + j0 + l16];
+            for (int ks = 0; ks < NKD; ++ks) P.A[u][ks] = ld16(Psi + ((long)(tr * NKD + ks) * 64 + lane) * VEC);
+            {
+                const float4 nv = *reinterpret_cast<const float4*>(Nm + ((long)(tr * (D / 16) + jb) * 64 + lane) * 4);
+                P.N[u][0] = nv.x; P.N[u][1] = nv.y; P.N[u][2] = nv.z; P.N[u][3] = nv.w;
+            }
         }
         P.c = a.ws_c[sid * G + g];
     };
@@ -700,7 +730,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         f32x4 acc[TPW], accl[TPW];
 #pragma unroll
         for (int u = 0; u < TPW; ++u) {
-            const int tr = wv * TPW + u;
+            const int tr = (wv * TPW + u + jb) & (NTD - 1);   // rotated by the strip: see load()
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[u][i] = P.N[u][i] + P.c * XT[l16][16 * tr + 4 * lg + i];
             accl[u] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -737,36 +767,49 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
         for (int u = 0; u < TPW; ++u)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc[u][i] += accl[u][i];
-        // every load of the step (this Psi / N / c, issued a step ago, and the next one, issued before the MFMAs)
-        // has had the MFMA time to land; draining here keeps the compiler from interleaving waits for late current-step
-        // data with the next prefetch, and also retires the previous step's stores
-        wait_vmem_all();
+        // no drain of the vector-memory counter here: it would also wait for the next step's prefetch and for this
+        // workgroup's state stores, putting their latency on the sequential path; the compiler waits only for the
+        // prefetched registers the next step reads
         __syncthreads();
         float* dst = a.ws_sin + ((sid + 1) * G + g) * D * D;
 #pragma unroll
         for (int u = 0; u < TPW; ++u) {
-            const int tr = wv * TPW + u;
+            const int tr = (wv * TPW + u + jb) & (NTD - 1);   // rotated by the strip: see load()
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int d = 16 * tr + 4 * lg + i;
-                XT[l16][d] = acc[u][i];
-                dst[(long)d * D + j0 + l16] = acc[u][i];
-            }
+            for (int i = 0; i < 4; ++i) XT[l16][16 * tr + 4 * lg + i] = acc[u][i];
+            *reinterpret_cast<float4*>(dst + ((long)(tr * (D / 16) + jb) * 64 + lane) * 4) =
+                make_float4(acc[u][0], acc[u][1], acc[u][2], acc[u][3]);
         }
         __syncthreads();
     };
 
     const int steps = nseg - 1;
+    // L2 warm-up: while step p runs, workgroup jb touches rows 16 jb .. 16 jb + 15 of Psi_{p+2}, so the 16 strips of a
+    // head together bring the whole matrix into their XCD's L2 before any of them prefetches it. The touch is an LDS
+    // DMA into a discarded 1 KB area (a real, tracked load whose data is never read).
+    __shared__ __align__(16) uint4 dump[64];
+    auto touch = [&](int p) {
+        if (p >= steps) return;
+        const T* Psi = reinterpret_cast<const T*>(a.ws_phi) + ((long)(first + p) * G + g) * D * D;
+        const char* rows = reinterpret_cast<const char*>(Psi + (long)16 * jb * D);   // row tile jb (fragment order)
+        constexpr int BYTES = 16 * D * (int)sizeof(T);
+        for (int off = wv * 1024; off < BYTES; off += 4 * 1024)
+            __builtin_amdgcn_global_load_lds(rows + off + 16 * lane, (__attribute__((address_space(3))) void*)dump, 16,
+                                             0, 0);
+    };
     if constexpr (DBUF) {
         Pre P0, P1;
         load(P0, 0);
+        touch(1);
         __syncthreads();
         for (int p = 0;;) {
             if (p + 1 < steps) load(P1, p + 1);
+            touch(p + 2);
             __builtin_amdgcn_sched_barrier(0);
             step(P0, p);
             if (++p >= steps) break;
             if (p + 1 < steps) load(P0, p + 1);
+            touch(p + 2);
             __builtin_amdgcn_sched_barrier(0);
             step(P1, p);
             if (++p >= steps) break;

@@ -8,8 +8,8 @@
 // next to the inputs q, k, v, and nothing of size C x D is written back here.
 //
 // gdn_prep_kernel, grid (chunks, G), 4 waves: K and q tiles are staged in LDS (buffer_load ... lds); the waves compute
-// the attn tiles of the R query heads, then A, by MFMA; one wave inverts (I + A) by forward substitution (one column
-// per lane, fp32).
+// the attn tiles of the R query heads, then A, by MFMA; (I + A) is inverted in fp32 by 16 x 16 blocks (diagonal blocks
+// by forward substitution, the rest by fp32 MFMA block products, one block column per wave).
 //
 // Workspace written (chunk id cid, KV head g, query head h):
 //   gcum [cid][g][C] f32 | T [cid][g][C][C] in_dtype | attn [cid][h][C][C] in_dtype
@@ -25,11 +25,17 @@ constexpr int NT = 256;    // threads per workgroup (4 waves)
 // tiles are done the q region holds A.
 template <class E, int D>
 struct __align__(16) PrepLds {
-    typename E::T K[CH * D];
+    // the inverse X overlays K once A is built, where K is large enough
+    static constexpr bool XK = CH * D * sizeof(typename E::T) >= CH * (CH + 4) * sizeof(float);
+    union {
+        typename E::T K[CH * D];
+        float XoK[XK ? CH : 1][CH + 4];
+    };
     union {
         typename E::T Q[CH * D];
         float A[CH][CH + 4];
     };
+    float Xs[XK ? 1 : CH][CH + 4];
     float gc[CH];
     float beta[CH];
 };
@@ -132,23 +138,63 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(GdnArgs a) {
     }
     __syncthreads();
 
-    // (I + A)^-1 by forward substitution, one column per lane: x_i = [i == j] - sum_{m < i} A[i][m] x_m;
-    // T'[i][j] = x_i beta_j (rows of tokens past the end are zero because their A rows and beta are). The wave doing
-    // it rotates with the chunk so that workgroups sharing a CU use different SIMDs.
-    if (wv == (int)(blockIdx.x % nw)) {
-        const int j = lane;
-        float x[CH];
+    // (I + A)^-1, blocked over 16 x 16 blocks (L = I + A unit lower triangular, X = L^-1):
+    //   X_bb = L_bb^-1 for the 4 diagonal blocks: forward substitution, one column per lane (wave 0, lane 16 b + c);
+    //   X_ij = -X_ii sum_{k=j}^{i-1} A_ik X_kj for i > j: wave j walks i = j+1 .. 3 with fp32 MFMAs; every 16 x 16
+    //   accumulator (lane: column l16, rows 4 lg ..) is already laid out as the B operand of the next product.
+    // T'[i][j] = X[i][j] beta_j (rows of tokens past the end are zero because their A rows and beta are).
+    float (*X)[CH + 4] = PrepLds<E, D>::XK ? sm.XoK : sm.Xs;
+    if (wv == 0) {
+        const int bb = lane >> 4, c = lane & 15, o = 16 * bb;
+        float x[16];
 #pragma unroll
-        for (int i = 0; i < CH; ++i) {
-            float acc = i == j ? 1.f : 0.f;
+        for (int i = 0; i < 16; ++i) {
+            float acc = i == c ? 1.f : 0.f;
 #pragma unroll
-            for (int m = 0; m < i; ++m) acc -= sm.A[i][m] * x[m];
+            for (int m = 0; m < i; ++m) acc -= sm.A[o + i][o + m] * x[m];
             x[i] = acc;
         }
-        const float bj = sm.beta[j];
-        T* Tp = reinterpret_cast<T*>(a.ws_T) + (cid * G + g) * CH * CH + j;
 #pragma unroll
-        for (int i = 0; i < CH; ++i) Tp[i * CH] = E::from_f(x[i] * bj);
+        for (int i = 0; i < 16; ++i) X[o + i][o + c] = x[i];
+    }
+    __syncthreads();
+    {
+        const int j = wv;                                  // block column of this wave
+        T* Tg = reinterpret_cast<T*>(a.ws_T) + (cid * G + g) * CH * CH;
+        const float bj = sm.beta[16 * j + l16];
+        auto put = [&](int i, const f32x4& v) {            // block (i, j) of T' from an accumulator tile
+#pragma unroll
+            for (int e = 0; e < 4; ++e) Tg[(16 * i + 4 * lg + e) * CH + 16 * j + l16] = E::from_f(v[e] * bj);
+        };
+        // A fragment of a 16 x 16 fp32 block of an LDS matrix M (rows r0.., columns c0..): lane row l16, k = 4 lg ..
+        auto afrag = [&](const float (*M)[CH + 4], int r0, int c0) {
+            const float4 v = *reinterpret_cast<const float4*>(&M[r0 + l16][c0 + 4 * lg]);
+            return make_uint4(__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w));
+        };
+        auto bfrag = [](const f32x4& v) {
+            return make_uint4(__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3]));
+        };
+        f32x4 xc[4];                                       // X_kj, k = j .. 3, as accumulator tiles
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xc[j][e] = X[16 * j + 4 * lg + e][16 * j + l16];
+        put(j, xc[j]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if (i <= j) {
+                if (i < j) put(i, f32x4{0.f, 0.f, 0.f, 0.f});   // above the diagonal
+                continue;
+            }
+            f32x4 msum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (k >= j && k < i) mma<F32>(msum, afrag(sm.A, 16 * i, 16 * k), bfrag(xc[k]));
+            f32x4 xi = {0.f, 0.f, 0.f, 0.f};
+            mma<F32>(xi, afrag(X, 16 * i, 16 * i), bfrag(msum));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) xi[e] = -xi[e];
+            xc[i] = xi;
+            put(i, xi);
+        }
     }
 }
 

@@ -50,14 +50,28 @@ def make_inputs(T, H, D, dev, seed=0):
     return q, k, v, g, beta
 
 
-def gdn_flops(T, H, D):
-    """Algorithmic FLOPs of the chunked form per phase (per chunk and head). prep: K K^T and the masked q K^T
-    (2 * 2C^2D); the sequential part of the reference algorithm: w S, q S, k_tail^T v_new (3 * 2CD^2) and
-    attn v_new (2C^2D). The output kernel performs that whole sequential part from each segment's entry state."""
-    chunks = (T + C - 1) // C
-    prep = 4 * C * C * D * chunks * H
-    scan = (6 * C * D * D + 2 * C * C * D) * chunks * H
-    return prep, scan
+def gdn_kernel_flops(T, G, R, D, L):
+    """Algorithmic FLOPs of one launch of each kernel of bf_gdn_fwd for one sequence of T tokens, G KV heads, R query
+    heads per KV head, segments of L chunks (C = 64). Per chunk and KV head:
+      prep     2C^2D (K K^T) + R 2C^2D (q K^T) + C^3/3 (unit-triangular inverse)
+      summary  the chunk map on the 2D columns [N | Phi]: K S and K^T v_new 2 * 2C(D)(2D), T' y 2C^2(2D), T' V 2C^2D
+               = 8CD^2 + 6C^2D, for the chunks of every segment but the last
+      output   K S, K^T v_new 4CD^2, T'(V - e^g K S) 4C^2D, and per query head q S 2CD^2 + attn v_new 2C^2D
+    combine    per segment step and KV head: Psi X, 2D^3 (the split-bf16 second pass is not counted)."""
+    n = (T + C - 1) // C
+    nseg = (n + L - 1) // L
+    n_sum = n - ((n - 1) % L + 1)                  # chunks outside the last segment
+    return {
+        "prep": n * G * ((1 + R) * 2 * C * C * D + C ** 3 / 3),
+        "summary": n_sum * G * (8 * C * D * D + 6 * C * C * D),
+        "combine": max(nseg - 1, 0) * G * 2 * D ** 3,
+        "output": n * G * (4 * C * D * D + 4 * C * C * D + R * (2 * C * D * D + 2 * C * C * D)),
+    }
+
+
+def reference_flops(T, H, D):
+    """FLOPs of the reference's chunked algorithm (kernels.py:94-129) per head: T (10CD + 6D^2)."""
+    return T * H * (10 * C * D + 6 * D * D)
 
 
 def gdn_bytes(T, H, D):
@@ -74,12 +88,12 @@ def traffic_from_profile(kernel: str):
         return None
 
 
-PHASES = ("prep", "states", "output")
+PHASES = ("prep", "summary", "combine", "output")
 
 
 def run_gdn(steps, warmup, dev, segment_chunks=0):
-    """Headline workload; each step runs the three phases of bf_gdn_fwd (PREP, STATES, OUTPUT) back to back on one
-    stream, with HIP events between them (the events sit on the stream the kernels are launched on)."""
+    """Headline workload; each step runs the four phases of bf_gdn_fwd (PREP, SUMMARY, COMBINE, OUTPUT) back to back on
+    one stream, with HIP events between them (the events sit on the stream the kernels are launched on)."""
     from heimdall_amd import _lib
     from heimdall_amd._device import gdn_forward, workspace
 
@@ -87,22 +101,23 @@ def run_gdn(steps, warmup, dev, segment_chunks=0):
     q, k, v, g, beta = make_inputs(T, H, D, dev)
     o = torch.empty(T, H, D, dtype=torch.float32, device=dev)
     s = torch.empty(1, H, D, D, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    L = segment_chunks if segment_chunks > 0 else lib.bf_gdn_segment_chunks(T, 1, H, 1, D)
     nbytes = _lib.ctypes.c_size_t(0)
-    _lib.check(_lib.load().bf_gdn_workspace_size(T, 1, H, 1, D, _lib.DTYPE_BF16, segment_chunks,
-                                                 _lib.ctypes.byref(nbytes)), "bf_gdn_workspace_size")
+    _lib.check(lib.bf_gdn_workspace_size(T, 1, H, 1, D, _lib.DTYPE_BF16, L, _lib.ctypes.byref(nbytes)),
+               "bf_gdn_workspace_size")
     ws = workspace(nbytes.value, dev)
-    bits = (_lib.PHASE_PREP, _lib.PHASE_STATES, _lib.PHASE_OUTPUT)
+    bits = (_lib.PHASE_PREP, _lib.PHASE_SUMMARY, _lib.PHASE_COMBINE, _lib.PHASE_OUTPUT)
 
     def phase(p):
-        gdn_forward(q, k, v, g, beta, num_seqs=1, out=o, final_state=s, ws=ws, phases=p,
-                    segment_chunks=segment_chunks)
+        gdn_forward(q, k, v, g, beta, num_seqs=1, out=o, final_state=s, ws=ws, phases=p, segment_chunks=L)
 
     for _ in range(warmup):
         for p in bits:
             phase(p)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(bits) + 1)] for _ in range(steps)]
     t0 = time.perf_counter()
     for i in range(steps):
         ev[i][0].record(stream)
@@ -112,7 +127,7 @@ def run_gdn(steps, warmup, dev, segment_chunks=0):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms = {name: sum(e[j].elapsed_time(e[j + 1]) for e in ev) / steps for j, name in enumerate(PHASES)}
-    return dict(T=T, H=H, D=D, wall=wall, phase_ms=ms, inputs=(q, k, v, g, beta))
+    return dict(T=T, H=H, D=D, L=L, wall=wall, phase_ms=ms, inputs=(q, k, v, g, beta))
 
 
 def cpu_baseline(inputs, budget_s=30.0):
@@ -205,6 +220,44 @@ def window_pairs(T, W, S):
     return sum(min(p + 1, W + S) for p in range(T))
 
 
+def run_window(steps, warmup, dev, T=32768):
+    """The window kernel alone on the layer prefill's shapes (B=1, H=24, G=4, D=256, W=2048 + 4 sinks, bf16, from
+    position 0 with the first 4 tokens as sinks, no ring, no mix): bf_window_fwd timed with HIP events on the launch
+    stream. Algorithmic work: 4 D FLOP per visible (query, key) pair and query head."""
+    from heimdall_amd import _lib
+    from heimdall_amd._device import stream_ptr
+
+    B, H, G, D, W, S = 1, 24, 4, 256, 2048, 4
+    gen = torch.Generator(device=dev).manual_seed(3)
+    qr = F.normalize(torch.randn(B, H, T, D, device=dev, generator=gen), dim=-1).bfloat16()
+    kr = F.normalize(torch.randn(B, G, T, D, device=dev, generator=gen), dim=-1).bfloat16()
+    v = torch.randn(B, T, G, D, device=dev, generator=gen).bfloat16()
+    sk, sv = kr[:, :, :S].contiguous(), v.transpose(1, 2)[:, :, :S].contiguous()
+    o = torch.empty(B, T, H, D, dtype=torch.float32, device=dev)
+    lse = torch.empty(B, H, T, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    st = lambda t_, dims: tuple(int(t_.stride(i)) for i in dims)
+    args = (B, G, H // G, D, T, W, S, 0, _lib.DTYPE_BF16, qr.data_ptr(), *st(qr, (0, 1, 2)), kr.data_ptr(),
+            *st(kr, (0, 1, 2)), v.data_ptr(), *st(v, (0, 2, 1)), None, None, None, sk.data_ptr(), sv.data_ptr(), S, 0,
+            None, None, None, None, o.data_ptr(), _lib.DTYPE_F32, lse.data_ptr(), stream_ptr(dev))
+    for _ in range(warmup):
+        _lib.check(lib.bf_window_fwd(*args), "bf_window_fwd")
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        lib.bf_window_fwd(*args)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / steps
+    flops = 4 * D * window_pairs(T, W, S) * H
+    tf = flops / (us * 1e-6) / 1e12
+    return {"kernel": "window_fa_kernel<256>", "us": us, "flops": flops,
+            "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": tf / BF16_PEAK_TFLOPS}}
+
+
 def run_layer(steps, warmup, dev, T=32768):
     """Full converted-layer prefill at 32K: B=1, T=32768, H=24, G=4, D=256, W=2048 + 4 sinks, bf16 activations,
     fp32 state; x/q/k/v/qr/kr synthetic (q, k L2-normalised), init-time gates (fq = fk = I). One step =
@@ -255,7 +308,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the decode and layer-prefill legs")
     ap.add_argument("--copy-probe", action="store_true", help="run one 256 MiB device copy first (counter scaling)")
     ap.add_argument("--segment-chunks", type=int, default=0, help="chunks per scan segment (0 = library default)")
-    ap.add_argument("--only", choices=("decode", "layer", "layer131k"), default=None,
+    ap.add_argument("--only", choices=("decode", "layer", "layer131k", "window"), default=None,
                     help="run one secondary leg alone and print its JSON object (for per-workload profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -275,17 +328,21 @@ def main():
     if args.only:
         leg = {"decode": lambda: run_decode(args.steps, args.warmup, dev),
                "layer": lambda: run_layer(args.steps, args.warmup, dev),
-               "layer131k": lambda: run_layer(args.steps, args.warmup, dev, T=131072)}[args.only]
+               "layer131k": lambda: run_layer(args.steps, args.warmup, dev, T=131072),
+               "window": lambda: run_window(args.steps, args.warmup, dev)}[args.only]
         print(json.dumps(leg()), flush=True)
         return
 
     r = run_gdn(args.steps, args.warmup, dev, args.segment_chunks)
-    T, H, D = r["T"], r["H"], r["D"]
+    T, H, D, L = r["T"], r["H"], r["D"], r["L"]
     ms = r["wall"] * 1e3 / args.steps
-    prep_f, scan_f = gdn_flops(T, H, D)
     pm = r["phase_ms"]
-    out_ms = pm["output"]
-    achieved = scan_f / (out_ms * 1e-3) / 1e12
+    kf = gdn_kernel_flops(T, H, 1, D, L)
+    dominant = max(pm, key=pm.get)                 # the kernel with the largest share of the step
+    achieved = kf[dominant] / (pm[dominant] * 1e-3) / 1e12
+    kernels = {"prep": "gdn_prep_kernel", "summary": "gdn_seg_kernel (segment summary)",
+               "combine": "gdn_combine_kernel", "output": "gdn_seg_kernel (output scan)"}
+    ref_f = reference_flops(T, H, D)
     line = {
         "metric": METRIC,
         "value": T / (ms * 1e-3),
@@ -300,17 +357,21 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "gdn_prefill", "B": 1, "T": T, "H": H, "G": H, "D": D, "chunk": C,
-                   "inputs": "bf16 q/k/v, fp32 g/beta/state/output", "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "kernel": "gdn_seg_kernel (output scan)", "achieved": achieved,
+                   "segment_chunks": L, "inputs": "bf16 q/k/v, fp32 g/beta/state/output",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": kernels[dominant], "achieved": achieved,
                      "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS,
-                     "traffic": traffic_from_profile("gdn_output")},
+                     "traffic": traffic_from_profile("gdn_" + dominant)},
         "phases_ms": pm,
-        "hbm": {"algorithmic_bytes": gdn_bytes(T, H, D),
-                "achieved_GBs": gdn_bytes(T, H, D) / (ms * 1e-3) / 1e9, "peak_GBs": HBM_PEAK_GBS},
+        "kernel_tflops": {k_: kf[k_] / (pm[k_] * 1e-3) / 1e12 for k_ in PHASES},
+        "operator": {"reference_flops": ref_f, "tflops": ref_f / (ms * 1e-3) / 1e12,
+                     "algorithmic_bytes": gdn_bytes(T, H, D),
+                     "achieved_GBs": gdn_bytes(T, H, D) / (ms * 1e-3) / 1e9, "peak_GBs": HBM_PEAK_GBS},
     }
     if not args.no_extra:
         line["decode"] = run_decode(100, 10, dev)
         line["layer_prefill_32k"] = run_layer(3, 1, dev)
+        line["layer_prefill_32k"]["window_kernel"] = run_window(5, 1, dev)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(r["inputs"])
     print(json.dumps(line), flush=True)

@@ -8,7 +8,8 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libbifrost_hip.so"
 
 DTYPE_F32, DTYPE_BF16 = 0, 1
-PHASE_PREP, PHASE_STATES, PHASE_OUTPUT, PHASE_ALL = 1, 2, 4, 7
+PHASE_PREP, PHASE_SUMMARY, PHASE_OUTPUT, PHASE_COMBINE = 1, 2, 4, 8
+PHASE_STATES, PHASE_ALL = PHASE_SUMMARY | PHASE_COMBINE, 15
 
 _c_int, _c_i64, _c_sz, _vp, _fp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_float
 
@@ -16,6 +17,7 @@ _c_int, _c_i64, _c_sz, _vp, _fp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t,
 SIGNATURES = {
     "bf_version": (_c_int, []),
     "bf_status_string": (ctypes.c_char_p, [_c_int]),
+    "bf_gdn_segment_chunks": (_c_int, [_c_i64, _c_int, _c_int, _c_int, _c_int]),
     "bf_gdn_workspace_size": (_c_int, [_c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                        ctypes.POINTER(_c_sz)]),
     "bf_gdn_fwd": (_c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_int, _fp, _vp,

@@ -46,7 +46,7 @@ struct GdnArgs {
 };
 
 int gdn_prep(const GdnArgs& a, hipStream_t stream);
-int gdn_states(const GdnArgs& a, hipStream_t stream);
+int gdn_states(const GdnArgs& a, hipStream_t stream, bool summary, bool combine);
 int gdn_output(const GdnArgs& a, hipStream_t stream);
 
 

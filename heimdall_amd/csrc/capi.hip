@@ -68,6 +68,12 @@ const char* bf_status_string(int status) {
     return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
 }
 
+int bf_gdn_segment_chunks(int64_t total_tokens, int num_seqs, int G, int R, int D) {
+    if (total_tokens < 0 || num_seqs <= 0 || G <= 0 || R <= 0) return BF_STATUS_INVALID;
+    if (!supported_dim(D)) return BF_STATUS_UNSUPPORTED;
+    return auto_segment_chunks((int)(total_tokens / kChunk) + num_seqs, G, R, D);
+}
+
 int bf_gdn_workspace_size(int64_t total_tokens, int num_seqs, int G, int R, int D, int in_dtype,
                           int segment_chunks, size_t* bytes) {
     if (!bytes || total_tokens < 0 || num_seqs <= 0 || G <= 0 || R <= 0 || segment_chunks < 0)
@@ -117,7 +123,9 @@ int bf_gdn_fwd(const void* q, const void* k, const void* v, const float* g, cons
     const hipStream_t st = static_cast<hipStream_t>(stream);
     int rc = 0;
     if ((phases & BF_GDN_PHASE_PREP) && total_tokens > 0 && (rc = bf::gdn_prep(a, st))) return rc;
-    if ((phases & BF_GDN_PHASE_STATES) && (rc = bf::gdn_states(a, st))) return rc;
+    if ((phases & BF_GDN_PHASE_STATES) &&
+        (rc = bf::gdn_states(a, st, phases & BF_GDN_PHASE_SUMMARY, phases & BF_GDN_PHASE_COMBINE)))
+        return rc;
     if (phases & BF_GDN_PHASE_OUTPUT) return bf::gdn_output(a, st);
     return BF_STATUS_OK;
 }

@@ -5,26 +5,28 @@
 //   Y = K S,   v_new = T' (V - e^{gc} Y),   o_r = scale e^{gc} q_r S + attn_r v_new,
 //   S' = e^{gc_last} S + K^T (e^{gc_last - gc} v_new).
 // S' is affine in S, so each sequence is cut into segments of L chunks and three kernels run in turn:
-//   gdn_summary_kernel  per (segment, KV head, column group): the chunk map applied to the 2D columns [N | Phi]
-//                       from [0 | I], with V for the N columns and zero for the Phi columns, gives the segment's
-//                       map S_end = Phi S_start + N (the last segment of a sequence is skipped).
+//   gdn_seg_kernel<.., OUT=false>  (summary) per (segment, KV head, column group): the chunk map applied to the 2D
+//                       columns [N | Phi] from [0 | I], with V for the N columns and zero for the Phi columns, gives the
+//                       segment's map S_end = Phi S_start + N (the last segment of a sequence is skipped).
 //   gdn_combine_kernel  per (sequence, KV head, 16-column strip): X_0 = S0, X_{p+1} = Phi_p X_p + N_p in fp32
-//                       (bf16 runs: three split-bf16 MFMAs per product), the entry state of every segment.
-//   gdn_output_kernel   per (segment, KV head, column group, query head): the chunk map with outputs from the
-//                       segment's entry state; the last segment of a sequence writes the final state.
+//                       (bf16 runs: Psi = Phi - cI in bf16 times X split into bf16 high and low parts, plus the exact
+//                       c X term), the entry state of every segment.
+//   gdn_seg_kernel<.., OUT=true>   (output) per (segment, KV head, column group, query head): the chunk map with
+//                       outputs from the segment's entry state; the last segment of a sequence writes the final state.
 //
-// Inside a workgroup each wave owns 32 state columns (two 16-column MFMA tiles) for all D rows, held in registers as
+// Inside a workgroup each wave owns 16 state columns (one 16-column MFMA tile) for all D rows, held in registers as
 // MFMA accumulators, so the per-chunk chain runs inside the wave with no exchange between waves:
 //   K S, q S      A = K / q rows (LDS),     B = S packed from the accumulators
 //   T' y          A = T' rows (LDS),        B = the Y accumulators after y = V - e^{gc} Y
-//   attn v_new    A = attn rows (global, prefetched one chunk ahead), B = the v_new accumulators
-//   K^T v'        A = K^T gathered from the K tile in LDS,  B = the v_new accumulators scaled by e^{gc_last - gc}
+//   attn v_new    A = attn rows (LDS),      B = the v_new accumulators
+//   K^T v'        A = K^T through transposing reads of the K tile in LDS,  B = the v_new accumulators scaled by
+//                 e^{gc_last - gc}
 // An accumulator tile holds rows 4g..4g+3 of its 16 rows in lane group g, while an MFMA operand fragment holds VEC
 // consecutive K indices per lane group. Tiles over the token and state-row dimensions therefore use the row
 // permutation prow(tile, m): rows 4g..4g+3 of the HP = VEC/4 tiles of one K fragment are that fragment's VEC values
 // of group g, so accumulators feed the next product directly. A rows are read through the same permutation.
 //
-// The chunk operands all waves share (K, q of the workgroup's query head, T', gc) are staged in LDS with
+// The chunk operands all waves share (K, q of the workgroup's query head, T', attn, gc, V) are staged in LDS with
 // buffer_load ... lds (no registers, out-of-range rows read as zero); bf16 runs double-buffer the stage so chunk c+1
 // is in flight while chunk c is computed. LDS rows are swizzled by 16-byte blocks (swz) so that the fragment reads
 // of 16 rows hit distinct banks.
@@ -836,11 +838,14 @@ dim3 seg_grid(const GdnArgs& a) {
 }
 
 template <class E, int D>
-int launch_states(const GdnArgs& a, hipStream_t stream) {
-    const dim3 grid = seg_grid<E, D, false>(a), block(SegCfg<E, D, false>::NW * 64);
-    hipLaunchKernelGGL((gdn_seg_kernel<E, D, false, false>), grid, block, 0, stream, a);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return (int)e;
+int launch_states(const GdnArgs& a, hipStream_t stream, bool summary, bool combine) {
+    if (summary) {
+        const dim3 grid = seg_grid<E, D, false>(a), block(SegCfg<E, D, false>::NW * 64);
+        hipLaunchKernelGGL((gdn_seg_kernel<E, D, false, false>), grid, block, 0, stream, a);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return (int)e;
+    }
+    if (!combine) return 0;
     const int groups = a.num_seqs * a.G;
     hipLaunchKernelGGL((gdn_combine_kernel<E, D>), dim3(NXCD * ((groups + NXCD - 1) / NXCD) * (D / 16)), dim3(256), 0,
                        stream, a);
@@ -859,13 +864,14 @@ int launch_output(const GdnArgs& a, hipStream_t stream) {
 
 }  // namespace
 
-int gdn_states(const GdnArgs& a, hipStream_t stream) {
+int gdn_states(const GdnArgs& a, hipStream_t stream, bool summary, bool combine) {
     if (!a.multi_seg) return 0;
     const bool bf = a.in_dtype == DT_BF16;
+    const bool su = summary, co = combine;
     switch (a.D) {
-        case 64: return bf ? launch_states<BF16, 64>(a, stream) : launch_states<F32, 64>(a, stream);
-        case 128: return bf ? launch_states<BF16, 128>(a, stream) : launch_states<F32, 128>(a, stream);
-        case 256: return bf ? launch_states<BF16, 256>(a, stream) : launch_states<F32, 256>(a, stream);
+        case 64: return bf ? launch_states<BF16, 64>(a, stream, su, co) : launch_states<F32, 64>(a, stream, su, co);
+        case 128: return bf ? launch_states<BF16, 128>(a, stream, su, co) : launch_states<F32, 128>(a, stream, su, co);
+        case 256: return bf ? launch_states<BF16, 256>(a, stream, su, co) : launch_states<F32, 256>(a, stream, su, co);
         default: return BF_ERR_UNSUPPORTED;
     }
 }

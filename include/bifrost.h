@@ -33,15 +33,19 @@ extern "C" {
 #define BF_STATUS_UNSUPPORTED (-2) /* head dim, dtype or chunk size outside the supported set */
 #define BF_STATUS_WORKSPACE (-3)   /* workspace missing or smaller than the size query returned */
 
-/* Phases of bf_gdn_fwd (bit mask), run in this order; BF_GDN_PHASE_ALL runs the whole operator.
- *   PREP    per-chunk quantities that do not depend on the state (decay, (I + A)^-1, masked q.k^T)
- *   STATES  state entering every segment: per-segment affine summaries S_end = Phi S_start + N, then their
- *           sequential composition per sequence (skipped when every sequence is a single segment)
- *   OUTPUT  per-segment scan from the segment's entry state: outputs and the final state */
+/* Phases of bf_gdn_fwd (bit mask), run in the order PREP, SUMMARY, COMBINE, OUTPUT; BF_GDN_PHASE_ALL runs the whole
+ * operator.
+ *   PREP     per-chunk quantities that do not depend on the state (decay, (I + A)^-1, masked q.k^T)
+ *   SUMMARY  per-segment affine maps S_end = Phi S_start + N (skipped when every sequence is a single segment)
+ *   COMBINE  their sequential composition per sequence: the state entering every segment (same condition)
+ *   OUTPUT   per-segment scan from the segment's entry state: outputs and the final state
+ * BF_GDN_PHASE_STATES is SUMMARY | COMBINE. */
 #define BF_GDN_PHASE_PREP 1
-#define BF_GDN_PHASE_STATES 2
+#define BF_GDN_PHASE_SUMMARY 2
 #define BF_GDN_PHASE_OUTPUT 4
-#define BF_GDN_PHASE_ALL 7
+#define BF_GDN_PHASE_COMBINE 8
+#define BF_GDN_PHASE_STATES (BF_GDN_PHASE_SUMMARY | BF_GDN_PHASE_COMBINE)
+#define BF_GDN_PHASE_ALL 15
 
 /* Library version (major * 10000 + minor * 100 + patch). */
 int bf_version(void);
@@ -70,10 +74,14 @@ const char* bf_status_string(int status);
  *   segment_chunks: each sequence is cut into segments of this many 64-token chunks that are scanned in parallel
  *     (their entry states come from the STATES phase); 0 picks a length from the problem size. The result does not
  *     depend on it beyond rounding.
- *   phases: BF_GDN_PHASE_ALL, or PREP, STATES, OUTPUT in separate calls with the same arguments and workspace.
+ *   phases: BF_GDN_PHASE_ALL, or PREP, SUMMARY, COMBINE, OUTPUT in separate calls (in that order) with the same
+ *     arguments and workspace.
  * Chunk length is 64. Arithmetic: MFMA in in_dtype with fp32 accumulation; state, decay and the triangular
  * inverse in fp32; segment entry states composed in fp32 (split-bf16 MFMA for bf16 runs).
  */
+/* Segment length (64-token chunks) that bf_gdn_fwd uses when segment_chunks is 0, or a negative status. */
+int bf_gdn_segment_chunks(int64_t total_tokens, int num_seqs, int G, int R, int D);
+
 int bf_gdn_workspace_size(int64_t total_tokens, int num_seqs, int G, int R, int D, int in_dtype,
                           int segment_chunks, size_t* bytes);
 

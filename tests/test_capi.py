@@ -70,8 +70,10 @@ def test_status_codes_without_gpu(cpu_lib):
     assert st == -3
     st = cpu_lib.bf_gdn_fwd(1, 1, 1, 1, 1, None, 3, 64, 4, 1, 256, 1, 1.0, None, 1, 0, None, 0, None, 0, 7, None)
     assert st == -1                                                                            # 64 % 3 != 0
-    st = cpu_lib.bf_gdn_fwd(1, 1, 1, 1, 1, None, 1, 64, 4, 1, 256, 1, 1.0, None, 1, 0, None, 0, None, 0, 8, None)
+    st = cpu_lib.bf_gdn_fwd(1, 1, 1, 1, 1, None, 1, 64, 4, 1, 256, 1, 1.0, None, 1, 0, None, 0, None, 0, 16, None)
     assert st == -1                                                                            # unknown phase bit
+    st = cpu_lib.bf_gdn_fwd(1, 1, 1, 1, 1, None, 1, 64, 4, 1, 256, 1, 1.0, None, 1, 0, None, 0, None, 0, 0, None)
+    assert st == -1                                                                            # no phase
 
 
 def test_workspace_size_grows_with_tokens(cpu_lib):

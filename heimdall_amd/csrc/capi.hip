@@ -18,17 +18,31 @@ struct GdnLayout {
     int max_chunks, seg_chunks, max_segs;
 };
 
-// Segment length (chunks) when the caller passes 0: enough segments that the output scan has about
-// kSegTargetWgs workgroups in flight (each (segment, KV head) pair runs D/128 column groups per query head),
-// and at least kSegMinChunks chunks per segment so the per-segment summary and combine stay small.
-constexpr int kSegTargetWgs = 256;
-constexpr int kSegMinChunks = 8;
+// Segment length (chunks) when the caller passes 0: the L that minimises a cost model of the three sequential-part
+// kernels on an MI355X (256 CUs, one scan workgroup per CU), with per-chunk and per-step times measured at D = 256:
+//   output   ceil(segments x G x D/128 x R / 256) rounds of L chunks, ~6 us per chunk
+//   summary  ceil((segments - 1) x G x 2D/128 / 256) rounds of L chunks, ~3.7 us per chunk
+//   combine  (segments - 1) sequential steps, ~2.6 us each
+// Times scale with D^2 for the scan kernels and D^3 for the combine, which only shifts the balance for D < 256.
+constexpr int kSegMinChunks = 4;
 
 int auto_segment_chunks(int max_chunks, int G, int R, int D) {
-    const long per_seg = (long)G * R * (D >= 128 ? D / 128 : 1);
-    const long want_segs = kSegTargetWgs / per_seg > 1 ? kSegTargetWgs / per_seg : 1;
-    const long L = (max_chunks + want_segs - 1) / want_segs;
-    return (int)(L > kSegMinChunks ? L : kSegMinChunks);
+    const double f = (double)D / 256.0;
+    const double t_out = 6.0 * f * f, t_sum = 3.7 * f * f, t_comb = 2.6 * f * f * f;
+    const int cg = D >= 128 ? D / 128 : 1;
+    int best_L = max_chunks > kSegMinChunks ? max_chunks : kSegMinChunks;
+    double best = 1e300;
+    for (int L = kSegMinChunks; L <= (max_chunks > kSegMinChunks ? max_chunks : kSegMinChunks); ++L) {
+        const long nseg = (max_chunks + L - 1) / L;
+        const long out_rounds = (nseg * G * cg * R + 255) / 256;
+        const long sum_rounds = ((nseg - 1) * G * 2 * cg + 255) / 256;
+        const double t = out_rounds * L * t_out + sum_rounds * L * t_sum + (nseg - 1) * t_comb;
+        if (t < best - 1e-9) {
+            best = t;
+            best_L = L;
+        }
+    }
+    return best_L;
 }
 
 GdnLayout gdn_layout(int64_t total_tokens, int num_seqs, int G, int R, int D, int in_dtype, int segment_chunks) {

@@ -220,6 +220,41 @@ def window_pairs(T, W, S):
     return sum(min(p + 1, W + S) for p in range(T))
 
 
+def run_varlen(steps, warmup, dev):
+    """Native Gated DeltaNet core on packed variable-length input: 4 sequences {8192, 16384, 24576, 16384} via
+    cu_seqlens, H=32, D=128, bf16 q/k/v (k L2-normalised, q unscaled), g ~ U[-5e-3, 0], beta = sigmoid(N(0,1)), zero
+    initial states, final states returned: kernels.delta_rule_varlen timed with HIP events on the launch stream."""
+    from heimdall_amd import kernels
+
+    lens = (8192, 16384, 24576, 16384)
+    H, D = 32, 128
+    N = sum(lens)
+    cu = torch.tensor([0, 8192, 24576, 49152, 65536], dtype=torch.int32, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(4)
+    q = torch.randn(1, N, H, D, device=dev, generator=gen).bfloat16()
+    k = F.normalize(torch.randn(1, N, H, D, device=dev, generator=gen), dim=-1).bfloat16()
+    v = torch.randn(1, N, H, D, device=dev, generator=gen).bfloat16()
+    beta = torch.sigmoid(torch.randn(1, N, H, device=dev, generator=gen))
+    g = -torch.rand(1, N, H, device=dev, generator=gen) * 5e-3
+    with torch.no_grad():
+        for _ in range(warmup):
+            kernels.delta_rule_varlen(q, k, v, g, beta, cu)
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            kernels.delta_rule_varlen(q, k, v, g, beta, cu)
+        e1.record(stream)
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = reference_flops(N, H, D)
+    nbytes = gdn_bytes(N, H, D) - H * D * D * 4 + len(lens) * H * D * D * 4
+    return {"workload": "varlen gated delta rule, 4 seqs {8192,16384,24576,16384}, H=32, D=128, bf16",
+            "ms_per_step": ms, "tokens_per_s": N / (ms * 1e-3), "steps": steps,
+            "tflops_reference": flops / (ms * 1e-3) / 1e12, "GBs": nbytes / (ms * 1e-3) / 1e9}
+
+
 def run_window(steps, warmup, dev, T=32768):
     """The window kernel alone on the layer prefill's shapes (B=1, H=24, G=4, D=256, W=2048 + 4 sinks, bf16, from
     position 0 with the first 4 tokens as sinks, no ring, no mix): bf_window_fwd timed with HIP events on the launch
@@ -308,7 +343,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the decode and layer-prefill legs")
     ap.add_argument("--copy-probe", action="store_true", help="run one 256 MiB device copy first (counter scaling)")
     ap.add_argument("--segment-chunks", type=int, default=0, help="chunks per scan segment (0 = library default)")
-    ap.add_argument("--only", choices=("decode", "layer", "layer131k", "window"), default=None,
+    ap.add_argument("--only", choices=("decode", "layer", "layer131k", "window", "varlen"), default=None,
                     help="run one secondary leg alone and print its JSON object (for per-workload profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -329,7 +364,8 @@ def main():
         leg = {"decode": lambda: run_decode(args.steps, args.warmup, dev),
                "layer": lambda: run_layer(args.steps, args.warmup, dev),
                "layer131k": lambda: run_layer(args.steps, args.warmup, dev, T=131072),
-               "window": lambda: run_window(args.steps, args.warmup, dev)}[args.only]
+               "window": lambda: run_window(args.steps, args.warmup, dev),
+               "varlen": lambda: run_varlen(args.steps, args.warmup, dev)}[args.only]
         print(json.dumps(leg()), flush=True)
         return
 
@@ -371,7 +407,8 @@ def main():
     if not args.no_extra:
         line["decode"] = run_decode(100, 10, dev)
         line["layer_prefill_32k"] = run_layer(3, 1, dev)
-        line["layer_prefill_32k"]["window_kernel"] = run_window(5, 1, dev)
+        line["layer_prefill_32k"]["window_kernel"] = run_window(10, 3, dev)
+        line["varlen_gdn"] = run_varlen(10, 3, dev)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(r["inputs"])
     print(json.dumps(line), flush=True)

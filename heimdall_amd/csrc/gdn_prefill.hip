@@ -50,7 +50,10 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(GdnArgs a) {
     const int g = blockIdx.y, G = a.G, R = a.R, H = G * R;
     const long cid = blockIdx.x;
     const int lane = lane_id(), wv = wave_id(), l16 = lane & 15, lg = lane >> 4;
-    const auto sw_row = [](int row) { return swz<E>(row, ROWB / 16); };
+    // LDS block permutation of the K and q tiles: a fragment read covers 16 consecutive rows at one 16-byte block, so
+    // the block is XORed with row & 15 (rows of >= 16 blocks) or (row >> 1) & 7 (8 blocks: two rows share a 256-byte
+    // bank window), putting the 16 rows on 16 distinct bank groups.
+    const auto sw_row = [](int row) { return ROWB / 16 >= 16 ? (row & 15) : ((row >> 1) & 7); };
     const int nw = NT / WAVE;
 
     const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.k) + (si.tok0 * G + g) * D * ES,
@@ -83,7 +86,7 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(GdnArgs a) {
     // fragment of rows 16*tile + l16 of a swizzled tile, K index KF*ks + VEC*lg .. (16 bytes)
     auto frag = [&](const T* base, int tile, int ks) {
         const int row = 16 * tile + l16;
-        return lds16(base, row * ROWB + (((4 * ks + lg) ^ swz<E>(row, ROWB / 16)) << 4));
+        return lds16(base, row * ROWB + (((4 * ks + lg) ^ sw_row(row)) << 4));
     };
 
     // attn_r^T = K q_r^T (rows t' = key, cols t = query), masked to t' <= t, decayed and scaled; the 6 tiles above

@@ -49,6 +49,17 @@ constexpr int WG_COLS = 128;
 constexpr int SEG_THREADS = WG_COLS / WCOLS * 64;
 constexpr int SEG_WAVES_PER_EU = SEG_THREADS / 256;
 
+// 16-byte block permutation of the 64 x 64 T' and attn tiles. bf16 rows are 128 bytes (8 blocks, two rows per 256-byte
+// bank window); a fragment read covers the 16 rows tp + {0..3, 8..11, 16..19, 24..27} at one block, and bits 1, 3
+// and 4 of those rows tell apart the 8 rows of each row parity, so each half-window gets 8 distinct blocks. The value
+// does not change with the tile offsets tp (multiples of 4 and 32 only touch bits 2 and 5+). fp32 rows (16 blocks)
+// keep swz.
+template <class E>
+__device__ __forceinline__ int swz_t(int row, int nblk) {
+    if constexpr (E::VEC == 8) return ((row >> 1) & 1) | (((row >> 3) & 1) << 1) | (((row >> 4) & 1) << 2);
+    else return swz<E>(row, nblk);
+}
+
 template <class E>
 __device__ __forceinline__ int prow(int tile, int m) {
     constexpr int VEC = E::VEC, KF = E::KF, HP = VEC / 4;
@@ -235,7 +246,7 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
     const int lt = VEC * (l16 >> 2) + (l16 & 3);         // fragment row offset inside a tile
     // K / q fragment of K index group (ks, lg) at row tp(tile) + lt: block (4ks + lg) ^ swz(row), and the swizzle of
     // those rows depends on the lane only, so the block is 4*NX*(ks / NX) + xb[ks % NX]
-    const int sl = swz<E>(lt, NBLK), tsl = swz<E>(lt, TNBLK);
+    const int sl = swz<E>(lt, NBLK), tsl = swz_t<E>(lt, TNBLK);
     int kq_base[NX], t_base[2];
 #pragma unroll
     for (int c = 0; c < NX; ++c) kq_base[c] = lt * ROWB + 16 * (4 * (c ^ (sl >> 2)) + (lg ^ (sl & 3)));
@@ -313,7 +324,7 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
         return (int)(rem < SC ? rem : SC);
     };
     const auto sw_row = [](int row) { return swz<E>(row, ROWB / 16); };
-    const auto sw_t = [](int row) { return swz<E>(row, TROWB / 16); };
+    const auto sw_t = [](int row) { return swz_t<E>(row, TROWB / 16); };
     const auto sw_v = [](int row) { return swz_v(row, VROWB / 16); };
     auto load_chunk = [&](auto& cl, int c) {
         const long t0 = chunk_tok0(c);

@@ -274,7 +274,7 @@ def run_window(steps, warmup, dev, T=32768):
     st = lambda t_, dims: tuple(int(t_.stride(i)) for i in dims)
     args = (B, G, H // G, D, T, W, S, 0, _lib.DTYPE_BF16, qr.data_ptr(), *st(qr, (0, 1, 2)), kr.data_ptr(),
             *st(kr, (0, 1, 2)), v.data_ptr(), *st(v, (0, 2, 1)), None, None, None, sk.data_ptr(), sv.data_ptr(), S, 0,
-            None, None, None, None, o.data_ptr(), _lib.DTYPE_F32, lse.data_ptr(), stream_ptr(dev))
+            None, 0, None, None, None, o.data_ptr(), _lib.DTYPE_F32, lse.data_ptr(), stream_ptr(dev))
     for _ in range(warmup):
         _lib.check(lib.bf_window_fwd(*args), "bf_window_fwd")
     torch.cuda.synchronize()

@@ -115,7 +115,8 @@ struct WinArgs {
     const void* sink_v;
     int n_sinks;
     int mix_on;
-    const float* o_mem;       // [B][T][H][D]
+    const void* o_mem;        // [B][T][H][D] in o_mem_dtype
+    int o_mem_dtype;
     const float* z;           // [B][T][H]
     const float* mix_lse;     // [H]
     const float* mem_scale;   // [H]
@@ -124,6 +125,16 @@ struct WinArgs {
 };
 
 int window_dispatch(const WinArgs& a, hipStream_t stream);
+
+// 4 consecutive elements of the memory read (fp32 or bf16) at element index i (a multiple of 4) as fp32.
+__device__ __forceinline__ float4 load_om4(const WinArgs& a, long i) {
+    if (a.o_mem_dtype == DT_BF16) {
+        const uint2 v = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.o_mem) + i);
+        return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
+                           __uint_as_float(v.y & 0xffff0000u));
+    }
+    return *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.o_mem) + i);
+}
 
 struct MemProjArgs {
     const void* x;            // bf16 rows: token t, head h at x + t * x_st + h * x_sh (elements), D contiguous

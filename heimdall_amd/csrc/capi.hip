@@ -204,7 +204,7 @@ int bf_window_fwd(int B, int G, int R, int D, int T, int W, int sinks, int64_t s
                   int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
                   const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, const void* ring_k, const void* ring_v,
                   const int64_t* ring_pos, const void* sink_k, const void* sink_v, int n_sinks, int mix,
-                  const float* o_mem, const float* z, const float* mix_lse, const float* mem_scale, void* o,
+                  const void* o_mem, int o_mem_dtype, const float* z, const float* mix_lse, const float* mem_scale, void* o,
                   int o_dtype, float* lse, void* stream) {
     if (B <= 0 || G <= 0 || R <= 0 || T <= 0 || W <= 0 || sinks < 0 || start < 0) return BF_STATUS_INVALID;
     if (!supported_dim(D) || !supported_dtype(in_dtype) || !supported_dtype(o_dtype)) return BF_STATUS_UNSUPPORTED;
@@ -212,6 +212,7 @@ int bf_window_fwd(int B, int G, int R, int D, int T, int W, int sinks, int64_t s
     if ((ring_k == nullptr) != (ring_v == nullptr) || (ring_k && !ring_pos)) return BF_STATUS_INVALID;
     if (n_sinks < 0 || n_sinks > sinks || (n_sinks && (!sink_k || !sink_v))) return BF_STATUS_INVALID;
     if (mix && (!o_mem || !z || !mix_lse || !mem_scale)) return BF_STATUS_INVALID;
+    if (mix && !supported_dtype(o_mem_dtype)) return BF_STATUS_UNSUPPORTED;
     bf::WinArgs a{};
     a.B = B; a.G = G; a.R = R; a.D = D; a.T = T; a.W = W; a.sinks = sinks; a.start = start;
     a.in_dtype = in_dtype; a.o_dtype = o_dtype;
@@ -220,7 +221,7 @@ int bf_window_fwd(int B, int G, int R, int D, int T, int W, int sinks, int64_t s
     a.v = v; a.v_sb = v_sb; a.v_sh = v_sh; a.v_st = v_st;
     a.ring_k = ring_k; a.ring_v = ring_v; a.ring_pos = ring_pos;
     a.sink_k = sink_k; a.sink_v = sink_v; a.n_sinks = n_sinks;
-    a.mix_on = mix; a.o_mem = o_mem; a.z = z; a.mix_lse = mix_lse; a.mem_scale = mem_scale;
+    a.mix_on = mix; a.o_mem = o_mem; a.o_mem_dtype = o_mem_dtype; a.z = z; a.mix_lse = mix_lse; a.mem_scale = mem_scale;
     a.o = o; a.lse = lse;
     return bf::window_dispatch(a, static_cast<hipStream_t>(stream));
 }

@@ -337,7 +337,7 @@ __global__ __launch_bounds__(NT_WIN) void window_kernel(WinArgs a) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) r4[e] = o[dt][qt][e] * inv;
             if (gam != 0.f) {
-                const float4 om = *reinterpret_cast<const float4*>(a.o_mem + orow + d0);
+                const float4 om = load_om4(a, orow + d0);
                 r4[0] += gam * (ms * om.x - r4[0]);
                 r4[1] += gam * (ms * om.y - r4[1]);
                 r4[2] += gam * (ms * om.z - r4[2]);

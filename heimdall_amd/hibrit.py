@@ -201,9 +201,9 @@ def _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, mem
     if use_mem and start == 0 and s0 is None:
         n = t - w
         sl = lambda z, a_, e_: z[:, a_:e_].reshape(b * (e_ - a_), *z.shape[2:])
-        o_mem = torch.empty(b, t, H, D, dtype=torch.float32, device=dev)      # rows < W are never read
+        o_mem = torch.empty(b, t, H, D, dtype=cdt, device=dev)      # rows < W are never read
         om, s_new = gdn_forward(sl(qm, w, t).to(cdt), sl(km, 0, n).to(cdt), sl(v, 0, n).to(cdt), sl(g, 0, n),
-                                sl(beta, 0, n), num_seqs=b, out=o_mem[0, w:] if b == 1 else None)
+                                sl(beta, 0, n), num_seqs=b, out_dtype=cdt, out=o_mem[0, w:] if b == 1 else None)
         if b > 1:
             o_mem[:, w:] = om.view(b, n, H, D)
         z = F.linear(xf if xf is not None else x.float(), self.mix.weight.float(), self.mix.bias.float()).contiguous()
@@ -218,7 +218,7 @@ def _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, mem
         wb = torch.cat((st["ring_beta"][:, idx] * vf, beta), 1)[:, :t]
         o_mem, s_new = gdn_forward(qm.to(cdt).reshape(b * t, H, D), wk.to(cdt).reshape(b * t, G, D),
                                    wv.to(cdt).reshape(b * t, G, D), wg.reshape(b * t, G), wb.reshape(b * t, G),
-                                   num_seqs=b, initial_state=None if s0 is None else s0.float())
+                                   num_seqs=b, initial_state=None if s0 is None else s0.float(), out_dtype=cdt)
         o_mem = o_mem.view(b, t, H, D)
         z = F.linear(xf if xf is not None else x.float(), self.mix.weight.float(), self.mix.bias.float()).contiguous()
     # window + sinks + LSE (+ mix)
@@ -240,7 +240,8 @@ def _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, mem
     check(lib.bf_window_fwd(b, G, r, D, t, w, self.sinks, start, dtype_code(cdt),
                             ptr(q_), *_strides(q_, (0, 1, 2)), ptr(k_), *_strides(k_, (0, 1, 2)),
                             ptr(v_), *_strides(v_, (0, 2, 1)), ptr(rk), ptr(rv), ptr(st["ring_pos"]), ptr(sk),
-                            ptr(sv), ns, int(use_mem), ptr(o_mem), ptr(z), ptr(mix_lse), ptr(mem_scale), ptr(o),
+                            ptr(sv), ns, int(use_mem), ptr(o_mem), dtype_code(o_mem.dtype if use_mem else cdt), ptr(z),
+                            ptr(mix_lse), ptr(mem_scale), ptr(o),
                             dtype_code(torch.float32), ptr(lse), stream_ptr(dev)), "bf_window_fwd")
     # cache write-back: the last min(t, W) tokens take their ring slots
     n = min(t, w)

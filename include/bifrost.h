@@ -139,14 +139,15 @@ int bf_decode_fwd(int B, int G, int R, int D, int W, int sinks, int64_t pos, int
  * Layouts: q, k, v given by element strides (batch, head, token) with D contiguous: q over the H = G*R query heads,
  * k and v over the G KV heads (e.g. q [B][H][T][D] -> strides (H*T*D, T*D, D); v [B][T][G][D] -> (T*G*D, D, G*D)).
  * ring_k/ring_v [B][G][W][D], ring_pos [W] int64, sink_k/sink_v [B][G][n_sinks][D], all in in_dtype.
- * o_mem [B][T][H][D] f32, z [B][T][H] f32, mix_lse/mem_scale [H] f32; o [B][T][H][D] in o_dtype; lse [B][H][T] f32 or
+ * o_mem [B][T][H][D] in o_mem_dtype (fp32 or bf16), z [B][T][H] f32, mix_lse/mem_scale [H] f32; o [B][T][H][D] in o_dtype; lse [B][H][T] f32 or
  * null. Arithmetic: MFMA in in_dtype (bf16 probabilities for bf16 inputs) with fp32 accumulation and softmax.
  */
 int bf_window_fwd(int B, int G, int R, int D, int T, int W, int sinks, int64_t start, int in_dtype, const void* q,
                   int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
                   const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, const void* ring_k, const void* ring_v,
                   const int64_t* ring_pos, const void* sink_k, const void* sink_v, int n_sinks, int mix,
-                  const float* o_mem, const float* z, const float* mix_lse, const float* mem_scale, void* o,
+                  const void* o_mem, int o_mem_dtype, const float* z, const float* mix_lse, const float* mem_scale,
+                  void* o,
                   int o_dtype, float* lse, void* stream);
 
 /*

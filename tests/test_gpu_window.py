@@ -93,7 +93,8 @@ def run(c, dev, o_dtype=torch.float32, o_mem=None, z=None, mix_lse=None, mem_sca
                                  ptr(d["ring_k"]) if use_ring else None, ptr(d["ring_v"]) if use_ring else None,
                                  ptr(d["ring_pos"]) if use_ring else None,
                                  ptr(d["sink_k"]) if ns else None, ptr(d["sink_v"]) if ns else None, ns, int(mix),
-                                 ptr(om), ptr(zz), ptr(ml), ptr(ms), ptr(o), dtype_code(o_dtype), ptr(lse),
+                                 ptr(om), dtype_code(om.dtype) if mix else 0, ptr(zz), ptr(ml), ptr(ms), ptr(o),
+                                 dtype_code(o_dtype), ptr(lse),
                                  stream_ptr(dev)), "bf_window_fwd")
     torch.cuda.synchronize()
     return o.float().cpu(), lse.cpu()
@@ -139,6 +140,11 @@ def test_mix_and_bf16_output(dev):
     mem_scale = torch.full((4,), 16.0)
     check(c, dev, o_mem=o_mem, z=z, mix_lse=mix_lse, mem_scale=mem_scale)
     check(c, dev, o_dtype=torch.bfloat16, o_mem=o_mem, z=z, mix_lse=mix_lse, mem_scale=mem_scale)
+    # memory read stored as bf16 (the layer's bf16 path); the oracle mixes the same bf16-rounded values
+    omb = o_mem.bfloat16()
+    o, lse = run(c, dev, o_mem=omb, z=z, mix_lse=mix_lse, mem_scale=mem_scale)
+    o_ref, _ = oracle(c, o_mem=omb.float(), z=z, mix_lse=mix_lse, mem_scale=mem_scale)
+    assert rel(o, o_ref) < TOL_O, rel(o, o_ref)
 
 
 def test_production_geometry_bf16(dev):

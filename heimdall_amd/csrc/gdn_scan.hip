@@ -799,16 +799,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int steps = nseg - 1;
     // L2 warm-up: while step p runs, workgroup jb touches rows 16 jb .. 16 jb + 15 of Psi_{p+2}, so the 16 strips of a
     // head together bring the whole matrix into their XCD's L2 before any of them prefetches it. The touch is an LDS
-    // DMA into a discarded 1 KB area (a real, tracked load whose data is never read).
+    // DMA into a discarded 1 KB area (a real, tracked load whose data is never read), issued as a buffer load: a
+    // global load into LDS would count as a flat access and drain every LDS wait of the step to zero.
     __shared__ __align__(16) uint4 dump[64];
     auto touch = [&](int p) {
         if (p >= steps) return;
         const T* Psi = reinterpret_cast<const T*>(a.ws_phi) + ((long)(first + p) * G + g) * D * D;
-        const char* rows = reinterpret_cast<const char*>(Psi + (long)16 * jb * D);   // row tile jb (fragment order)
         constexpr int BYTES = 16 * D * (int)sizeof(T);
+        const rsrc_t rows = make_rsrc(Psi + (long)16 * jb * D, (uint32_t)BYTES);   // row tile jb (fragment order)
         for (int off = wv * 1024; off < BYTES; off += 4 * 1024)
-            __builtin_amdgcn_global_load_lds(rows + off + 16 * lane, (__attribute__((address_space(3))) void*)dump, 16,
-                                             0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rows, (__attribute__((address_space(3))) void*)dump, 16,
+                                                     (uint32_t)(off + 16 * lane), 0, 0, 0);
     };
     if constexpr (DBUF) {
         Pre P0, P1;

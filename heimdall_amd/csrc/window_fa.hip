@@ -15,8 +15,10 @@
 // max exceeds it by more than 8 (log2 units), so O is rescaled rarely and P stays <= 2^8.
 //
 // Keys come in blocks of 64 rows from one contiguous source (sinks, ring before / after its wrap point, chunk). A
-// block's K and V tiles are copied global -> LDS with buffer_load ... lds (no registers), double-buffered: block i+1
-// is in flight while block i is computed. Per wave, blocks no query of the wave can see are skipped and blocks every
+// block's K and V tiles are copied global -> LDS with buffer_load ... lds (no registers; one buffer descriptor per
+// source, lanes of other sources masked off), double-buffered: block i+1 is in flight while block i is computed.
+// Buffer rather than global loads: the compiler counts a global load into LDS as a flat access that may touch LDS
+// and then drains every LDS wait to zero while one is in flight, which serialised the fragment reads. Per wave, blocks no query of the wave can see are skipped and blocks every
 // query sees skip the mask. Workgroups are mapped XCD-aware: consecutive workgroups of one XCD take the R query
 // heads of one query block, then the next query block of the same KV head, so one L2 serves their K / V re-reads.
 #include "bf_common.h"
@@ -63,10 +65,6 @@ __device__ __forceinline__ uint2 fa_tr16(const char* p) {
     return make_uint2((uint16_t)v[0] | ((uint32_t)(uint16_t)v[1] << 16), (uint16_t)v[2] | ((uint32_t)(uint16_t)v[3] << 16));
 }
 
-// global_load_lds_dwordx4: 16 bytes from each lane's own address into LDS at dst + 16 * lane (dst wave-uniform).
-__device__ __forceinline__ void fa_g2l(const void* src, void* dst) {
-    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, 0, 0);
-}
 
 }  // namespace
 
@@ -133,37 +131,42 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
     const int slot_lo = rk ? (int)(kp_lo % a.W) : 0;               // ring slot of kp_lo (one division)
     const long start = a.start;
 
-    // row `row` of block i: key and value source addresses (an invalid row reads a valid dummy row)
-    auto row_src = [&](int i, int row, const uint16_t*& kr_, const uint16_t*& vr_) {
-        if (has_sink && i == 0) {
-            const int rr = row < ns ? row : 0;
-            kr_ = sk + (long)rr * D;
-            vr_ = sv + (long)rr * D;
-            return;
-        }
-        long kp = kp_lo + (long)(i - has_sink) * FA_KB + row;
-        kp = kp <= p_last ? kp : p_last;
-        if (kp >= start || !rk) {                      // no ring: rows before the chunk read chunk row 0 (masked)
-            const long cr = kp >= start ? kp - start : 0;
-            kr_ = ck + cr * a.k_st;
-            vr_ = cv + cr * a.v_st;
-        } else {
-            int slot = slot_lo + (int)(kp - kp_lo);
-            slot = slot >= a.W ? slot - a.W : slot;
-            kr_ = rk + (long)slot * D;
-            vr_ = rv + (long)slot * D;
-        }
+    // copy block i's K and V rows into tile t (row r's 16-byte block pb holds the row's block pb ^ sw(r)) with
+    // buffer_load ... lds: one descriptor per source (sinks, ring, chunk), lanes of other sources masked off
+    const rsrc_t rsk = make_rsrc(sk, (uint32_t)(ns * ROWB)), rsv = make_rsrc(sv, (uint32_t)(ns * ROWB));
+    const rsrc_t rrk = make_rsrc(rk, rk ? (uint32_t)(a.W * ROWB) : 0u), rrv = make_rsrc(rv, rv ? (uint32_t)(a.W * ROWB) : 0u);
+    const rsrc_t rck = make_rsrc(ck, (uint32_t)(((long)(a.T - 1) * a.k_st + D) * 2));
+    const rsrc_t rcv = make_rsrc(cv, (uint32_t)(((long)(a.T - 1) * a.v_st + D) * 2));
+    auto dma = [](rsrc_t r, void* dst, uint32_t off) {   // 16 bytes at byte offset off (per lane) -> dst + 16 lane
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, off, 0, 0, 0);
     };
-    // copy block i's K and V rows into tile t (row r's 16-byte block pb holds the row's block pb ^ sw(r))
     auto stage = [&](FaTile<D>& t, int i) {
+        const bool sinkblk = has_sink && i == 0;
 #pragma unroll
         for (int j = 0; j < NLD; ++j) {
             const int c = (wv + NW * j) * 64 + lane;                   // 16-byte slot of the tile
             const int row = c / NBLK, pb = c % NBLK;
-            const uint16_t *kr_, *vr_;
-            row_src(i, row, kr_, vr_);
-            fa_g2l(kr_ + 8 * (pb ^ fa_swk<NBLK>(row)), reinterpret_cast<char*>(t.k) + (wv + NW * j) * 1024);
-            fa_g2l(vr_ + 8 * (pb ^ fa_swv<NBLK>(row)), reinterpret_cast<char*>(t.v) + (wv + NW * j) * 1024);
+            const uint32_t kb = 16u * (pb ^ fa_swk<NBLK>(row)), vb = 16u * (pb ^ fa_swv<NBLK>(row));
+            char* dk = reinterpret_cast<char*>(t.k) + (wv + NW * j) * 1024;
+            char* dv = reinterpret_cast<char*>(t.v) + (wv + NW * j) * 1024;
+            if (sinkblk) {
+                const uint32_t rr = row < ns ? (uint32_t)row : 0u;
+                dma(rsk, dk, rr * ROWB + kb);
+                dma(rsv, dv, rr * ROWB + vb);
+                continue;
+            }
+            long kp = kp_lo + (long)(i - has_sink) * FA_KB + row;
+            kp = kp <= p_last ? kp : p_last;
+            if (kp >= start || !rk) {                  // no ring: rows before the chunk read chunk row 0 (masked)
+                const long cr = kp >= start ? kp - start : 0;
+                dma(rck, dk, (uint32_t)(cr * a.k_st * 2) + kb);
+                dma(rcv, dv, (uint32_t)(cr * a.v_st * 2) + vb);
+            } else {
+                int slot = slot_lo + (int)(kp - kp_lo);
+                slot = slot >= a.W ? slot - a.W : slot;
+                dma(rrk, dk, (uint32_t)slot * ROWB + kb);
+                dma(rrv, dv, (uint32_t)slot * ROWB + vb);
+            }
         }
     };
     // ring_pos of row `lane` of block i (0 when the row is not a ring row)
@@ -403,6 +406,9 @@ int launch_window_fa(const WinArgs& a, hipStream_t stream) {
     const long nwork = (long)a.B * a.G * nqb * a.R;
     const long per = (nwork + FA_NXCD - 1) / FA_NXCD;
     if (FA_NXCD * per > 0x7fffffffL) return BF_STATUS_INVALID;
+    // chunk K / V rows are addressed by 32-bit buffer offsets
+    if (((long)(a.T - 1) * a.k_st + D) * 2 > 0xffffffffL || ((long)(a.T - 1) * a.v_st + D) * 2 > 0xffffffffL)
+        return BF_ERR_UNSUPPORTED;
     const dim3 grid((unsigned)(FA_NXCD * per)), block(FaShape<D>::NT);
     if (a.o_dtype == DT_BF16) hipLaunchKernelGGL((window_fa_kernel<D, true>), grid, block, 0, stream, a);
     else hipLaunchKernelGGL((window_fa_kernel<D, false>), grid, block, 0, stream, a);

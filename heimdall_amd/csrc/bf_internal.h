@@ -147,6 +147,44 @@ struct MemProjArgs {
 };
 
 int mem_project_dispatch(const MemProjArgs& a, hipStream_t stream);
-int window_fa_dispatch(const WinArgs& a, hipStream_t stream);   // bf16 operands
+int window_fa_dispatch(const WinArgs& a, hipStream_t stream);
+
+struct GdnInArgs {
+    const void* z;            // [N_tok][C] in_dtype rows (C = (2 HK + HV) D channels [q | k | v]), z_st elements apart
+    long z_st;
+    const void* prefix;       // [num_seqs][K - 1][C] in_dtype: the rows before each sequence's start, or null (zeros)
+    int in_dtype;
+    const float* w;           // [C][K] conv weights, column K - 1 = the current token
+    const float* a;           // [N_tok][HV]
+    const float* b;           // [N_tok][HV]
+    const float* A_log;       // [HV]
+    const float* dt_bias;     // [HV]
+    const int32_t* cu_seqlens;  // [num_seqs + 1]
+    int num_seqs;
+    long n_tok;
+    int HK, HV, D, K;
+    int out_dtype;
+    float eps, q_scale;
+    void* q;                  // [N_tok][HV][D] out_dtype
+    void* k;                  // [N_tok][HV][D] out_dtype
+    void* v;                  // [N_tok][HV][D] out_dtype
+    float* g;                 // [N_tok][HV]
+    float* beta;              // [N_tok][HV]
+};
+int gdn_conv_inputs_dispatch(const GdnInArgs& a, hipStream_t stream);
+
+struct GatedNormArgs {
+    const void* o;            // [rows][D] o_dtype
+    int o_dtype;
+    const void* z;            // [rows][D] io_dtype gate
+    const float* w;           // [D]
+    void* out;                // [rows][D] io_dtype
+    int io_dtype;
+    long rows;
+    int D;
+    float eps;
+};
+int gated_norm_dispatch(const GatedNormArgs& a, hipStream_t stream);
+   // bf16 operands
 
 }  // namespace bf

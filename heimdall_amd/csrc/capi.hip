@@ -239,4 +239,40 @@ int bf_mem_project(const void* x, int64_t n_tok, int nh, int D, int64_t x_st, in
     return bf::mem_project_dispatch(a, static_cast<hipStream_t>(stream));
 }
 
+int bf_gdn_conv_inputs(const void* z, int64_t z_st, const void* prefix, int in_dtype, const float* conv_w, int K,
+                       const float* a, const float* b, const float* A_log, const float* dt_bias,
+                       const int32_t* cu_seqlens, int num_seqs, int64_t n_tok, int HK, int HV, int D, float eps,
+                       float q_scale, void* q, void* k, void* v, float* g, float* beta, int out_dtype, void* stream) {
+    if (n_tok < 0 || num_seqs <= 0 || HK <= 0 || HV <= 0 || HV % HK || K < 1 || K > 16) return BF_STATUS_INVALID;
+    if (!supported_dim(D) || !supported_dtype(in_dtype) || !supported_dtype(out_dtype)) return BF_STATUS_UNSUPPORTED;
+    if (n_tok == 0) return BF_STATUS_OK;
+    if (!z || !conv_w || !a || !b || !A_log || !dt_bias || !cu_seqlens || !q || !k || !v || !g || !beta)
+        return BF_STATUS_INVALID;
+    if (z_st < (int64_t)(2 * HK + HV) * D || z_st % 8) return BF_STATUS_INVALID;
+    // 16-byte vector accesses: rows of 8 elements start 16-byte aligned
+    auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    if (!al16(z) || !al16(prefix) || !al16(conv_w) || !al16(q) || !al16(k) || !al16(v)) return BF_STATUS_INVALID;
+    bf::GdnInArgs x{};
+    x.z = z; x.z_st = z_st; x.prefix = prefix; x.in_dtype = in_dtype;
+    x.w = conv_w; x.a = a; x.b = b; x.A_log = A_log; x.dt_bias = dt_bias;
+    x.cu_seqlens = cu_seqlens; x.num_seqs = num_seqs; x.n_tok = n_tok;
+    x.HK = HK; x.HV = HV; x.D = D; x.K = K; x.out_dtype = out_dtype; x.eps = eps; x.q_scale = q_scale;
+    x.q = q; x.k = k; x.v = v; x.g = g; x.beta = beta;
+    return bf::gdn_conv_inputs_dispatch(x, static_cast<hipStream_t>(stream));
+}
+
+int bf_gated_norm(const void* o, int o_dtype, const void* z, const float* w, int64_t rows, int D, float eps,
+                  void* out, int io_dtype, void* stream) {
+    if (rows < 0) return BF_STATUS_INVALID;
+    if (!supported_dim(D) || !supported_dtype(o_dtype) || !supported_dtype(io_dtype)) return BF_STATUS_UNSUPPORTED;
+    if (rows == 0) return BF_STATUS_OK;
+    if (!o || !z || !w || !out) return BF_STATUS_INVALID;
+    auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    if (!al16(o) || !al16(z) || !al16(out)) return BF_STATUS_INVALID;
+    bf::GatedNormArgs x{};
+    x.o = o; x.o_dtype = o_dtype; x.z = z; x.w = w; x.out = out; x.io_dtype = io_dtype;
+    x.rows = rows; x.D = D; x.eps = eps;
+    return bf::gated_norm_dispatch(x, static_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"

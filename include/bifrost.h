@@ -165,6 +165,37 @@ int bf_window_fwd(int B, int G, int R, int D, int T, int W, int sinks, int64_t s
 int bf_mem_project(const void* x, int64_t n_tok, int nh, int D, int64_t x_st, int64_t x_sh, const void* ft,
                    float scale, void* out, int in_dtype, void* stream);
 
+/*
+ * Native Gated DeltaNet layer, the pass before the delta rule: GatedDeltaNet.forward up to delta_rule
+ * (Heimdall/heimdall/hibrit.py:159-179) with causal_conv (Heimdall/heimdall/kernels.py:29-37) and l2norm
+ * (hibrit.py:132-133), for packed sequences.
+ *   y = SiLU(causal depthwise conv of z), y_c[t] = sum_j conv_w[c][K-1-j] z[t-j][c], rows before a sequence's first
+ *       token taken from `prefix` (the reference's cache["conv"]) or zero;
+ *   q_h = q_scale * l2norm(y_q[h / r]), k_h = l2norm(y_k[h / r]), v_h = y_v[h] for the HV value heads (r = HV / HK,
+ *       the reference's repeat_interleave), l2norm(x) = x / sqrt(sum x^2 + eps);
+ *   beta = sigmoid(b), g = -exp(A_log) * softplus(a + dt_bias) (softplus threshold 20).
+ * Layouts: z [n_tok][C] in in_dtype with C = (2 HK + HV) D channels ordered [q | k | v] and z_st >= C elements
+ * between tokens; prefix [num_seqs][K-1][C] in in_dtype or null; conv_w [C][K] f32 (column K-1 = the current token); a, b
+ * [n_tok][HV] f32; A_log, dt_bias [HV] f32; cu_seqlens [num_seqs + 1] int32 (device); q, k, v [n_tok][HV][D] in
+ * out_dtype; g, beta [n_tok][HV] f32. D_k = D_v = D. z, prefix, conv_w, q, k, v 16-byte aligned and z_st a multiple
+ * of 8. The new conv cache (the last K-1 rows of [prefix; z] per
+ * sequence) is the caller's slice.
+ */
+int bf_gdn_conv_inputs(const void* z, int64_t z_st, const void* prefix, int in_dtype, const float* conv_w, int K,
+                       const float* a, const float* b, const float* A_log, const float* dt_bias,
+                       const int32_t* cu_seqlens, int num_seqs, int64_t n_tok, int HK, int HV, int D, float eps,
+                       float q_scale, void* q, void* k, void* v, float* g, float* beta, int out_dtype, void* stream);
+
+/*
+ * GatedNorm of the native layer's output (Heimdall/heimdall/hibrit.py:118-129, applied at :183), per row of D:
+ *   io_dtype fp32: out = w * o * rsqrt(mean(o^2) + eps) * SiLU(z);
+ *   io_dtype bf16: out = bf16(bf16(w * bf16(o_b * rsqrt(mean(o_b^2) + eps))) * SiLU(z)), o_b = o rounded to bf16
+ *                  (the rounding points of the reference's bf16 layer).
+ * o [rows][D] in o_dtype, z [rows][D] and out [rows][D] in io_dtype (o, z, out 16-byte aligned), w [D] f32.
+ */
+int bf_gated_norm(const void* o, int o_dtype, const void* z, const float* w, int64_t rows, int D, float eps,
+                  void* out, int io_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

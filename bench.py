@@ -255,6 +255,74 @@ def run_varlen(steps, warmup, dev):
             "tflops_reference": flops / (ms * 1e-3) / 1e12, "GBs": nbytes / (ms * 1e-3) / 1e9}
 
 
+def run_gdn_layer(steps, warmup, dev):
+    """The native Gated DeltaNet layer between its frozen projections on configuration 4's packed input (4 sequences
+    {8192, 16384, 24576, 16384}, H = 32 key and value heads, D = 128, conv width 4, bf16): z = in_proj_qkv(x),
+    a, b, zg synthetic (the projections are PyTorch matrix products outside the measured core). One step =
+    bf_gdn_conv_inputs -> bf_gdn_fwd (varlen) -> bf_gated_norm, with HIP events between the three on the launch
+    stream. The two memory-bound passes are priced against HBM by their algorithmic bytes (each tensor read or
+    written once)."""
+    from heimdall_amd import gdn_layer as gl
+    from heimdall_amd._device import gdn_forward
+
+    lens = (8192, 16384, 24576, 16384)
+    hk = hv = 32
+    D, K = 128, 4
+    N = sum(lens)
+    C = (2 * hk + hv) * D
+    cu = torch.tensor([0, 8192, 24576, 49152, 65536], dtype=torch.int32, device=dev)
+    torch.manual_seed(5)
+    m = gl.GatedDeltaNet(gl.GdnLayerConfig(d=64, lin_hk=hk, lin_hv=hv, lin_dk=D, lin_dv=D, conv_k=K))
+    with torch.no_grad():
+        m.conv1d.weight.normal_(0, 0.5)
+        m.A_log.uniform_(-6, -2)
+        m.dt_bias.normal_()
+    m = m.to(dev)
+    gen = torch.Generator(device=dev).manual_seed(6)
+    z = torch.randn(N, C, device=dev, generator=gen).bfloat16()
+    a = torch.randn(N, hv, device=dev, generator=gen)
+    b = torch.randn(N, hv, device=dev, generator=gen)
+    zg = torch.randn(N, hv * D, device=dev, generator=gen).bfloat16()
+    w = m.conv1d.weight[:, 0].detach()
+
+    def step(ev=None):
+        q, k, v, g, beta = gl.conv_inputs(z, w, None, a, b, m.A_log.detach(), m.dt_bias.detach(), hk, hv, D,
+                                          cu_seqlens=cu)
+        if ev:
+            ev[1].record(stream)
+        o, s = gdn_forward(q, k, v, g, beta, num_seqs=len(lens), cu_seqlens=cu, out_dtype=torch.bfloat16)
+        if ev:
+            ev[2].record(stream)
+        return gl.gated_norm(o, zg.view(N, hv, D), m.norm.weight.detach())
+
+    stream = torch.cuda.current_stream(dev)
+    with torch.no_grad():
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+        for ev in evs:
+            ev[0].record(stream)
+            step(ev)
+            ev[3].record(stream)
+        torch.cuda.synchronize()
+    parts = [sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps for j in range(3)]
+    ms = sum(parts)
+    conv_bytes = N * (C * 2 + 2 * hv * 4 + 3 * hv * D * 2 + 2 * hv * 4) + C * K * 4
+    norm_bytes = N * hv * D * 2 * 3
+    gb = lambda nbytes, t: nbytes / (t * 1e-3) / 1e9
+    return {"workload": "native Gated DeltaNet layer core, 4 packed seqs {8192,16384,24576,16384}, H=32, D=128, "
+                        "conv 4, bf16",
+            "ms_per_step": ms, "tokens_per_s": N / (ms * 1e-3), "steps": steps,
+            "ms": {"conv_inputs": parts[0], "delta_rule": parts[1], "gated_norm": parts[2]},
+            "conv_inputs_roofline": {"bound": "hbm", "achieved": gb(conv_bytes, parts[0]), "peak": HBM_PEAK_GBS,
+                                     "unit": "GB/s", "frac": gb(conv_bytes, parts[0]) / HBM_PEAK_GBS,
+                                     "bytes": conv_bytes},
+            "gated_norm_roofline": {"bound": "hbm", "achieved": gb(norm_bytes, parts[2]), "peak": HBM_PEAK_GBS,
+                                    "unit": "GB/s", "frac": gb(norm_bytes, parts[2]) / HBM_PEAK_GBS,
+                                    "bytes": norm_bytes}}
+
+
 def run_window(steps, warmup, dev, T=32768):
     """The window kernel alone on the layer prefill's shapes (B=1, H=24, G=4, D=256, W=2048 + 4 sinks, bf16, from
     position 0 with the first 4 tokens as sinks, no ring, no mix): bf_window_fwd timed with HIP events on the launch
@@ -343,7 +411,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the decode and layer-prefill legs")
     ap.add_argument("--copy-probe", action="store_true", help="run one 256 MiB device copy first (counter scaling)")
     ap.add_argument("--segment-chunks", type=int, default=0, help="chunks per scan segment (0 = library default)")
-    ap.add_argument("--only", choices=("decode", "layer", "layer131k", "window", "varlen"), default=None,
+    ap.add_argument("--only", choices=("decode", "layer", "layer131k", "window", "varlen", "gdn_layer"), default=None,
                     help="run one secondary leg alone and print its JSON object (for per-workload profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -365,7 +433,8 @@ def main():
                "layer": lambda: run_layer(args.steps, args.warmup, dev),
                "layer131k": lambda: run_layer(args.steps, args.warmup, dev, T=131072),
                "window": lambda: run_window(args.steps, args.warmup, dev),
-               "varlen": lambda: run_varlen(args.steps, args.warmup, dev)}[args.only]
+               "varlen": lambda: run_varlen(args.steps, args.warmup, dev),
+               "gdn_layer": lambda: run_gdn_layer(args.steps, args.warmup, dev)}[args.only]
         print(json.dumps(leg()), flush=True)
         return
 
@@ -409,6 +478,7 @@ def main():
         line["layer_prefill_32k"] = run_layer(3, 1, dev)
         line["layer_prefill_32k"]["window_kernel"] = run_window(10, 3, dev)
         line["varlen_gdn"] = run_varlen(10, 3, dev)
+        line["gdn_layer"] = run_gdn_layer(10, 3, dev)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(r["inputs"])
     print(json.dumps(line), flush=True)

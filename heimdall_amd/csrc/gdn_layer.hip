@@ -8,8 +8,8 @@
 //                                                   carried prefix (or zero)
 //   q_h = D^-1/2 l2norm(y_q(h / r)), k_h = l2norm(y_k(h / r)), v_h = y_v(h)     for the HV value heads, r = HV / HK
 //   beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias)
-// One unit = one (token, q / k / v head) of D channels, handled by D / 8 consecutive lanes of 8 channels each; the
-// l2norm sum is a butterfly over those lanes. q and k are written once per value head that reads them (the
+// One unit = one q / k / v head of D channels, handled by D / 8 consecutive lanes of 8 channels each; the l2norm sum
+// is a butterfly over those lanes. q and k are written once per value head that reads them (the
 // reference's repeat_interleave), so the delta rule sees one key per state.
 //
 // gated_norm_kernel: out = w * RMSNorm(o) * SiLU(zg) per row of D; a bf16 layer keeps the reference's bf16 rounding
@@ -162,6 +162,91 @@ __global__ __launch_bounds__(256) void gdn_conv_inputs_kernel(GdnInArgs a) {
     }
 }
 
+// Conv width K = 4 (the models'): a thread keeps one unit's 8 channels over a block of CT consecutive tokens, with
+// the channels' weights and the previous three rows in registers, so z is read once and the weights once per block
+// (the per-token kernel above re-reads 4 rows and 128 bytes of weights for every 16 bytes of output).
+constexpr int CT = 32;
+
+template <int D, bool BF>
+__global__ __launch_bounds__(256) void gdn_conv_inputs_k4_kernel(GdnInArgs a) {
+    constexpr int LPU = D / 8, UPB = 256 / LPU;
+    const int U = 2 * a.HK + a.HV;
+    const int ugroups = (U + UPB - 1) / UPB;
+    const long n0 = (long)(blockIdx.x / ugroups) * CT;
+    const int u = (blockIdx.x % ugroups) * UPB + (int)threadIdx.x / LPU;
+    const int s = (int)threadIdx.x % LPU;
+    const bool uv = u < U;                                // the unit exists (all lanes of a unit agree)
+    const int uu = uv ? u : 0;
+    const int kind = uu < a.HK ? 0 : (uu < 2 * a.HK ? 1 : 2);
+    const int head = kind == 0 ? uu : (kind == 1 ? uu - a.HK : uu - 2 * a.HK);
+    const long C = (long)U * D;
+    const int c0 = (kind == 0 ? head * D : (kind == 1 ? (a.HK + head) * D : 2 * a.HK * D + head * D)) + 8 * s;
+    const long n1 = n0 + CT < a.n_tok ? n0 + CT : a.n_tok;
+
+    float w[4][8];                                        // w[j][e]: tap j (token n - j) of channel c0 + e
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float4 wc = uv ? *reinterpret_cast<const float4*>(a.w + (long)(c0 + e) * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+        w[0][e] = wc.w; w[1][e] = wc.z; w[2][e] = wc.y; w[3][e] = wc.x;
+    }
+    // sequence of n0
+    int seq = 0, hi = a.num_seqs;
+    while (hi - seq > 1) {
+        const int mid = (seq + hi) >> 1;
+        if (a.cu_seqlens[mid] <= n0) seq = mid;
+        else hi = mid;
+    }
+    long seq0 = a.cu_seqlens[seq], seq_end = a.cu_seqlens[seq + 1];
+    // rows n - 1, n - 2, n - 3 of the current token n
+    float r1[8], r2[8], r3[8];
+    auto fill = [&](long n) {
+        load_tap<BF>(a, uv, n, 1, seq0, seq, C, c0, r1);
+        load_tap<BF>(a, uv, n, 2, seq0, seq, C, c0, r2);
+        load_tap<BF>(a, uv, n, 3, seq0, seq, C, c0, r3);
+    };
+    fill(n0);
+    const int r = a.HV / a.HK;
+    for (long n = n0; n < n1; ++n) {
+        while (n == seq_end) {                            // a new sequence starts at n: rows before it from its prefix
+            ++seq;
+            seq0 = n;
+            seq_end = a.cu_seqlens[seq + 1];
+            fill(n);
+        }
+        float x[8], y[8];
+        load8<BF>(a.z, n * a.z_st + c0, uv, x);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            y[e] = silu(w[0][e] * x[e] + w[1][e] * r1[e] + w[2][e] * r2[e] + w[3][e] * r3[e]);
+            r3[e] = r2[e];
+            r2[e] = r1[e];
+            r1[e] = x[e];
+        }
+        if (kind < 2) {
+            float ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += y[e] * y[e];
+            ss = unit_sum<LPU>(ss);
+            const float f = rsqrtf(ss + a.eps) * (kind == 0 ? a.q_scale : 1.f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) y[e] *= f;
+            if (uv) {
+                void* dst = kind == 0 ? a.q : a.k;
+                for (int rr = 0; rr < r; ++rr) store8(dst, (n * a.HV + head * r + rr) * D + 8 * s, a.out_dtype, y);
+            }
+        } else if (uv) {
+            store8(a.v, (n * a.HV + head) * D + 8 * s, a.out_dtype, y);
+            if (s == 0) {
+                const long gi = n * a.HV + head;
+                const float xg = a.a[gi] + a.dt_bias[head];
+                const float sp = xg > 20.f ? xg : log1pf(__expf(xg));
+                a.g[gi] = -__expf(a.A_log[head]) * sp;
+                a.beta[gi] = 1.f / (1.f + __expf(-a.b[gi]));
+            }
+        }
+    }
+}
+
 template <int D, bool BF>
 __global__ __launch_bounds__(256) void gated_norm_kernel(GatedNormArgs a) {
     constexpr int LPR = D / 8;
@@ -203,6 +288,23 @@ __global__ __launch_bounds__(256) void gated_norm_kernel(GatedNormArgs a) {
 int gdn_conv_inputs_dispatch(const GdnInArgs& a, hipStream_t stream) {
     const long threads = a.n_tok * (2 * a.HK + a.HV) * (a.D / 8);
     if (threads == 0) return 0;
+    if (a.K == 4) {
+        const int upb = 256 / (a.D / 8), U = 2 * a.HK + a.HV;
+        const long blocks = ((a.n_tok + CT - 1) / CT) * ((U + upb - 1) / upb);
+        if (blocks > 0x7fffffffL) return BF_STATUS_INVALID;
+        const dim3 grid((unsigned)blocks), block(256);
+        const bool bf = a.in_dtype == DT_BF16;
+        switch (a.D) {
+            case 64: if (bf) hipLaunchKernelGGL((gdn_conv_inputs_k4_kernel<64, true>), grid, block, 0, stream, a);
+                     else hipLaunchKernelGGL((gdn_conv_inputs_k4_kernel<64, false>), grid, block, 0, stream, a); break;
+            case 128: if (bf) hipLaunchKernelGGL((gdn_conv_inputs_k4_kernel<128, true>), grid, block, 0, stream, a);
+                      else hipLaunchKernelGGL((gdn_conv_inputs_k4_kernel<128, false>), grid, block, 0, stream, a); break;
+            case 256: if (bf) hipLaunchKernelGGL((gdn_conv_inputs_k4_kernel<256, true>), grid, block, 0, stream, a);
+                      else hipLaunchKernelGGL((gdn_conv_inputs_k4_kernel<256, false>), grid, block, 0, stream, a); break;
+            default: return BF_ERR_UNSUPPORTED;
+        }
+        return (int)hipGetLastError();
+    }
     const long blocks = (threads + 255) / 256;
     if (blocks > 0x7fffffffL) return BF_STATUS_INVALID;
     const dim3 grid((unsigned)blocks), block(256);

@@ -323,6 +323,37 @@ def run_gdn_layer(steps, warmup, dev):
                                     "bytes": norm_bytes}}
 
 
+def run_teacher(steps, warmup, dev, T=32768):
+    """The conversion teacher's causal GQA attention (motor.blockwise_attention, Heimdall/heimdall/motor.py:41-67) on
+    the layer's shapes (B=1, H=24, G=4, D=256, bf16, fp32 output): bf_window_fwd with W = T and no sinks, timed with
+    HIP events. Algorithmic work: 4 D FLOP per (query, key <= query) pair and query head."""
+    from heimdall_amd import motor
+
+    B, H, G, D = 1, 24, 4, 256
+    gen = torch.Generator(device=dev).manual_seed(7)
+    qr = F.normalize(torch.randn(B, H, T, D, device=dev, generator=gen), dim=-1).bfloat16()
+    kr = F.normalize(torch.randn(B, G, T, D, device=dev, generator=gen), dim=-1).bfloat16()
+    vt = torch.randn(B, G, T, D, device=dev, generator=gen).bfloat16()
+    with torch.no_grad():
+        for _ in range(warmup):
+            motor.blockwise_attention(qr, kr, vt)
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            motor.blockwise_attention(qr, kr, vt)
+        e1.record(stream)
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = 4 * D * H * T * (T + 1) // 2
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"workload": f"teacher causal attention B=1 T={T} H=24 G=4 D=256 bf16", "ms_per_step": ms,
+            "tokens_per_s": T / (ms * 1e-3), "steps": steps, "flops": flops,
+            "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": tf / BF16_PEAK_TFLOPS}}
+
+
 def run_window(steps, warmup, dev, T=32768):
     """The window kernel alone on the layer prefill's shapes (B=1, H=24, G=4, D=256, W=2048 + 4 sinks, bf16, from
     position 0 with the first 4 tokens as sinks, no ring, no mix): bf_window_fwd timed with HIP events on the launch
@@ -411,7 +442,7 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the decode and layer-prefill legs")
     ap.add_argument("--copy-probe", action="store_true", help="run one 256 MiB device copy first (counter scaling)")
     ap.add_argument("--segment-chunks", type=int, default=0, help="chunks per scan segment (0 = library default)")
-    ap.add_argument("--only", choices=("decode", "layer", "layer131k", "window", "varlen", "gdn_layer"), default=None,
+    ap.add_argument("--only", choices=("decode", "layer", "layer131k", "window", "varlen", "gdn_layer", "teacher"), default=None,
                     help="run one secondary leg alone and print its JSON object (for per-workload profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -434,7 +465,8 @@ def main():
                "layer131k": lambda: run_layer(args.steps, args.warmup, dev, T=131072),
                "window": lambda: run_window(args.steps, args.warmup, dev),
                "varlen": lambda: run_varlen(args.steps, args.warmup, dev),
-               "gdn_layer": lambda: run_gdn_layer(args.steps, args.warmup, dev)}[args.only]
+               "gdn_layer": lambda: run_gdn_layer(args.steps, args.warmup, dev),
+               "teacher": lambda: run_teacher(args.steps, args.warmup, dev)}[args.only]
         print(json.dumps(leg()), flush=True)
         return
 

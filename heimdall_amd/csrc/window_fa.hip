@@ -20,7 +20,9 @@
 // Buffer rather than global loads: the compiler counts a global load into LDS as a flat access that may touch LDS
 // and then drains every LDS wait to zero while one is in flight, which serialised the fragment reads. Per wave, blocks no query of the wave can see are skipped and blocks every
 // query sees skip the mask. Workgroups are mapped XCD-aware: consecutive workgroups of one XCD take the R query
-// heads of one query block, then the next query block of the same KV head, so one L2 serves their K / V re-reads.
+// heads of one query block, then the previous query block of the same KV head, so one L2 serves their K / V
+// re-reads; query blocks go from last to first, so with a window as long as the chunk (causal attention, the
+// teacher's blockwise attention) the longest workgroups start first.
 #include "bf_common.h"
 #include "bf_internal.h"
 
@@ -90,7 +92,7 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
     if (wi >= nwork) return;
     const int r = (int)(wi % R);
     long rest = wi / R;
-    const int qb = (int)(rest % nqb);
+    const int qb = nqb - 1 - (int)(rest % nqb);        // later query blocks (the most keys) are dispatched first
     rest /= nqb;
     const int g = (int)(rest % G), b = (int)(rest / G);
     const int h = g * R + r;

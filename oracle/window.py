@@ -5,6 +5,8 @@ position p, the visible keys are the sinks j < min(S, p + 1) and the window keys
 (mask of ``hibrit.py:356``). Scores are (q . k) / sqrt(D), the LSE is the natural-log normaliser over the visible
 keys, and the output is the softmax-weighted sum of V. Computed in fp32 (or fp64 for fp64 inputs) in query blocks
 of W rows, as the reference does, so memory stays O(T * W).
+
+``blockwise_attention`` restates the teacher's causal GQA attention (``Heimdall/heimdall/motor.py:41-67``).
 """
 import torch
 
@@ -54,3 +56,21 @@ def window_attention_from_start(qr, kr, vt, window: int, sinks: int):
     n = min(sinks, t)
     return window_attention_lse(qr, ext_k, ext_v, ext_pos, kr[:, :, :n] if n else None,
                                 vt[:, :, :n] if n else None, pos, window, sinks)
+
+
+def blockwise_attention(qr, kr, vt):
+    """Causal full attention with GQA (``Heimdall/heimdall/motor.py:41-67``; the reference computes it with an
+    online softmax over key blocks, which is the same function). qr [B, H, T, D], kr / vt [B, G, T, D] ->
+    o [B, T, H, D] in the compute dtype."""
+    dt = torch.float64 if qr.dtype == torch.float64 else torch.float32
+    b, h, t, d = qr.shape
+    g = kr.size(1)
+    q = qr.to(dt).reshape(b, g, h // g, t, d) * d ** -0.5
+    outs = []
+    for q0 in range(0, t, 1024):
+        q1 = min(t, q0 + 1024)
+        sc = torch.matmul(q[:, :, :, q0:q1], kr.to(dt)[:, :, None, :q1].transpose(-1, -2).contiguous())
+        mask = torch.arange(q1)[None, :] > torch.arange(q0, q1)[:, None]
+        p = torch.softmax(sc.masked_fill(mask, float("-inf")), -1)
+        outs.append(torch.matmul(p, vt.to(dt)[:, :, None, :q1]))
+    return torch.cat(outs, 3).reshape(b, h, t, d).transpose(1, 2).contiguous()

@@ -157,3 +157,22 @@ def test_production_geometry_ring_bf16(dev):
     print("window bf16 production ring: H=8 G=2 D=256 W=2048 S=4 T=700 start=5000", flush=True)
     c = make_case(1, 8, 2, 256, 700, 2048, 4, 5000, seed=6)
     check(c, dev)
+
+
+@pytest.mark.parametrize("dtype,D,T", [(torch.bfloat16, 64, 777), (torch.bfloat16, 128, 300), (torch.bfloat16, 256, 1000),
+                                       (torch.float32, 128, 500), (torch.bfloat16, 256, 4096)])
+def test_teacher_causal_attention(dev, dtype, D, T):
+    """motor.blockwise_attention (the teacher's causal GQA attention) on bf_window_fwd with W = T and no sinks."""
+    from heimdall_amd.motor import blockwise_attention
+    B, H, G = (2, 6, 2) if T < 4096 else (1, 8, 2)
+    print(f"teacher causal attention {dtype} B={B} H={H} G={G} D={D} T={T}", flush=True)
+    gen = torch.Generator().manual_seed(T + D)
+    qr = torch.randn(B, H, T, D, generator=gen).to(dtype)
+    kr = torch.randn(B, G, T, D, generator=gen).to(dtype)
+    vt = torch.randn(B, G, T, D, generator=gen).to(dtype)
+    o = blockwise_attention(qr.to(dev), kr.to(dev), vt.to(dev))
+    torch.cuda.synchronize()
+    ref = owin.blockwise_attention(qr.float(), kr.float(), vt.float())
+    err = rel(o, ref)
+    print(f"  rel(o)={err:.2e}", flush=True)
+    assert err < (1e-4 if dtype == torch.float32 else TOL_O), err

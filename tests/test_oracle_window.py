@@ -79,3 +79,19 @@ def test_ring_split_equals_single_call():
     ext_pos = torch.cat((torch.arange(a - w, a), pos))
     o, lse = win.window_attention_lse(qr[:, :, a:], ext_k, ext_v, ext_pos, kr[:, :, :s], vt[:, :, :s], pos, w, s)
     assert (o - o_full[:, a:]).abs().max() < 1e-12 and (lse - lse_full[:, :, a:]).abs().max() < 1e-12
+
+
+def test_blockwise_attention_matches_causal_sdpa_and_full_window():
+    """The teacher's causal attention: against torch's causal scaled_dot_product_attention with the KV heads
+    repeated, and against the window oracle with a window as long as the sequence and no sinks."""
+    import torch.nn.functional as F
+    g = torch.Generator().manual_seed(11)
+    B, H, G, T, D = 2, 6, 2, 150, 32
+    qr, kr, vt = torch.randn(B, H, T, D, generator=g), torch.randn(B, G, T, D, generator=g), torch.randn(B, G, T, D, generator=g)
+    o = win.blockwise_attention(qr, kr, vt)
+    rep = lambda t: t.repeat_interleave(H // G, 1)
+    ref = F.scaled_dot_product_attention(qr, rep(kr), rep(vt), is_causal=True).transpose(1, 2)
+    assert (o - ref).abs().max() < 1e-5
+    pos = torch.arange(T)
+    ow, _ = win.window_attention_lse(qr, kr, vt, pos, None, None, pos, T, 0)
+    assert (o - ow).abs().max() < 1e-5

@@ -93,7 +93,7 @@ __device__ __forceinline__ void state_slab(const float* s_in, float* s_out, cons
     const int jc = j0 + 4 * cg;
     float4 s[RPT];
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) s[i] = *reinterpret_cast<const float4*>(s_in + (long)(r0 + 32 * i) * D + jc);
+    for (int i = 0; i < RPT; ++i) s[i] = nt_ldf4(s_in + (long)(r0 + 32 * i) * D + jc);    // streamed: read once
     if (write) {
         const float a = __expf(wg);
         float rc[4] = {0.f, 0.f, 0.f, 0.f};
@@ -116,7 +116,7 @@ __device__ __forceinline__ void state_slab(const float* s_in, float* s_out, cons
         }
     }
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) *reinterpret_cast<float4*>(s_out + (long)(r0 + 32 * i) * D + jc) = s[i];
+    for (int i = 0; i < RPT; ++i) nt_stf4(s_out + (long)(r0 + 32 * i) * D + jc, s[i]);
     if (!om) return;
     float acc[RMAX * 4];
 #pragma unroll

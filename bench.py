@@ -506,7 +506,7 @@ def main():
                      "achieved_GBs": gdn_bytes(T, H, D) / (ms * 1e-3) / 1e9, "peak_GBs": HBM_PEAK_GBS},
     }
     if not args.no_extra:
-        line["decode"] = run_decode(100, 10, dev)
+        line["decode"] = run_decode(100, 50, dev)
         line["layer_prefill_32k"] = run_layer(3, 1, dev)
         line["layer_prefill_32k"]["window_kernel"] = run_window(10, 3, dev)
         line["varlen_gdn"] = run_varlen(10, 3, dev)

@@ -3,7 +3,7 @@
 //   y_{t,h} = scale * normalize(x_{t,h} F_h),   normalize(u) = u / max(||u||_2, 1e-12)
 // used for qm (x = q, F = fq, scale = D^-1/2) and km (x = k, F = fk, scale = 1), for bf16 activations.
 //
-// One workgroup owns one head h and a strided set of 64-token tiles. F_h^T (D x D bf16, 128 KB at D = 256) is staged
+// One workgroup owns one head h and a strided set of 64-token tiles (one round of workgroups over the CUs). F_h^T (D x D bf16, 128 KB at D = 256) is staged
 // in LDS once; each of the 4 waves computes 16 tokens x D outputs per tile as Y^T = F_h^T X^T with
 // v_mfma_f32_16x16x32_bf16 (A = rows of F_h^T from LDS, B = the token rows of x from global memory, loaded one tile
 // ahead), so every lane holds 4 consecutive outputs of one token: the row norm is a sum over the lane's values and
@@ -17,6 +17,7 @@ namespace {
 
 constexpr int MP_WAVES = 4;
 constexpr int MP_TILE = 16 * MP_WAVES;       // tokens per tile
+constexpr int MP_AHEAD = 8;                  // A fragment reads in flight ahead of their MFMAs
 
 template <int NBLK>
 __device__ __forceinline__ int mp_sw(int row) { return NBLK >= 16 ? (row & 15) : ((row >> 1) & 7); }
@@ -58,23 +59,35 @@ __global__ __launch_bounds__(64 * MP_WAVES, 1) void mem_project_kernel(MemProjAr
         for (int ks = 0; ks < NKD; ++ks)
             xf[ks] = buf_ld16(rx, (uint32_t)((l16 * a.x_st + 32 * ks + 8 * lg) * 2));
     };
-    uint4 xf[NKD];
+    // x is read two tiles ahead of its use (the pass streams x in and out once; more bytes in flight per CU)
+    uint4 xf[NKD], x1[NKD];
     load_x(tg, xf);
+    load_x(tg + ntg, x1);
     wait_vmem_all();
     __syncthreads();
 
     for (long t = tg; t < ntiles; t += ntg) {
-        uint4 xn[NKD];
-        load_x(t + ntg, xn);                        // next tile (out of range: reads zero)
+        uint4 x2[NKD];
+        load_x(t + 2 * ntg, x2);                    // out of range: reads zero
         f32x4 acc[NDT];
 #pragma unroll
         for (int jt = 0; jt < NDT; ++jt) acc[jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        // the NKD x NDT products in one sequence (k step outer, so consecutive MFMAs use distinct accumulators),
+        // each A fragment read MP_AHEAD products ahead of its MFMA so LDS latency overlaps the MFMAs
+        constexpr int NP = NKD * NDT;
+        auto read_a = [&](int i) {
+            const int ks = i / NDT, jt = i % NDT;
+            return lds16(Fb, abase[ks % NKB] + 16 * jt * ROWB + 256 * (ks / NKB));
+        };
+        uint4 af[MP_AHEAD];
 #pragma unroll
-        for (int ks = 0; ks < NKD; ++ks) {
+        for (int i = 0; i < MP_AHEAD; ++i) af[i] = read_a(i);
 #pragma unroll
-            for (int jt = 0; jt < NDT; ++jt)
-                mma<BF16>(acc[jt], lds16(Fb, abase[ks % NKB] + 16 * jt * ROWB + 256 * (ks / NKB)), xf[ks]);
-            __builtin_amdgcn_sched_barrier(0);
+        for (int i = 0; i < NP; ++i) {
+            const uint4 a_i = af[i % MP_AHEAD];
+            if (i + MP_AHEAD < NP) af[i % MP_AHEAD] = read_a(i + MP_AHEAD);
+            mma<BF16>(acc[i % NDT], a_i, xf[i / NDT]);
+            __builtin_amdgcn_sched_barrier(0);       // keeps the reads in their slots (no hoisting of all 128)
         }
         float ss = 0.f;
 #pragma unroll
@@ -96,14 +109,19 @@ __global__ __launch_bounds__(64 * MP_WAVES, 1) void mem_project_kernel(MemProjAr
             }
         }
 #pragma unroll
-        for (int ks = 0; ks < NKD; ++ks) xf[ks] = xn[ks];
+        for (int ks = 0; ks < NKD; ++ks) {
+            xf[ks] = x1[ks];
+            x1[ks] = x2[ks];
+        }
     }
 }
 
 int mem_project_dispatch(const MemProjArgs& a, hipStream_t stream) {
     const long ntiles = (a.n_tok + MP_TILE - 1) / MP_TILE;
-    const long want = (512 + a.nh - 1) / a.nh;                  // ~512 workgroups over all heads
-    const int ntg = (int)(ntiles < want ? ntiles : want);
+    // one round of workgroups over the 256 CUs (F_h^T takes D * D * 2 bytes of LDS per workgroup)
+    const long per_cu = (long)(160 * 1024) / ((long)a.D * a.D * 2);
+    const long want = (256 * (per_cu > 0 ? per_cu : 1)) / a.nh;
+    const int ntg = (int)(ntiles < want ? ntiles : (want > 0 ? want : 1));
     const dim3 grid((unsigned)(a.nh * (ntg > 0 ? ntg : 1))), block(64 * MP_WAVES);
     switch (a.D) {
         case 64: hipLaunchKernelGGL(mem_project_kernel<64>, grid, block, 0, stream, a); break;

@@ -3,11 +3,12 @@
 //   y_{t,h} = scale * normalize(x_{t,h} F_h),   normalize(u) = u / max(||u||_2, 1e-12)
 // used for qm (x = q, F = fq, scale = D^-1/2) and km (x = k, F = fk, scale = 1), for bf16 activations.
 //
-// One workgroup owns one head h and a strided set of 64-token tiles (one round of workgroups over the CUs). F_h^T (D x D bf16, 128 KB at D = 256) is staged
-// in LDS once; each of the 4 waves computes 16 tokens x D outputs per tile as Y^T = F_h^T X^T with
-// v_mfma_f32_16x16x32_bf16 (A = rows of F_h^T from LDS, B = the token rows of x from global memory, loaded one tile
-// ahead), so every lane holds 4 consecutive outputs of one token: the row norm is a sum over the lane's values and
-// two cross-lane steps, and the bf16 result is stored 8 bytes at a time.
+// One workgroup owns one head h and a strided set of 64-token tiles (one round of workgroups over the CUs). F_h^T
+// (D x D bf16, 128 KB at D = 256) is staged in LDS once; each of the 4 waves computes 16 tokens x D outputs per tile
+// as Y^T = F_h^T X^T with v_mfma_f32_16x16x32_bf16 (A = rows of F_h^T from LDS, read 8 MFMAs ahead; B = the token
+// rows of x from global memory, loaded two tiles ahead), so every lane holds 4 consecutive outputs of one token: the
+// row norm is a sum over the lane's values and two cross-lane steps, and the bf16 result is stored 8 bytes at a
+// time. The pass reads x and writes y once (806 MB at T = 32768, 24 heads, D = 256).
 #include "bf_common.h"
 #include "bf_internal.h"
 

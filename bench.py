@@ -354,6 +354,62 @@ def run_teacher(steps, warmup, dev, T=32768):
                          "frac": tf / BF16_PEAK_TFLOPS}}
 
 
+def run_teacher_decode(steps, warmup, dev, retrieval=True, n=32768):
+    """One decode step of a kept full-attention layer over a KV cache of n = 32768 positions (B=64, H=16, G=4, D=256,
+    bf16): the ``_teacher`` drop-in (heimdall_amd.teacher.teacher, Heimdall/heimdall/hibrit.py:275-290) appending the
+    new key / value and attending, with retrieval (k=16 blocks of 64, window 2048, 4 sinks: set_retrieval's defaults,
+    hibrit.py:292) or over the whole cache. Timed with HIP events over whole steps (every launch of the step).
+    Algorithmic bytes: the attended K and V rows (bf16) plus, with retrieval, the block summaries read by the
+    selection (2 x fp32 x D per candidate block)."""
+    from heimdall_amd.teacher import set_retrieval, teacher
+
+    B, H, G, D = 64, 16, 4, 256
+    S, L, W, K = 4, 64, 2048, 16
+    cap = n + steps + warmup + 64
+    gen = torch.Generator(device=dev).manual_seed(11)
+    kb = F.normalize(torch.randn(B, G, cap, D, device=dev, generator=gen), dim=-1).bfloat16()
+    vb = torch.randn(B, G, cap, D, device=dev, generator=gen).bfloat16()
+    cache = {"k_buf": kb, "v_buf": vb, "k": kb[:, :, :n], "v": vb[:, :, :n]}
+    q = F.normalize(torch.randn(B, H, 1, D, device=dev, generator=gen), dim=-1).bfloat16()
+    k1 = F.normalize(torch.randn(B, G, 1, D, device=dev, generator=gen), dim=-1).bfloat16()
+    v1 = torch.randn(B, 1, G, D, device=dev, generator=gen).bfloat16()
+
+    class _Layer:
+        retrieval = None
+    m = _Layer()
+    if retrieval:
+        set_retrieval(m, k=K, block=L, window=W, sinks=S)
+    with torch.no_grad():
+        for _ in range(warmup):
+            teacher(m, q, k1, v1, cache)
+        torch.cuda.synchronize()
+        n0 = cache["k"].shape[2]
+        stream = torch.cuda.current_stream(dev)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            teacher(m, q, k1, v1, cache)
+        e1.record(stream)
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    nm = n0 + steps // 2                                    # mean cache length over the timed steps
+    if retrieval:
+        nb = (nm - S) // L
+        nc = (nm - 1 - W + 1 - S) // L
+        keys = S + K * L + (nm - (S + nc * L))
+        nbytes = B * G * (keys * D * 2 * 2 + nc * D * 4 * 2)
+    else:
+        keys = nm
+        nbytes = B * G * keys * D * 2 * 2
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"workload": f"teacher decode B={B} H={H} G={G} D={D} n={n} bf16 "
+                        + (f"retrieval k={K} block={L} window={W} sinks={S}" if retrieval else "full attention"),
+            "ms_per_step": ms, "us_per_step": ms * 1e3, "tokens_per_s": B / (ms * 1e-3), "steps": steps,
+            "attended_keys": keys, "algorithmic_bytes": nbytes,
+            "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": gbs / HBM_PEAK_GBS}}
+
+
 def run_window(steps, warmup, dev, T=32768):
     """The window kernel alone on the layer prefill's shapes (B=1, H=24, G=4, D=256, W=2048 + 4 sinks, bf16, from
     position 0 with the first 4 tokens as sinks, no ring, no mix): bf_window_fwd timed with HIP events on the launch
@@ -442,7 +498,8 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the decode and layer-prefill legs")
     ap.add_argument("--copy-probe", action="store_true", help="run one 256 MiB device copy first (counter scaling)")
     ap.add_argument("--segment-chunks", type=int, default=0, help="chunks per scan segment (0 = library default)")
-    ap.add_argument("--only", choices=("decode", "layer", "layer131k", "window", "varlen", "gdn_layer", "teacher"), default=None,
+    ap.add_argument("--only", choices=("decode", "layer", "layer131k", "window", "varlen", "gdn_layer", "teacher",
+                                       "teacher_decode", "teacher_decode_full"), default=None,
                     help="run one secondary leg alone and print its JSON object (for per-workload profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -466,7 +523,9 @@ def main():
                "window": lambda: run_window(args.steps, args.warmup, dev),
                "varlen": lambda: run_varlen(args.steps, args.warmup, dev),
                "gdn_layer": lambda: run_gdn_layer(args.steps, args.warmup, dev),
-               "teacher": lambda: run_teacher(args.steps, args.warmup, dev)}[args.only]
+               "teacher": lambda: run_teacher(args.steps, args.warmup, dev),
+               "teacher_decode": lambda: run_teacher_decode(args.steps, args.warmup, dev),
+               "teacher_decode_full": lambda: run_teacher_decode(args.steps, args.warmup, dev, retrieval=False)}[args.only]
         print(json.dumps(leg()), flush=True)
         return
 
@@ -511,6 +570,7 @@ def main():
         line["layer_prefill_32k"]["window_kernel"] = run_window(10, 3, dev)
         line["varlen_gdn"] = run_varlen(10, 3, dev)
         line["gdn_layer"] = run_gdn_layer(10, 3, dev)
+        line["teacher_decode"] = run_teacher_decode(50, 10, dev)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(r["inputs"])
     print(json.dumps(line), flush=True)

@@ -10,6 +10,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libbifrost_hip.so"
 DTYPE_F32, DTYPE_BF16 = 0, 1
 PHASE_PREP, PHASE_SUMMARY, PHASE_OUTPUT, PHASE_COMBINE = 1, 2, 4, 8
 PHASE_STATES, PHASE_ALL = PHASE_SUMMARY | PHASE_COMBINE, 15
+KV_MAX_K, KV_MAX_BLOCKS = 64, 16384      # bf_kv_select limits
 
 _c_int, _c_i64, _c_sz, _vp, _fp = ctypes.c_int, ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_float
 
@@ -31,6 +32,13 @@ SIGNATURES = {
     "bf_gdn_conv_inputs": (_c_int, [_vp, _c_i64, _vp, _c_int, _vp, _c_int] + [_vp] * 5 + [_c_int, _c_i64]
                            + [_c_int] * 3 + [_fp, _fp] + [_vp] * 5 + [_c_int, _vp]),
     "bf_gated_norm": (_c_int, [_vp, _c_int, _vp, _vp, _c_i64, _c_int, _fp, _vp, _c_int, _vp]),
+    "bf_kv_block_summary": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64] + [_c_int] * 5
+                            + [_vp, _vp, _vp]),
+    "bf_kv_select": (_c_int, [_vp] + [_c_int] * 6 + [_c_i64, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _c_int, _vp,
+                                                     _vp]),
+    "bf_kv_attention_workspace_size": (_c_int, [_c_int] * 5 + [_c_i64] + [_c_int] * 5 + [ctypes.POINTER(_c_sz)]),
+    "bf_kv_attention": (_c_int, [_vp, _vp, _vp] + [_c_int] * 6 + [_c_i64] * 5 + [_c_int] * 4
+                        + [_vp, _c_int, _fp, _vp, _c_sz, _vp, _c_int, _vp]),
 }
 
 _LIB = None

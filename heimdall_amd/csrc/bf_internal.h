@@ -149,6 +149,38 @@ struct MemProjArgs {
 int mem_project_dispatch(const MemProjArgs& a, hipStream_t stream);
 int window_fa_dispatch(const WinArgs& a, hipStream_t stream);
 
+struct KvArgs {
+    int B, T, G, R, D, dtype;       // T queries per sequence at positions n - T .. n - 1; q, k, v dtype (f32 / bf16)
+    const void* q;                  // [B][T][G*R][D]
+    const void* k;                  // key (b, g) rows at k + (b * G + g) * k_sbg + pos * k_st
+    const void* v;                  // value rows, same addressing with v_sbg / v_st
+    long k_sbg, k_st, v_sbg, v_st;
+    long n;                         // cached keys (positions 0 .. n - 1)
+    int retrieval;                  // 0: each query attends to every key up to its position
+    int sinks, window, L;           // S, W, block length; blocks start after the first S keys
+    int nb;                         // full blocks after the sinks, (n - S) / L
+    // summaries
+    int sum_first, nb_cap;          // summarise blocks [sum_first, nb); arrays hold nb_cap blocks per (b, g)
+    float* kmin;                    // [B][G][nb_cap][D]
+    float* kmax;
+    // selection
+    int K;                          // blocks to select
+    int* sel;                       // [B][T][G][K] block ids, -1 = none
+    // attention
+    float scale;
+    int nsplit;
+    float* ws_part;                 // [B][T][G][nsplit][R][D + 2]
+    void* o;                        // [B][T][G*R][D] o_dtype
+    int o_dtype;
+};
+int kv_dispatch(const KvArgs& a, int what, hipStream_t stream);   // what: 0 summaries, 1 selection, 2 attention
+long kv_max_keys(const KvArgs& a);   // attended keys of one query at most
+int kv_nsplit(long max_keys);
+int kv_max_k();
+int kv_max_blocks();
+int kv_max_splits();
+
+
 struct GdnInArgs {
     const void* z;            // [N_tok][C] in_dtype rows (C = (2 HK + HV) D channels [q | k | v]), z_st elements apart
     long z_st;

@@ -275,4 +275,89 @@ int bf_gated_norm(const void* o, int o_dtype, const void* z, const float* w, int
     return bf::gated_norm_dispatch(x, static_cast<hipStream_t>(stream));
 }
 
+static bool kv_aligned(const void* p, int64_t s1, int64_t s2) {
+    return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && s1 % 8 == 0 && s2 % 8 == 0;
+}
+
+int bf_kv_block_summary(const void* k, int dtype, int B, int G, int D, int64_t k_sbg, int64_t k_st, int sinks, int L,
+                        int first_block, int nb, int nb_cap, float* kmin, float* kmax, void* stream) {
+    if (B <= 0 || G <= 0 || L <= 0 || sinks < 0 || first_block < 0 || nb < first_block || nb > nb_cap || k_st <= 0 ||
+        k_sbg < 0)
+        return BF_STATUS_INVALID;
+    if (!supported_dim(D) || !supported_dtype(dtype)) return BF_STATUS_UNSUPPORTED;
+    if (nb == first_block) return BF_STATUS_OK;
+    if (!k || !kmin || !kmax || !kv_aligned(k, k_sbg, k_st) || !kv_aligned(kmin, 0, 0) || !kv_aligned(kmax, 0, 0))
+        return BF_STATUS_INVALID;
+    bf::KvArgs a{};
+    a.B = B; a.T = 1; a.G = G; a.R = 1; a.D = D; a.dtype = dtype; a.k = k; a.k_sbg = k_sbg; a.k_st = k_st;
+    a.sinks = sinks; a.L = L; a.sum_first = first_block; a.nb = nb; a.nb_cap = nb_cap; a.kmin = kmin; a.kmax = kmax;
+    return bf::kv_dispatch(a, 0, static_cast<hipStream_t>(stream));
+}
+
+// the shared checks of the selection and the attention; fills the geometry fields of a
+static int kv_geometry(bf::KvArgs& a, int B, int T, int G, int R, int D, int64_t n, int dtype, int retrieval, int sinks,
+                       int window, int L, int K) {
+    if (B <= 0 || T <= 0 || G <= 0 || R <= 0 || n <= 0 || T > n || K < 0) return BF_STATUS_INVALID;
+    if ((int64_t)B * T > (int64_t)1 << 22 || (int64_t)B * G > 65535) return BF_STATUS_UNSUPPORTED;
+    if (R > 8 || !supported_dim(D) || !supported_dtype(dtype) || K > bf::kv_max_k()) return BF_STATUS_UNSUPPORTED;
+    a.B = B; a.T = T; a.G = G; a.R = R; a.D = D; a.dtype = dtype; a.n = n; a.retrieval = retrieval ? 1 : 0;
+    if (a.retrieval) {
+        if (sinks < 0 || window <= 0 || L <= 0 || sinks > n) return BF_STATUS_INVALID;
+        a.sinks = sinks; a.window = window; a.L = L; a.K = K;
+        const int64_t nb = (n - sinks) / L;
+        if (nb > bf::kv_max_blocks()) return BF_STATUS_UNSUPPORTED;
+        a.nb = (int)nb;
+    } else {
+        a.sinks = 0; a.window = 0; a.L = 1; a.K = 0; a.nb = 0;
+    }
+    return BF_STATUS_OK;
+}
+
+int bf_kv_select(const void* q, int dtype, int B, int T, int G, int R, int D, int64_t n, int sinks, int window, int L,
+                 const float* kmin, const float* kmax, int nb_cap, int K, int* sel, void* stream) {
+    bf::KvArgs a{};
+    const int st = kv_geometry(a, B, T, G, R, D, n, dtype, 1, sinks, window, L, K);
+    if (st != BF_STATUS_OK) return st;
+    if (a.nb > nb_cap) return BF_STATUS_INVALID;
+    if (K == 0) return BF_STATUS_OK;
+    if (!q || !sel || !kv_aligned(q, 0, 0) || (a.nb > 0 && (!kmin || !kmax || !kv_aligned(kmin, 0, 0) ||
+                                                             !kv_aligned(kmax, 0, 0))))
+        return BF_STATUS_INVALID;
+    a.q = q; a.kmin = const_cast<float*>(kmin); a.kmax = const_cast<float*>(kmax); a.nb_cap = nb_cap; a.sel = sel;
+    return bf::kv_dispatch(a, 1, static_cast<hipStream_t>(stream));
+}
+
+int bf_kv_attention_workspace_size(int B, int T, int G, int R, int D, int64_t n, int retrieval, int sinks, int window,
+                                   int L, int K, size_t* bytes) {
+    if (!bytes) return BF_STATUS_INVALID;
+    bf::KvArgs a{};
+    const int st = kv_geometry(a, B, T, G, R, D, n, BF_DTYPE_F32, retrieval, sinks, window, L, K);
+    if (st != BF_STATUS_OK) return st;
+    const int ns = bf::kv_nsplit(bf::kv_max_keys(a));
+    if (ns > bf::kv_max_splits()) return BF_STATUS_UNSUPPORTED;
+    *bytes = (size_t)B * T * G * ns * R * (D + 2) * sizeof(float);
+    return BF_STATUS_OK;
+}
+
+int bf_kv_attention(const void* q, const void* k, const void* v, int dtype, int B, int T, int G, int R, int D,
+                    int64_t n, int64_t k_sbg, int64_t k_st, int64_t v_sbg, int64_t v_st, int retrieval, int sinks,
+                    int window, int L, const int* sel, int K, float scale, void* workspace, size_t workspace_bytes,
+                    void* o, int o_dtype, void* stream) {
+    bf::KvArgs a{};
+    const int st = kv_geometry(a, B, T, G, R, D, n, dtype, retrieval, sinks, window, L, K);
+    if (st != BF_STATUS_OK) return st;
+    if (!supported_dtype(o_dtype)) return BF_STATUS_UNSUPPORTED;
+    if (k_st <= 0 || v_st <= 0 || k_sbg < 0 || v_sbg < 0) return BF_STATUS_INVALID;
+    if (!q || !k || !v || !o || (a.retrieval && K > 0 && !sel)) return BF_STATUS_INVALID;
+    if (!kv_aligned(q, 0, 0) || !kv_aligned(k, k_sbg, k_st) || !kv_aligned(v, v_sbg, v_st)) return BF_STATUS_INVALID;
+    const int nsplit = bf::kv_nsplit(bf::kv_max_keys(a));
+    if (nsplit > bf::kv_max_splits()) return BF_STATUS_UNSUPPORTED;
+    const size_t need = (size_t)B * T * G * nsplit * R * (D + 2) * sizeof(float);
+    if (!workspace || workspace_bytes < need) return BF_STATUS_WORKSPACE;
+    a.q = q; a.k = k; a.v = v; a.k_sbg = k_sbg; a.k_st = k_st; a.v_sbg = v_sbg; a.v_st = v_st;
+    a.sel = const_cast<int*>(sel); a.scale = scale; a.nsplit = nsplit; a.ws_part = static_cast<float*>(workspace);
+    a.o = o; a.o_dtype = o_dtype;
+    return bf::kv_dispatch(a, 2, static_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"

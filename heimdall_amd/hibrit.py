@@ -11,7 +11,9 @@ The window + sink attention, the delta-rule memory and the gamma mix run in ``li
   t > 1   -> ``bf_gdn_fwd`` (memory branch) then ``bf_window_fwd`` (window + sinks + LSE, fused gamma mix)
 The frozen projections and the small per-token gate GEMMs (fq/fk, ab, mix) stay in PyTorch.
 
-``student`` can be bound onto the reference class as a drop-in: ``HybridAttention._student = student``.
+``student`` can be bound onto the reference class as a drop-in: ``HybridAttention._student = student``; likewise the
+teacher path of the kept full-attention layers, ``HybridAttention._teacher = teacher`` and ``set_retrieval``
+(``heimdall_amd.teacher``: KV-cache attention with Quest-style retrieval).
 """
 import math
 from typing import Optional
@@ -23,6 +25,7 @@ import torch.nn.functional as F
 from . import _lib
 from ._device import (BifrostError, check, dtype_code, gdn_forward, require_device, require_no_grad, stream_ptr,
                       workspace)
+from .teacher import set_retrieval, teacher
 
 NEW = ("fq", "fk", "ab", "mix", "mix_lse", "mem_scale", "A_log", "dt_bias")
 
@@ -301,6 +304,8 @@ class BifrostCore(nn.Module):
 
     _mem_inputs = mem_inputs
     _student = student
+    _teacher = teacher
+    set_retrieval = set_retrieval
 
     def forward(self, x, q, k, v, qr, kr, start: int = 0, cache: Optional[dict] = None, memory: bool = True):
         return self._student(x, q, k, v, qr, kr, start, cache, memory)

@@ -196,6 +196,38 @@ int bf_gdn_conv_inputs(const void* z, int64_t z_st, const void* prefix, int in_d
 int bf_gated_norm(const void* o, int o_dtype, const void* z, const float* w, int64_t rows, int D, float eps,
                   void* out, int io_dtype, void* stream);
 
+/*
+ * Attention of the kept full-attention layers over a dense KV cache, for the T most recent queries of each sequence
+ * (T = 1: one decode step), with optional retrieval (Quest-style block selection): HybridAttention._teacher
+ * (Heimdall/heimdall/hibrit.py:275-290) and _retrieval_mask (:301-324). Key (b, g) row of position p at
+ * k + (b * G + g) * k_sbg + p * k_st (elements; v likewise, D contiguous); the cache holds positions 0 .. n - 1 and
+ * query i of a sequence sits at position p = n - T + i. With S = sinks, W = window, L = block length, block j holds the
+ * keys S + j L .. S + j L + L - 1 and nb = (n - S) / L.
+ *   retrieval == 0: query p attends to the keys 0 .. p.
+ *   retrieval != 0: query p attends to the keys 0 .. S - 1, the selected blocks (sel) among its candidates
+ *                   j < nc = min(max(p - W + 1 - S, 0) / L, nb), and the window S + nc L .. p.
+ *
+ * bf_kv_block_summary: per-dimension key min / max of blocks [first_block, nb) into kmin / kmax [B][G][nb_cap][D] f32
+ *   (a growing cache summarises only its new full blocks).
+ * bf_kv_select: per (b, query, g), the K candidate blocks with the highest upper bound
+ *   max_r sum_d max(q_rd kmin_jd, q_rd kmax_jd) over the R query heads of the KV head, into sel [B][T][G][K] int32
+ *   (-1 past the candidates; ties to the lower block id). K <= 64, nb <= 16384.
+ * bf_kv_attention: softmax(q . k * scale) v per query head over the attended keys. q [B][T][G*R][D] in dtype, o
+ *   [B][T][G*R][D] in o_dtype; sel as bf_kv_select wrote it (retrieval only); workspace from
+ *   bf_kv_attention_workspace_size with the same geometry.
+ * q, k, v, kmin, kmax 16-byte aligned; k / v strides multiples of 8 elements. R <= 8.
+ */
+int bf_kv_block_summary(const void* k, int dtype, int B, int G, int D, int64_t k_sbg, int64_t k_st, int sinks, int L,
+                        int first_block, int nb, int nb_cap, float* kmin, float* kmax, void* stream);
+int bf_kv_select(const void* q, int dtype, int B, int T, int G, int R, int D, int64_t n, int sinks, int window, int L,
+                 const float* kmin, const float* kmax, int nb_cap, int K, int* sel, void* stream);
+int bf_kv_attention_workspace_size(int B, int T, int G, int R, int D, int64_t n, int retrieval, int sinks, int window,
+                                   int L, int K, size_t* bytes);
+int bf_kv_attention(const void* q, const void* k, const void* v, int dtype, int B, int T, int G, int R, int D,
+                    int64_t n, int64_t k_sbg, int64_t k_st, int64_t v_sbg, int64_t v_st, int retrieval, int sinks,
+                    int window, int L, const int* sel, int K, float scale, void* workspace, size_t workspace_bytes,
+                    void* o, int o_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -360,7 +360,7 @@ def run_teacher_decode(steps, warmup, dev, retrieval=True, n=32768):
     new key / value and attending, with retrieval (k=16 blocks of 64, window 2048, 4 sinks: set_retrieval's defaults,
     hibrit.py:292) or over the whole cache. Timed with HIP events over whole steps (every launch of the step).
     Algorithmic bytes: the attended K and V rows (bf16) plus, with retrieval, the block summaries read by the
-    selection (2 x fp32 x D per candidate block)."""
+    selection (min and max, bf16 like the keys, D each per candidate block)."""
     from heimdall_amd.teacher import set_retrieval, teacher
 
     B, H, G, D = 64, 16, 4, 256
@@ -397,7 +397,7 @@ def run_teacher_decode(steps, warmup, dev, retrieval=True, n=32768):
         nb = (nm - S) // L
         nc = (nm - 1 - W + 1 - S) // L
         keys = S + K * L + (nm - (S + nc * L))
-        nbytes = B * G * (keys * D * 2 * 2 + nc * D * 4 * 2)
+        nbytes = B * G * (keys * D * 2 * 2 + nc * D * 2 * 2)     # summaries are bf16 like the keys
     else:
         keys = nm
         nbytes = B * G * keys * D * 2 * 2

@@ -32,6 +32,8 @@ SIGNATURES = {
     "bf_gdn_conv_inputs": (_c_int, [_vp, _c_i64, _vp, _c_int, _vp, _c_int] + [_vp] * 5 + [_c_int, _c_i64]
                            + [_c_int] * 3 + [_fp, _fp] + [_vp] * 5 + [_c_int, _vp]),
     "bf_gated_norm": (_c_int, [_vp, _c_int, _vp, _vp, _c_i64, _c_int, _fp, _vp, _c_int, _vp]),
+    "bf_kv_append": (_c_int, [_vp, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i64] + [_c_int] * 5
+                     + [_vp, _vp, _c_i64, _c_i64, _vp]),
     "bf_kv_block_summary": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64] + [_c_int] * 5
                             + [_vp, _vp, _vp]),
     "bf_kv_select": (_c_int, [_vp] + [_c_int] * 6 + [_c_i64, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _c_int, _vp,

@@ -77,7 +77,7 @@ struct DecodeArgs {
     float* state;             // [B][G][D][D]
     float* o;                 // [B][H][D]
     float* lse;               // [B][H] or null
-    int nsplit;               // window splits of 256 ring slots
+    int nsplit;               // window splits of 512 ring slots
     float* ws_om;             // [B][H][D] memory read
     float* ws_part;           // [B][G][nsplit][R][D + 2] window partials
 };
@@ -161,21 +161,32 @@ struct KvArgs {
     int nb;                         // full blocks after the sinks, (n - S) / L
     // summaries
     int sum_first, nb_cap;          // summarise blocks [sum_first, nb); arrays hold nb_cap blocks per (b, g)
-    float* kmin;                    // [B][G][nb_cap][D]
-    float* kmax;
+    void* kmin;                     // key dtype, [B][G][D / GS][nb_cap][GS], GS = 16 bytes / element
+    void* kmax;
     // selection
     int K;                          // blocks to select
     int* sel;                       // [B][T][G][K] block ids, -1 = none
     // attention
     float scale;
-    int nsplit;
+    int slen, nsplit;               // keys per split (<= 512), splits
     float* ws_part;                 // [B][T][G][nsplit][R][D + 2]
     void* o;                        // [B][T][G*R][D] o_dtype
     int o_dtype;
 };
 int kv_dispatch(const KvArgs& a, int what, hipStream_t stream);   // what: 0 summaries, 1 selection, 2 attention
+
+struct KvAppendArgs {
+    const void* k_new;              // row (b, g, i) at k_new + b * k_sb + g * k_sg + i * k_st (elements)
+    const void* v_new;
+    long k_sb, k_sg, k_st, v_sb, v_sg, v_st;
+    int B, G, t, D, esz;            // esz: bytes per element
+    void* k_buf;                    // [B][G][cap][D]
+    void* v_buf;
+    long cap, n0;                   // rows go to positions n0 .. n0 + t - 1
+};
+int kv_append(const KvAppendArgs& a, hipStream_t stream);
 long kv_max_keys(const KvArgs& a);   // attended keys of one query at most
-int kv_nsplit(long max_keys);
+void kv_split_plan(const KvArgs& a, int* slen, int* nsplit);
 int kv_max_k();
 int kv_max_blocks();
 int kv_max_splits();

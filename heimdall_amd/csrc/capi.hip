@@ -279,8 +279,25 @@ static bool kv_aligned(const void* p, int64_t s1, int64_t s2) {
     return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && s1 % 8 == 0 && s2 % 8 == 0;
 }
 
+int bf_kv_append(const void* k_new, int64_t k_sb, int64_t k_sg, int64_t k_st, const void* v_new, int64_t v_sb,
+                 int64_t v_sg, int64_t v_st, int dtype, int B, int G, int t, int D, void* k_buf, void* v_buf,
+                 int64_t cap, int64_t n0, void* stream) {
+    if (B <= 0 || G <= 0 || t < 0 || cap <= 0 || n0 < 0 || n0 + t > cap) return BF_STATUS_INVALID;
+    if (!supported_dim(D) || !supported_dtype(dtype)) return BF_STATUS_UNSUPPORTED;
+    if (t == 0) return BF_STATUS_OK;
+    if (!k_new || !v_new || !k_buf || !v_buf) return BF_STATUS_INVALID;
+    if (!kv_aligned(k_new, k_sb, k_sg) || !kv_aligned(v_new, v_sb, v_sg) || k_st % 8 || v_st % 8 ||
+        !kv_aligned(k_buf, 0, 0) || !kv_aligned(v_buf, 0, 0))
+        return BF_STATUS_INVALID;
+    bf::KvAppendArgs a{};
+    a.k_new = k_new; a.v_new = v_new; a.k_sb = k_sb; a.k_sg = k_sg; a.k_st = k_st; a.v_sb = v_sb; a.v_sg = v_sg;
+    a.v_st = v_st; a.B = B; a.G = G; a.t = t; a.D = D; a.esz = dtype == BF_DTYPE_BF16 ? 2 : 4;
+    a.k_buf = k_buf; a.v_buf = v_buf; a.cap = cap; a.n0 = n0;
+    return bf::kv_append(a, static_cast<hipStream_t>(stream));
+}
+
 int bf_kv_block_summary(const void* k, int dtype, int B, int G, int D, int64_t k_sbg, int64_t k_st, int sinks, int L,
-                        int first_block, int nb, int nb_cap, float* kmin, float* kmax, void* stream) {
+                        int first_block, int nb, int nb_cap, void* kmin, void* kmax, void* stream) {
     if (B <= 0 || G <= 0 || L <= 0 || sinks < 0 || first_block < 0 || nb < first_block || nb > nb_cap || k_st <= 0 ||
         k_sbg < 0)
         return BF_STATUS_INVALID;
@@ -298,7 +315,7 @@ int bf_kv_block_summary(const void* k, int dtype, int B, int G, int D, int64_t k
 static int kv_geometry(bf::KvArgs& a, int B, int T, int G, int R, int D, int64_t n, int dtype, int retrieval, int sinks,
                        int window, int L, int K) {
     if (B <= 0 || T <= 0 || G <= 0 || R <= 0 || n <= 0 || T > n || K < 0) return BF_STATUS_INVALID;
-    if ((int64_t)B * T > (int64_t)1 << 22 || (int64_t)B * G > 65535) return BF_STATUS_UNSUPPORTED;
+    if ((int64_t)B * T > (int64_t)1 << 22 || (int64_t)B * G > 65535 || n > INT32_MAX) return BF_STATUS_UNSUPPORTED;
     if (R > 8 || !supported_dim(D) || !supported_dtype(dtype) || K > bf::kv_max_k()) return BF_STATUS_UNSUPPORTED;
     a.B = B; a.T = T; a.G = G; a.R = R; a.D = D; a.dtype = dtype; a.n = n; a.retrieval = retrieval ? 1 : 0;
     if (a.retrieval) {
@@ -314,7 +331,7 @@ static int kv_geometry(bf::KvArgs& a, int B, int T, int G, int R, int D, int64_t
 }
 
 int bf_kv_select(const void* q, int dtype, int B, int T, int G, int R, int D, int64_t n, int sinks, int window, int L,
-                 const float* kmin, const float* kmax, int nb_cap, int K, int* sel, void* stream) {
+                 const void* kmin, const void* kmax, int nb_cap, int K, int* sel, void* stream) {
     bf::KvArgs a{};
     const int st = kv_geometry(a, B, T, G, R, D, n, dtype, 1, sinks, window, L, K);
     if (st != BF_STATUS_OK) return st;
@@ -323,7 +340,7 @@ int bf_kv_select(const void* q, int dtype, int B, int T, int G, int R, int D, in
     if (!q || !sel || !kv_aligned(q, 0, 0) || (a.nb > 0 && (!kmin || !kmax || !kv_aligned(kmin, 0, 0) ||
                                                              !kv_aligned(kmax, 0, 0))))
         return BF_STATUS_INVALID;
-    a.q = q; a.kmin = const_cast<float*>(kmin); a.kmax = const_cast<float*>(kmax); a.nb_cap = nb_cap; a.sel = sel;
+    a.q = q; a.kmin = const_cast<void*>(kmin); a.kmax = const_cast<void*>(kmax); a.nb_cap = nb_cap; a.sel = sel;
     return bf::kv_dispatch(a, 1, static_cast<hipStream_t>(stream));
 }
 
@@ -333,7 +350,8 @@ int bf_kv_attention_workspace_size(int B, int T, int G, int R, int D, int64_t n,
     bf::KvArgs a{};
     const int st = kv_geometry(a, B, T, G, R, D, n, BF_DTYPE_F32, retrieval, sinks, window, L, K);
     if (st != BF_STATUS_OK) return st;
-    const int ns = bf::kv_nsplit(bf::kv_max_keys(a));
+    int sl = 0, ns = 0;
+    bf::kv_split_plan(a, &sl, &ns);
     if (ns > bf::kv_max_splits()) return BF_STATUS_UNSUPPORTED;
     *bytes = (size_t)B * T * G * ns * R * (D + 2) * sizeof(float);
     return BF_STATUS_OK;
@@ -350,12 +368,14 @@ int bf_kv_attention(const void* q, const void* k, const void* v, int dtype, int 
     if (k_st <= 0 || v_st <= 0 || k_sbg < 0 || v_sbg < 0) return BF_STATUS_INVALID;
     if (!q || !k || !v || !o || (a.retrieval && K > 0 && !sel)) return BF_STATUS_INVALID;
     if (!kv_aligned(q, 0, 0) || !kv_aligned(k, k_sbg, k_st) || !kv_aligned(v, v_sbg, v_st)) return BF_STATUS_INVALID;
-    const int nsplit = bf::kv_nsplit(bf::kv_max_keys(a));
+    int slen = 0, nsplit = 0;
+    bf::kv_split_plan(a, &slen, &nsplit);
     if (nsplit > bf::kv_max_splits()) return BF_STATUS_UNSUPPORTED;
     const size_t need = (size_t)B * T * G * nsplit * R * (D + 2) * sizeof(float);
     if (!workspace || workspace_bytes < need) return BF_STATUS_WORKSPACE;
     a.q = q; a.k = k; a.v = v; a.k_sbg = k_sbg; a.k_st = k_st; a.v_sbg = v_sbg; a.v_st = v_st;
-    a.sel = const_cast<int*>(sel); a.scale = scale; a.nsplit = nsplit; a.ws_part = static_cast<float*>(workspace);
+    a.sel = const_cast<int*>(sel); a.scale = scale; a.slen = slen; a.nsplit = nsplit;
+    a.ws_part = static_cast<float*>(workspace);
     a.o = o; a.o_dtype = o_dtype;
     return bf::kv_dispatch(a, 2, static_cast<hipStream_t>(stream));
 }

@@ -54,20 +54,34 @@ def _kv_view(t: torch.Tensor):
     return t, t.stride(1), t.stride(2)
 
 
+def summary_buffers(B: int, G: int, D: int, nb_cap: int, dtype: torch.dtype, dev):
+    """Empty block summaries (kmin, kmax) in the keys' dtype and the kernels' layout [B, G, D / GS, nb_cap, GS],
+    GS = 16 bytes / element (a block's min / max of a key dimension is one of the key values: no rounding)."""
+    gs = 16 // torch.empty(0, dtype=dtype).element_size()
+    kmin = torch.empty(B, G, D // gs, nb_cap, gs, dtype=dtype, device=dev)
+    return kmin, torch.empty_like(kmin)
+
+
+def summaries_as_blocks(s: torch.Tensor) -> torch.Tensor:
+    """[B, G, D / GS, nb_cap, GS] -> [B, G, nb_cap, D] (a copy for inspection)."""
+    B, G, C, nb, gs = s.shape
+    return s.permute(0, 1, 3, 2, 4).reshape(B, G, nb, gs * C)
+
+
 def kv_block_summary(k: torch.Tensor, sinks: int, block: int, first_block: int, nb: int, kmin: torch.Tensor,
                      kmax: torch.Tensor) -> None:
-    """kmin / kmax [B, G, nb_cap, D] fp32 (written in place) <- the per-dimension key minimum and maximum of the blocks
+    """kmin / kmax (``summary_buffers``; written in place) <- the per-dimension key minimum and maximum of the blocks
     first_block .. nb - 1 of k [B, G, n, D] (block j = keys sinks + j block ..)."""
     dev = require_device(k, kmin, kmax)
     k, s_bg, s_p = _kv_view(k)
     B, G, _, D = k.shape
     check(_lib.load().bf_kv_block_summary(k.data_ptr(), dtype_code(k.dtype), B, G, D, s_bg, s_p, sinks, block,
-                                          first_block, nb, kmin.shape[2], kmin.data_ptr(), kmax.data_ptr(),
+                                          first_block, nb, kmin.shape[3], kmin.data_ptr(), kmax.data_ptr(),
                                           stream_ptr(dev)), "bf_kv_block_summary")
 
 
 def kv_select(q: torch.Tensor, n: int, ret: dict, kmin: torch.Tensor, kmax: torch.Tensor) -> torch.Tensor:
-    """q [B, T, H, D] (the queries at positions n - T .. n - 1), summaries [B, G, nb_cap, D] -> the selected block ids
+    """q [B, T, H, D] (the queries at positions n - T .. n - 1), summaries from ``kv_block_summary`` -> the selected block ids
     [B, T, G, k] int32 (-1 past the candidates)."""
     dev = require_device(q, kmin, kmax)
     B, T, H, D = q.shape
@@ -75,7 +89,7 @@ def kv_select(q: torch.Tensor, n: int, ret: dict, kmin: torch.Tensor, kmax: torc
     q = q.contiguous()
     sel = torch.empty(B, T, G, max(ret["k"], 1), dtype=torch.int32, device=dev)
     check(_lib.load().bf_kv_select(q.data_ptr(), dtype_code(q.dtype), B, T, G, H // G, D, n, ret["sinks"],
-                                   ret["window"], ret["block"], kmin.data_ptr(), kmax.data_ptr(), kmin.shape[2],
+                                   ret["window"], ret["block"], kmin.data_ptr(), kmax.data_ptr(), kmin.shape[3],
                                    ret["k"], sel.data_ptr(), stream_ptr(dev)), "bf_kv_select")
     return sel
 
@@ -116,6 +130,11 @@ def kv_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, n: int, ret:
     return o
 
 
+def _appendable(x: torch.Tensor) -> bool:
+    """Rows the append kernel reads directly: D contiguous, 16-byte aligned, strides in whole 16-byte vectors."""
+    return x.stride(-1) == 1 and x.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in x.stride()[:3])
+
+
 def _append(cache: dict, kr: torch.Tensor, vt: torch.Tensor):
     """Appends the new rows kr / vt [B, G, t, D] to the cache's capacity buffers; cache["k"] / cache["v"] become
     [B, G, n, D] views of them. Returns (k_buf, v_buf, n, adopted) — adopted: the history came from plain tensors."""
@@ -138,37 +157,39 @@ def _append(cache: dict, kr: torch.Tensor, vt: torch.Tensor):
         kb, vb = nk, nv
         cache["k_buf"], cache["v_buf"] = kb, vb
         cache.pop("ring_pos", None)
-    kb[:, :, n0:n] = kr
-    vb[:, :, n0:n] = vt
+    kr = kr if _appendable(kr) else kr.contiguous()
+    vt = vt if _appendable(vt) else vt.contiguous()
+    check(_lib.load().bf_kv_append(kr.data_ptr(), kr.stride(0), kr.stride(1), kr.stride(2), vt.data_ptr(),
+                                   vt.stride(0), vt.stride(1), vt.stride(2), dtype_code(kb.dtype), B, G, t, D,
+                                   kb.data_ptr(), vb.data_ptr(), kb.shape[2], n0, stream_ptr(kr.device)),
+          "bf_kv_append")
     cache["k"], cache["v"] = kb[:, :, :n], vb[:, :, :n]
     return kb, vb, n, adopted
 
 
 def _summaries(cache: Optional[dict], k: torch.Tensor, n: int, ret: dict, fresh: bool):
-    """Block min / max of the full blocks of k's first n rows, [B, G, nb_cap, D] fp32; kept in the cache
+    """Block min / max of the full blocks of k's first n rows (``summary_buffers`` layout); kept in the cache
     ("kv_kmin", "kv_kmax", "kv_sum") so each call summarises only blocks completed since the last one."""
     B, G, cap, D = k.shape
     S, L = ret["sinks"], ret["block"]
     nb = max(0, (n - S) // L)
     meta = None if cache is None or fresh else cache.get("kv_sum")
-    kmin = kmax = None
-    done = 0
-    if meta is not None and meta["S"] == S and meta["L"] == L and meta["nb_cap"] >= nb:
-        kmin, kmax, done = cache["kv_kmin"], cache["kv_kmax"], min(meta["nb"], nb)
-    if kmin is None:
-        nb_cap = max(1, (max(cap, n) - S) // L + 1)
-        kmin = torch.empty(B, G, nb_cap, D, dtype=torch.float32, device=k.device)
-        kmax = torch.empty_like(kmin)
-        if meta is not None and meta["S"] == S and meta["L"] == L:     # grown cache: keep the finished blocks
-            old = min(meta["nb"], nb)
-            kmin[:, :, :old] = cache["kv_kmin"][:, :, :old]
-            kmax[:, :, :old] = cache["kv_kmax"][:, :, :old]
-            done = old
+    if meta is not None and (meta["S"] != S or meta["L"] != L or cache["kv_kmin"].dtype != k.dtype or
+                             cache["kv_kmin"].shape[:2] != (B, G)):
+        meta = None
+    done = 0 if meta is None else min(meta["nb"], nb)
+    if meta is not None and meta["nb_cap"] >= nb:
+        kmin, kmax = cache["kv_kmin"], cache["kv_kmax"]
+    else:
+        kmin, kmax = summary_buffers(B, G, D, max(1, (max(cap, n) - S) // L + 1), k.dtype, k.device)
+        if done:                                        # grown cache: keep the finished blocks
+            kmin[:, :, :, :done] = cache["kv_kmin"][:, :, :, :done]
+            kmax[:, :, :, :done] = cache["kv_kmax"][:, :, :, :done]
     if nb > done:
         kv_block_summary(k, S, L, done, nb, kmin, kmax)
     if cache is not None:
         cache["kv_kmin"], cache["kv_kmax"] = kmin, kmax
-        cache["kv_sum"] = dict(S=S, L=L, nb=nb, nb_cap=kmin.shape[2])
+        cache["kv_sum"] = dict(S=S, L=L, nb=nb, nb_cap=kmin.shape[3])
     return kmin, kmax
 
 

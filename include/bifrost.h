@@ -207,20 +207,29 @@ int bf_gated_norm(const void* o, int o_dtype, const void* z, const float* w, int
  *   retrieval != 0: query p attends to the keys 0 .. S - 1, the selected blocks (sel) among its candidates
  *                   j < nc = min(max(p - W + 1 - S, 0) / L, nb), and the window S + nc L .. p.
  *
- * bf_kv_block_summary: per-dimension key min / max of blocks [first_block, nb) into kmin / kmax [B][G][nb_cap][D] f32
- *   (a growing cache summarises only its new full blocks).
+ * bf_kv_block_summary: per-dimension key min / max of blocks [first_block, nb) into kmin / kmax, in the key dtype
+ *   (exact: each is one of the key values) with the layout [B][G][D / GS][nb_cap][GS], GS = 16 bytes / element (dims
+ *   GS c .. GS c + GS - 1 of block j at ((b G + g) D / GS + c) nb_cap + j); a growing cache summarises only its new
+ *   full blocks.
  * bf_kv_select: per (b, query, g), the K candidate blocks with the highest upper bound
- *   max_r sum_d max(q_rd kmin_jd, q_rd kmax_jd) over the R query heads of the KV head, into sel [B][T][G][K] int32
- *   (-1 past the candidates; ties to the lower block id). K <= 64, nb <= 16384.
+ *   max_r sum_d max(q_rd kmin_jd, q_rd kmax_jd) (fp32) over the R query heads of the KV head, into sel [B][T][G][K]
+ *   int32 in descending bound order (-1 past the candidates; ties to the lower block id). K <= 64, nb <= 16384. q and
+ *   the summaries share dtype. bf_kv_attention reads the valid ids of sel in any order.
  * bf_kv_attention: softmax(q . k * scale) v per query head over the attended keys. q [B][T][G*R][D] in dtype, o
  *   [B][T][G*R][D] in o_dtype; sel as bf_kv_select wrote it (retrieval only); workspace from
  *   bf_kv_attention_workspace_size with the same geometry.
  * q, k, v, kmin, kmax 16-byte aligned; k / v strides multiples of 8 elements. R <= 8.
  */
+/* bf_kv_append: the t new rows k_new / v_new (row (b, g, i) at b k_sb + g k_sg + i k_st elements) written to
+ * positions n0 .. n0 + t - 1 of the cache buffers k_buf / v_buf [B][G][cap][D] (the torch.cat of _teacher,
+ * hibrit.py:277-279, into preallocated capacity). One launch for both tensors. */
+int bf_kv_append(const void* k_new, int64_t k_sb, int64_t k_sg, int64_t k_st, const void* v_new, int64_t v_sb,
+                 int64_t v_sg, int64_t v_st, int dtype, int B, int G, int t, int D, void* k_buf, void* v_buf,
+                 int64_t cap, int64_t n0, void* stream);
 int bf_kv_block_summary(const void* k, int dtype, int B, int G, int D, int64_t k_sbg, int64_t k_st, int sinks, int L,
-                        int first_block, int nb, int nb_cap, float* kmin, float* kmax, void* stream);
+                        int first_block, int nb, int nb_cap, void* kmin, void* kmax, void* stream);
 int bf_kv_select(const void* q, int dtype, int B, int T, int G, int R, int D, int64_t n, int sinks, int window, int L,
-                 const float* kmin, const float* kmax, int nb_cap, int K, int* sel, void* stream);
+                 const void* kmin, const void* kmax, int nb_cap, int K, int* sel, void* stream);
 int bf_kv_attention_workspace_size(int B, int T, int G, int R, int D, int64_t n, int retrieval, int sinks, int window,
                                    int L, int K, size_t* bytes);
 int bf_kv_attention(const void* q, const void* k, const void* v, int dtype, int B, int T, int G, int R, int D,

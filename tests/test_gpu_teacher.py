@@ -34,32 +34,34 @@ def cache_tensors(seed, B, G, n, D, dtype, cap=None):
 
 @pytest.mark.parametrize("dtype,D", [(torch.float32, 64), (torch.bfloat16, 128), (torch.bfloat16, 256)])
 def test_block_summary_exact_and_incremental(dev, dtype, D):
-    from heimdall_amd.teacher import kv_block_summary
+    from heimdall_amd.teacher import kv_block_summary, summaries_as_blocks, summary_buffers
     B, G, n, S, L = 2, 3, 300, 4, 16
     kb, _ = cache_tensors(1, B, G, n + 37, D, dtype)
     nb = (n - S) // L
-    kmin = torch.full((B, G, nb + 5, D), 7.0, device=dev)
-    kmax = torch.full_like(kmin, 7.0)
+    kmin, kmax = summary_buffers(B, G, D, nb + 5, dtype, dev)
+    kmin.fill_(7.0)
+    kmax.fill_(7.0)
     k = kb.to(dev)
     print(f"summary {dtype} D={D}", flush=True)
     kv_block_summary(k, S, L, 10, nb, kmin, kmax)             # blocks 10 .. nb - 1 only
-    assert (kmin[:, :, :10] == 7.0).all() and (kmin[:, :, nb:] == 7.0).all()
+    lo_b, hi_b = summaries_as_blocks(kmin), summaries_as_blocks(kmax)
+    assert (lo_b[:, :, :10] == 7.0).all() and (lo_b[:, :, nb:] == 7.0).all() and (hi_b[:, :, nb:] == 7.0).all()
     kv_block_summary(k, S, L, 0, 10, kmin, kmax)
     lo, hi = ot.block_summary(kb[:, :, :n].float(), S, L)
-    assert torch.equal(kmin[:, :, :nb].cpu().double(), lo) and torch.equal(kmax[:, :, :nb].cpu().double(), hi)
+    lo_b, hi_b = summaries_as_blocks(kmin), summaries_as_blocks(kmax)
+    assert torch.equal(lo_b[:, :, :nb].cpu().double(), lo) and torch.equal(hi_b[:, :, :nb].cpu().double(), hi)
 
 
 @pytest.mark.parametrize("dtype,D,R,T,K", [(torch.float32, 64, 1, 1, 4), (torch.bfloat16, 128, 4, 1, 16),
                                            (torch.bfloat16, 256, 8, 3, 8), (torch.float32, 128, 2, 5, 64)])
 def test_select_matches_oracle(dev, dtype, D, R, T, K):
-    from heimdall_amd.teacher import kv_block_summary, kv_select
+    from heimdall_amd.teacher import kv_block_summary, kv_select, summary_buffers
     B, G, n, S, L, W = 2, 2, 1500, 4, 16, 200
     g = torch.Generator().manual_seed(2)
     kb, _ = cache_tensors(3, B, G, n, D, dtype)
     q = torch.randn(B, T, G * R, D, generator=g).to(dtype)
     nb = (n - S) // L
-    kmin = torch.empty(B, G, nb, D, device=dev)
-    kmax = torch.empty_like(kmin)
+    kmin, kmax = summary_buffers(B, G, D, nb, dtype, dev)
     kv_block_summary(kb.to(dev), S, L, 0, nb, kmin, kmax)
     ret = dict(k=K, block=L, window=W, sinks=S)
     print(f"select {dtype} D={D} R={R} T={T} K={K}", flush=True)
@@ -77,18 +79,38 @@ def test_select_matches_oracle(dev, dtype, D, R, T, K):
 
 def test_select_fewer_candidates_than_k(dev):
     """Early in a sequence fewer than k blocks lie before the window: the rest of sel is -1."""
-    from heimdall_amd.teacher import kv_block_summary, kv_select
+    from heimdall_amd.teacher import kv_block_summary, kv_select, summary_buffers
     B, G, D, S, L, W, K = 1, 1, 64, 4, 8, 40, 16
     n = S + W + 5 * L                       # 5 candidates for the last query
     kb, _ = cache_tensors(4, B, G, n, D, torch.float32)
     q = torch.randn(B, 1, 2, D, generator=torch.Generator().manual_seed(5))
     nb = (n - S) // L
-    kmin = torch.empty(B, G, nb, D, device=dev)
-    kmax = torch.empty_like(kmin)
+    kmin, kmax = summary_buffers(B, G, D, nb, torch.float32, dev)
     kv_block_summary(kb.to(dev), S, L, 0, nb, kmin, kmax)
     sel = kv_select(q.to(dev), n, dict(k=K, block=L, window=W, sinks=S), kmin, kmax).cpu()
     assert sorted(sel[0, 0, 0, :5].tolist()) == [0, 1, 2, 3, 4]
     assert (sel[0, 0, 0, 5:] == -1).all()
+
+
+@pytest.mark.parametrize("K", [1, 17, 64])
+def test_select_ties_and_many_blocks(dev, K):
+    """3000 candidate blocks (several per lane of every wave's slice), whose contents repeat with period 7, so equal
+    bounds abound: the selection keeps the lower block ids, as the oracle's stable order does."""
+    from heimdall_amd.teacher import kv_block_summary, kv_select, summary_buffers
+    B, G, R, D, S, L, W = 1, 2, 3, 64, 4, 8, 64
+    n = S + 3000 * L + W
+    g = torch.Generator().manual_seed(13)
+    base = torch.randn(B, G, 7 * L, D, generator=g)
+    kb = torch.cat((torch.randn(B, G, S, D, generator=g), base.repeat(1, 1, n // (7 * L) + 1, 1)), 2)[:, :, :n]
+    q = torch.randn(B, 1, G * R, D, generator=g)
+    nb = (n - S) // L
+    kmin, kmax = summary_buffers(B, G, D, nb, torch.float32, dev)
+    kv_block_summary(kb.to(dev), S, L, 0, nb, kmin, kmax)
+    print(f"select ties K={K} nb={nb}", flush=True)
+    sel = kv_select(q.to(dev), n, dict(k=K, block=L, window=W, sinks=S), kmin, kmax).cpu()
+    want, nc = ot.select_blocks(q.transpose(1, 2), kb, K, L, W, S)
+    for gg in range(G):
+        assert sorted(sel[0, 0, gg].tolist()) == torch.nonzero(want[0, gg, 0]).flatten().tolist(), gg
 
 
 @pytest.mark.parametrize("dtype,D,R,T,n", [(torch.float32, 64, 2, 1, 700), (torch.bfloat16, 128, 4, 1, 3000),
@@ -111,14 +133,13 @@ def test_kv_attention_causal(dev, dtype, D, R, T, n):
                                            (torch.bfloat16, 256, 8, 1, 4), (torch.bfloat16, 128, 2, 6, 0),
                                            (torch.float32, 128, 4, 5, 64)])
 def test_kv_attention_retrieval(dev, dtype, D, R, T, K):
-    from heimdall_amd.teacher import kv_attention, kv_block_summary, kv_select
+    from heimdall_amd.teacher import kv_attention, kv_block_summary, kv_select, summary_buffers
     B, G, n, S, L, W = 2, 2, 2600, 4, 32, 300
     kb, vb = cache_tensors(8, B, G, n, D, dtype)
     q = torch.randn(B, T, G * R, D, generator=torch.Generator().manual_seed(9)).to(dtype)
     ret = dict(k=K, block=L, window=W, sinks=S)
     nb = (n - S) // L
-    kmin = torch.empty(B, G, nb, D, device=dev)
-    kmax = torch.empty_like(kmin)
+    kmin, kmax = summary_buffers(B, G, D, nb, dtype, dev)
     k, v, qd = kb.to(dev), vb.to(dev), q.to(dev)
     print(f"kv retrieval {dtype} D={D} R={R} T={T} K={K}", flush=True)
     kv_block_summary(k, S, L, 0, nb, kmin, kmax)

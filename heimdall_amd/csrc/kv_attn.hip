@@ -95,6 +95,25 @@ __device__ __forceinline__ void ldf(const float* s, float (&x)[N]) {
     }
 }
 
+// the DPL dims of one of LPK lanes sharing a row of D elements: with whole 16-byte chunks per lane, lane l takes chunks
+// l, l + LPK, l + 2 LPK, ... (each load instruction of the LPK lanes reads a contiguous span of the row); with less
+// than a chunk per lane, the DPL consecutive dims from l DPL.
+template <class E, int D, int LPK>
+__device__ __forceinline__ void ld_rowpart(const void* base, long row, int l, float (&x)[D / LPK]) {
+    constexpr int DPL = D / LPK, VE = 16 / (int)sizeof(typename E::T);
+    if constexpr (DPL >= VE) {
+#pragma unroll
+        for (int c = 0; c < DPL / VE; ++c) {
+            float y[VE];
+            ldv<E, VE>(base, row + (long)(l + LPK * c) * VE, y);
+#pragma unroll
+            for (int e = 0; e < VE; ++e) x[c * VE + e] = y[e];
+        }
+    } else {
+        ldv<E, DPL>(base, row + (long)l * DPL, x);
+    }
+}
+
 // the 16 / sizeof(T) elements of a 16-byte vector as fp32
 template <class E>
 __device__ __forceinline__ void unpack16(const uint4& u, float (&x)[16 / sizeof(typename E::T)]) {
@@ -371,14 +390,14 @@ __global__ __launch_bounds__(KV_NT) void kv_split_kernel(KvArgs a) {
         kpos[k] = (int)kv_key_pos(a, qi, blk, nsel, v0 + (k < nk ? k : nk - 1));
     __syncthreads();
 
-    // scores: 16 lanes per key, dims (lane % 16) * DPL .. + DPL - 1
+    // scores: 16 lanes per key (dims of lane l: ld_rowpart)
     {
-        const int kl = lane / LPK, dl = (lane % LPK) * DPL;
+        const int kl = lane / LPK, ll = lane % LPK;
         float q[RM][DPL];
 #pragma unroll
         for (int r = 0; r < RM; ++r) {
             if (r < R) {
-                ldv<E, DPL>(a.q, ((long)bt * H + g * R + r) * D + dl, q[r]);
+                ld_rowpart<E, D, LPK>(a.q, ((long)bt * H + g * R + r) * D, ll, q[r]);
 #pragma unroll
                 for (int e = 0; e < DPL; ++e) q[r][e] *= a.scale;
             } else {
@@ -393,7 +412,7 @@ __global__ __launch_bounds__(KV_NT) void kv_split_kernel(KvArgs a) {
             for (int u = 0; u < US; ++u) {
                 const int k = k0 + u * STEP;
                 const long pos = kpos[k < KV_SPLIT ? k : KV_SPLIT - 1];
-                ldv<E, DPL>(a.k, bg * a.k_sbg + pos * a.k_st + dl, kx[u]);
+                ld_rowpart<E, D, LPK>(a.k, bg * a.k_sbg + pos * a.k_st, ll, kx[u]);
             }
 #pragma unroll
             for (int u = 0; u < US; ++u) {

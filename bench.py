@@ -410,6 +410,75 @@ def run_teacher_decode(steps, warmup, dev, retrieval=True, n=32768):
                          "frac": gbs / HBM_PEAK_GBS}}
 
 
+FP32_PEAK_TFLOPS = 157.3      # MI355X dense fp32 MFMA, TFLOP/s
+
+
+def gdn_bwd_flops(T, G, R, D, C=64):
+    """FLOPs of the products bf_gdn_bwd computes (per chunk and KV head: (18 + 10R) C^2 D + (14 + 4R) C D^2 + 4 C^3;
+    the masked triangular products counted whole)."""
+    n = -(-T // C)
+    return n * G * ((18 + 10 * R) * C * C * D + (14 + 4 * R) * C * D * D + 4 * C ** 3)
+
+
+def run_gdn_bwd(steps, warmup, dev, T=8192):
+    """The conversion training's delta-rule backward on one time segment (motor.seq_loss with --parca 8192, the
+    layer's head geometry G=4 KV heads x R=6 query heads, D=256, fp32 as the reference trains): bf_gdn_bwd alone
+    (inputs, output gradient and final-state gradient resident), timed with HIP events; plus the whole
+    forward + backward through motor.delta_rule_gqa's autograd."""
+    from heimdall_amd import _lib, motor
+    from heimdall_amd._device import stream_ptr
+
+    B, G, R, D = 1, 4, 6, 256
+    gen = torch.Generator(device=dev).manual_seed(21)
+    rn = lambda *s: torch.randn(*s, device=dev, generator=gen)
+    q = rn(B, T, G, R, D) * D ** -0.5
+    k = F.normalize(rn(B, T, G, D), dim=-1)
+    v = rn(B, T, G, D)
+    g = -torch.rand(B, T, G, device=dev, generator=gen) * 0.05
+    beta = torch.sigmoid(rn(B, T, G))
+    s0 = rn(B, G, D, D) * 0.02
+    do, dsf = rn(B, T, G, R, D), rn(B, G, D, D) * 0.02
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dg, db, ds0 = torch.empty_like(g), torch.empty_like(beta), torch.empty_like(s0)
+    lib = _lib.load()
+    nbytes = _lib.ctypes.c_size_t(0)
+    _lib.check(lib.bf_gdn_bwd_workspace_size(B, T, G, R, D, _lib.ctypes.byref(nbytes)), "bf_gdn_bwd_workspace_size")
+    ws = torch.empty(nbytes.value, dtype=torch.uint8, device=dev)
+
+    def bwd():
+        _lib.check(lib.bf_gdn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
+                                  s0.data_ptr(), 1.0, do.data_ptr(), dsf.data_ptr(), B, T, G, R, D, dq.data_ptr(),
+                                  dk.data_ptr(), dv.data_ptr(), dg.data_ptr(), db.data_ptr(), ds0.data_ptr(),
+                                  ws.data_ptr(), nbytes.value, stream_ptr(dev)), "bf_gdn_bwd")
+
+    def fwd_bwd():
+        xs = [x.requires_grad_(True) for x in (q.clone(), k.clone(), v.clone(), g.clone(), beta.clone())]
+        st = s0.clone().requires_grad_(True)
+        o, s = motor.delta_rule_gqa(*xs, 64, st)
+        torch.autograd.grad((o, s), xs + [st], (do, dsf))
+
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+    for name, fn, n in (("bwd", bwd, steps), ("fwd_bwd", fwd_bwd, max(1, steps // 2))):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        res[name] = e0.elapsed_time(e1) / n
+    fl = gdn_bwd_flops(T, G, R, D)
+    tf = fl / (res["bwd"] * 1e-3) / 1e12
+    return {"workload": f"delta-rule backward B=1 T={T} G={G} R={R} D={D} fp32 (one training segment)",
+            "ms_per_step": res["bwd"], "fwd_bwd_ms": res["fwd_bwd"], "tokens_per_s": T / (res["bwd"] * 1e-3),
+            "steps": steps, "flops": fl, "workspace_bytes": nbytes.value,
+            "roofline": {"bound": "mfma", "achieved": tf, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": tf / FP32_PEAK_TFLOPS}}
+
+
 def run_window(steps, warmup, dev, T=32768):
     """The window kernel alone on the layer prefill's shapes (B=1, H=24, G=4, D=256, W=2048 + 4 sinks, bf16, from
     position 0 with the first 4 tokens as sinks, no ring, no mix): bf_window_fwd timed with HIP events on the launch
@@ -499,7 +568,7 @@ def main():
     ap.add_argument("--copy-probe", action="store_true", help="run one 256 MiB device copy first (counter scaling)")
     ap.add_argument("--segment-chunks", type=int, default=0, help="chunks per scan segment (0 = library default)")
     ap.add_argument("--only", choices=("decode", "layer", "layer131k", "window", "varlen", "gdn_layer", "teacher",
-                                       "teacher_decode", "teacher_decode_full"), default=None,
+                                       "teacher_decode", "teacher_decode_full", "gdn_bwd"), default=None,
                     help="run one secondary leg alone and print its JSON object (for per-workload profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -525,7 +594,8 @@ def main():
                "gdn_layer": lambda: run_gdn_layer(args.steps, args.warmup, dev),
                "teacher": lambda: run_teacher(args.steps, args.warmup, dev),
                "teacher_decode": lambda: run_teacher_decode(args.steps, args.warmup, dev),
-               "teacher_decode_full": lambda: run_teacher_decode(args.steps, args.warmup, dev, retrieval=False)}[args.only]
+               "teacher_decode_full": lambda: run_teacher_decode(args.steps, args.warmup, dev, retrieval=False),
+               "gdn_bwd": lambda: run_gdn_bwd(args.steps, args.warmup, dev)}[args.only]
         print(json.dumps(leg()), flush=True)
         return
 

@@ -175,6 +175,21 @@ struct KvArgs {
 };
 int kv_dispatch(const KvArgs& a, int what, hipStream_t stream);   // what: 0 summaries, 1 selection, 2 attention
 
+struct GdnBwdArgs {
+    // inputs, fp32, token-major: q, dO [N_tok][G*R][D]; k, v [N_tok][G][D]; g, beta [N_tok][G]; N_tok = num_seqs *
+    // n_chunks * 64; s0, dsf [num_seqs][G][D][D] or null (zero)
+    const float *q, *k, *v, *g, *beta, *s0, *dO, *dsf;
+    float scale;
+    int num_seqs, n_chunks, G, R, D;
+    // outputs (same layouts); ds0 may be null
+    float *dq, *dk, *dv, *dg, *dbeta, *ds0;
+    // workspace, chunk-major [chunk][g][...] (cg = chunk * G + g)
+    float *gam, *dgz, *P, *Am, *Mi, *dA, *kb, *vb, *kbe, *ktl, *u, *w, *QK, *attn, *dattn, *qd, *dqd, *Sc, *E2, *dSx;
+    float *E1, *dvn, *vn, *dkt, *dw, *dvb, *dkbe, *dkb, *dkacc;
+};
+size_t gdn_bwd_workspace(int num_seqs, long T, int G, int R, int D);
+int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t stream);
+
 struct KvAppendArgs {
     const void* k_new;              // row (b, g, i) at k_new + b * k_sb + g * k_sg + i * k_st (elements)
     const void* v_new;

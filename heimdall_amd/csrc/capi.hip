@@ -279,6 +279,33 @@ static bool kv_aligned(const void* p, int64_t s1, int64_t s2) {
     return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && s1 % 8 == 0 && s2 % 8 == 0;
 }
 
+int bf_gdn_bwd_workspace_size(int num_seqs, int64_t seq_len, int G, int R, int D, size_t* bytes) {
+    if (!bytes || num_seqs <= 0 || seq_len <= 0 || G <= 0 || R <= 0) return BF_STATUS_INVALID;
+    if (!supported_dim(D) || seq_len % 64) return BF_STATUS_UNSUPPORTED;
+    *bytes = bf::gdn_bwd_workspace(num_seqs, seq_len, G, R, D);
+    return BF_STATUS_OK;
+}
+
+int bf_gdn_bwd(const float* q, const float* k, const float* v, const float* g, const float* beta, const float* s0,
+               float scale, const float* dO, const float* ds_final, int num_seqs, int64_t seq_len, int G, int R, int D,
+               float* dq, float* dk, float* dv, float* dg, float* dbeta, float* ds0, void* workspace,
+               size_t workspace_bytes, void* stream) {
+    if (num_seqs <= 0 || seq_len <= 0 || G <= 0 || R <= 0) return BF_STATUS_INVALID;
+    if (!supported_dim(D) || seq_len % 64) return BF_STATUS_UNSUPPORTED;
+    if ((int64_t)num_seqs * (seq_len / 64) * G * R > INT32_MAX) return BF_STATUS_UNSUPPORTED;
+    if (!q || !k || !v || !g || !beta || !dO || !dq || !dk || !dv || !dg || !dbeta) return BF_STATUS_INVALID;
+    for (const void* p : {(const void*)q, (const void*)k, (const void*)v, (const void*)dO, (const void*)s0,
+                          (const void*)ds_final, (const void*)dq, (const void*)dk, (const void*)dv, (const void*)ds0})
+        if (reinterpret_cast<uintptr_t>(p) & 15) return BF_STATUS_INVALID;
+    const size_t need = bf::gdn_bwd_workspace(num_seqs, seq_len, G, R, D);
+    if (!workspace || workspace_bytes < need || (reinterpret_cast<uintptr_t>(workspace) & 255)) return BF_STATUS_WORKSPACE;
+    bf::GdnBwdArgs a{};
+    a.q = q; a.k = k; a.v = v; a.g = g; a.beta = beta; a.s0 = s0; a.dO = dO; a.dsf = ds_final; a.scale = scale;
+    a.num_seqs = num_seqs; a.n_chunks = (int)(seq_len / 64); a.G = G; a.R = R; a.D = D;
+    a.dq = dq; a.dk = dk; a.dv = dv; a.dg = dg; a.dbeta = dbeta; a.ds0 = ds0;
+    return bf::gdn_bwd(a, workspace, static_cast<hipStream_t>(stream));
+}
+
 int bf_kv_append(const void* k_new, int64_t k_sb, int64_t k_sg, int64_t k_st, const void* v_new, int64_t v_sb,
                  int64_t v_sg, int64_t v_st, int dtype, int B, int G, int t, int D, void* k_buf, void* v_buf,
                  int64_t cap, int64_t n0, void* stream) {

@@ -1,0 +1,556 @@
+// Backward of the chunked GQA gated delta rule (reference: autograd through motor.delta_rule_gqa,
+// Heimdall/heimdall/motor.py:70-102, as motor.seq_loss uses it, :149-193), fp32 like the reference's training path.
+//
+// Per chunk of C = 64 tokens and KV head (gc = in-chunk cumulative log decay, e = exp, C' = last row):
+//   A = strict_lower((k b) k^T * e^(gc_i - gc_j)),  M = (I + A)^-1,  u = M (v b),  w = M (k b e^gc)
+//   attn_r = tril((s q_r) k^T * e^(gc_i - gc_j)),  qd_r = s q_r e^gc,  kt = k e^(gc_C' - gc)
+//   v_new = u - w S,  o_r = qd_r S + attn_r v_new,  S' = e^(gc_C') S + kt^T v_new
+// The gradient of a chunk's entry state is affine in the gradient of its exit state (columns independent):
+//   dvn = kt dS' + sum_r attn_r^T dO_r,   dS = e^(gc_C') dS' + sum_r qd_r^T dO_r - w^T dvn
+// so with every chunk's entry state S (a forward walk) and exit-state gradient dS' (a reverse walk), the gradients of
+// q, k, v, b and g are dense per-chunk products, all chunks at once:
+//   dattn_r = tril(dO_r v_new^T), dqd_r = dO_r S^T, dkt = v_new dS'^T, dw = -dvn S^T,
+//   d(v b) = M^T dvn, d(k b e^gc) = M^T dw, dM = dvn (v b)^T + dw (k b e^gc)^T, dA = -strict_lower(M^T dM M^T)
+// followed by the decay, gate and cumulative-sum chains (chunk_final_kernel).
+//
+// Kernels: bgemm_kernel (batched strided fp32 GEMM on v_mfma_f32_16x16x4f32, optional triangular mask, addend and
+// accumulate), chunk_prep_kernel, decay_mask_kernel, unit_lower_inverse_kernel, walk_fwd_kernel, walk_bwd_kernel,
+// decay_grad_kernel, chunk_final_kernel.
+#include "bf_common.h"
+#include "bf_internal.h"
+
+namespace bf {
+
+namespace {
+
+constexpr int BC = 64;                  // chunk length
+constexpr int BW_NT = 256;
+
+// ------------------------------------------------------------------------------------ batched strided fp32 GEMM
+// C[z] (M x N) = add[z] + alpha * A[z] (M x K) B[z] (K x N)   (or C += alpha A B when acc), z = (z0, z1, z2);
+// element (m, k) of A at A + z0 sa0 + z1 sa1 + z2 sa2 + m am + k ak (B, C, add likewise). M, N multiples of 64,
+// K of 16. mask 1 keeps m >= n, mask 2 keeps m > n (the rest is written 0, or left unchanged when accumulating).
+struct BgArgs {
+    int M, N, K, n1, n2, nz;
+    const float* A; long sa0, sa1, sa2, am, ak;
+    const float* B; long sb0, sb1, sb2, bk, bn;
+    float* C; long sc0, sc1, sc2, cm, cn;
+    const float* add;                   // same strides as C, or null
+    float alpha;
+    int acc, mask;
+};
+
+template <bool AK1, bool BK1>
+__global__ __launch_bounds__(BW_NT) void bgemm_kernel(BgArgs a) {
+    const int lane = lane_id(), wv = wave_id();
+    const long z = blockIdx.x;
+    const long z2 = z % a.n2, z1 = (z / a.n2) % a.n1, z0 = z / ((long)a.n1 * a.n2);
+    const float* A = a.A + z0 * a.sa0 + z1 * a.sa1 + z2 * a.sa2;
+    const float* B = a.B + z0 * a.sb0 + z1 * a.sb1 + z2 * a.sb2;
+    const long coff = z0 * a.sc0 + z1 * a.sc1 + z2 * a.sc2;
+    const int m0 = blockIdx.y * 64 + (wv >> 1) * 32, n0 = blockIdx.z * 64 + (wv & 1) * 32;
+    const int i = lane & 15, q = lane >> 4;
+    f32x4 acc[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const bool skip = (a.mask == 1 && m0 + 31 < n0) || (a.mask == 2 && m0 + 31 <= n0);
+    if (!skip) {
+        for (int k0 = 0; k0 < a.K; k0 += 16) {
+            uint4 af[2], bf[2];
+            const int kk = k0 + 4 * q;
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const float* pa = A + (long)(m0 + 16 * t + i) * a.am;
+                if constexpr (AK1) {
+                    af[t] = ld16(pa + kk);
+                } else {
+                    af[t] = make_uint4(__float_as_uint(pa[(long)kk * a.ak]), __float_as_uint(pa[(long)(kk + 1) * a.ak]),
+                                       __float_as_uint(pa[(long)(kk + 2) * a.ak]),
+                                       __float_as_uint(pa[(long)(kk + 3) * a.ak]));
+                }
+                const float* pb = B + (long)(n0 + 16 * t + i) * a.bn;
+                if constexpr (BK1) {
+                    bf[t] = ld16(pb + kk);
+                } else {
+                    bf[t] = make_uint4(__float_as_uint(pb[(long)kk * a.bk]), __float_as_uint(pb[(long)(kk + 1) * a.bk]),
+                                       __float_as_uint(pb[(long)(kk + 2) * a.bk]),
+                                       __float_as_uint(pb[(long)(kk + 3) * a.bk]));
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int u = 0; u < 2; ++u) mma<F32>(acc[t][u], af[t], bf[u]);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int m = m0 + 16 * t + 4 * q + v, n = n0 + 16 * u + i;
+                const bool keep = a.mask == 0 || (a.mask == 1 && m >= n) || (a.mask == 2 && m > n);
+                const long at = coff + (long)m * a.cm + (long)n * a.cn;
+                float val = keep ? a.alpha * acc[t][u][v] : 0.f;
+                if (a.acc) {
+                    if (keep) a.C[at] += val;
+                } else {
+                    if (a.add) val += a.add[at];
+                    a.C[at] = val;
+                }
+            }
+}
+
+// ------------------------------------------------------------------------------------ per-chunk elementwise prep
+// one workgroup per (chunk, KV head): gc, k b, v b, k b e^gc, kt, and qd_r = s q_r e^gc for the R query heads
+__global__ __launch_bounds__(BW_NT) void chunk_prep_kernel(GdnBwdArgs a) {
+    const long bc = blockIdx.x;
+    const int g = blockIdx.y, tid = threadIdx.x;
+    const int D = a.D, G = a.G, R = a.R, H = G * R;
+    __shared__ float gc[BC], eg[BC];
+    const long cg = bc * G + g;
+    if (tid < 64) {
+        // inclusive prefix sum of g over the chunk (one wave, shuffle scan)
+        float x = a.g[(bc * BC + tid) * G + g];
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float y = __shfl_up(x, off);
+            if (tid >= off) x += y;
+        }
+        gc[tid] = x;
+        eg[tid] = expf(x);
+        a.gam[cg * BC + tid] = x;
+    }
+    __syncthreads();
+    const float gl = gc[BC - 1];
+    for (int e = tid; e < BC * D; e += BW_NT) {
+        const int i = e / D, d = e % D;
+        const long tok = bc * BC + i;
+        const float be = a.beta[tok * G + g];
+        const float kx = a.k[(tok * G + g) * D + d], vx = a.v[(tok * G + g) * D + d];
+        const long o = (cg * BC + i) * D + d;
+        a.kb[o] = kx * be;
+        a.vb[o] = vx * be;
+        a.kbe[o] = kx * be * eg[i];
+        a.ktl[o] = kx * expf(gl - gc[i]);
+        for (int r = 0; r < R; ++r)
+            a.qd[((cg * R + r) * BC + i) * D + d] = a.scale * a.q[(tok * H + g * R + r) * D + d] * eg[i];
+    }
+}
+
+// dst = src * e^(gc_i - gc_j) on the kept triangle (mask 1: i >= j, 2: i > j), 0 elsewhere; nmat matrices per
+// (chunk, KV head), C x C each
+__global__ __launch_bounds__(BW_NT) void decay_mask_kernel(const float* src, float* dst, const float* gam, int nmat,
+                                                           int mask) {
+    const long cg = blockIdx.x;
+    __shared__ float gc[BC];
+    if (threadIdx.x < BC) gc[threadIdx.x] = gam[cg * BC + threadIdx.x];
+    __syncthreads();
+    for (int e = threadIdx.x; e < nmat * BC * BC; e += BW_NT) {
+        const int ij = e % (BC * BC), i = ij / BC, j = ij % BC;
+        const bool keep = mask == 1 ? i >= j : i > j;
+        const long at = cg * nmat * BC * BC + e;
+        dst[at] = keep ? src[at] * expf(gc[i] - gc[j]) : 0.f;
+    }
+}
+
+// M = (I + A)^-1 for a strictly lower A (C x C): forward substitution, lane j owns column j
+__global__ __launch_bounds__(64) void unit_lower_inverse_kernel(const float* Am, float* Mi) {
+    const long cg = blockIdx.x;
+    __shared__ float As[BC][BC + 1];
+    __shared__ float Ms[BC][BC + 1];
+    const int j = threadIdx.x;
+    for (int i = 0; i < BC; ++i) As[i][j] = Am[(cg * BC + i) * BC + j];
+    __syncthreads();
+    for (int i = 0; i < BC; ++i) {
+        float s = i == j ? 1.f : 0.f;
+        for (int k = 0; k < i; ++k) s -= As[i][k] * Ms[k][j];
+        Ms[i][j] = s;
+    }
+    for (int i = 0; i < BC; ++i) Mi[(cg * BC + i) * BC + j] = Ms[i][j];
+}
+
+// ------------------------------------------------------------------------------------ state walks
+// forward: every chunk's entry state; grid (sequences, G, D / 16), the workgroup owns 16 state columns
+__global__ __launch_bounds__(BW_NT) void walk_fwd_kernel(GdnBwdArgs a) {
+    const int b = blockIdx.x, g = blockIdx.y, col0 = blockIdx.z * 16, tid = threadIdx.x;
+    const int D = a.D, G = a.G, n = a.n_chunks;
+    __shared__ float Ss[256][16];
+    __shared__ float Vs[BC][16];
+    for (int e = tid; e < D * 16; e += BW_NT) {
+        const int d = e / 16, j = e % 16;
+        Ss[d][j] = a.s0 ? a.s0[(((long)b * G + g) * D + d) * D + col0 + j] : 0.f;
+    }
+    __syncthreads();
+    const int vi = tid / 4, vj = (tid % 4) * 4;
+    for (int c = 0; c < n; ++c) {
+        const long bc = (long)b * n + c, cg = bc * G + g;
+        for (int e = tid; e < D * 4; e += BW_NT) {              // entry state
+            const int d = e / 4, j = (e % 4) * 4;
+            *reinterpret_cast<float4*>(a.Sc + (cg * D + d) * D + col0 + j) =
+                make_float4(Ss[d][j], Ss[d][j + 1], Ss[d][j + 2], Ss[d][j + 3]);
+        }
+        // v_new strip = u - w S
+        const float* wr = a.w + (cg * BC + vi) * D;
+        float4 acc = *reinterpret_cast<const float4*>(a.u + (cg * BC + vi) * D + col0 + vj);
+        for (int d = 0; d < D; ++d) {
+            const float x = wr[d];
+            acc.x -= x * Ss[d][vj]; acc.y -= x * Ss[d][vj + 1]; acc.z -= x * Ss[d][vj + 2]; acc.w -= x * Ss[d][vj + 3];
+        }
+        __syncthreads();
+        Vs[vi][vj] = acc.x; Vs[vi][vj + 1] = acc.y; Vs[vi][vj + 2] = acc.z; Vs[vi][vj + 3] = acc.w;
+        __syncthreads();
+        const float ec = expf(a.gam[cg * BC + BC - 1]);
+        if (tid < D) {
+            float s[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) s[j] = ec * Ss[tid][j];
+            for (int i = 0; i < BC; ++i) {
+                const float kt = a.ktl[(cg * BC + i) * D + tid];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) s[j] += kt * Vs[i][j];
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) Ss[tid][j] = s[j];
+        }
+        __syncthreads();
+    }
+}
+
+// reverse: every chunk's exit-state gradient dS' and dvn, and ds0; same grid
+__global__ __launch_bounds__(BW_NT) void walk_bwd_kernel(GdnBwdArgs a) {
+    const int b = blockIdx.x, g = blockIdx.y, col0 = blockIdx.z * 16, tid = threadIdx.x;
+    const int D = a.D, G = a.G, n = a.n_chunks;
+    __shared__ float Ls[256][16];
+    __shared__ float Vs[BC][16];
+    for (int e = tid; e < D * 16; e += BW_NT) {
+        const int d = e / 16, j = e % 16;
+        Ls[d][j] = a.dsf ? a.dsf[(((long)b * G + g) * D + d) * D + col0 + j] : 0.f;
+    }
+    __syncthreads();
+    const int vi = tid / 4, vj = (tid % 4) * 4;
+    for (int c = n - 1; c >= 0; --c) {
+        const long bc = (long)b * n + c, cg = bc * G + g;
+        for (int e = tid; e < D * 4; e += BW_NT) {              // exit-state gradient of chunk c
+            const int d = e / 4, j = (e % 4) * 4;
+            *reinterpret_cast<float4*>(a.dSx + (cg * D + d) * D + col0 + j) =
+                make_float4(Ls[d][j], Ls[d][j + 1], Ls[d][j + 2], Ls[d][j + 3]);
+        }
+        // dvn strip = kt dS' + E1
+        const float* kr = a.ktl + (cg * BC + vi) * D;
+        float4 acc = *reinterpret_cast<const float4*>(a.E1 + (cg * BC + vi) * D + col0 + vj);
+        for (int d = 0; d < D; ++d) {
+            const float x = kr[d];
+            acc.x += x * Ls[d][vj]; acc.y += x * Ls[d][vj + 1]; acc.z += x * Ls[d][vj + 2]; acc.w += x * Ls[d][vj + 3];
+        }
+        *reinterpret_cast<float4*>(a.dvn + (cg * BC + vi) * D + col0 + vj) = acc;
+        __syncthreads();
+        Vs[vi][vj] = acc.x; Vs[vi][vj + 1] = acc.y; Vs[vi][vj + 2] = acc.z; Vs[vi][vj + 3] = acc.w;
+        __syncthreads();
+        const float ec = expf(a.gam[cg * BC + BC - 1]);
+        if (tid < D) {
+            float s[16];
+            const float* e2 = a.E2 + (cg * D + tid) * D + col0;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) s[j] = ec * Ls[tid][j] + e2[j];
+            for (int i = 0; i < BC; ++i) {
+                const float wx = a.w[(cg * BC + i) * D + tid];
+#pragma unroll
+                for (int j = 0; j < 16; ++j) s[j] -= wx * Vs[i][j];
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) Ls[tid][j] = s[j];
+        }
+        __syncthreads();
+    }
+    if (a.ds0)
+        for (int e = tid; e < D * 16; e += BW_NT) {
+            const int d = e / 16, j = e % 16;
+            a.ds0[(((long)b * G + g) * D + d) * D + col0 + j] = Ls[d][j];
+        }
+}
+
+// ------------------------------------------------------------------------------------ decay gradients
+// dAd = dA * decay (in place), dattn_r *= decay (in place), and the decay's share of d gc:
+// Z = dAd * P + sum_r dattn_r * QK_r, dgz_i = sum_j Z_ij - sum_j Z_ji
+__global__ __launch_bounds__(BW_NT) void decay_grad_kernel(GdnBwdArgs a) {
+    const long cg = blockIdx.x;
+    const int tid = threadIdx.x, R = a.R;
+    __shared__ float gc[BC];
+    __shared__ float Z[BC][BC + 1];
+    if (tid < BC) gc[tid] = a.gam[cg * BC + tid];
+    __syncthreads();
+    for (int e = tid; e < BC * BC; e += BW_NT) {
+        const int i = e / BC, j = e % BC;
+        float z = 0.f;
+        if (i >= j) {
+            const float dec = expf(gc[i] - gc[j]);
+            const long at = cg * BC * BC + e;
+            if (i > j) {
+                const float d = a.dA[at] * dec;
+                a.dA[at] = d;
+                z = d * a.P[at];
+            } else {
+                a.dA[at] = 0.f;
+            }
+            for (int r = 0; r < R; ++r) {
+                const long ar = (cg * R + r) * BC * BC + e;
+                const float d = a.dattn[ar] * dec;
+                a.dattn[ar] = d;
+                z += d * a.QK[ar];
+            }
+        }
+        Z[i][j] = z;
+    }
+    __syncthreads();
+    if (tid < BC) {
+        float s = 0.f;
+        for (int j = 0; j < BC; ++j) s += Z[tid][j] - Z[j][tid];
+        a.dgz[cg * BC + tid] = s;
+    }
+}
+
+// ------------------------------------------------------------------------------------ final assembly
+// one workgroup per (chunk, KV head): dq += s dqd e^gc, dk, dv, d beta, d gc -> dg (reverse cumulative sum)
+__global__ __launch_bounds__(BW_NT) void chunk_final_kernel(GdnBwdArgs a) {
+    const long bc = blockIdx.x;
+    const int g = blockIdx.y, tid = threadIdx.x, lane = lane_id(), wv = wave_id();
+    const int D = a.D, G = a.G, R = a.R, H = G * R;
+    const long cg = bc * G + g;
+    __shared__ float gc[BC], dgam[BC], dbe[BC], red[BW_NT / 64];
+    if (tid < BC) {
+        gc[tid] = a.gam[cg * BC + tid];
+        dgam[tid] = a.dgz[cg * BC + tid];
+        dbe[tid] = 0.f;
+    }
+    __syncthreads();
+    const float gl = gc[BC - 1], ec = expf(gl);
+    // <S, dS'> and sum(dkt * kt) for the last row's gc
+    float sdot = 0.f;
+    for (long e = tid; e < (long)D * D; e += BW_NT) sdot += a.Sc[cg * D * D + e] * a.dSx[cg * D * D + e];
+    // rows: wave w handles rows w, w + 4, ...; lanes over dims
+    float ktsum = 0.f;
+    for (int i = wv; i < BC; i += BW_NT / 64) {
+        const long tok = bc * BC + i;
+        const float egi = expf(gc[i]), eti = expf(gl - gc[i]);
+        const float be = a.beta[tok * G + g];
+        float dgi = 0.f, dbi = 0.f;
+        for (int d = lane; d < D; d += 64) {
+            const long o = (cg * BC + i) * D + d;
+            float dqsum = 0.f;
+            for (int r = 0; r < R; ++r) {
+                const long orr = ((cg * R + r) * BC + i) * D + d;
+                const float dqd = a.dqd[orr];
+                dqsum += dqd * a.qd[orr];
+                a.dq[(tok * H + g * R + r) * D + d] += a.scale * dqd * egi;
+            }
+            const float dkt = a.dkt[o], kt = a.ktl[o];
+            const float dkbe = a.dkbe[o];
+            const float dkbt = a.dkb[o] + dkbe * egi;
+            const float kx = a.k[(tok * G + g) * D + d], vx = a.v[(tok * G + g) * D + d];
+            const float dvb = a.dvb[o];
+            dgi += dqsum + dkbe * a.kbe[o] - dkt * kt;
+            ktsum += dkt * kt;
+            dbi += dkbt * kx + dvb * vx;
+            a.dk[(tok * G + g) * D + d] = a.dkacc[o] + dkt * eti + dkbt * be;
+            a.dv[(tok * G + g) * D + d] = dvb * be;
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            dgi += __shfl_xor(dgi, off);
+            dbi += __shfl_xor(dbi, off);
+        }
+        if (lane == 0) {
+            dgam[i] += dgi;
+            dbe[i] = dbi;
+        }
+    }
+    // block sums of sdot and ktsum -> the last row's d gc
+    float t = sdot * ec + ktsum;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off);
+    __syncthreads();
+    if (lane == 0) red[wv] = t;
+    __syncthreads();
+    if (tid == 0) {
+        float s = 0.f;
+        for (int w = 0; w < BW_NT / 64; ++w) s += red[w];
+        dgam[BC - 1] += s;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        // dg_j = sum_{i >= j} d gc_i: reverse inclusive scan in one wave
+        float x = dgam[BC - 1 - tid];
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float y = __shfl_up(x, off);
+            if (tid >= off) x += y;
+        }
+        const long tok = bc * BC + (BC - 1 - tid);
+        a.dg[tok * G + g] = x;
+        a.dbeta[bc * BC * G + tid * G + g] = dbe[tid];
+    }
+}
+
+// ------------------------------------------------------------------------------------ host side
+int bgemm(const BgArgs& a, hipStream_t s) {
+    const dim3 grid((unsigned)a.nz, a.M / 64, a.N / 64);
+    const bool ak1 = a.ak == 1, bk1 = a.bk == 1;
+    if (ak1 && bk1) hipLaunchKernelGGL((bgemm_kernel<true, true>), grid, dim3(BW_NT), 0, s, a);
+    else if (ak1) hipLaunchKernelGGL((bgemm_kernel<true, false>), grid, dim3(BW_NT), 0, s, a);
+    else if (bk1) hipLaunchKernelGGL((bgemm_kernel<false, true>), grid, dim3(BW_NT), 0, s, a);
+    else hipLaunchKernelGGL((bgemm_kernel<false, false>), grid, dim3(BW_NT), 0, s, a);
+    return (int)hipGetLastError();
+}
+
+// a matrix operand: base pointer, batch strides over (chunk, KV head, query head), row and column strides
+struct Op {
+    const float* p;
+    long s0, s1, s2, rs, cs;
+};
+
+// C (M x N) per (chunk, g[, r]) = add + alpha * A B, with A, B given as Op (transposes by swapping strides)
+int gemm(int M, int N, int K, int nz, int n1, int n2, Op A, Op B, float* C, long c0, long c1, long c2, long cm,
+         long cn, float alpha, int acc, int mask, const float* add, hipStream_t s) {
+    BgArgs g{};
+    g.M = M; g.N = N; g.K = K; g.n1 = n1; g.n2 = n2; g.nz = nz;
+    g.A = A.p; g.sa0 = A.s0; g.sa1 = A.s1; g.sa2 = A.s2; g.am = A.rs; g.ak = A.cs;
+    g.B = B.p; g.sb0 = B.s0; g.sb1 = B.s1; g.sb2 = B.s2; g.bk = B.rs; g.bn = B.cs;
+    g.C = C; g.sc0 = c0; g.sc1 = c1; g.sc2 = c2; g.cm = cm; g.cn = cn;
+    g.alpha = alpha; g.acc = acc; g.mask = mask; g.add = add;
+    return bgemm(g, s);
+}
+
+Op tr(Op o) { std::swap(o.rs, o.cs); return o; }
+
+}  // namespace
+
+size_t gdn_bwd_workspace(int num_seqs, long T, int G, int R, int D) {
+    const long n = T / BC, NC = (long)num_seqs * n * G;             // chunk-heads
+    const long cc = BC * BC, cd = (long)BC * D, dd = (long)D * D;
+    const long floats = NC * (BC * 2                                 // gam, dgz
+                              + cc * 4                               // P, Am, M, dA
+                              + cd * 6                               // kb, vb, kbe, ktl, u, w
+                              + (long)R * (cc * 3 + cd * 2)          // QK, attn, dattn; qd, dqd
+                              + dd * 3                               // Sc, E2, dSx
+                              + cd * 9                               // E1, dvn, vn, dkt, dw, dvb, dkbe, dkb, dkacc
+                              + cc * 2);                             // dM, T1
+    return (size_t)floats * sizeof(float) + 256 * 48;                // each buffer rounded up to 256 bytes
+}
+
+int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
+    const int D = a.D, G = a.G, R = a.R, H = G * R;
+    const long n = a.n_chunks, NB = (long)a.num_seqs * n, NC = NB * G;
+    const long cc = BC * BC, cd = (long)BC * D, dd = (long)D * D;
+    char* p = static_cast<char*>(ws);
+    auto take = [&](long count) {
+        float* r = reinterpret_cast<float*>(p);
+        p += ((count * (long)sizeof(float) + 255) / 256) * 256;
+        return r;
+    };
+    a.gam = take(NC * BC); a.dgz = take(NC * BC);
+    a.P = take(NC * cc); a.Am = take(NC * cc); a.Mi = take(NC * cc); a.dA = take(NC * cc);
+    a.kb = take(NC * cd); a.vb = take(NC * cd); a.kbe = take(NC * cd); a.ktl = take(NC * cd);
+    a.u = take(NC * cd); a.w = take(NC * cd);
+    a.QK = take(NC * R * cc); a.attn = take(NC * R * cc); a.dattn = take(NC * R * cc);
+    a.qd = take(NC * R * cd); a.dqd = take(NC * R * cd);
+    a.Sc = take(NC * dd); a.E2 = take(NC * dd); a.dSx = take(NC * dd);
+    a.E1 = take(NC * cd); a.dvn = take(NC * cd); a.vn = take(NC * cd); a.dkt = take(NC * cd); a.dw = take(NC * cd);
+    a.dvb = take(NC * cd); a.dkbe = take(NC * cd); a.dkb = take(NC * cd); a.dkacc = take(NC * cd);
+    float* dM = take(NC * cc);
+    float* T1 = take(NC * cc);
+
+    int e = 0;
+    auto ok = [&](int r) { if (r != 0 && e == 0) e = r; };
+    // every product batches over z = (chunk, g, r) with n1 = G, n2 = R (or 1)
+    // token-major inputs, chunk views: k [C x D] of (chunk, g); q_r, dO_r [C x D] of (chunk, g, r)
+    auto kT = [&]() { return Op{a.k, (long)BC * G * D, D, 0, (long)G * D, 1}; };
+    auto qR = [&]() { return Op{a.q, (long)BC * H * D, (long)R * D, D, (long)H * D, 1}; };   // q_r chunk
+    auto dOR = [&]() { return Op{a.dO, (long)BC * H * D, (long)R * D, D, (long)H * D, 1}; }; // dO_r chunk
+    // per (chunk, g) workspace arrays addressed with z = (chunk, g): s0 = G * size, s1 = size
+    auto W = [&](const float* q, long rows, long cols) { return Op{q, (long)G * rows * cols, rows * cols, 0, cols, 1}; };
+    auto WR = [&](const float* q, long rows, long cols) {
+        return Op{q, (long)G * R * rows * cols, (long)R * rows * cols, rows * cols, cols, 1};
+    };
+    const int nzg = (int)NC, nzr = (int)(NC * R);
+
+    // prep
+    hipLaunchKernelGGL(chunk_prep_kernel, dim3((unsigned)NB, G), dim3(BW_NT), 0, s, a);
+    ok((int)hipGetLastError());
+    // P = (k b) k^T ; Am = strict_lower(P * decay)
+    ok(gemm(BC, BC, D, nzg, G, 1, W(a.kb, BC, D), tr(kT()), a.P, (long)G * cc, cc, 0, BC, 1, 1.f, 0, 0, nullptr, s));
+    hipLaunchKernelGGL(decay_mask_kernel, dim3((unsigned)NC), dim3(BW_NT), 0, s, a.P, a.Am, a.gam, 1, 2);
+    ok((int)hipGetLastError());
+    hipLaunchKernelGGL(unit_lower_inverse_kernel, dim3((unsigned)NC), dim3(64), 0, s, a.Am, a.Mi);
+    ok((int)hipGetLastError());
+    // u = M (v b), w = M (k b e^gc)
+    ok(gemm(BC, D, BC, nzg, G, 1, W(a.Mi, BC, BC), W(a.vb, BC, D), a.u, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0, nullptr, s));
+    ok(gemm(BC, D, BC, nzg, G, 1, W(a.Mi, BC, BC), W(a.kbe, BC, D), a.w, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0, nullptr, s));
+    // QK_r = s q_r k^T (lower incl.), attn_r = tril(QK_r * decay)
+    ok(gemm(BC, BC, D, nzr, G, R, qR(), tr(Op{a.k, (long)BC * G * D, D, 0, (long)G * D, 1}), a.QK, (long)G * R * cc,
+            (long)R * cc, cc, BC, 1, a.scale, 0, 1, nullptr, s));
+    hipLaunchKernelGGL(decay_mask_kernel, dim3((unsigned)NC), dim3(BW_NT), 0, s, a.QK, a.attn, a.gam, R, 1);
+    ok((int)hipGetLastError());
+    // E1 = sum_r attn_r^T dO_r  [C x D],  E2 = sum_r qd_r^T dO_r  [D x D]
+    for (int r = 0; r < R; ++r) {
+        Op at = tr(WR(a.attn + r * cc, BC, BC));
+        at.s0 = (long)G * R * cc; at.s1 = (long)R * cc; at.s2 = 0;
+        Op dO = Op{a.dO + (long)r * D, (long)BC * H * D, (long)R * D, 0, (long)H * D, 1};
+        ok(gemm(BC, D, BC, nzg, G, 1, at, dO, a.E1, (long)G * cd, cd, 0, D, 1, 1.f, r > 0, 0, nullptr, s));
+        Op qd = tr(Op{a.qd + r * cd, (long)G * R * cd, (long)R * cd, 0, D, 1});
+        ok(gemm(D, D, BC, nzg, G, 1, qd, dO, a.E2, (long)G * dd, dd, 0, D, 1, 1.f, r > 0, 0, nullptr, s));
+    }
+    // walks
+    hipLaunchKernelGGL(walk_fwd_kernel, dim3(a.num_seqs, G, D / 16), dim3(BW_NT), 0, s, a);
+    ok((int)hipGetLastError());
+    hipLaunchKernelGGL(walk_bwd_kernel, dim3(a.num_seqs, G, D / 16), dim3(BW_NT), 0, s, a);
+    ok((int)hipGetLastError());
+    // v_new = u - w S
+    ok(gemm(BC, D, D, nzg, G, 1, W(a.w, BC, D), W(a.Sc, D, D), a.vn, (long)G * cd, cd, 0, D, 1, -1.f, 0, 0, a.u, s));
+    // dattn_r = tril(dO_r v_new^T), dqd_r = dO_r S^T
+    ok(gemm(BC, BC, D, nzr, G, R, dOR(), tr(Op{a.vn, (long)G * cd, cd, 0, D, 1}), a.dattn, (long)G * R * cc,
+            (long)R * cc, cc, BC, 1, 1.f, 0, 1, nullptr, s));
+    ok(gemm(BC, D, D, nzr, G, R, dOR(), tr(Op{a.Sc, (long)G * dd, dd, 0, D, 1}), a.dqd, (long)G * R * cd, (long)R * cd,
+            cd, D, 1, 1.f, 0, 0, nullptr, s));
+    // dkt = v_new dS'^T, dw = -dvn S^T
+    ok(gemm(BC, D, D, nzg, G, 1, W(a.vn, BC, D), tr(W(a.dSx, D, D)), a.dkt, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0,
+            nullptr, s));
+    ok(gemm(BC, D, D, nzg, G, 1, W(a.dvn, BC, D), tr(W(a.Sc, D, D)), a.dw, (long)G * cd, cd, 0, D, 1, -1.f, 0, 0,
+            nullptr, s));
+    // d(v b) = M^T dvn, d(k b e^gc) = M^T dw
+    ok(gemm(BC, D, BC, nzg, G, 1, tr(W(a.Mi, BC, BC)), W(a.dvn, BC, D), a.dvb, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0,
+            nullptr, s));
+    ok(gemm(BC, D, BC, nzg, G, 1, tr(W(a.Mi, BC, BC)), W(a.dw, BC, D), a.dkbe, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0,
+            nullptr, s));
+    // dM = dvn (v b)^T + dw (k b e^gc)^T ; T1 = M^T dM ; dA = -strict_lower(T1 M^T)
+    ok(gemm(BC, BC, D, nzg, G, 1, W(a.dvn, BC, D), tr(W(a.vb, BC, D)), dM, (long)G * cc, cc, 0, BC, 1, 1.f, 0, 0,
+            nullptr, s));
+    ok(gemm(BC, BC, D, nzg, G, 1, W(a.dw, BC, D), tr(W(a.kbe, BC, D)), dM, (long)G * cc, cc, 0, BC, 1, 1.f, 1, 0,
+            nullptr, s));
+    ok(gemm(BC, BC, BC, nzg, G, 1, tr(W(a.Mi, BC, BC)), W(dM, BC, BC), T1, (long)G * cc, cc, 0, BC, 1, 1.f, 0, 0,
+            nullptr, s));
+    ok(gemm(BC, BC, BC, nzg, G, 1, W(T1, BC, BC), tr(W(a.Mi, BC, BC)), a.dA, (long)G * cc, cc, 0, BC, 1, -1.f, 0, 2,
+            nullptr, s));
+    // decay: dA *= decay, dattn_r *= decay, d gc share
+    hipLaunchKernelGGL(decay_grad_kernel, dim3((unsigned)NC), dim3(BW_NT), 0, s, a);
+    ok((int)hipGetLastError());
+    // d(k b) from A: dAd k ; dk from A: dAd^T (k b) ; from attn: sum_r dattn_r^T (s q_r) ; dq_r = s dattn_r k
+    ok(gemm(BC, D, BC, nzg, G, 1, W(a.dA, BC, BC), kT(), a.dkb, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0, nullptr, s));
+    ok(gemm(BC, D, BC, nzg, G, 1, tr(W(a.dA, BC, BC)), W(a.kb, BC, D), a.dkacc, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0,
+            nullptr, s));
+    for (int r = 0; r < R; ++r) {
+        Op da = tr(Op{a.dattn + r * cc, (long)G * R * cc, (long)R * cc, 0, BC, 1});
+        Op q = Op{a.q + (long)r * D, (long)BC * H * D, (long)R * D, 0, (long)H * D, 1};
+        ok(gemm(BC, D, BC, nzg, G, 1, da, q, a.dkacc, (long)G * cd, cd, 0, D, 1, a.scale, 1, 0, nullptr, s));
+    }
+    ok(gemm(BC, D, BC, nzr, G, R, WR(a.dattn, BC, BC), Op{a.k, (long)BC * G * D, D, 0, (long)G * D, 1}, a.dq,
+            (long)BC * H * D, (long)R * D, D, (long)H * D, 1, a.scale, 0, 0, nullptr, s));
+    hipLaunchKernelGGL(chunk_final_kernel, dim3((unsigned)NB, G), dim3(BW_NT), 0, s, a);
+    ok((int)hipGetLastError());
+    return e;
+}
+
+}  // namespace bf

@@ -8,17 +8,71 @@ from . import _lib
 from ._device import BifrostError, check, dtype_code, gdn_forward, require_device, require_no_grad, stream_ptr
 
 
+def _pad_tokens(x: torch.Tensor, T: int, pad: int) -> torch.Tensor:
+    """[B, T, ...] -> [B, T + pad, ...] with zeros after the sequence (dim 1)."""
+    if pad == 0:
+        return x.contiguous()
+    return torch.cat((x, x.new_zeros((x.shape[0], pad) + tuple(x.shape[2:]))), 1)
+
+
+class _DeltaRuleGQA(torch.autograd.Function):
+    """Forward: ``bf_gdn_fwd`` in fp32. Backward: ``bf_gdn_bwd`` (gradients of q, k, v, g, beta and the initial
+    state, given those of o and of the final state)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, state):
+        B, T, G, R, D = q.shape
+        o, s = gdn_forward(q.reshape(B * T, G * R, D), k.reshape(B * T, G, D), v.reshape(B * T, G, D),
+                           g.reshape(B * T, G), beta.reshape(B * T, G), num_seqs=B, initial_state=state)
+        ctx.save_for_backward(q, k, v, g, beta, state)
+        return o.view(B, T, G, R, D), s
+
+    @staticmethod
+    def backward(ctx, do, ds):
+        q, k, v, g, beta, state = ctx.saved_tensors
+        B, T, G, R, D = q.shape
+        dev = q.device
+        pad = (-T) % 64                              # beta = g = 0 on the padding: the state passes unchanged
+        Tp = T + pad
+        qp, kp, vp, gp, bp = (_pad_tokens(x.float(), T, pad) for x in (q, k, v, g, beta))
+        dop = _pad_tokens(do.float() if do is not None else torch.zeros_like(q, dtype=torch.float32), T, pad)
+        dsf = ds.float().contiguous() if ds is not None else None
+        s0 = state.float().contiguous() if state is not None else None
+        dq, dk, dv = torch.empty_like(qp), torch.empty_like(kp), torch.empty_like(vp)
+        dg, dbeta = torch.empty_like(gp), torch.empty_like(bp)
+        ds0 = torch.empty_like(s0) if s0 is not None else None
+        lib = _lib.load()
+        nbytes = _lib.ctypes.c_size_t(0)
+        check(lib.bf_gdn_bwd_workspace_size(B, Tp, G, R, D, _lib.ctypes.byref(nbytes)), "bf_gdn_bwd_workspace_size")
+        ws = torch.empty(nbytes.value, dtype=torch.uint8, device=dev)
+        ptr = lambda x: x.data_ptr() if x is not None else None
+        check(lib.bf_gdn_bwd(qp.data_ptr(), kp.data_ptr(), vp.data_ptr(), gp.data_ptr(), bp.data_ptr(), ptr(s0), 1.0,
+                             dop.data_ptr(), ptr(dsf), B, Tp, G, R, D, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+                             dg.data_ptr(), dbeta.data_ptr(), ptr(ds0), ws.data_ptr(), nbytes.value,
+                             stream_ptr(dev)), "bf_gdn_bwd")
+        cut = lambda x: x[:, :T]
+        return (cut(dq).to(q.dtype), cut(dk).to(k.dtype), cut(dv).to(v.dtype), cut(dg).to(g.dtype),
+                cut(dbeta).to(beta.dtype), ds0.to(state.dtype) if ds0 is not None else None)
+
+
 def delta_rule_gqa(q, k, v, g, beta, chunk: int = 64,
                    state: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Gated delta rule with one state per KV head, read by its R query heads.
 
     q [B, T, G, R, Dk], k [B, T, G, Dk], v [B, T, G, Dv], g / beta [B, T, G], state [B, G, Dk, Dv]
     -> (o [B, T, G, R, Dv] fp32, S [B, G, Dk, Dv] fp32). ``chunk`` is accepted for interface compatibility (the
-    result is chunk-length invariant; the kernels use 64). Forward only.
+    result is chunk-length invariant; the kernels use 64). Differentiable like the reference (fp32 throughout): with
+    grad enabled and an input that requires it, the backward runs ``bf_gdn_bwd``.
     """
     require_device(q, k, v, g, beta, state)
-    require_no_grad(q, k, v, g, beta, state)
     B, T, G, R, D = q.shape
+    if v.shape[-1] != D:
+        raise BifrostError("the kernels need Dk == Dv")
+    inputs = (q, k, v, g, beta, state)
+    if torch.is_grad_enabled() and any(x is not None and x.requires_grad for x in inputs):
+        q, k, v, g, beta = (x.float() for x in (q, k, v, g, beta))
+        state = state.float() if state is not None else None
+        return _DeltaRuleGQA.apply(q, k, v, g, beta, state)
     o, s = gdn_forward(q.reshape(B * T, G * R, D), k.reshape(B * T, G, D), v.reshape(B * T, G, v.shape[-1]),
                        g.reshape(B * T, G), beta.reshape(B * T, G), num_seqs=B, initial_state=state)
     return o.view(B, T, G, R, -1), s

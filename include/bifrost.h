@@ -197,6 +197,22 @@ int bf_gated_norm(const void* o, int o_dtype, const void* z, const float* w, int
                   void* out, int io_dtype, void* stream);
 
 /*
+ * Backward of the chunked GQA gated delta rule: the gradients that autograd takes through motor.delta_rule_gqa
+ * (Heimdall/heimdall/motor.py:70-102) in the conversion training's loss (motor.seq_loss, :149-193), fp32 like the
+ * reference's training path. Inputs as bf_gdn_fwd with fp32 q, k, v for num_seqs sequences of seq_len tokens each
+ * (seq_len a multiple of 64; pad with zeros and g = beta = 0 as the reference does): q, dO [N][G*R][D], k, v
+ * [N][G][D], g, beta [N][G], s0 and ds_final [num_seqs][G][D][D] or null (zero), o = forward(q * scale, ...). dO is
+ * the gradient of o, ds_final that of the final state. Writes dq, dk, dv [same layouts], dg, dbeta [N][G] and, if
+ * non-null, ds0 [num_seqs][G][D][D]. Pointers 16-byte aligned; workspace from bf_gdn_bwd_workspace_size, 256-byte
+ * aligned.
+ */
+int bf_gdn_bwd_workspace_size(int num_seqs, int64_t seq_len, int G, int R, int D, size_t* bytes);
+int bf_gdn_bwd(const float* q, const float* k, const float* v, const float* g, const float* beta, const float* s0,
+               float scale, const float* dO, const float* ds_final, int num_seqs, int64_t seq_len, int G, int R, int D,
+               float* dq, float* dk, float* dv, float* dg, float* dbeta, float* ds0, void* workspace,
+               size_t workspace_bytes, void* stream);
+
+/*
  * Attention of the kept full-attention layers over a dense KV cache, for the T most recent queries of each sequence
  * (T = 1: one decode step), with optional retrieval (Quest-style block selection): HybridAttention._teacher
  * (Heimdall/heimdall/hibrit.py:275-290) and _retrieval_mask (:301-324). Key (b, g) row of position p at

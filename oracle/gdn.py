@@ -27,15 +27,16 @@ def unit_lower_inverse(a: torch.Tensor) -> torch.Tensor:
     forward-substitution fallback; both give the same matrix).
     """
     c = a.size(-1)
-    inv = torch.zeros_like(a)
     eye = torch.eye(c, dtype=a.dtype, device=a.device)
-    # row i of X = (I + A)^-1 solves X[i] = e_i - sum_{m<i} A[i, m] X[m]
+    # row i of X = (I + A)^-1 solves X[i] = e_i - sum_{m<i} A[i, m] X[m]; rows are collected, not written in place,
+    # so autograd can differentiate through the solve
+    rows = []
     for i in range(c):
-        row = eye[i].expand_as(inv[..., i, :]).clone()
+        row = eye[i].expand(a.shape[:-2] + (c,))
         if i:
-            row = row - (a[..., i, :i, None] * inv[..., :i, :]).sum(-2)
-        inv[..., i, :] = row
-    return inv
+            row = row - (a[..., i, :i, None] * torch.stack(rows, -2)).sum(-2)
+        rows.append(row)
+    return torch.stack(rows, -2)
 
 
 def _compute_dtype(x: torch.Tensor) -> torch.dtype:
@@ -122,12 +123,13 @@ def delta_rule_gqa(q, k, v, g, beta, chunk: int = 64,
     q_dec = qf * gc.exp()[:, :, None, :, :, None]
     k_tail = kf * (gc[..., -1:] - gc).exp()[..., None]
     tail = gc[..., -1].exp()[..., None, None]
-    s = (torch.zeros(b, G, dk, dv, dtype=dt) if state is None else state.to(dt).clone())
-    out = torch.empty(b, G, R, n, c, dv, dtype=dt)
+    s = (torch.zeros(b, G, dk, dv, dtype=dt) if state is None else state.to(dt))
+    outs = []
     for i in range(n):
         v_new = u[:, :, i] - w[:, :, i] @ s                                          # [b, G, c, dv]
-        out[:, :, :, i] = q_dec[:, :, :, i] @ s[:, :, None] + attn[:, :, :, i] @ v_new[:, :, None]
+        outs.append(q_dec[:, :, :, i] @ s[:, :, None] + attn[:, :, :, i] @ v_new[:, :, None])
         s = s * tail[:, :, i] + k_tail[:, :, i].transpose(-1, -2) @ v_new
+    out = torch.stack(outs, 3)                                                      # [b, G, R, n, c, dv]
     o = out.reshape(b, G, R, n * c, dv)[:, :, :, :t].permute(0, 3, 1, 2, 4).contiguous()
     return o, s
 
@@ -177,3 +179,18 @@ def delta_rule_varlen(q, k, v, g, beta, cu_seqlens, chunk_size: int = 64, initia
         outs.append(o)
         states.append(s)
     return torch.cat(outs, 1), torch.cat(states, 0)
+
+
+def delta_rule_gqa_grads(q, k, v, g, beta, state, do, ds=None, chunk: int = 64):
+    """The gradients the reference's conversion training takes through ``motor.delta_rule_gqa``
+    (``Heimdall/heimdall/motor.py:70-102`` inside ``seq_loss``, ``:149-193``): autograd of <o, do> + <S_final, ds>
+    with respect to (q, k, v, g, beta, state), in fp64. Returns the six gradients (state's is None without a state)."""
+    xs = [x.detach().double().requires_grad_(True) for x in (q, k, v, g, beta)]
+    s0 = state.detach().double().requires_grad_(True) if state is not None else None
+    with torch.enable_grad():
+        o, s = delta_rule_gqa(*xs, chunk=chunk, state=s0)
+        loss = (o * do.double()).sum()
+        if ds is not None:
+            loss = loss + (s * ds.double()).sum()
+        grads = torch.autograd.grad(loss, xs + ([s0] if s0 is not None else []))
+    return tuple(grads) + ((None,) if s0 is None else ())

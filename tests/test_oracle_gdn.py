@@ -146,3 +146,54 @@ def test_matches_transformers_restatement():
     rel = lambda a, b: ((a.double() - b.double()).norm() / b.double().norm()).item()
     assert rel(o_tc, o) < 1e-5 and rel(s_tc, s) < 1e-5
     assert rel(o_tr, o) < 1e-5 and rel(s_tr, s) < 1e-5
+
+
+def _gqa_inputs(B, T, G, R, D, seed):
+    gen = torch.Generator().manual_seed(seed)
+    mk = lambda *s: torch.randn(*s, generator=gen, dtype=torch.float64)
+    q = mk(B, T, G, R, D)
+    k = torch.nn.functional.normalize(mk(B, T, G, D), dim=-1)
+    v = mk(B, T, G, D)
+    g = -torch.rand(B, T, G, generator=gen, dtype=torch.float64) * 0.5
+    beta = torch.rand(B, T, G, generator=gen, dtype=torch.float64)
+    s0 = mk(B, G, D, D) * 0.3
+    return q, k, v, g, beta, s0
+
+
+def test_gqa_grads_gradcheck():
+    """The oracle's backward (autograd of delta_rule_gqa) against finite differences of its forward, all six inputs,
+    a sequence that is not a multiple of the chunk."""
+    q, k, v, g, beta, s0 = (x.requires_grad_(True) for x in _gqa_inputs(1, 19, 2, 2, 4, seed=20))
+    f = lambda *a: gdn.delta_rule_gqa(*a[:5], chunk=8, state=a[5])
+    assert torch.autograd.gradcheck(f, (q, k, v, g, beta, s0), eps=1e-6, atol=1e-6)
+
+
+def test_gqa_grads_match_token_recurrence():
+    """delta_rule_gqa_grads equals autograd through the brute-force token recurrence on the R-repeated heads (the
+    repeats' gradients summed), an independent formulation of the same function."""
+    B, T, G, R, D = 2, 37, 2, 3, 8
+    q, k, v, g, beta, s0 = _gqa_inputs(B, T, G, R, D, seed=21)
+    gen = torch.Generator().manual_seed(22)
+    do = torch.randn(B, T, G, R, D, generator=gen, dtype=torch.float64)
+    ds = torch.randn(B, G, D, D, generator=gen, dtype=torch.float64)
+    got = gdn.delta_rule_gqa_grads(q, k, v, g, beta, s0, do, ds, chunk=16)
+    xs = [x.clone().requires_grad_(True) for x in (q, k, v, g, beta, s0)]
+    rep = lambda z: z.repeat_interleave(R, 2)
+    o, s = gdn.delta_rule_recurrent(xs[0].reshape(B, T, G * R, D), rep(xs[1]), rep(xs[2]), rep(xs[3]), rep(xs[4]),
+                                    xs[5].repeat_interleave(R, 1))
+    # every repeat carries the same state; the final state of KV head g is that of its first query head
+    loss = (o.reshape(B, T, G, R, D) * do).sum() + (s[:, ::R] * ds).sum()
+    want = torch.autograd.grad(loss, xs)
+    for a, b in zip(got, want):
+        assert ((a - b).norm() / b.norm()).item() < 1e-10
+
+
+def test_gqa_grads_chunk_invariant():
+    B, T, G, R, D = 1, 50, 1, 2, 8
+    q, k, v, g, beta, s0 = _gqa_inputs(B, T, G, R, D, seed=23)
+    gen = torch.Generator().manual_seed(24)
+    do = torch.randn(B, T, G, R, D, generator=gen, dtype=torch.float64)
+    a = gdn.delta_rule_gqa_grads(q, k, v, g, beta, s0, do, None, chunk=8)
+    b = gdn.delta_rule_gqa_grads(q, k, v, g, beta, s0, do, None, chunk=64)
+    for x, y in zip(a, b):
+        assert ((x - y).norm() / y.norm()).item() < 1e-10

@@ -420,7 +420,7 @@ def gdn_bwd_flops(T, G, R, D, C=64):
     return n * G * ((18 + 10 * R) * C * C * D + (14 + 4 * R) * C * D * D + 4 * C ** 3)
 
 
-def run_gdn_bwd(steps, warmup, dev, T=8192):
+def run_gdn_bwd(steps, warmup, dev, T=8192, cpu=False):
     """The conversion training's delta-rule backward on one time segment (motor.seq_loss with --parca 8192, the
     layer's head geometry G=4 KV heads x R=6 query heads, D=256, fp32 as the reference trains): bf_gdn_bwd alone
     (inputs, output gradient and final-state gradient resident), timed with HIP events; plus the whole
@@ -472,11 +472,24 @@ def run_gdn_bwd(steps, warmup, dev, T=8192):
         res[name] = e0.elapsed_time(e1) / n
     fl = gdn_bwd_flops(T, G, R, D)
     tf = fl / (res["bwd"] * 1e-3) / 1e12
-    return {"workload": f"delta-rule backward B=1 T={T} G={G} R={R} D={D} fp32 (one training segment)",
-            "ms_per_step": res["bwd"], "fwd_bwd_ms": res["fwd_bwd"], "tokens_per_s": T / (res["bwd"] * 1e-3),
-            "steps": steps, "flops": fl, "workspace_bytes": nbytes.value,
-            "roofline": {"bound": "mfma", "achieved": tf, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": tf / FP32_PEAK_TFLOPS}}
+    out = {"workload": f"delta-rule backward B=1 T={T} G={G} R={R} D={D} fp32 (one training segment)",
+           "ms_per_step": res["bwd"], "fwd_bwd_ms": res["fwd_bwd"], "tokens_per_s": T / (res["bwd"] * 1e-3),
+           "steps": steps, "flops": fl, "workspace_bytes": nbytes.value,
+           "roofline": {"bound": "mfma", "achieved": tf, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": tf / FP32_PEAK_TFLOPS}}
+    if cpu:
+        # the oracle's gradients (autograd of the restated reference, fp32) on the host, on the same segment
+        from oracle import gdn as ogdn
+        torch.set_num_threads(len(os.sched_getaffinity(0)))
+        n = T
+        xs = [x[:, :n].cpu() for x in (q, k, v, g, beta, do)]
+        t0 = time.perf_counter()
+        ogdn.delta_rule_gqa_grads(xs[0], xs[1], xs[2], xs[3], xs[4], s0.cpu(), xs[5], dsf.cpu(), dtype=torch.float32)
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": n / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+                               "sample": f"oracle delta_rule_gqa_grads fp32 (autograd), T={n} G={G} R={R} D={D}, "
+                                         f"one run, {cpu_model()}"}
+    return out
 
 
 def run_window(steps, warmup, dev, T=32768):
@@ -595,7 +608,7 @@ def main():
                "teacher": lambda: run_teacher(args.steps, args.warmup, dev),
                "teacher_decode": lambda: run_teacher_decode(args.steps, args.warmup, dev),
                "teacher_decode_full": lambda: run_teacher_decode(args.steps, args.warmup, dev, retrieval=False),
-               "gdn_bwd": lambda: run_gdn_bwd(args.steps, args.warmup, dev)}[args.only]
+               "gdn_bwd": lambda: run_gdn_bwd(args.steps, args.warmup, dev, cpu=not args.no_cpu)}[args.only]
         print(json.dumps(leg()), flush=True)
         return
 
@@ -641,6 +654,7 @@ def main():
         line["varlen_gdn"] = run_varlen(10, 3, dev)
         line["gdn_layer"] = run_gdn_layer(10, 3, dev)
         line["teacher_decode"] = run_teacher_decode(50, 10, dev)
+        line["gdn_bwd"] = run_gdn_bwd(10, 2, dev, cpu=not args.no_cpu)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(r["inputs"])
     print(json.dumps(line), flush=True)

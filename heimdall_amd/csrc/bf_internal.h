@@ -184,7 +184,8 @@ struct GdnBwdArgs {
     // outputs (same layouts); ds0 may be null
     float *dq, *dk, *dv, *dg, *dbeta, *ds0;
     // workspace, chunk-major [chunk][g][...] (cg = chunk * G + g)
-    float *gam, *dgz, *P, *Am, *Mi, *dA, *kb, *vb, *kbe, *ktl, *u, *w, *QK, *attn, *dattn, *qd, *dqd, *Sc, *E2, *dSx;
+    float *gam, *dgz, *P, *Am, *Mi, *dA, *kb, *vb, *kbe, *ktl, *ktlT, *u, *w, *wT, *QK, *attn, *dattn, *qd, *dqd, *qc, *dOc;
+    float *Sc, *E2, *dSx, *part;
     float *E1, *dvn, *vn, *dkt, *dw, *dvb, *dkbe, *dkb, *dkacc;
 };
 size_t gdn_bwd_workspace(int num_seqs, long T, int G, int R, int D);

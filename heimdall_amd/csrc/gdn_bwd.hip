@@ -14,8 +14,8 @@
 // followed by the decay, gate and cumulative-sum chains (chunk_final_kernel).
 //
 // Kernels: bgemm_kernel (batched strided fp32 GEMM on v_mfma_f32_16x16x4f32, optional triangular mask, addend and
-// accumulate), chunk_prep_kernel, decay_mask_kernel, unit_lower_inverse_kernel, walk_fwd_kernel, walk_bwd_kernel,
-// decay_grad_kernel, chunk_final_kernel.
+// accumulate), chunk_prep_kernel, decay_mask_kernel, unit_lower_inverse_kernel, walk_kernel (both state walks in one
+// launch), decay_grad_kernel, chunk_final_kernel, dg_scan_kernel.
 #include "bf_common.h"
 #include "bf_internal.h"
 
@@ -29,7 +29,8 @@ constexpr int BW_NT = 256;
 // ------------------------------------------------------------------------------------ batched strided fp32 GEMM
 // C[z] (M x N) = add[z] + alpha * A[z] (M x K) B[z] (K x N)   (or C += alpha A B when acc), z = (z0, z1, z2);
 // element (m, k) of A at A + z0 sa0 + z1 sa1 + z2 sa2 + m am + k ak (B, C, add likewise). M, N multiples of 64,
-// K of 16. mask 1 keeps m >= n, mask 2 keeps m > n (the rest is written 0, or left unchanged when accumulating).
+// K of 16, each operand contiguous along one dimension, 16-byte aligned. mask 1 keeps m >= n, mask 2 keeps m > n (the
+// rest is written 0, or left unchanged when accumulating).
 struct BgArgs {
     int M, N, K, n1, n2, nz;
     const float* A; long sa0, sa1, sa2, am, ak;
@@ -40,44 +41,65 @@ struct BgArgs {
     int acc, mask;
 };
 
-template <bool AK1, bool BK1>
+// Operand tiles go through LDS: per K step of 16, a 64 x 16 tile of A and a 16 x 64 tile of B are read with one
+// 16-byte load per thread each, along whichever dimension is contiguous (AK: A's k, else its m; BK: B's k, else its n),
+// stored k-contiguous per row (As[m][k], Bs[n][k]) so every MFMA fragment is one 16-byte LDS read; the next step's
+// loads are issued before the current step's MFMAs.
+template <bool AK, bool BK>
 __global__ __launch_bounds__(BW_NT) void bgemm_kernel(BgArgs a) {
-    const int lane = lane_id(), wv = wave_id();
+    const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
     const long z = blockIdx.x;
     const long z2 = z % a.n2, z1 = (z / a.n2) % a.n1, z0 = z / ((long)a.n1 * a.n2);
     const float* A = a.A + z0 * a.sa0 + z1 * a.sa1 + z2 * a.sa2;
     const float* B = a.B + z0 * a.sb0 + z1 * a.sb1 + z2 * a.sb2;
     const long coff = z0 * a.sc0 + z1 * a.sc1 + z2 * a.sc2;
-    const int m0 = blockIdx.y * 64 + (wv >> 1) * 32, n0 = blockIdx.z * 64 + (wv & 1) * 32;
+    const int tm = blockIdx.y * 64, tn = blockIdx.z * 64;
+    const int m0 = (wv >> 1) * 32, n0 = (wv & 1) * 32;      // the wave's 32 x 32 block inside the tile
     const int i = lane & 15, q = lane >> 4;
+    __shared__ float As[64][20];
+    __shared__ float Bs[64][20];
     f32x4 acc[2][2];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int u = 0; u < 2; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const bool skip = (a.mask == 1 && m0 + 31 < n0) || (a.mask == 2 && m0 + 31 <= n0);
+    // the block-level skip of a masked tile wholly outside the kept triangle
+    const bool skip = (a.mask == 1 && tm + 63 < tn) || (a.mask == 2 && tm + 63 <= tn);
+    // load slots: k-contiguous operand: row t / 4, k (t % 4) * 4; otherwise k t / 16, rows (t % 16) * 4 .. + 3
+    const int ra = AK ? tid / 4 : (tid % 16) * 4, ka = AK ? (tid % 4) * 4 : tid / 16;
+    const int rb = BK ? tid / 4 : (tid % 16) * 4, kb = BK ? (tid % 4) * 4 : tid / 16;
+    auto load_a = [&](int k0) {
+        return AK ? *reinterpret_cast<const float4*>(A + (long)(tm + ra) * a.am + k0 + ka)
+                  : *reinterpret_cast<const float4*>(A + (long)(k0 + ka) * a.ak + tm + ra);
+    };
+    auto load_b = [&](int k0) {
+        return BK ? *reinterpret_cast<const float4*>(B + (long)(tn + rb) * a.bn + k0 + kb)
+                  : *reinterpret_cast<const float4*>(B + (long)(k0 + kb) * a.bk + tn + rb);
+    };
     if (!skip) {
+        float4 xa = load_a(0), xb = load_b(0);
         for (int k0 = 0; k0 < a.K; k0 += 16) {
+            __syncthreads();
+            if (AK) {
+                *reinterpret_cast<float4*>(&As[ra][ka]) = xa;
+            } else {
+                As[ra][ka] = xa.x; As[ra + 1][ka] = xa.y; As[ra + 2][ka] = xa.z; As[ra + 3][ka] = xa.w;
+            }
+            if (BK) {
+                *reinterpret_cast<float4*>(&Bs[rb][kb]) = xb;
+            } else {
+                Bs[rb][kb] = xb.x; Bs[rb + 1][kb] = xb.y; Bs[rb + 2][kb] = xb.z; Bs[rb + 3][kb] = xb.w;
+            }
+            __syncthreads();
+            if (k0 + 16 < a.K) {
+                xa = load_a(k0 + 16);
+                xb = load_b(k0 + 16);
+            }
             uint4 af[2], bf[2];
-            const int kk = k0 + 4 * q;
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                const float* pa = A + (long)(m0 + 16 * t + i) * a.am;
-                if constexpr (AK1) {
-                    af[t] = ld16(pa + kk);
-                } else {
-                    af[t] = make_uint4(__float_as_uint(pa[(long)kk * a.ak]), __float_as_uint(pa[(long)(kk + 1) * a.ak]),
-                                       __float_as_uint(pa[(long)(kk + 2) * a.ak]),
-                                       __float_as_uint(pa[(long)(kk + 3) * a.ak]));
-                }
-                const float* pb = B + (long)(n0 + 16 * t + i) * a.bn;
-                if constexpr (BK1) {
-                    bf[t] = ld16(pb + kk);
-                } else {
-                    bf[t] = make_uint4(__float_as_uint(pb[(long)kk * a.bk]), __float_as_uint(pb[(long)(kk + 1) * a.bk]),
-                                       __float_as_uint(pb[(long)(kk + 2) * a.bk]),
-                                       __float_as_uint(pb[(long)(kk + 3) * a.bk]));
-                }
+                af[t] = *reinterpret_cast<const uint4*>(&As[m0 + 16 * t + i][4 * q]);
+                bf[t] = *reinterpret_cast<const uint4*>(&Bs[n0 + 16 * t + i][4 * q]);
             }
 #pragma unroll
             for (int t = 0; t < 2; ++t)
@@ -91,7 +113,7 @@ __global__ __launch_bounds__(BW_NT) void bgemm_kernel(BgArgs a) {
         for (int u = 0; u < 2; ++u)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int m = m0 + 16 * t + 4 * q + v, n = n0 + 16 * u + i;
+                const int m = tm + m0 + 16 * t + 4 * q + v, n = tn + n0 + 16 * u + i;
                 const bool keep = a.mask == 0 || (a.mask == 1 && m >= n) || (a.mask == 2 && m > n);
                 const long at = coff + (long)m * a.cm + (long)n * a.cn;
                 float val = keep ? a.alpha * acc[t][u][v] : 0.f;
@@ -108,7 +130,7 @@ __global__ __launch_bounds__(BW_NT) void bgemm_kernel(BgArgs a) {
 // one workgroup per (chunk, KV head): gc, k b, v b, k b e^gc, kt, and qd_r = s q_r e^gc for the R query heads
 __global__ __launch_bounds__(BW_NT) void chunk_prep_kernel(GdnBwdArgs a) {
     const long bc = blockIdx.x;
-    const int g = blockIdx.y, tid = threadIdx.x;
+    const int g = blockIdx.y, r0 = blockIdx.z * 16, tid = threadIdx.x;   // rows r0 .. r0 + 15 of the chunk
     const int D = a.D, G = a.G, R = a.R, H = G * R;
     __shared__ float gc[BC], eg[BC];
     const long cg = bc * G + g;
@@ -122,12 +144,12 @@ __global__ __launch_bounds__(BW_NT) void chunk_prep_kernel(GdnBwdArgs a) {
         }
         gc[tid] = x;
         eg[tid] = expf(x);
-        a.gam[cg * BC + tid] = x;
+        if (blockIdx.z == 0) a.gam[cg * BC + tid] = x;
     }
     __syncthreads();
     const float gl = gc[BC - 1];
-    for (int e = tid; e < BC * D; e += BW_NT) {
-        const int i = e / D, d = e % D;
+    for (int e = tid; e < 16 * D; e += BW_NT) {
+        const int i = r0 + e / D, d = e % D;
         const long tok = bc * BC + i;
         const float be = a.beta[tok * G + g];
         const float kx = a.k[(tok * G + g) * D + d], vx = a.v[(tok * G + g) * D + d];
@@ -136,8 +158,17 @@ __global__ __launch_bounds__(BW_NT) void chunk_prep_kernel(GdnBwdArgs a) {
         a.vb[o] = vx * be;
         a.kbe[o] = kx * be * eg[i];
         a.ktl[o] = kx * expf(gl - gc[i]);
-        for (int r = 0; r < R; ++r)
-            a.qd[((cg * R + r) * BC + i) * D + d] = a.scale * a.q[(tok * H + g * R + r) * D + d] * eg[i];
+        for (int r = 0; r < R; ++r) {
+            const long oc = ((cg * R + r) * BC + i) * D + d;
+            const float qx = a.q[(tok * H + g * R + r) * D + d];
+            a.qd[oc] = a.scale * qx * eg[i];
+            a.qc[oc] = qx;
+            a.dOc[oc] = a.dO[(tok * H + g * R + r) * D + d];
+        }
+    }
+    for (int e = tid; e < 16 * D; e += BW_NT) {              // kt transposed [D][C], token index fastest
+        const int d = e / 16, i = r0 + e % 16;
+        a.ktlT[(cg * D + d) * BC + i] = a.k[((bc * BC + i) * G + g) * D + d] * expf(gl - gc[i]);
     }
 }
 
@@ -174,103 +205,186 @@ __global__ __launch_bounds__(64) void unit_lower_inverse_kernel(const float* Am,
 }
 
 // ------------------------------------------------------------------------------------ state walks
-// forward: every chunk's entry state; grid (sequences, G, D / 16), the workgroup owns 16 state columns
-__global__ __launch_bounds__(BW_NT) void walk_fwd_kernel(GdnBwdArgs a) {
-    const int b = blockIdx.x, g = blockIdx.y, col0 = blockIdx.z * 16, tid = threadIdx.x;
-    const int D = a.D, G = a.G, n = a.n_chunks;
-    __shared__ float Ss[256][16];
-    __shared__ float Vs[BC][16];
-    for (int e = tid; e < D * 16; e += BW_NT) {
-        const int d = e / 16, j = e % 16;
-        Ss[d][j] = a.s0 ? a.s0[(((long)b * G + g) * D + d) * D + col0 + j] : 0.f;
-    }
-    __syncthreads();
-    const int vi = tid / 4, vj = (tid % 4) * 4;
+// Grid (sequences, G, D / 16): a workgroup owns 16 state columns and walks the chunks in order, the strip held in
+// fp32 MFMA accumulators (wave w: rows [w D/4, (w + 1) D/4)); per chunk two products on v_mfma_f32_16x16x4f32 with the
+// strip (and v_new) passed through LDS transposed, so every operand fragment is one 16-byte read.
+template <int D>
+__device__ __forceinline__ void walk_fwd(const GdnBwdArgs& a, int strip) {
+    constexpr int RT = D / 64;                            // 16-row tiles of the strip per wave
+    constexpr int KD = D / 16, KC = BC / 16;              // 16-wide k steps over D and over the chunk
+    const int b = blockIdx.x, g = blockIdx.y, col0 = strip * 16;
+    const int lane = lane_id(), wv = wave_id(), i16 = lane & 15, q = lane >> 4;
+    const int G = a.G, n = a.n_chunks;
+    __shared__ float ST[16][D + 4];                       // strip transposed: ST[col][row]
+    __shared__ float VT[16][BC + 4];                      // v_new strip transposed: VT[col][token]
+    f32x4 S[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int row = (wv * RT + t) * 16 + 4 * q + v;
+            S[t][v] = a.s0 ? a.s0[(((long)b * G + g) * D + row) * D + col0 + i16] : 0.f;
+        }
+    // one chunk's operands, loaded a chunk ahead: w row fragments, kt^T fragments, the u strip, the chunk decay
+    float4 wf[KD], kf[RT][KC];
+    float uf[4], gl;
+    auto fetch = [&](int c) {
+        const long cg = ((long)b * n + c) * G + g;
+        const float* wr = a.w + (cg * BC + 16 * wv + i16) * D + 4 * q;
+#pragma unroll
+        for (int k = 0; k < KD; ++k) wf[k] = *reinterpret_cast<const float4*>(wr + 16 * k);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            const float* kr = a.ktlT + (cg * D + (wv * RT + t) * 16 + i16) * BC + 4 * q;
+#pragma unroll
+            for (int k = 0; k < KC; ++k) kf[t][k] = *reinterpret_cast<const float4*>(kr + 16 * k);
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) uf[v] = a.u[(cg * BC + 16 * wv + 4 * q + v) * D + col0 + i16];
+        gl = a.gam[cg * BC + BC - 1];
+    };
+    fetch(0);
     for (int c = 0; c < n; ++c) {
-        const long bc = (long)b * n + c, cg = bc * G + g;
-        for (int e = tid; e < D * 4; e += BW_NT) {              // entry state
-            const int d = e / 4, j = (e % 4) * 4;
-            *reinterpret_cast<float4*>(a.Sc + (cg * D + d) * D + col0 + j) =
-                make_float4(Ss[d][j], Ss[d][j + 1], Ss[d][j + 2], Ss[d][j + 3]);
-        }
-        // v_new strip = u - w S
-        const float* wr = a.w + (cg * BC + vi) * D;
-        float4 acc = *reinterpret_cast<const float4*>(a.u + (cg * BC + vi) * D + col0 + vj);
-        for (int d = 0; d < D; ++d) {
-            const float x = wr[d];
-            acc.x -= x * Ss[d][vj]; acc.y -= x * Ss[d][vj + 1]; acc.z -= x * Ss[d][vj + 2]; acc.w -= x * Ss[d][vj + 3];
-        }
-        __syncthreads();
-        Vs[vi][vj] = acc.x; Vs[vi][vj + 1] = acc.y; Vs[vi][vj + 2] = acc.z; Vs[vi][vj + 3] = acc.w;
-        __syncthreads();
-        const float ec = expf(a.gam[cg * BC + BC - 1]);
-        if (tid < D) {
-            float s[16];
+        const long cg = ((long)b * n + c) * G + g;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) s[j] = ec * Ss[tid][j];
-            for (int i = 0; i < BC; ++i) {
-                const float kt = a.ktl[(cg * BC + i) * D + tid];
+        for (int t = 0; t < RT; ++t)
 #pragma unroll
-                for (int j = 0; j < 16; ++j) s[j] += kt * Vs[i][j];
+            for (int v = 0; v < 4; ++v) {
+                const int row = (wv * RT + t) * 16 + 4 * q + v;
+                a.Sc[(cg * D + row) * D + col0 + i16] = S[t][v];     // entry state of chunk c
+                ST[i16][row] = S[t][v];
             }
+        __syncthreads();
+        // v_new rows [16 wv, 16 wv + 16) = u - w S (four partial accumulators: shorter MFMA dependency chains)
+        f32x4 part[4] = {f32x4{uf[0], uf[1], uf[2], uf[3]}, f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f},
+                         f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-            for (int j = 0; j < 16; ++j) Ss[tid][j] = s[j];
+        for (int k = 0; k < KD; ++k) {
+            const uint4 af = make_uint4(__float_as_uint(-wf[k].x), __float_as_uint(-wf[k].y), __float_as_uint(-wf[k].z),
+                                        __float_as_uint(-wf[k].w));
+            const uint4 bf = *reinterpret_cast<const uint4*>(&ST[i16][16 * k + 4 * q]);
+            mma<F32>(part[k & 3], af, bf);
         }
+        const f32x4 acc = (part[0] + part[1]) + (part[2] + part[3]);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) VT[i16][16 * wv + 4 * q + v] = acc[v];
+        __syncthreads();
+        // S = e^(gc_C') S + kt^T v_new
+        const float ec = expf(gl);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) S[t][v] *= ec;
+#pragma unroll
+            for (int k = 0; k < KC; ++k) {
+                const uint4 bf = *reinterpret_cast<const uint4*>(&VT[i16][16 * k + 4 * q]);
+                mma<F32>(S[t], __builtin_bit_cast(uint4, kf[t][k]), bf);
+            }
+        }
+        if (c + 1 < n) fetch(c + 1);
         __syncthreads();
     }
 }
 
-// reverse: every chunk's exit-state gradient dS' and dvn, and ds0; same grid
-__global__ __launch_bounds__(BW_NT) void walk_bwd_kernel(GdnBwdArgs a) {
-    const int b = blockIdx.x, g = blockIdx.y, col0 = blockIdx.z * 16, tid = threadIdx.x;
-    const int D = a.D, G = a.G, n = a.n_chunks;
-    __shared__ float Ls[256][16];
-    __shared__ float Vs[BC][16];
-    for (int e = tid; e < D * 16; e += BW_NT) {
-        const int d = e / 16, j = e % 16;
-        Ls[d][j] = a.dsf ? a.dsf[(((long)b * G + g) * D + d) * D + col0 + j] : 0.f;
-    }
-    __syncthreads();
-    const int vi = tid / 4, vj = (tid % 4) * 4;
+// reverse: every chunk's exit-state gradient dS' and dvn, and ds0; same grid and layout
+template <int D>
+__device__ __forceinline__ void walk_bwd(const GdnBwdArgs& a, int strip) {
+    constexpr int RT = D / 64;
+    constexpr int KD = D / 16, KC = BC / 16;
+    const int b = blockIdx.x, g = blockIdx.y, col0 = strip * 16;
+    const int lane = lane_id(), wv = wave_id(), i16 = lane & 15, q = lane >> 4;
+    const int G = a.G, n = a.n_chunks;
+    __shared__ float LT[16][D + 4];
+    __shared__ float VT[16][BC + 4];
+    f32x4 L[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int row = (wv * RT + t) * 16 + 4 * q + v;
+            L[t][v] = a.dsf ? a.dsf[(((long)b * G + g) * D + row) * D + col0 + i16] : 0.f;
+        }
+    // one chunk's operands, a chunk ahead: kt row fragments, w^T fragments, the E1 and E2 strips, the chunk decay
+    float4 kf[KD], wf[RT][KC];
+    float e1[4], e2[RT][4], gl;
+    auto fetch = [&](int c) {
+        const long cg = ((long)b * n + c) * G + g;
+        const float* kr = a.ktl + (cg * BC + 16 * wv + i16) * D + 4 * q;
+#pragma unroll
+        for (int k = 0; k < KD; ++k) kf[k] = *reinterpret_cast<const float4*>(kr + 16 * k);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+            const float* wr = a.wT + (cg * D + (wv * RT + t) * 16 + i16) * BC + 4 * q;
+#pragma unroll
+            for (int k = 0; k < KC; ++k) wf[t][k] = *reinterpret_cast<const float4*>(wr + 16 * k);
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                e2[t][v] = a.E2[(cg * D + (wv * RT + t) * 16 + 4 * q + v) * D + col0 + i16];
+        }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) e1[v] = a.E1[(cg * BC + 16 * wv + 4 * q + v) * D + col0 + i16];
+        gl = a.gam[cg * BC + BC - 1];
+    };
+    fetch(n - 1);
     for (int c = n - 1; c >= 0; --c) {
-        const long bc = (long)b * n + c, cg = bc * G + g;
-        for (int e = tid; e < D * 4; e += BW_NT) {              // exit-state gradient of chunk c
-            const int d = e / 4, j = (e % 4) * 4;
-            *reinterpret_cast<float4*>(a.dSx + (cg * D + d) * D + col0 + j) =
-                make_float4(Ls[d][j], Ls[d][j + 1], Ls[d][j + 2], Ls[d][j + 3]);
-        }
-        // dvn strip = kt dS' + E1
-        const float* kr = a.ktl + (cg * BC + vi) * D;
-        float4 acc = *reinterpret_cast<const float4*>(a.E1 + (cg * BC + vi) * D + col0 + vj);
-        for (int d = 0; d < D; ++d) {
-            const float x = kr[d];
-            acc.x += x * Ls[d][vj]; acc.y += x * Ls[d][vj + 1]; acc.z += x * Ls[d][vj + 2]; acc.w += x * Ls[d][vj + 3];
-        }
-        *reinterpret_cast<float4*>(a.dvn + (cg * BC + vi) * D + col0 + vj) = acc;
-        __syncthreads();
-        Vs[vi][vj] = acc.x; Vs[vi][vj + 1] = acc.y; Vs[vi][vj + 2] = acc.z; Vs[vi][vj + 3] = acc.w;
-        __syncthreads();
-        const float ec = expf(a.gam[cg * BC + BC - 1]);
-        if (tid < D) {
-            float s[16];
-            const float* e2 = a.E2 + (cg * D + tid) * D + col0;
+        const long cg = ((long)b * n + c) * G + g;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) s[j] = ec * Ls[tid][j] + e2[j];
-            for (int i = 0; i < BC; ++i) {
-                const float wx = a.w[(cg * BC + i) * D + tid];
+        for (int t = 0; t < RT; ++t)
 #pragma unroll
-                for (int j = 0; j < 16; ++j) s[j] -= wx * Vs[i][j];
+            for (int v = 0; v < 4; ++v) {
+                const int row = (wv * RT + t) * 16 + 4 * q + v;
+                a.dSx[(cg * D + row) * D + col0 + i16] = L[t][v];    // exit-state gradient of chunk c
+                LT[i16][row] = L[t][v];
             }
+        __syncthreads();
+        // dvn rows [16 wv, 16 wv + 16) = E1 + kt dS' (four partial accumulators)
+        f32x4 part[4] = {f32x4{e1[0], e1[1], e1[2], e1[3]}, f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f},
+                         f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-            for (int j = 0; j < 16; ++j) Ls[tid][j] = s[j];
+        for (int k = 0; k < KD; ++k) {
+            const uint4 bf = *reinterpret_cast<const uint4*>(&LT[i16][16 * k + 4 * q]);
+            mma<F32>(part[k & 3], __builtin_bit_cast(uint4, kf[k]), bf);
         }
+        const f32x4 acc = (part[0] + part[1]) + (part[2] + part[3]);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            a.dvn[(cg * BC + 16 * wv + 4 * q + v) * D + col0 + i16] = acc[v];
+            VT[i16][16 * wv + 4 * q + v] = acc[v];
+        }
+        __syncthreads();
+        // dS = e^(gc_C') dS' + E2 - w^T dvn
+        const float ec = expf(gl);
+#pragma unroll
+        for (int t = 0; t < RT; ++t) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) L[t][v] = ec * L[t][v] + e2[t][v];
+#pragma unroll
+            for (int k = 0; k < KC; ++k) {
+                const uint4 af = make_uint4(__float_as_uint(-wf[t][k].x), __float_as_uint(-wf[t][k].y),
+                                            __float_as_uint(-wf[t][k].z), __float_as_uint(-wf[t][k].w));
+                const uint4 bf = *reinterpret_cast<const uint4*>(&VT[i16][16 * k + 4 * q]);
+                mma<F32>(L[t], af, bf);
+            }
+        }
+        if (c > 0) fetch(c - 1);
         __syncthreads();
     }
     if (a.ds0)
-        for (int e = tid; e < D * 16; e += BW_NT) {
-            const int d = e / 16, j = e % 16;
-            a.ds0[(((long)b * G + g) * D + d) * D + col0 + j] = Ls[d][j];
-        }
+#pragma unroll
+        for (int t = 0; t < RT; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int row = (wv * RT + t) * 16 + 4 * q + v;
+                a.ds0[(((long)b * G + g) * D + row) * D + col0 + i16] = L[t][v];
+            }
+}
+
+// the two walks are independent (the reverse one needs E1, E2, kt, w, not the entry states): one launch, grid
+// (sequences, G, 2 D / 16), the first D / 16 strips walk forward, the others backward
+template <int D>
+__global__ __launch_bounds__(BW_NT) void walk_kernel(GdnBwdArgs a) {
+    if ((int)blockIdx.z < D / 16) walk_fwd<D>(a, blockIdx.z);
+    else walk_bwd<D>(a, blockIdx.z - D / 16);
 }
 
 // ------------------------------------------------------------------------------------ decay gradients
@@ -314,26 +428,23 @@ __global__ __launch_bounds__(BW_NT) void decay_grad_kernel(GdnBwdArgs a) {
 }
 
 // ------------------------------------------------------------------------------------ final assembly
-// one workgroup per (chunk, KV head): dq += s dqd e^gc, dk, dv, d beta, d gc -> dg (reverse cumulative sum)
+// grid (chunks, G, 4): rows r0 .. r0 + 15 of (chunk, KV head): dq += s dqd e^gc, dk, dv, d beta, and each row's share
+// of d gc (into dgz, which holds the decay's share); the last row's extra terms (sum dkt kt and e^(gc_C') <S, dS'>,
+// the latter over a quarter of the D x D entries) into part[cg][z]
 __global__ __launch_bounds__(BW_NT) void chunk_final_kernel(GdnBwdArgs a) {
     const long bc = blockIdx.x;
-    const int g = blockIdx.y, tid = threadIdx.x, lane = lane_id(), wv = wave_id();
+    const int g = blockIdx.y, z = blockIdx.z, r0 = z * 16, tid = threadIdx.x, lane = lane_id(), wv = wave_id();
     const int D = a.D, G = a.G, R = a.R, H = G * R;
     const long cg = bc * G + g;
-    __shared__ float gc[BC], dgam[BC], dbe[BC], red[BW_NT / 64];
-    if (tid < BC) {
-        gc[tid] = a.gam[cg * BC + tid];
-        dgam[tid] = a.dgz[cg * BC + tid];
-        dbe[tid] = 0.f;
-    }
+    __shared__ float gc[BC], red[BW_NT / 64];
+    if (tid < BC) gc[tid] = a.gam[cg * BC + tid];
     __syncthreads();
     const float gl = gc[BC - 1], ec = expf(gl);
-    // <S, dS'> and sum(dkt * kt) for the last row's gc
     float sdot = 0.f;
-    for (long e = tid; e < (long)D * D; e += BW_NT) sdot += a.Sc[cg * D * D + e] * a.dSx[cg * D * D + e];
-    // rows: wave w handles rows w, w + 4, ...; lanes over dims
+    const long q4 = (long)D * D / 4;
+    for (long e = z * q4 + tid; e < (z + 1) * q4; e += BW_NT) sdot += a.Sc[cg * D * D + e] * a.dSx[cg * D * D + e];
     float ktsum = 0.f;
-    for (int i = wv; i < BC; i += BW_NT / 64) {
+    for (int i = r0 + wv; i < r0 + 16; i += BW_NT / 64) {
         const long tok = bc * BC + i;
         const float egi = expf(gc[i]), eti = expf(gl - gc[i]);
         const float be = a.beta[tok * G + g];
@@ -364,44 +475,47 @@ __global__ __launch_bounds__(BW_NT) void chunk_final_kernel(GdnBwdArgs a) {
             dbi += __shfl_xor(dbi, off);
         }
         if (lane == 0) {
-            dgam[i] += dgi;
-            dbe[i] = dbi;
+            a.dgz[cg * BC + i] += dgi;
+            a.dbeta[tok * G + g] = dbi;
         }
     }
-    // block sums of sdot and ktsum -> the last row's d gc
     float t = sdot * ec + ktsum;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off);
-    __syncthreads();
     if (lane == 0) red[wv] = t;
     __syncthreads();
     if (tid == 0) {
         float s = 0.f;
         for (int w = 0; w < BW_NT / 64; ++w) s += red[w];
-        dgam[BC - 1] += s;
+        a.part[cg * 4 + z] = s;
     }
-    __syncthreads();
-    if (tid < 64) {
-        // dg_j = sum_{i >= j} d gc_i: reverse inclusive scan in one wave
-        float x = dgam[BC - 1 - tid];
+}
+
+// per (chunk, KV head), one wave: dg_j = sum_{i >= j} d gc_i (the last row with its extra terms)
+__global__ __launch_bounds__(64) void dg_scan_kernel(GdnBwdArgs a) {
+    const long cg = blockIdx.x;
+    const int tid = threadIdx.x, G = a.G;
+    const long bc = cg / G;
+    const int g = (int)(cg % G);
+    float x = a.dgz[cg * BC + BC - 1 - tid];
+    if (tid == 0) x += a.part[cg * 4] + a.part[cg * 4 + 1] + a.part[cg * 4 + 2] + a.part[cg * 4 + 3];
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float y = __shfl_up(x, off);
-            if (tid >= off) x += y;
-        }
-        const long tok = bc * BC + (BC - 1 - tid);
-        a.dg[tok * G + g] = x;
-        a.dbeta[bc * BC * G + tid * G + g] = dbe[tid];
+    for (int off = 1; off < 64; off <<= 1) {
+        const float y = __shfl_up(x, off);
+        if (tid >= off) x += y;
     }
+    a.dg[(bc * BC + (BC - 1 - tid)) * G + g] = x;
 }
 
 // ------------------------------------------------------------------------------------ host side
 int bgemm(const BgArgs& a, hipStream_t s) {
+    // each operand must be contiguous along k or along its other dimension (16-byte tile loads)
+    if ((a.ak != 1 && a.am != 1) || (a.bk != 1 && a.bn != 1)) return BF_ERR_UNSUPPORTED;
     const dim3 grid((unsigned)a.nz, a.M / 64, a.N / 64);
-    const bool ak1 = a.ak == 1, bk1 = a.bk == 1;
-    if (ak1 && bk1) hipLaunchKernelGGL((bgemm_kernel<true, true>), grid, dim3(BW_NT), 0, s, a);
-    else if (ak1) hipLaunchKernelGGL((bgemm_kernel<true, false>), grid, dim3(BW_NT), 0, s, a);
-    else if (bk1) hipLaunchKernelGGL((bgemm_kernel<false, true>), grid, dim3(BW_NT), 0, s, a);
+    const bool ak = a.ak == 1, bk = a.bk == 1;
+    if (ak && bk) hipLaunchKernelGGL((bgemm_kernel<true, true>), grid, dim3(BW_NT), 0, s, a);
+    else if (ak) hipLaunchKernelGGL((bgemm_kernel<true, false>), grid, dim3(BW_NT), 0, s, a);
+    else if (bk) hipLaunchKernelGGL((bgemm_kernel<false, true>), grid, dim3(BW_NT), 0, s, a);
     else hipLaunchKernelGGL((bgemm_kernel<false, false>), grid, dim3(BW_NT), 0, s, a);
     return (int)hipGetLastError();
 }
@@ -431,10 +545,10 @@ Op tr(Op o) { std::swap(o.rs, o.cs); return o; }
 size_t gdn_bwd_workspace(int num_seqs, long T, int G, int R, int D) {
     const long n = T / BC, NC = (long)num_seqs * n * G;             // chunk-heads
     const long cc = BC * BC, cd = (long)BC * D, dd = (long)D * D;
-    const long floats = NC * (BC * 2                                 // gam, dgz
+    const long floats = NC * (BC * 2 + 4                             // gam, dgz, part
                               + cc * 4                               // P, Am, M, dA
-                              + cd * 6                               // kb, vb, kbe, ktl, u, w
-                              + (long)R * (cc * 3 + cd * 2)          // QK, attn, dattn; qd, dqd
+                              + cd * 8                               // kb, vb, kbe, ktl, u, w, ktlT, wT
+                              + (long)R * (cc * 3 + cd * 4)          // QK, attn, dattn; qd, dqd, qc, dOc
                               + dd * 3                               // Sc, E2, dSx
                               + cd * 9                               // E1, dvn, vn, dkt, dw, dvb, dkbe, dkb, dkacc
                               + cc * 2);                             // dM, T1
@@ -451,12 +565,12 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
         p += ((count * (long)sizeof(float) + 255) / 256) * 256;
         return r;
     };
-    a.gam = take(NC * BC); a.dgz = take(NC * BC);
+    a.gam = take(NC * BC); a.dgz = take(NC * BC); a.part = take(NC * 4);
     a.P = take(NC * cc); a.Am = take(NC * cc); a.Mi = take(NC * cc); a.dA = take(NC * cc);
     a.kb = take(NC * cd); a.vb = take(NC * cd); a.kbe = take(NC * cd); a.ktl = take(NC * cd);
-    a.u = take(NC * cd); a.w = take(NC * cd);
+    a.u = take(NC * cd); a.w = take(NC * cd); a.ktlT = take(NC * cd); a.wT = take(NC * cd);
     a.QK = take(NC * R * cc); a.attn = take(NC * R * cc); a.dattn = take(NC * R * cc);
-    a.qd = take(NC * R * cd); a.dqd = take(NC * R * cd);
+    a.qd = take(NC * R * cd); a.dqd = take(NC * R * cd); a.qc = take(NC * R * cd); a.dOc = take(NC * R * cd);
     a.Sc = take(NC * dd); a.E2 = take(NC * dd); a.dSx = take(NC * dd);
     a.E1 = take(NC * cd); a.dvn = take(NC * cd); a.vn = take(NC * cd); a.dkt = take(NC * cd); a.dw = take(NC * cd);
     a.dvb = take(NC * cd); a.dkbe = take(NC * cd); a.dkb = take(NC * cd); a.dkacc = take(NC * cd);
@@ -478,7 +592,7 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
     const int nzg = (int)NC, nzr = (int)(NC * R);
 
     // prep
-    hipLaunchKernelGGL(chunk_prep_kernel, dim3((unsigned)NB, G), dim3(BW_NT), 0, s, a);
+    hipLaunchKernelGGL(chunk_prep_kernel, dim3((unsigned)NB, G, 4), dim3(BW_NT), 0, s, a);
     ok((int)hipGetLastError());
     // P = (k b) k^T ; Am = strict_lower(P * decay)
     ok(gemm(BC, BC, D, nzg, G, 1, W(a.kb, BC, D), tr(kT()), a.P, (long)G * cc, cc, 0, BC, 1, 1.f, 0, 0, nullptr, s));
@@ -489,24 +603,25 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
     // u = M (v b), w = M (k b e^gc)
     ok(gemm(BC, D, BC, nzg, G, 1, W(a.Mi, BC, BC), W(a.vb, BC, D), a.u, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0, nullptr, s));
     ok(gemm(BC, D, BC, nzg, G, 1, W(a.Mi, BC, BC), W(a.kbe, BC, D), a.w, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0, nullptr, s));
+    ok(gemm(BC, D, BC, nzg, G, 1, W(a.Mi, BC, BC), W(a.kbe, BC, D), a.wT, (long)G * cd, cd, 0, 1, BC, 1.f, 0, 0, nullptr,
+            s));                                          // the same product stored transposed [D][C]
     // QK_r = s q_r k^T (lower incl.), attn_r = tril(QK_r * decay)
     ok(gemm(BC, BC, D, nzr, G, R, qR(), tr(Op{a.k, (long)BC * G * D, D, 0, (long)G * D, 1}), a.QK, (long)G * R * cc,
             (long)R * cc, cc, BC, 1, a.scale, 0, 1, nullptr, s));
     hipLaunchKernelGGL(decay_mask_kernel, dim3((unsigned)NC), dim3(BW_NT), 0, s, a.QK, a.attn, a.gam, R, 1);
     ok((int)hipGetLastError());
-    // E1 = sum_r attn_r^T dO_r  [C x D],  E2 = sum_r qd_r^T dO_r  [D x D]
-    for (int r = 0; r < R; ++r) {
-        Op at = tr(WR(a.attn + r * cc, BC, BC));
-        at.s0 = (long)G * R * cc; at.s1 = (long)R * cc; at.s2 = 0;
-        Op dO = Op{a.dO + (long)r * D, (long)BC * H * D, (long)R * D, 0, (long)H * D, 1};
-        ok(gemm(BC, D, BC, nzg, G, 1, at, dO, a.E1, (long)G * cd, cd, 0, D, 1, 1.f, r > 0, 0, nullptr, s));
-        Op qd = tr(Op{a.qd + r * cd, (long)G * R * cd, (long)R * cd, 0, D, 1});
-        ok(gemm(D, D, BC, nzg, G, 1, qd, dO, a.E2, (long)G * dd, dd, 0, D, 1, 1.f, r > 0, 0, nullptr, s));
-    }
+    // E1 = sum_r attn_r^T dO_r [C x D], E2 = sum_r qd_r^T dO_r [D x D]: one product each over K = R C, the (r, token)
+    // pairs of the chunk-major copies [cg][r C + i][...]
+    const Op dOc{a.dOc, (long)G * R * cd, (long)R * cd, 0, D, 1};
+    ok(gemm(BC, D, R * BC, nzg, G, 1, tr(Op{a.attn, (long)G * R * cc, (long)R * cc, 0, BC, 1}), dOc, a.E1, (long)G * cd,
+            cd, 0, D, 1, 1.f, 0, 0, nullptr, s));
+    ok(gemm(D, D, R * BC, nzg, G, 1, tr(Op{a.qd, (long)G * R * cd, (long)R * cd, 0, D, 1}), dOc, a.E2, (long)G * dd, dd, 0,
+            D, 1, 1.f, 0, 0, nullptr, s));
     // walks
-    hipLaunchKernelGGL(walk_fwd_kernel, dim3(a.num_seqs, G, D / 16), dim3(BW_NT), 0, s, a);
-    ok((int)hipGetLastError());
-    hipLaunchKernelGGL(walk_bwd_kernel, dim3(a.num_seqs, G, D / 16), dim3(BW_NT), 0, s, a);
+    const dim3 wgrid(a.num_seqs, G, 2 * D / 16);
+    if (D == 64) hipLaunchKernelGGL(walk_kernel<64>, wgrid, dim3(BW_NT), 0, s, a);
+    else if (D == 128) hipLaunchKernelGGL(walk_kernel<128>, wgrid, dim3(BW_NT), 0, s, a);
+    else hipLaunchKernelGGL(walk_kernel<256>, wgrid, dim3(BW_NT), 0, s, a);
     ok((int)hipGetLastError());
     // v_new = u - w S
     ok(gemm(BC, D, D, nzg, G, 1, W(a.w, BC, D), W(a.Sc, D, D), a.vn, (long)G * cd, cd, 0, D, 1, -1.f, 0, 0, a.u, s));
@@ -541,14 +656,13 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
     ok(gemm(BC, D, BC, nzg, G, 1, W(a.dA, BC, BC), kT(), a.dkb, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0, nullptr, s));
     ok(gemm(BC, D, BC, nzg, G, 1, tr(W(a.dA, BC, BC)), W(a.kb, BC, D), a.dkacc, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0,
             nullptr, s));
-    for (int r = 0; r < R; ++r) {
-        Op da = tr(Op{a.dattn + r * cc, (long)G * R * cc, (long)R * cc, 0, BC, 1});
-        Op q = Op{a.q + (long)r * D, (long)BC * H * D, (long)R * D, 0, (long)H * D, 1};
-        ok(gemm(BC, D, BC, nzg, G, 1, da, q, a.dkacc, (long)G * cd, cd, 0, D, 1, a.scale, 1, 0, nullptr, s));
-    }
+    ok(gemm(BC, D, R * BC, nzg, G, 1, tr(Op{a.dattn, (long)G * R * cc, (long)R * cc, 0, BC, 1}),
+            Op{a.qc, (long)G * R * cd, (long)R * cd, 0, D, 1}, a.dkacc, (long)G * cd, cd, 0, D, 1, a.scale, 1, 0, nullptr,
+            s));                                          // sum_r dattn_r^T (s q_r), K = R C
     ok(gemm(BC, D, BC, nzr, G, R, WR(a.dattn, BC, BC), Op{a.k, (long)BC * G * D, D, 0, (long)G * D, 1}, a.dq,
             (long)BC * H * D, (long)R * D, D, (long)H * D, 1, a.scale, 0, 0, nullptr, s));
-    hipLaunchKernelGGL(chunk_final_kernel, dim3((unsigned)NB, G), dim3(BW_NT), 0, s, a);
+    hipLaunchKernelGGL(chunk_final_kernel, dim3((unsigned)NB, G, 4), dim3(BW_NT), 0, s, a);
+    hipLaunchKernelGGL(dg_scan_kernel, dim3((unsigned)NC), dim3(64), 0, s, a);
     ok((int)hipGetLastError());
     return e;
 }

@@ -181,16 +181,17 @@ def delta_rule_varlen(q, k, v, g, beta, cu_seqlens, chunk_size: int = 64, initia
     return torch.cat(outs, 1), torch.cat(states, 0)
 
 
-def delta_rule_gqa_grads(q, k, v, g, beta, state, do, ds=None, chunk: int = 64):
+def delta_rule_gqa_grads(q, k, v, g, beta, state, do, ds=None, chunk: int = 64, dtype=torch.float64):
     """The gradients the reference's conversion training takes through ``motor.delta_rule_gqa``
     (``Heimdall/heimdall/motor.py:70-102`` inside ``seq_loss``, ``:149-193``): autograd of <o, do> + <S_final, ds>
-    with respect to (q, k, v, g, beta, state), in fp64. Returns the six gradients (state's is None without a state)."""
-    xs = [x.detach().double().requires_grad_(True) for x in (q, k, v, g, beta)]
-    s0 = state.detach().double().requires_grad_(True) if state is not None else None
+    with respect to (q, k, v, g, beta, state), in fp64 (or ``dtype``). Returns the six gradients (state's is None
+    without a state)."""
+    xs = [x.detach().to(dtype).requires_grad_(True) for x in (q, k, v, g, beta)]
+    s0 = state.detach().to(dtype).requires_grad_(True) if state is not None else None
     with torch.enable_grad():
         o, s = delta_rule_gqa(*xs, chunk=chunk, state=s0)
-        loss = (o * do.double()).sum()
+        loss = (o * do.to(dtype)).sum()
         if ds is not None:
-            loss = loss + (s * ds.double()).sum()
+            loss = loss + (s * ds.to(dtype)).sum()
         grads = torch.autograd.grad(loss, xs + ([s0] if s0 is not None else []))
     return tuple(grads) + ((None,) if s0 is None else ())

@@ -492,6 +492,48 @@ def run_gdn_bwd(steps, warmup, dev, T=8192, cpu=False):
     return out
 
 
+def run_llama_state(steps, warmup, dev):
+    """The llama.cpp state-row formats at the decode geometry (B=64 sequences, G=4, D=256, W=2048, 4 sinks, bf16 ring,
+    position 100000): bf_llama_state_pack and bf_llama_state_unpack, each timed with HIP events. Algorithmic bytes:
+    the cache read (ring k, v bf16; k_mem, g, beta, state f32) and the rows written (43.7 MB per sequence), and the
+    reverse for unpack."""
+    from heimdall_amd import formats
+
+    B, G, D, W, S, n = 64, 4, 256, 2048, 4, 100000
+    gen = torch.Generator(device=dev).manual_seed(31)
+    rn = lambda *s: torch.randn(*s, device=dev, generator=gen)
+    c = dict(ring_k=rn(B, G, W, D).bfloat16(), ring_v=rn(B, G, W, D).bfloat16(), ring_km=rn(B, W, G, D),
+             ring_g=-torch.rand(B, W, G, device=dev, generator=gen), ring_beta=torch.rand(B, W, G, device=dev,
+                                                                                       generator=gen),
+             ring_pos=torch.empty(W, dtype=torch.long, device=dev), S=rn(B, G, D, D) * 0.02,
+             sink_k=rn(B, G, S, D).bfloat16(), sink_v=rn(B, G, S, D).bfloat16())
+    pos = torch.arange(n - W, n, device=dev)
+    c["ring_pos"][pos % W] = pos
+    cache_bytes = sum(t.numel() * t.element_size() for t in c.values())
+    row_bytes = B * formats.llama_state_floats(G, D, W, S) * 4
+    stream = torch.cuda.current_stream(dev)
+    rows = formats.pack_llama_state(c, n, W, S)
+    res = {}
+    for name, fn in (("pack", lambda: formats.pack_llama_state(c, n, W, S)),
+                     ("unpack", lambda: formats.unpack_llama_state(rows, n, W, S, G, D, torch.bfloat16))):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        gbs = (cache_bytes + row_bytes) / (ms * 1e-3) / 1e9
+        res[name] = {"ms": ms, "GBs": gbs, "frac": gbs / HBM_PEAK_GBS}
+    return {"workload": f"llama.cpp state rows B={B} G={G} D={D} W={W} S={S} bf16 ring", "bytes": cache_bytes + row_bytes,
+            "pack": res["pack"], "unpack": res["unpack"], "ms_per_step": res["pack"]["ms"] + res["unpack"]["ms"],
+            "roofline": {"bound": "hbm", "achieved": res["pack"]["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": res["pack"]["frac"], "kernel": "llama_state_pack_kernel"}}
+
+
 def run_window(steps, warmup, dev, T=32768):
     """The window kernel alone on the layer prefill's shapes (B=1, H=24, G=4, D=256, W=2048 + 4 sinks, bf16, from
     position 0 with the first 4 tokens as sinks, no ring, no mix): bf_window_fwd timed with HIP events on the launch
@@ -581,7 +623,8 @@ def main():
     ap.add_argument("--copy-probe", action="store_true", help="run one 256 MiB device copy first (counter scaling)")
     ap.add_argument("--segment-chunks", type=int, default=0, help="chunks per scan segment (0 = library default)")
     ap.add_argument("--only", choices=("decode", "layer", "layer131k", "window", "varlen", "gdn_layer", "teacher",
-                                       "teacher_decode", "teacher_decode_full", "gdn_bwd"), default=None,
+                                       "teacher_decode", "teacher_decode_full", "gdn_bwd", "llama_state"),
+                    default=None,
                     help="run one secondary leg alone and print its JSON object (for per-workload profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -608,7 +651,8 @@ def main():
                "teacher": lambda: run_teacher(args.steps, args.warmup, dev),
                "teacher_decode": lambda: run_teacher_decode(args.steps, args.warmup, dev),
                "teacher_decode_full": lambda: run_teacher_decode(args.steps, args.warmup, dev, retrieval=False),
-               "gdn_bwd": lambda: run_gdn_bwd(args.steps, args.warmup, dev, cpu=not args.no_cpu)}[args.only]
+               "gdn_bwd": lambda: run_gdn_bwd(args.steps, args.warmup, dev, cpu=not args.no_cpu),
+               "llama_state": lambda: run_llama_state(args.steps, args.warmup, dev)}[args.only]
         print(json.dumps(leg()), flush=True)
         return
 
@@ -655,6 +699,7 @@ def main():
         line["gdn_layer"] = run_gdn_layer(10, 3, dev)
         line["teacher_decode"] = run_teacher_decode(50, 10, dev)
         line["gdn_bwd"] = run_gdn_bwd(10, 2, dev, cpu=not args.no_cpu)
+        line["llama_state"] = run_llama_state(5, 2, dev)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(r["inputs"])
     print(json.dumps(line), flush=True)

@@ -191,6 +191,20 @@ struct GdnBwdArgs {
 size_t gdn_bwd_workspace(int num_seqs, long T, int G, int R, int D);
 int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t stream);
 
+struct LlamaStateArgs {
+    int B, G, D, W, S, kv_dtype, n_sinks;
+    long n, LR, row;                // tokens seen; region slots; floats per row
+    const void *ring_k, *ring_v, *sink_k, *sink_v;
+    const float *ring_km, *ring_g, *ring_beta, *state;
+    const int64_t* ring_pos;
+    float* rows;                    // [B][row]: written by pack, read by unpack
+    void *ring_k_out, *ring_v_out, *sink_k_out, *sink_v_out;
+    float *ring_km_out, *ring_g_out, *ring_beta_out, *state_out;
+    int64_t* ring_pos_out;
+};
+long llama_state_floats(int G, int D, int W, int S);
+int llama_state(const LlamaStateArgs& a, bool pack, hipStream_t stream);
+
 struct KvAppendArgs {
     const void* k_new;              // row (b, g, i) at k_new + b * k_sb + g * k_sg + i * k_st (elements)
     const void* v_new;

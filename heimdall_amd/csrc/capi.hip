@@ -306,6 +306,55 @@ int bf_gdn_bwd(const float* q, const float* k, const float* v, const float* g, c
     return bf::gdn_bwd(a, workspace, static_cast<hipStream_t>(stream));
 }
 
+int bf_llama_state_floats(int G, int D, int W, int S, int64_t* floats) {
+    if (!floats || G <= 0 || D <= 0 || W <= 0 || S < 0) return BF_STATUS_INVALID;
+    *floats = bf::llama_state_floats(G, D, W, S);
+    return BF_STATUS_OK;
+}
+
+static int llama_geometry(bf::LlamaStateArgs& a, int B, int G, int D, int W, int S, int64_t n, int kv_dtype,
+                          int n_sinks) {
+    if (B <= 0 || G <= 0 || W <= 0 || S < 0 || n < 0 || n_sinks < 0 || n_sinks > S || n_sinks > n)
+        return BF_STATUS_INVALID;
+    if (!supported_dim(D) || !supported_dtype(kv_dtype)) return BF_STATUS_UNSUPPORTED;
+    a.B = B; a.G = G; a.D = D; a.W = W; a.S = S; a.n = n; a.kv_dtype = kv_dtype; a.n_sinks = n_sinks;
+    a.LR = (S + W + 2 + 31) / 32 * 32;
+    a.row = bf::llama_state_floats(G, D, W, S);
+    return BF_STATUS_OK;
+}
+
+int bf_llama_state_pack(int B, int G, int D, int W, int S, int64_t n, int kv_dtype, const void* ring_k,
+                        const void* ring_v, const float* ring_km, const float* ring_g, const float* ring_beta,
+                        const int64_t* ring_pos, const void* sink_k, const void* sink_v, int n_sinks,
+                        const float* state, float* rows, void* stream) {
+    bf::LlamaStateArgs a{};
+    const int st = llama_geometry(a, B, G, D, W, S, n, kv_dtype, n_sinks);
+    if (st != BF_STATUS_OK) return st;
+    if (!ring_k || !ring_v || !ring_km || !ring_g || !ring_beta || !ring_pos || !state || !rows ||
+        (n_sinks && (!sink_k || !sink_v)))
+        return BF_STATUS_INVALID;
+    a.ring_k = ring_k; a.ring_v = ring_v; a.ring_km = ring_km; a.ring_g = ring_g; a.ring_beta = ring_beta;
+    a.ring_pos = ring_pos; a.sink_k = sink_k; a.sink_v = sink_v; a.state = state; a.rows = rows;
+    return bf::llama_state(a, true, static_cast<hipStream_t>(stream));
+}
+
+int bf_llama_state_unpack(int B, int G, int D, int W, int S, int64_t n, int kv_dtype, const float* rows, void* ring_k,
+                          void* ring_v, float* ring_km, float* ring_g, float* ring_beta, int64_t* ring_pos,
+                          void* sink_k, void* sink_v, int n_sinks, float* state, void* stream) {
+    bf::LlamaStateArgs a{};
+    const int st = llama_geometry(a, B, G, D, W, S, n, kv_dtype, n_sinks);
+    if (st != BF_STATUS_OK) return st;
+    if (n_sinks != (n < S ? n : S)) return BF_STATUS_INVALID;
+    if (!rows || !ring_k || !ring_v || !ring_km || !ring_g || !ring_beta || !ring_pos || !state ||
+        (n_sinks && (!sink_k || !sink_v)))
+        return BF_STATUS_INVALID;
+    a.rows = const_cast<float*>(rows);
+    a.ring_k_out = ring_k; a.ring_v_out = ring_v; a.ring_km_out = ring_km; a.ring_g_out = ring_g;
+    a.ring_beta_out = ring_beta; a.ring_pos_out = ring_pos; a.sink_k_out = sink_k; a.sink_v_out = sink_v;
+    a.state_out = state;
+    return bf::llama_state(a, false, static_cast<hipStream_t>(stream));
+}
+
 int bf_kv_append(const void* k_new, int64_t k_sb, int64_t k_sg, int64_t k_st, const void* v_new, int64_t v_sb,
                  int64_t v_sg, int64_t v_st, int dtype, int B, int G, int t, int D, void* k_buf, void* v_buf,
                  int64_t cap, int64_t n0, void* stream) {

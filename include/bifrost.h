@@ -197,6 +197,26 @@ int bf_gated_norm(const void* o, int o_dtype, const void* z, const float* w, int
                   void* out, int io_dtype, void* stream);
 
 /*
+ * The llama.cpp per-sequence Bifrost state row (Heimdall/llamacpp/bifrost.patch:221-239, the views of
+ * build_layer_bifrost :1000-1013) <-> the student cache (sink_k, sink_v, ring_k, ring_v, ring_km, ring_g, ring_beta,
+ * ring_pos, S of HybridAttention._student, Heimdall/heimdall/hibrit.py:363-424), so a llama.cpp build and these
+ * kernels can hand sequences to each other. Row (f32, bf_llama_state_floats floats): region [LR][C] (LR =
+ * ceil((S + W + 2) / 32) * 32 slots: sinks, ring slot S + p mod (W + 1), scratch; C = 3 G D + 2 G channels
+ * [k_rope | v | k_mem | g | beta]), K plane [G][LR][D], transposed V plane [G][D][LR], delta [G][dv][dk].
+ * Cache layouts as bf_decode_fwd (ring of W slots, slot p mod W), n = tokens seen, n_sinks sink rows (unpack:
+ * min(S, n)), state [B][G][D][D] f32. Rows [B][floats]. A sink slot's k_mem / g / beta are packed from the ring while
+ * the sink is still in it, else 0 (never read by the layer).
+ */
+int bf_llama_state_floats(int G, int D, int W, int S, int64_t* floats);
+int bf_llama_state_pack(int B, int G, int D, int W, int S, int64_t n, int kv_dtype, const void* ring_k,
+                        const void* ring_v, const float* ring_km, const float* ring_g, const float* ring_beta,
+                        const int64_t* ring_pos, const void* sink_k, const void* sink_v, int n_sinks,
+                        const float* state, float* rows, void* stream);
+int bf_llama_state_unpack(int B, int G, int D, int W, int S, int64_t n, int kv_dtype, const float* rows, void* ring_k,
+                          void* ring_v, float* ring_km, float* ring_g, float* ring_beta, int64_t* ring_pos,
+                          void* sink_k, void* sink_v, int n_sinks, float* state, void* stream);
+
+/*
  * Backward of the chunked GQA gated delta rule: the gradients that autograd takes through motor.delta_rule_gqa
  * (Heimdall/heimdall/motor.py:70-102) in the conversion training's loss (motor.seq_loss, :149-193), fp32 like the
  * reference's training path. Inputs as bf_gdn_fwd with fp32 q, k, v for num_seqs sequences of seq_len tokens each

@@ -495,8 +495,8 @@ def run_gdn_bwd(steps, warmup, dev, T=8192, cpu=False):
 def run_llama_state(steps, warmup, dev):
     """The llama.cpp state-row formats at the decode geometry (B=64 sequences, G=4, D=256, W=2048, 4 sinks, bf16 ring,
     position 100000): bf_llama_state_pack and bf_llama_state_unpack, each timed with HIP events. Algorithmic bytes:
-    the cache read (ring k, v bf16; k_mem, g, beta, state f32) and the rows written (43.7 MB per sequence), and the
-    reverse for unpack."""
+    pack reads the cache (ring k, v bf16; k_mem, g, beta, state f32) and writes the rows (43.7 MB per sequence);
+    unpack reads the rows' region and delta block and writes the cache."""
     from heimdall_amd import formats
 
     B, G, D, W, S, n = 64, 4, 256, 2048, 4, 100000
@@ -511,6 +511,8 @@ def run_llama_state(steps, warmup, dev):
     c["ring_pos"][pos % W] = pos
     cache_bytes = sum(t.numel() * t.element_size() for t in c.values())
     row_bytes = B * formats.llama_state_floats(G, D, W, S) * 4
+    LR, C_ = (S + W + 2 + 31) // 32 * 32, 3 * G * D + 2 * G
+    read_back = B * (LR * C_ + D * D * G) * 4                # unpack reads the region and the delta, not the planes
     stream = torch.cuda.current_stream(dev)
     rows = formats.pack_llama_state(c, n, W, S)
     res = {}
@@ -526,12 +528,13 @@ def run_llama_state(steps, warmup, dev):
         e1.record(stream)
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / steps
-        gbs = (cache_bytes + row_bytes) / (ms * 1e-3) / 1e9
-        res[name] = {"ms": ms, "GBs": gbs, "frac": gbs / HBM_PEAK_GBS}
-    return {"workload": f"llama.cpp state rows B={B} G={G} D={D} W={W} S={S} bf16 ring", "bytes": cache_bytes + row_bytes,
+        nbytes = cache_bytes + (row_bytes if name == "pack" else read_back)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"ms": ms, "bytes": nbytes, "GBs": gbs, "frac": gbs / HBM_PEAK_GBS}
+    return {"workload": f"llama.cpp state rows B={B} G={G} D={D} W={W} S={S} bf16 ring",
             "pack": res["pack"], "unpack": res["unpack"], "ms_per_step": res["pack"]["ms"] + res["unpack"]["ms"],
             "roofline": {"bound": "hbm", "achieved": res["pack"]["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                         "frac": res["pack"]["frac"], "kernel": "llama_state_pack_kernel"}}
+                         "frac": res["pack"]["frac"], "kernel": "bf_llama_state_pack (region, V plane, delta kernels)"}}
 
 
 def run_window(steps, warmup, dev, T=32768):

@@ -13,6 +13,9 @@
 // [B][G][ns][D] (ns = min(S, n)), state [B][G][dk][dv]. The ring holds positions max(0, n - W) .. n - 1.
 // A sink slot's k_mem, g and beta are taken from the ring while the sink position is still in it, else written 0 (the
 // layer never reads them: a sink's beta is 0 and its row is attended through k_rope / v only).
+// Kernels: the row is written section by section (region rows and the K plane with four channels per thread, the V
+// plane and the delta block through 64 x 64 LDS tile transposes) and read back the same way (one cache ring slot or
+// sink per block, the state through tile transposes).
 #include "bf_common.h"
 #include "bf_internal.h"
 
@@ -37,136 +40,184 @@ __device__ __forceinline__ long llama_ring_pos(long r, long n, int W) {
     return p < n ? p : -1;
 }
 
-// value of cache quantity `kind` (0 k_rope, 1 v, 2 k_mem, 3 g, 4 beta) of llama.cpp slot l, head g, dim d
-__device__ float slot_value(const LlamaStateArgs& a, int b, long l, int kind, int g, int d) {
-    const int G = a.G, D = a.D, W = a.W, S = a.S;
-    long p = -1;                                          // position of the slot
-    bool sink = false;
-    if (l < S) {
-        p = l;
-        sink = p < a.n_sinks;
-        if (!sink) return 0.f;
-    } else if (l < S + W + 1) {
-        p = llama_ring_pos(l - S, a.n, W);
-        if (p < 0) return 0.f;
-    } else {
-        return 0.f;                                       // scratch / padding
+// what slot l of the region holds: the sink index (or -1) and the cache ring slot of its position (or -1)
+struct SlotSrc {
+    int sink, rs;
+};
+__device__ __forceinline__ SlotSrc slot_src(const LlamaStateArgs& a, long l) {
+    SlotSrc s{-1, -1};
+    long p = -1;
+    if (l < a.S) {
+        if (l < a.n_sinks) { s.sink = (int)l; p = l; }
+    } else if (l < a.S + a.W + 1) {
+        p = llama_ring_pos(l - a.S, a.n, a.W);
     }
-    if (sink && kind <= 1) {
-        const long at = (((long)b * G + g) * a.n_sinks + p) * D + d;
-        return ld_kv(kind == 0 ? a.sink_k : a.sink_v, at, a.kv_dtype);
-    }
-    const int rs = (int)(p % W);                          // the cache's ring slot
-    if (p < (a.n > W ? a.n - W : 0) || a.ring_pos[rs] != p) return 0.f;
-    switch (kind) {
-        case 0: return ld_kv(a.ring_k, (((long)b * G + g) * W + rs) * D + d, a.kv_dtype);
-        case 1: return ld_kv(a.ring_v, (((long)b * G + g) * W + rs) * D + d, a.kv_dtype);
-        case 2: return a.ring_km[(((long)b * W + rs) * G + g) * D + d];
-        case 3: return a.ring_g[((long)b * W + rs) * G + g];
-        default: return a.ring_beta[((long)b * W + rs) * G + g];
-    }
+    const long lo = a.n > a.W ? a.n - a.W : 0;
+    if (p >= lo && p < a.n && a.ring_pos[p % a.W] == p) s.rs = (int)(p % a.W);
+    return s;
+}
+
+// k_rope (kind 0) or v (kind 1) of a slot, head g, dim d
+__device__ __forceinline__ float slot_kv(const LlamaStateArgs& a, const SlotSrc& s, int b, int kind, int g, int d) {
+    if (s.sink >= 0)
+        return ld_kv(kind ? a.sink_v : a.sink_k, (((long)b * a.G + g) * a.n_sinks + s.sink) * a.D + d, a.kv_dtype);
+    if (s.rs >= 0)
+        return ld_kv(kind ? a.ring_v : a.ring_k, (((long)b * a.G + g) * a.W + s.rs) * a.D + d, a.kv_dtype);
+    return 0.f;
 }
 
 }  // namespace
 
-// ---- pack: one thread per f32 of the output rows [B][Nb]
-__global__ __launch_bounds__(FT) void llama_state_pack_kernel(LlamaStateArgs a) {
-    const long nb = a.row, e = (long)blockIdx.x * FT + threadIdx.x;
-    if (e >= (long)a.B * nb) return;
-    const int b = (int)(e / nb);
-    const long x = e % nb;
-    const int G = a.G, D = a.D;
-    const long LR = a.LR, C = 3L * G * D + 2 * G, GD = (long)G * D;
-    const long o_kp = LR * C, o_vp = o_kp + LR * GD, o_dl = o_vp + LR * GD;
-    float v;
-    if (x < o_kp) {
-        const long l = x / C, c = x % C;
-        if (c < 3 * GD) v = slot_value(a, b, l, (int)(c / GD), (int)((c % GD) / D), (int)(c % D));
-        else v = slot_value(a, b, l, c < 3 * GD + G ? 3 : 4, (int)((c - 3 * GD) % G), 0);
-    } else if (x < o_vp) {                                // K plane [G][LR][D]
-        const long y = x - o_kp;
-        v = slot_value(a, b, (y / D) % LR, 0, (int)(y / (LR * D)), (int)(y % D));
-    } else if (x < o_dl) {                                // V plane [G][D][LR]
-        const long y = x - o_vp;
-        v = slot_value(a, b, y % LR, 1, (int)(y / (LR * D)), (int)((y / LR) % D));
-    } else {                                              // delta [G][dv][dk] <- state [G][dk][dv]
-        const long y = x - o_dl;
-        const int g = (int)(y / ((long)D * D)), dv = (int)((y / D) % D), dk = (int)(y % D);
-        v = a.state[(((long)b * G + g) * D + dk) * D + dv];
+// four consecutive k_rope / v values of a slot (d a multiple of 4)
+__device__ __forceinline__ float4 slot_kv4(const LlamaStateArgs& a, const SlotSrc& s, int b, int kind, int g, int d) {
+    long at;
+    const void* src;
+    if (s.sink >= 0) {
+        src = kind ? a.sink_v : a.sink_k;
+        at = (((long)b * a.G + g) * a.n_sinks + s.sink) * a.D + d;
+    } else if (s.rs >= 0) {
+        src = kind ? a.ring_v : a.ring_k;
+        at = (((long)b * a.G + g) * a.W + s.rs) * a.D + d;
+    } else {
+        return make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    a.rows[e] = v;
+    if (a.kv_dtype == DT_BF16) {
+        const uint2 u = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(src) + at);
+        return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                           __uint_as_float(u.y & 0xffff0000u));
+    }
+    return *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(src) + at);
 }
 
-// ---- unpack: one thread per element of the cache (ring k / v, k_mem, g / beta, positions, sinks, state)
-__global__ __launch_bounds__(FT) void llama_state_unpack_kernel(LlamaStateArgs a) {
-    const long e = (long)blockIdx.x * FT + threadIdx.x;
-    const int B = a.B, G = a.G, D = a.D, W = a.W, S = a.S;
-    const long LR = a.LR, C = 3L * G * D + 2 * G, GD = (long)G * D, nb = a.row;
-    const long o_dl = LR * C + 2 * LR * GD;
-    const long n_ring = (long)B * G * W * D;              // ring_k, then ring_v
-    const long n_km = (long)B * W * G * D, n_gb = (long)B * W * G, n_sk = (long)B * G * a.n_sinks * D;
-    const long n_st = (long)B * G * D * D;
+// ---- pack, region rows and the K plane: grid (LR, B), four channels per thread; the k_rope channels also go to
+// K plane [G][LR][D]
+__global__ __launch_bounds__(FT) void llama_pack_region_kernel(LlamaStateArgs a) {
+    const long l = blockIdx.x;
+    const int b = blockIdx.y, G = a.G, D = a.D, GD = G * D, C = 3 * GD + 2 * G;
+    const SlotSrc s = slot_src(a, l);
+    float* row = a.rows + (long)b * a.row;
+    float* out = row + l * C;
+    float* kp = row + a.LR * C;
+    for (int c = 4 * threadIdx.x; c < 3 * GD; c += 4 * FT) {     // k_rope, v, k_mem: whole float4s
+        float4 v;
+        if (c < 2 * GD) {
+            const int g = (c % GD) / D, d = c % D;
+            v = slot_kv4(a, s, b, c / GD, g, d);
+            if (c < GD) *reinterpret_cast<float4*>(kp + ((long)g * a.LR + l) * D + d) = v;
+        } else {
+            v = s.rs >= 0 ? *reinterpret_cast<const float4*>(a.ring_km + ((long)b * a.W + s.rs) * GD + (c - 2 * GD))
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        *reinterpret_cast<float4*>(out + c) = v;
+    }
+    for (int c = 3 * GD + threadIdx.x; c < C; c += FT) {          // g, beta
+        float v = 0.f;
+        if (s.rs >= 0) {
+            const long base = (long)b * a.W + s.rs;
+            v = c < 3 * GD + G ? a.ring_g[base * G + (c - 3 * GD)] : a.ring_beta[base * G + (c - 3 * GD - G)];
+        }
+        out[c] = v;
+    }
+}
+
+// ---- pack, V plane [G][D][LR] (transposed through a 64 x 64 LDS tile, four dims per thread on the read, four
+// slots per thread on the write): grid (ceil(LR / 64), D / 64, G B)
+__global__ __launch_bounds__(FT) void llama_pack_vplane_kernel(LlamaStateArgs a) {
+    __shared__ float tile[64][65];
+    const int l0 = blockIdx.x * 64, d0 = blockIdx.y * 64, g = blockIdx.z % a.G, b = blockIdx.z / a.G;
+    const int t = threadIdx.x;
+    {
+        const int r0 = t / 16, dq = (t % 16) * 4;            // 16 threads per slot row, 16 rows per pass
+        for (int r = r0; r < 64; r += FT / 16) {
+            const long l = l0 + r;
+            const float4 v = l < a.LR ? slot_kv4(a, slot_src(a, l), b, 1, g, d0 + dq) : make_float4(0.f, 0.f, 0.f, 0.f);
+            tile[r][dq] = v.x; tile[r][dq + 1] = v.y; tile[r][dq + 2] = v.z; tile[r][dq + 3] = v.w;
+        }
+    }
+    __syncthreads();
+    const long C = 3L * a.G * a.D + 2 * a.G;
+    float* out = a.rows + (long)b * a.row + a.LR * C + (long)a.G * a.LR * a.D;
+    const int d_r = t / 16, lq = (t % 16) * 4;               // 16 threads per dim row, four slots each
+    for (int r = d_r; r < 64; r += FT / 16) {
+        const long l = l0 + lq;
+        float* o = out + ((long)g * a.D + d0 + r) * a.LR + l;
+        if (l + 3 < a.LR && ((a.LR & 3) == 0)) {
+            *reinterpret_cast<float4*>(o) = make_float4(tile[lq][r], tile[lq + 1][r], tile[lq + 2][r], tile[lq + 3][r]);
+        } else {
+            for (int j = 0; j < 4; ++j)
+                if (l + j < a.LR) o[j] = tile[lq + j][r];
+        }
+    }
+}
+
+// ---- pack, delta [G][dv][dk] <- state [G][dk][dv] (64 x 64 tiles): grid (D / 64, D / 64, G B)
+__global__ __launch_bounds__(FT) void llama_pack_delta_kernel(LlamaStateArgs a) {
+    __shared__ float tile[64][65];
+    const int k0 = blockIdx.x * 64, v0 = blockIdx.y * 64, g = blockIdx.z % a.G, b = blockIdx.z / a.G, D = a.D;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const float* st = a.state + ((long)b * a.G + g) * D * D;
+    for (int r = ty; r < 64; r += FT / 64) tile[r][tx] = st[(long)(k0 + r) * D + v0 + tx];   // [dk][dv]
+    __syncthreads();
+    const long C = 3L * a.G * D + 2 * a.G;
+    float* out = a.rows + (long)b * a.row + a.LR * C + 2L * a.G * a.LR * D + (long)g * D * D;
+    for (int r = ty; r < 64; r += FT / 64) out[(long)(v0 + r) * D + k0 + tx] = tile[tx][r];      // [dv][dk]
+}
+
+// ---- unpack, the ring: grid (W, B), one cache ring slot per block, the region row of its position, four channels
+// per thread
+__global__ __launch_bounds__(FT) void llama_unpack_ring_kernel(LlamaStateArgs a) {
+    const int s = blockIdx.x, b = blockIdx.y, G = a.G, D = a.D, W = a.W, GD = G * D;
+    const long C = 3L * GD + 2 * G;
     const long lo = a.n > W ? a.n - W : 0;
-    // cache ring slot s holds position p = lo + ((s - lo) mod W) when p < n
-    auto ring_p = [&](long s) {
-        const long p = lo + ((s - lo % W) % W + W) % W;
-        return p < a.n ? p : -1L;
-    };
-    auto region = [&](int b, long l, long c) { return a.rows[(long)b * nb + l * C + c]; };
-    long x = e;
-    if (x < 2 * n_ring) {
-        const bool is_v = x >= n_ring;
-        const long y = is_v ? x - n_ring : x;
-        const int d = (int)(y % D);
-        const long s = (y / D) % W;
-        const int g = (int)((y / ((long)D * W)) % G), b = (int)(y / ((long)D * W * G));
-        const long p = ring_p(s);
-        const float v = p < 0 ? 0.f : region(b, S + p % (W + 1), (is_v ? GD : 0) + (long)g * D + d);
-        st_kv(is_v ? a.ring_v_out : a.ring_k_out, y, v, a.kv_dtype);
-        return;
+    long p = lo + ((s - lo % W) % W + W) % W;
+    if (p >= a.n) p = -1;
+    const float* row = p < 0 ? nullptr : a.rows + (long)b * a.row + (a.S + p % (W + 1)) * C;
+    for (int c = 4 * threadIdx.x; c < 3 * GD; c += 4 * FT) {
+        const float4 v = row ? *reinterpret_cast<const float4*>(row + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (c < 2 * GD) {
+            const int g = (c % GD) / D, d = c % D;
+            const long at = (((long)b * G + g) * W + s) * D + d;
+            void* dst = c < GD ? a.ring_k_out : a.ring_v_out;
+            if (a.kv_dtype == DT_BF16) {
+                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(dst) + at) =
+                    make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+            } else {
+                *reinterpret_cast<float4*>(reinterpret_cast<float*>(dst) + at) = v;
+            }
+        } else {
+            *reinterpret_cast<float4*>(a.ring_km_out + ((long)b * W + s) * GD + (c - 2 * GD)) = v;
+        }
     }
-    x -= 2 * n_ring;
-    if (x < n_km) {
-        const int d = (int)(x % D), g = (int)((x / D) % G);
-        const long s = (x / GD) % W;
-        const int b = (int)(x / (GD * W));
-        const long p = ring_p(s);
-        a.ring_km_out[x] = p < 0 ? 0.f : region(b, S + p % (W + 1), 2 * GD + (long)g * D + d);
-        return;
+    for (int c = 3 * GD + threadIdx.x; c < C; c += FT) {
+        const float v = row ? row[c] : 0.f;
+        if (c < 3 * GD + G) a.ring_g_out[((long)b * W + s) * G + (c - 3 * GD)] = v;
+        else a.ring_beta_out[((long)b * W + s) * G + (c - 3 * GD - G)] = v;
     }
-    x -= n_km;
-    if (x < 2 * n_gb) {
-        const bool is_b = x >= n_gb;
-        const long y = is_b ? x - n_gb : x;
-        const int g = (int)(y % G);
-        const long s = (y / G) % W;
-        const int b = (int)(y / ((long)G * W));
-        const long p = ring_p(s);
-        const float v = p < 0 ? 0.f : region(b, S + p % (W + 1), 3 * GD + (is_b ? G : 0) + g);
-        (is_b ? a.ring_beta_out : a.ring_g_out)[y] = v;
-        return;
+    if (b == 0 && threadIdx.x == 0) a.ring_pos_out[s] = p;
+}
+
+// ---- unpack, the sinks: grid (n_sinks, B)
+__global__ __launch_bounds__(FT) void llama_unpack_sinks_kernel(LlamaStateArgs a) {
+    const int j = blockIdx.x, b = blockIdx.y, G = a.G, D = a.D, GD = G * D;
+    const long C = 3L * GD + 2 * G;
+    const float* row = a.rows + (long)b * a.row + (long)j * C;
+    for (int c = threadIdx.x; c < 2 * GD; c += FT) {
+        const int g = (c % GD) / D, d = c % D;
+        st_kv(c < GD ? a.sink_k_out : a.sink_v_out, (((long)b * G + g) * a.n_sinks + j) * D + d, row[c], a.kv_dtype);
     }
-    x -= 2 * n_gb;
-    if (x < W) {
-        a.ring_pos_out[x] = ring_p(x);
-        return;
-    }
-    x -= W;
-    if (x < 2 * n_sk) {
-        const bool is_v = x >= n_sk;
-        const long y = is_v ? x - n_sk : x;
-        const int d = (int)(y % D);
-        const long j = (y / D) % a.n_sinks;
-        const int g = (int)((y / ((long)D * a.n_sinks)) % G), b = (int)(y / ((long)D * a.n_sinks * G));
-        st_kv(is_v ? a.sink_v_out : a.sink_k_out, y, region(b, j, (is_v ? GD : 0) + (long)g * D + d), a.kv_dtype);
-        return;
-    }
-    x -= 2 * n_sk;
-    if (x < n_st) {                                       // state [B][G][dk][dv] <- delta [G][dv][dk]
-        const int dv = (int)(x % D), dk = (int)((x / D) % D), g = (int)((x / ((long)D * D)) % G);
-        const int b = (int)(x / ((long)D * D * G));
-        a.state_out[x] = a.rows[(long)b * nb + o_dl + ((long)g * D + dv) * D + dk];
-    }
+}
+
+// ---- unpack, the state [G][dk][dv] <- delta [G][dv][dk]: grid (D / 64, D / 64, G B)
+__global__ __launch_bounds__(FT) void llama_unpack_state_kernel(LlamaStateArgs a) {
+    __shared__ float tile[64][65];
+    const int v0 = blockIdx.x * 64, k0 = blockIdx.y * 64, g = blockIdx.z % a.G, b = blockIdx.z / a.G, D = a.D;
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+    const long C = 3L * a.G * D + 2 * a.G;
+    const float* dl = a.rows + (long)b * a.row + a.LR * C + 2L * a.G * a.LR * D + (long)g * D * D;
+    for (int r = ty; r < 64; r += FT / 64) tile[r][tx] = dl[(long)(v0 + r) * D + k0 + tx];      // [dv][dk]
+    __syncthreads();
+    float* st = a.state_out + ((long)b * a.G + g) * D * D;
+    for (int r = ty; r < 64; r += FT / 64) st[(long)(k0 + r) * D + v0 + tx] = tile[tx][r];       // [dk][dv]
 }
 
 long llama_state_floats(int G, int D, int W, int S) {
@@ -175,16 +226,17 @@ long llama_state_floats(int G, int D, int W, int S) {
 }
 
 int llama_state(const LlamaStateArgs& a, bool pack, hipStream_t stream) {
-    long total;
+    const dim3 blk(FT), tiles(a.D / 64, a.D / 64, a.G * a.B);
     if (pack) {
-        total = (long)a.B * a.row;
+        hipLaunchKernelGGL(llama_pack_region_kernel, dim3((unsigned)a.LR, a.B), blk, 0, stream, a);
+        hipLaunchKernelGGL(llama_pack_vplane_kernel, dim3((unsigned)((a.LR + 63) / 64), a.D / 64, a.G * a.B), blk, 0,
+                           stream, a);
+        hipLaunchKernelGGL(llama_pack_delta_kernel, tiles, blk, 0, stream, a);
     } else {
-        const long B = a.B, G = a.G, D = a.D, W = a.W;
-        total = 2 * B * G * W * D + B * W * G * D + 2 * B * W * G + W + 2 * B * G * a.n_sinks * D + B * G * D * D;
+        hipLaunchKernelGGL(llama_unpack_ring_kernel, dim3(a.W, a.B), blk, 0, stream, a);
+        if (a.n_sinks) hipLaunchKernelGGL(llama_unpack_sinks_kernel, dim3(a.n_sinks, a.B), blk, 0, stream, a);
+        hipLaunchKernelGGL(llama_unpack_state_kernel, tiles, blk, 0, stream, a);
     }
-    const unsigned blocks = (unsigned)((total + FT - 1) / FT);
-    if (pack) hipLaunchKernelGGL(llama_state_pack_kernel, dim3(blocks), dim3(FT), 0, stream, a);
-    else hipLaunchKernelGGL(llama_state_unpack_kernel, dim3(blocks), dim3(FT), 0, stream, a);
     return (int)hipGetLastError();
 }
 

@@ -129,7 +129,7 @@ def delta_rule_gqa(q, k, v, g, beta, chunk: int = 64,
         v_new = u[:, :, i] - w[:, :, i] @ s                                          # [b, G, c, dv]
         outs.append(q_dec[:, :, :, i] @ s[:, :, None] + attn[:, :, :, i] @ v_new[:, :, None])
         s = s * tail[:, :, i] + k_tail[:, :, i].transpose(-1, -2) @ v_new
-    out = torch.stack(outs, 3)                                                      # [b, G, R, n, c, dv]
+    out = torch.stack(outs, 3) if outs else torch.zeros(b, G, R, 0, c, dv, dtype=dt)   # [b, G, R, n, c, dv]
     o = out.reshape(b, G, R, n * c, dv)[:, :, :, :t].permute(0, 3, 1, 2, 4).contiguous()
     return o, s
 

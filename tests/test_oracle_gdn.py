@@ -197,3 +197,10 @@ def test_gqa_grads_chunk_invariant():
     b = gdn.delta_rule_gqa_grads(q, k, v, g, beta, s0, do, None, chunk=64)
     for x, y in zip(a, b):
         assert ((x - y).norm() / y.norm()).item() < 1e-10
+
+
+def test_gqa_empty_sequence_keeps_state():
+    """A sequence of no tokens: no output rows, the initial state unchanged."""
+    q, k, v, g, beta, s0 = _gqa_inputs(1, 0, 2, 3, 8, seed=25)
+    o, s = gdn.delta_rule_gqa(q, k, v, g, beta, 16, s0)
+    assert o.shape == (1, 0, 2, 3, 8) and torch.equal(s, s0)

@@ -158,6 +158,106 @@ def cpu_baseline(inputs, budget_s=30.0):
                       f"{len(times)} run(s), {cpu_model()}"}
 
 
+def _cpu(value_units: float, fn, unit: str, sample: str) -> dict:
+    """Time one call of an oracle function on all host cores: {"value": units per second, ...} ("port" baseline)."""
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    with torch.no_grad():
+        t = time.perf_counter()
+        fn()
+        dt = time.perf_counter() - t
+    return {"value": value_units / dt, "unit": unit, "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"{sample}, one run, {cpu_model()}"}
+
+
+def _oracle_layer(H, G, D, d, W, S):
+    import types
+    from oracle import layer as ol
+    m = types.SimpleNamespace(c=ol.Cfg(H, G, D, d))
+    ol.convert_params(m, W, S, 1)
+    return ol, m
+
+
+def cpu_decode(B=8):
+    """The oracle's student decode step (fp32, memory branch and mix included) for B = 8 of the decode leg's 64
+    sequences (H=16, G=4, D=256, W=2048 + 4 sinks, position 100000)."""
+    H, G, D, W, S, p, d = 16, 4, 256, 2048, 4, 100000, 1024
+    ol, m = _oracle_layer(H, G, D, d, W, S)
+    rn = lambda *s: torch.randn(*s)
+    pos = torch.arange(p - W, p)
+    ring_pos = torch.empty(W, dtype=torch.long)
+    ring_pos[pos % W] = pos
+    cache = dict(ring_k=rn(B, G, W, D), ring_v=rn(B, G, W, D), ring_km=F.normalize(rn(B, W, G, D), dim=-1),
+                 ring_g=-torch.rand(B, W, G) * 1e-3, ring_beta=torch.rand(B, W, G), ring_pos=ring_pos,
+                 sink_k=rn(B, G, S, D), sink_v=rn(B, G, S, D), S=rn(B, G, D, D) * 0.02)
+    x, q, k, v = rn(B, 1, d), rn(B, 1, H, D), rn(B, 1, G, D), rn(B, 1, G, D)
+    qr, kr = rn(B, H, 1, D), rn(B, G, 1, D)
+    return _cpu(B, lambda: ol.student(m, x, q, k, v, qr, kr, p, cache), "tokens/s",
+                f"oracle layer.student decode step fp32, B={B} of 64, H=16 G=4 D=256 W=2048+4")
+
+
+def cpu_layer(T=4096):
+    """The oracle's student prefill (fp32) from an empty cache on the first T = 4096 tokens of the layer leg's
+    geometry (H=24, G=4, D=256, W=2048 + 4 sinks; the memory is active after token 2048)."""
+    H, G, D, W, S, d = 24, 4, 256, 2048, 4, 1024
+    ol, m = _oracle_layer(H, G, D, d, W, S)
+    rn = lambda *s: torch.randn(*s)
+    x, q = rn(1, T, d), rn(1, T, H, D)
+    k, v = F.normalize(rn(1, T, G, D), dim=-1), rn(1, T, G, D)
+    qr, kr = F.normalize(rn(1, H, T, D), dim=-1), F.normalize(rn(1, G, T, D), dim=-1)
+    return _cpu(T, lambda: ol.student(m, x, q, k, v, qr, kr, 0, {}), "tokens/s",
+                f"oracle layer.student prefill fp32, T={T} of the T=32768 workload, H=24 G=4 D=256 W=2048+4")
+
+
+def cpu_varlen(n=8192):
+    """The oracle's per-sequence delta rule (fp32) on two packed sequences of n / 2 tokens, H=32, D=128."""
+    from oracle import gdn
+    H, D = 32, 128
+    q, v = torch.randn(1, n, H, D), torch.randn(1, n, H, D)
+    k = F.normalize(torch.randn(1, n, H, D), dim=-1)
+    g, beta = -torch.rand(1, n, H) * 5e-3, torch.rand(1, n, H)
+    cu = torch.tensor([0, n // 2, n])
+    return _cpu(n, lambda: gdn.delta_rule_varlen(q, k, v, g, beta, cu), "tokens/s",
+                f"oracle gdn.delta_rule_varlen fp32, 2 sequences of {n // 2}, H=32 D=128")
+
+
+def cpu_gdn_layer(n=4096):
+    """The oracle's Gated DeltaNet layer core (conv + norms + gates, delta rule, gated norm; fp32) on n tokens, H=32,
+    D=128, conv width 4."""
+    from oracle import gdn_layer as og
+    H, D, K = 32, 128, 4
+    C = 3 * H * D
+    z, a, b, zg = torch.randn(1, n, C), torch.randn(1, n, H), torch.randn(1, n, H), torch.randn(1, n, H * D)
+    w, A_log, dt, nw = torch.randn(C, K) * 0.5, torch.randn(H) * 0.5 - 2, torch.randn(H), torch.ones(D)
+    return _cpu(n, lambda: og.layer_core(z, a, b, zg, w, A_log, dt, nw, H, H, D), "tokens/s",
+                f"oracle gdn_layer.layer_core fp32, T={n}, H=32 D=128")
+
+
+def cpu_teacher_decode(B=1, n=32768):
+    """The oracle's teacher decode step with retrieval (block summaries, selection, masked attention; fp64 as the
+    oracle computes) for B = 1 of the leg's 64 sequences at cache length 32768."""
+    from oracle import teacher as ot
+    H, G, D = 16, 4, 256
+    ret = dict(k=16, block=64, window=2048, sinks=4)
+    qr = torch.randn(B, H, 1, D)
+    kr, vt = F.normalize(torch.randn(B, G, n, D), dim=-1), torch.randn(B, G, n, D)
+    return _cpu(B, lambda: ot.masked_attention(qr, kr, vt, ot.retrieval_mask(qr, kr, ret)), "tokens/s",
+                f"oracle teacher retrieval decode step (fp64), B={B} of 64, H=16 G=4 D=256 n={n}")
+
+
+def cpu_llama_state(B=2):
+    """The oracle's state-row builder for B = 2 of the leg's 64 sequences (G=4, D=256, W=2048, S=4)."""
+    from oracle import formats as of
+    G, D, W, S, n = 4, 256, 2048, 4, 100000
+    pos = torch.arange(n - W, n)
+    ring_pos = torch.empty(W, dtype=torch.long)
+    ring_pos[pos % W] = pos
+    c = dict(ring_k=torch.randn(B, G, W, D), ring_v=torch.randn(B, G, W, D), ring_km=torch.randn(B, W, G, D),
+             ring_g=torch.rand(B, W, G), ring_beta=torch.rand(B, W, G), ring_pos=ring_pos,
+             sink_k=torch.randn(B, G, S, D), sink_v=torch.randn(B, G, S, D), S=torch.randn(B, G, D, D))
+    return _cpu(B, lambda: [of.llama_state_row(c, b, n, W, S) for b in range(B)], "rows/s",
+                f"oracle formats.llama_state_row, B={B} of 64 rows, G=4 D=256 W=2048 S=4")
+
+
 def run_decode(steps, warmup, dev):
     """Decode step, B=64, H=16, G=4, D=256, W=2048 + 4 sinks, bf16 ring, fp32 state ~ N(0, 0.02), at position
     100000 (ring full, memory active): the bf_decode_fwd pass alone, inputs resident."""
@@ -703,6 +803,11 @@ def main():
         line["teacher_decode"] = run_teacher_decode(50, 10, dev)
         line["gdn_bwd"] = run_gdn_bwd(10, 2, dev, cpu=not args.no_cpu)
         line["llama_state"] = run_llama_state(5, 2, dev)
+        if not args.no_cpu:
+            for leg, fn in (("decode", cpu_decode), ("layer_prefill_32k", cpu_layer), ("varlen_gdn", cpu_varlen),
+                            ("gdn_layer", cpu_gdn_layer), ("teacher_decode", cpu_teacher_decode),
+                            ("llama_state", cpu_llama_state)):
+                line[leg]["cpu_baseline"] = fn()
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(r["inputs"])
     print(json.dumps(line), flush=True)

@@ -35,6 +35,10 @@ SIGNATURES = {
     "bf_gdn_bwd_workspace_size": (_c_int, [_c_int, _c_i64, _c_int, _c_int, _c_int, ctypes.POINTER(_c_sz)]),
     "bf_gdn_bwd": (_c_int, [_vp] * 6 + [_fp, _vp, _vp, _c_int, _c_i64, _c_int, _c_int, _c_int] + [_vp] * 7
                    + [_c_sz, _vp]),
+    "bf_layer_prefill_workspace_size": (_c_int, [_c_int] * 6 + [ctypes.POINTER(_c_sz)]),
+    "bf_layer_prefill_fwd": (_c_int, [_c_int] * 7 + [_c_i64, _c_int, _c_int] + ([_vp, _c_i64, _c_i64, _c_i64] * 3)
+                             + [_vp, _c_int, _vp, _c_int] + [_vp] * 7 + [_c_int] + [_vp] * 7 + [_c_int]
+                             + [_vp, _vp, _vp, _c_sz, _vp]),
     "bf_llama_state_floats": (_c_int, [_c_int] * 4 + [ctypes.POINTER(_c_i64)]),
     "bf_llama_state_pack": (_c_int, [_c_int] * 5 + [_c_i64, _c_int] + [_vp] * 8 + [_c_int, _vp, _vp, _vp]),
     "bf_llama_state_unpack": (_c_int, [_c_int] * 5 + [_c_i64, _c_int] + [_vp] * 9 + [_c_int, _vp, _vp]),

@@ -205,6 +205,28 @@ struct LlamaStateArgs {
 long llama_state_floats(int G, int D, int W, int S);
 int llama_state(const LlamaStateArgs& a, bool pack, hipStream_t stream);
 
+struct LayerArgs {
+    int B, G, R, D, T, W, Tq, qoff;     // chunk of T tokens; Tq memory queries from chunk token qoff on
+    long start;
+    int in_dtype, qm_dtype, km_dtype;
+    const void *qm, *km, *kr, *v;
+    const float *g, *beta;
+    long k_sb, k_sh, k_st, v_sb, v_sh, v_st;
+    const void* ring_v;
+    const float *ring_km, *ring_g, *ring_beta;
+    const int64_t* ring_pos;
+    void *wq, *wk, *wv;                 // the GDN inputs [B Tq][H | G][D]
+    float *wg, *wb;
+    const void* om;                     // the GDN output [B Tq][H][D]
+    void* o_mem;                        // [B][T][H][D]
+    void *ring_k_w, *ring_v_w;
+    float *ring_km_w, *ring_g_w, *ring_beta_w;
+    int64_t* ring_pos_w;
+    const float* s_new;
+    float* state;
+};
+int layer_launch(const LayerArgs& a, int what, hipStream_t s);   // 0 stream, 1 place, 2 write-back, 3 state, 4 query
+
 struct KvAppendArgs {
     const void* k_new;              // row (b, g, i) at k_new + b * k_sb + g * k_sg + i * k_st (elements)
     const void* v_new;

@@ -279,6 +279,109 @@ static bool kv_aligned(const void* p, int64_t s1, int64_t s2) {
     return (reinterpret_cast<uintptr_t>(p) & 15) == 0 && s1 % 8 == 0 && s2 % 8 == 0;
 }
 
+// workspace of bf_layer_prefill_fwd: the GDN inputs and outputs for up to B T memory queries, o_mem, the new state
+// and the GDN workspace
+struct LayerWs {
+    size_t wq, wk, wv, wg, wb, om, o_mem, s_new, gdn, total;
+};
+static LayerWs layer_ws(int B, int G, int R, int D, int T, int in_dtype) {
+    LayerWs w{};
+    const size_t esz = in_dtype == BF_DTYPE_BF16 ? 2 : 4, H = (size_t)G * R, BT = (size_t)B * T;
+    size_t at = 0;
+    auto put = [&](size_t& f, size_t n) { f = at; at += align256(n); };
+    put(w.wq, BT * H * D * esz);
+    put(w.wk, BT * G * D * esz);
+    put(w.wv, BT * G * D * esz);
+    put(w.wg, BT * G * 4);
+    put(w.wb, BT * G * 4);
+    put(w.om, BT * H * D * esz);
+    put(w.o_mem, BT * H * D * esz);
+    put(w.s_new, (size_t)B * G * D * D * 4);
+    put(w.gdn, gdn_layout((int64_t)B * T, B, G, R, D, in_dtype, 0).total);
+    w.total = at;
+    return w;
+}
+
+int bf_layer_prefill_workspace_size(int B, int G, int R, int D, int T, int in_dtype, size_t* bytes) {
+    if (!bytes || B <= 0 || G <= 0 || R <= 0 || T <= 0) return BF_STATUS_INVALID;
+    if (!supported_dim(D) || !supported_dtype(in_dtype)) return BF_STATUS_UNSUPPORTED;
+    *bytes = layer_ws(B, G, R, D, T, in_dtype).total;
+    return BF_STATUS_OK;
+}
+
+int bf_layer_prefill_fwd(int B, int G, int R, int D, int T, int W, int sinks, int64_t start, int memory, int in_dtype,
+                         const void* qr, int64_t q_sb, int64_t q_sh, int64_t q_st, const void* kr, int64_t k_sb,
+                         int64_t k_sh, int64_t k_st, const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                         const void* qm, int qm_dtype, const void* km, int km_dtype, const float* g,
+                         const float* beta, const float* z, const float* mix_lse, const float* mem_scale,
+                         const void* sink_k, const void* sink_v, int n_sinks, void* ring_k, void* ring_v,
+                         float* ring_km, float* ring_g, float* ring_beta, int64_t* ring_pos, float* state,
+                         int state_valid, float* o, float* lse, void* workspace, size_t workspace_bytes,
+                         void* stream) {
+    if (B <= 0 || G <= 0 || R <= 0 || T <= 0 || W <= 0 || sinks < 0 || start < 0) return BF_STATUS_INVALID;
+    if (!supported_dim(D) || !supported_dtype(in_dtype) || !supported_dtype(qm_dtype) || !supported_dtype(km_dtype))
+        return BF_STATUS_UNSUPPORTED;
+    if (!qr || !kr || !v || !qm || !km || !g || !beta || !ring_k || !ring_v || !ring_km || !ring_g || !ring_beta ||
+        !ring_pos || !state || !o)
+        return BF_STATUS_INVALID;
+    const bool use_mem = memory && start + T > W;
+    if (use_mem && (!z || !mix_lse || !mem_scale)) return BF_STATUS_INVALID;
+    const LayerWs L = layer_ws(B, G, R, D, T, in_dtype);
+    if (!workspace || workspace_bytes < L.total || (reinterpret_cast<uintptr_t>(workspace) & 255))
+        return BF_STATUS_WORKSPACE;
+    char* ws = static_cast<char*>(workspace);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    bf::LayerArgs a{};
+    a.B = B; a.G = G; a.R = R; a.D = D; a.T = T; a.W = W; a.start = start;
+    a.in_dtype = in_dtype; a.qm_dtype = qm_dtype; a.km_dtype = km_dtype;
+    a.qm = qm; a.km = km; a.kr = kr; a.v = v; a.g = g; a.beta = beta;
+    a.k_sb = k_sb; a.k_sh = k_sh; a.k_st = k_st; a.v_sb = v_sb; a.v_sh = v_sh; a.v_st = v_st;
+    a.ring_v = ring_v; a.ring_km = ring_km; a.ring_g = ring_g; a.ring_beta = ring_beta; a.ring_pos = ring_pos;
+    a.wq = ws + L.wq; a.wk = ws + L.wk; a.wv = ws + L.wv;
+    a.wg = reinterpret_cast<float*>(ws + L.wg); a.wb = reinterpret_cast<float*>(ws + L.wb);
+    a.om = ws + L.om; a.o_mem = ws + L.o_mem;
+    a.ring_k_w = ring_k; a.ring_v_w = ring_v; a.ring_km_w = ring_km; a.ring_g_w = ring_g; a.ring_beta_w = ring_beta;
+    a.ring_pos_w = ring_pos;
+    a.s_new = reinterpret_cast<float*>(ws + L.s_new); a.state = state;
+    int rc;
+    const void* o_mem = nullptr;
+    if (use_mem) {
+        // from an empty cache the queries before W never mix the memory in: the stream is the chunk shifted by W
+        const bool fresh = start == 0 && !state_valid;
+        a.qoff = fresh ? W : 0;
+        a.Tq = T - a.qoff;
+        const size_t esz = in_dtype == BF_DTYPE_BF16 ? 2 : 4, H = (size_t)G * R;
+        // a single sequence, or no shift, keeps the query and output rows contiguous: no staging copies
+        const bool rows = B == 1 || a.qoff == 0;
+        const void* wq = a.wq;
+        if (rows && qm_dtype == in_dtype) wq = static_cast<const char*>(qm) + a.qoff * H * D * esz;
+        else if ((rc = bf::layer_launch(a, 4, st))) return rc;
+        const void *wk = a.wk, *wv = a.wv;
+        const float *wg = a.wg, *wb = a.wb;
+        if (fresh && B == 1 && km_dtype == in_dtype && v_sh == D && v_st == (int64_t)G * D) {
+            wk = km; wv = v; wg = g; wb = beta;                 // the stream is the chunk's own rows 0 .. T - W - 1
+        } else if ((rc = bf::layer_launch(a, 0, st))) {
+            return rc;
+        }
+        void* om = rows ? static_cast<char*>(a.o_mem) + a.qoff * H * D * esz : ws + L.om;
+        a.om = om;
+        rc = bf_gdn_fwd(wq, wk, wv, wg, wb, nullptr, B, (int64_t)B * a.Tq, G, R, D, in_dtype, 1.f,
+                        state_valid ? state : nullptr, om, in_dtype, reinterpret_cast<float*>(ws + L.s_new), 0, ws + L.gdn, L.total - L.gdn,
+                        BF_GDN_PHASE_ALL, stream);
+        if (rc) return rc;
+        if (!rows && (rc = bf::layer_launch(a, 1, st))) return rc;
+        o_mem = a.o_mem;
+    }
+    rc = bf_window_fwd(B, G, R, D, T, W, sinks, start, in_dtype, qr, q_sb, q_sh, q_st, kr, k_sb, k_sh, k_st, v, v_sb,
+                       v_sh, v_st, ring_k, ring_v, ring_pos, sink_k, sink_v, n_sinks, use_mem ? 1 : 0, o_mem,
+                       in_dtype, use_mem ? z : nullptr, use_mem ? mix_lse : nullptr, use_mem ? mem_scale : nullptr, o,
+                       BF_DTYPE_F32, lse, stream);
+    if (rc) return rc;
+    if ((rc = bf::layer_launch(a, 2, st))) return rc;         // ring write-back after every read of the ring
+    if (use_mem && (rc = bf::layer_launch(a, 3, st))) return rc;
+    return BF_STATUS_OK;
+}
+
 int bf_gdn_bwd_workspace_size(int num_seqs, int64_t seq_len, int G, int R, int D, size_t* bytes) {
     if (!bytes || num_seqs <= 0 || seq_len <= 0 || G <= 0 || R <= 0) return BF_STATUS_INVALID;
     if (!supported_dim(D) || seq_len % 64) return BF_STATUS_UNSUPPORTED;

@@ -23,7 +23,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _lib
-from ._device import (BifrostError, check, dtype_code, gdn_forward, require_device, require_no_grad, stream_ptr,
+from ._device import (BifrostError, check, dtype_code, require_device, require_no_grad, stream_ptr,
                       workspace)
 from .teacher import set_retrieval, teacher
 
@@ -184,79 +184,57 @@ def _strides(t: torch.Tensor, dims):
 
 
 def _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memory, xf=None):
-    """A chunk of t > 1 tokens: memory branch on bf_gdn_fwd (write stream = ring rows leaving the window, then the
-    chunk's own rows, hibrit.py:391-408), then bf_window_fwd with the gamma mix fused (hibrit.py:385-411), then the
-    ring / sink / state write-back (hibrit.py:412-423).
-
-    From an empty cache (start 0, no state) the write stream of query i is token i - W of the chunk itself and the
-    queries before W never read the memory (gamma is 0 there), so the memory branch runs on views: queries W..t-1
-    against the writes of tokens 0..t-W-1."""
+    """A chunk of t > 1 tokens in one bf_layer_prefill_fwd call: the delta-rule memory on the write stream (ring rows
+    leaving the window, then the chunk's own rows, hibrit.py:391-408), the window + sinks + LSE with the gamma mix
+    (hibrit.py:385-411), then the ring / state write-back (hibrit.py:412-423). From an empty cache (start 0, no
+    state) the queries before W never read the memory, so the library runs the memory on queries W..t-1 against the
+    writes of tokens 0..t-W-1 only."""
     c = self.c
     b, t = x.shape[:2]
     H, G, D, w, r = c.h, c.hkv, c.dh, self.window, c.h // c.hkv
     dev = x.device
     cdt = torch.bfloat16 if qr.dtype in (torch.bfloat16, torch.float16) else torch.float32
     lib = _lib.load()
-    pos = torch.arange(start, start + t, device=dev)
     use_mem = memory and start + t > w
-    o_mem = z = None
-    s0 = st.get("S") if use_mem else None
-    if use_mem and start == 0 and s0 is None:
-        n = t - w
-        sl = lambda z, a_, e_: z[:, a_:e_].reshape(b * (e_ - a_), *z.shape[2:])
-        o_mem = torch.empty(b, t, H, D, dtype=cdt, device=dev)      # rows < W are never read
-        om, s_new = gdn_forward(sl(qm, w, t).to(cdt), sl(km, 0, n).to(cdt), sl(v, 0, n).to(cdt), sl(g, 0, n),
-                                sl(beta, 0, n), num_seqs=b, out_dtype=cdt, out=o_mem[0, w:] if b == 1 else None)
-        if b > 1:
-            o_mem[:, w:] = om.view(b, n, H, D)
+    for key in ("ring_k", "ring_v"):
+        if st[key].dtype != cdt or not st[key].is_contiguous():
+            st[key] = st[key].to(cdt).contiguous()
+    for key in ("ring_km", "ring_g", "ring_beta"):
+        if st[key].dtype != torch.float32 or not st[key].is_contiguous():
+            st[key] = st[key].float().contiguous()
+    S, valid = st.get("S"), 1
+    if S is None:
+        S, valid = torch.empty(b, G, D, D, dtype=torch.float32, device=dev), 0
+    elif not (S.dtype == torch.float32 and S.is_contiguous()):
+        S = S.float().contiguous()
+    z = mix_lse = mem_scale = None
+    if use_mem:
         z = F.linear(xf if xf is not None else x.float(), self.mix.weight.float(), self.mix.bias.float()).contiguous()
-    elif use_mem:
-        # write stream: token i - W is written before the query at position i reads (ext[:t] of the reference)
-        pp = torch.arange(start - w, start, device=dev)
-        idx = pp % w
-        vf = (st["ring_pos"][idx] == pp).float()[None, :, None]
-        wk = torch.cat((st["ring_km"][:, idx].float(), km), 1)[:, :t]
-        wv = torch.cat((st["ring_v"][:, :, idx].transpose(1, 2).float(), v.float()), 1)[:, :t]
-        wg = torch.cat((st["ring_g"][:, idx] * vf, g), 1)[:, :t]
-        wb = torch.cat((st["ring_beta"][:, idx] * vf, beta), 1)[:, :t]
-        o_mem, s_new = gdn_forward(qm.to(cdt).reshape(b * t, H, D), wk.to(cdt).reshape(b * t, G, D),
-                                   wv.to(cdt).reshape(b * t, G, D), wg.reshape(b * t, G), wb.reshape(b * t, G),
-                                   num_seqs=b, initial_state=None if s0 is None else s0.float(), out_dtype=cdt)
-        o_mem = o_mem.view(b, t, H, D)
-        z = F.linear(xf if xf is not None else x.float(), self.mix.weight.float(), self.mix.bias.float()).contiguous()
-    # window + sinks + LSE (+ mix)
-    q_ = qr.to(cdt)
-    q_ = q_ if q_.stride(-1) == 1 else q_.contiguous()
-    k_ = kr.to(cdt)
-    k_ = k_ if k_.stride(-1) == 1 else k_.contiguous()
-    v_ = v.to(cdt)
-    v_ = v_ if v_.stride(-1) == 1 else v_.contiguous()
-    rk, rv = st["ring_k"].to(cdt).contiguous(), st["ring_v"].to(cdt).contiguous()
+        mix_lse = self.mix_lse.float().contiguous()
+        mem_scale = self.mem_scale.float().contiguous()
+    mdt = lambda t_: t_.contiguous() if t_.dtype in (torch.float32, torch.bfloat16) else t_.to(cdt).contiguous()
+    qm_, km_ = mdt(qm), mdt(km)
+    g_, b_ = g.float().contiguous(), beta.float().contiguous()
+    unit = lambda t_: t_ if t_.stride(-1) == 1 else t_.contiguous()
+    q_, k_, v_ = unit(qr.to(cdt)), unit(kr.to(cdt)), unit(v.to(cdt))
     ns = 0 if sink_k is None else sink_k.size(2)
     sk = sink_k.to(cdt).contiguous() if ns else None
     sv = sink_v.to(cdt).contiguous() if ns else None
     o = torch.empty(b, t, H, D, dtype=torch.float32, device=dev)
-    lse = torch.empty(b, H, t, dtype=torch.float32, device=dev)
-    mix_lse = self.mix_lse.float().contiguous() if use_mem else None
-    mem_scale = self.mem_scale.float().contiguous() if use_mem else None
+    nbytes = _lib.ctypes.c_size_t(0)
+    check(lib.bf_layer_prefill_workspace_size(b, G, r, D, t, dtype_code(cdt), _lib.ctypes.byref(nbytes)),
+          "bf_layer_prefill_workspace_size")
+    ws = workspace(nbytes.value, dev)
     ptr = lambda t_: t_.data_ptr() if t_ is not None else None
-    check(lib.bf_window_fwd(b, G, r, D, t, w, self.sinks, start, dtype_code(cdt),
-                            ptr(q_), *_strides(q_, (0, 1, 2)), ptr(k_), *_strides(k_, (0, 1, 2)),
-                            ptr(v_), *_strides(v_, (0, 2, 1)), ptr(rk), ptr(rv), ptr(st["ring_pos"]), ptr(sk),
-                            ptr(sv), ns, int(use_mem), ptr(o_mem), dtype_code(o_mem.dtype if use_mem else cdt), ptr(z),
-                            ptr(mix_lse), ptr(mem_scale), ptr(o),
-                            dtype_code(torch.float32), ptr(lse), stream_ptr(dev)), "bf_window_fwd")
-    # cache write-back: the last min(t, W) tokens take their ring slots
-    n = min(t, w)
-    slot = pos[-n:] % w
-    st["ring_k"][:, :, slot] = kr[:, :, -n:].to(st["ring_k"].dtype)
-    st["ring_v"][:, :, slot] = v.transpose(1, 2)[:, :, -n:].to(st["ring_v"].dtype)
-    st["ring_km"][:, slot] = km[:, -n:].float()
-    st["ring_g"][:, slot] = g[:, -n:].float()
-    st["ring_beta"][:, slot] = beta[:, -n:].float()
-    st["ring_pos"][slot] = pos[-n:]
+    check(lib.bf_layer_prefill_fwd(
+        b, G, r, D, t, w, self.sinks, start, int(memory), dtype_code(cdt),
+        ptr(q_), *_strides(q_, (0, 1, 2)), ptr(k_), *_strides(k_, (0, 1, 2)), ptr(v_), *_strides(v_, (0, 2, 1)),
+        ptr(qm_), dtype_code(qm_.dtype), ptr(km_), dtype_code(km_.dtype), ptr(g_), ptr(b_), ptr(z), ptr(mix_lse),
+        ptr(mem_scale), ptr(sk), ptr(sv), ns, ptr(st["ring_k"]), ptr(st["ring_v"]), ptr(st["ring_km"]),
+        ptr(st["ring_g"]), ptr(st["ring_beta"]), ptr(st["ring_pos"]), ptr(S), valid, ptr(o), None, ptr(ws),
+        ws.numel(), stream_ptr(dev)), "bf_layer_prefill_fwd")
     if use_mem:
-        st["S"] = s_new
+        st["S"] = S
     return o
 
 

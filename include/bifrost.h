@@ -197,6 +197,29 @@ int bf_gated_norm(const void* o, int o_dtype, const void* z, const float* w, int
                   void* out, int io_dtype, void* stream);
 
 /*
+ * One prefill chunk of the converted layer: HybridAttention._student with t > 1 (Heimdall/heimdall/hibrit.py:363-424)
+ * on the student cache, in one call: the delta-rule write stream (the ring rows leaving the window, then the chunk's
+ * own rows; from an empty cache the chunk shifted by W), bf_gdn_fwd on it from the cached state, bf_window_fwd with
+ * the gamma mix (memory active when memory != 0 and start + T > W), then the write-back of the last min(T, W) tokens
+ * into the ring (slot = position mod W, ring_pos) and of the new state. qr, kr, v as bf_window_fwd (in_dtype, element
+ * strides); qm [B][T][H][D] and km [B][T][G][D] in qm_dtype / km_dtype (normalised, qm scaled by 1/sqrt(D)); g, beta
+ * [B][T][G] f32; z [B][T][H] f32 (mix logits); mix_lse, mem_scale [H]; sink_k / sink_v [B][G][n_sinks][D] already
+ * holding this chunk's sinks; ring_k / ring_v [B][G][W][D] in in_dtype, ring_km [B][W][G][D], ring_g / ring_beta
+ * [B][W][G], ring_pos [W], state [B][G][D][D] f32 (state_valid 0: no state yet) — all updated in place. o [B][T][H][D]
+ * f32, lse [B][H][T] f32 or null. Workspace from bf_layer_prefill_workspace_size, 256-byte aligned.
+ */
+int bf_layer_prefill_workspace_size(int B, int G, int R, int D, int T, int in_dtype, size_t* bytes);
+int bf_layer_prefill_fwd(int B, int G, int R, int D, int T, int W, int sinks, int64_t start, int memory, int in_dtype,
+                         const void* qr, int64_t q_sb, int64_t q_sh, int64_t q_st, const void* kr, int64_t k_sb,
+                         int64_t k_sh, int64_t k_st, const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st,
+                         const void* qm, int qm_dtype, const void* km, int km_dtype, const float* g,
+                         const float* beta, const float* z, const float* mix_lse, const float* mem_scale,
+                         const void* sink_k, const void* sink_v, int n_sinks, void* ring_k, void* ring_v,
+                         float* ring_km, float* ring_g, float* ring_beta, int64_t* ring_pos, float* state,
+                         int state_valid, float* o, float* lse, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/*
  * The llama.cpp per-sequence Bifrost state row (Heimdall/llamacpp/bifrost.patch:221-239, the views of
  * build_layer_bifrost :1000-1013) <-> the student cache (sink_k, sink_v, ring_k, ring_v, ring_km, ring_g, ring_beta,
  * ring_pos, S of HybridAttention._student, Heimdall/heimdall/hibrit.py:363-424), so a llama.cpp build and these

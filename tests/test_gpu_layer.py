@@ -95,3 +95,48 @@ def test_mem_inputs_bf16_fused_projection(dev, d):
     # rows are unit vectors times the scale
     nq = qm.float().norm(dim=-1).cpu()
     assert torch.allclose(nq, torch.full_like(nq, d ** -0.5), rtol=1e-2)
+
+
+@pytest.mark.parametrize("b", [1, 3])
+def test_fused_prefill_batch_bf16(dev, b):
+    """bf_layer_prefill_fwd over B sequences: a prefill from the empty cache past the window (the shifted write
+    stream; staged query and output rows when B > 1), a chunk whose stream starts in the ring, a decode token and a
+    chunk longer than the window, bf16 activations against the fp32 oracle; the final caches match."""
+    from heimdall_amd import hibrit
+    print(f"layer bf16 fused prefill B={b} H=6 G=2 D=128 W=16 S=2 chunks 20,7,1,40", flush=True)
+    m = make_core(6, 2, 128, 32, window=16, sinks=2)
+    mg = make_core(6, 2, 128, 32, window=16, sinks=2).to(dev)
+    args = make_inputs(m, b, 68, seed=14, dtype=torch.bfloat16)
+    argsf = tuple(z.float() for z in args)
+    c_ref, c_gpu, a = {}, {}, 0
+    with torch.no_grad():
+        for n in (20, 7, 1, 40):
+            o_ref = olayer.student(m, *split(argsf, a, a + n), a, c_ref)
+            o = hibrit.student(mg, *to_dev(split(args, a, a + n), dev), a, c_gpu)
+            print(f"  chunk {a}:{a + n} rel err {rel(o, o_ref):.2e}", flush=True)
+            assert rel(o, o_ref) < TOL_BF16
+            a += n
+    compare_caches(c_ref, c_gpu, TOL_BF16)
+
+
+def test_fused_prefill_mixed_memory_dtype(dev):
+    """fp32 memory inputs (qm, km) with bf16 window inputs: the library converts the memory rows to the compute
+    dtype (the query and stream kernels) instead of reading them in place; same result as all-bf16 inputs to
+    bf16 rounding."""
+    from heimdall_amd import hibrit
+    print("layer fused prefill fp32 qm/km with bf16 q/k/v, B=1 H=4 G=2 D=64 W=8", flush=True)
+    m = make_core(4, 2, 64, 32, window=8, sinks=2)
+    mg = make_core(4, 2, 64, 32, window=8, sinks=2).to(dev)
+    x, q, k, v, qr, kr = to_dev(make_inputs(m, 1, 40, seed=15, dtype=torch.bfloat16), dev)
+    pos = torch.arange(40, device=dev)
+    with torch.no_grad():
+        qm, km, g, beta = mg._mem_inputs(x.float(), q.float(), k.float(), pos)
+        outs = []
+        for mem_dt in (torch.float32, torch.bfloat16):
+            st = {}
+            st.update(hibrit._new_ring(1, 2, 8, 64, torch.bfloat16, torch.bfloat16, dev))
+            o = hibrit._prefill(mg, x, qr, kr, v, qm.to(mem_dt), km.to(mem_dt), g, beta, 0, st, kr[:, :, :2],
+                                v.transpose(1, 2)[:, :, :2], True)
+            outs.append((o, st["S"]))
+    assert rel(outs[0][0], outs[1][0]) < TOL_BF16
+    assert rel(outs[0][1], outs[1][1]) < TOL_BF16

@@ -144,6 +144,16 @@ __device__ __forceinline__ void transpose_block<BF16>(uint4 (&r)[8]) {
 // first iteration consumes loads issued ahead of it, so the compiler's wait analysis at the loop header starts clean.
 __device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// Workgroup barrier that orders LDS accesses only. __syncthreads() is a workgroup fence over every address space, and
+// the fence waits for all of the wave's outstanding global loads and stores (vmcnt(0)), which puts the latency of a
+// prefetch issued earlier on the path of every barrier. This barrier waits for the wave's LDS operations only; loads
+// into LDS by DMA (buffer_load ... lds) are vector-memory operations and still need wait_vmem_all() before it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (WAVE - 1); }
 // Wave index inside the workgroup, marked wave-uniform (readfirstlane) so that values derived from it (buffer
 // descriptors, LDS bases, loop bounds) live in SGPRs; plain threadIdx.x / 64 is treated as divergent and descriptors

@@ -145,14 +145,11 @@ __device__ __forceinline__ void transpose_block<BF16>(uint4 (&r)[8]) {
 __device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Workgroup barrier that orders LDS accesses only. __syncthreads() is a workgroup fence over every address space, and
-// the fence waits for all of the wave's outstanding global loads and stores (vmcnt(0)), which puts the latency of a
-// prefetch issued earlier on the path of every barrier. This barrier waits for the wave's LDS operations only; loads
-// into LDS by DMA (buffer_load ... lds) are vector-memory operations and still need wait_vmem_all() before it.
-__device__ __forceinline__ void lds_barrier() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
+// the fence waits for all of the wave's outstanding global loads and stores (vmcnt(0)), and an LDS-only fence still
+// waits for loads into LDS by DMA (buffer_load ... lds), which puts the latency of a prefetch issued earlier on the
+// path of every barrier. This barrier waits for the wave's LDS operations only (the memory clobber keeps the compiler
+// from moving memory accesses across it). A DMA load whose LDS data is read after it still needs wait_vmem_all().
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (WAVE - 1); }
 // Wave index inside the workgroup, marked wave-uniform (readfirstlane) so that values derived from it (buffer

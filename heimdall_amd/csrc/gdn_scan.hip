@@ -435,7 +435,7 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
         }
         if constexpr (QL) {
             if (prefetch) {
-                __syncthreads();                   // every wave is done with q of this chunk
+                lds_barrier();                     // every wave is done with q of this chunk (its LDS reads)
                 load_q(cn);
             }
         }

@@ -687,14 +687,22 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
 }
 
 // ------------------------------------------------------------------------------------------------ segment combine
-// One workgroup per (sequence, KV head, 16-column strip), 4 waves; wave w produces row tiles w*NTD/4 ..
-// (w+1)*NTD/4 - 1 of X_{p+1} = c_p X_p + Psi_p X_p + N_p (Psi_p = Phi_p - c_p I). The pure-decay part c_p X_p is exact
+// One workgroup per (sequence, KV head, 16-column strip), NW waves; wave w produces row tiles w*NTD/NW ..
+// (w+1)*NTD/NW - 1 of X_{p+1} = c_p X_p + Psi_p X_p + N_p (Psi_p = Phi_p - c_p I). The pure-decay part c_p X_p is exact
 // fp32; Psi_p X_p is an MFMA with Psi_p in in_dtype and, for bf16, X split into bf16 high and low parts. X^T is shared
 // through LDS between steps. bf16 prefetches the next step's Psi fragments, N and c while a step computes.
+// Waves per combine workgroup: 4 (one per SIMD, up to 512 registers); at D = 256, 8 (two per SIMD, 2 row tiles
+// each, 176 registers), so one wave's loads and LDS exchange overlap the other's MFMAs: 64 -> 60 us per launch at
+// T = 32768, H = 4.
+constexpr int kCombineWaves256 = 8;
+template <int D>
+constexpr int combine_waves() { return D == 256 ? kCombineWaves256 : 4; }
+
 template <class E, int D>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void gdn_combine_kernel(GdnArgs a) {
+__global__ __launch_bounds__(64 * combine_waves<D>())
+__attribute__((amdgpu_waves_per_eu(combine_waves<D>() / 4, combine_waves<D>() / 4))) void gdn_combine_kernel(GdnArgs a) {
     using T = typename E::T;
-    constexpr int VEC = E::VEC, KF = E::KF, NTD = D / 16, NKD = D / KF, TPW = NTD / 4;
+    constexpr int VEC = E::VEC, KF = E::KF, NTD = D / 16, NKD = D / KF, TPW = NTD / combine_waves<D>();
     constexpr bool DBUF = E::VEC == 8;
     __shared__ __align__(16) float XT[16][D + 4];
     // XCD-aware mapping: all strips of one (sequence, KV head) read the same Psi, so they go to one XCD (one L2)
@@ -895,7 +903,8 @@ int launch_states(const GdnArgs& a, hipStream_t stream, bool summary, bool combi
     }
     if (!combine) return 0;
     const int groups = a.num_seqs * a.G;
-    hipLaunchKernelGGL((gdn_combine_kernel<E, D>), dim3(NXCD * ((groups + NXCD - 1) / NXCD) * (D / 16)), dim3(256), 0,
+    hipLaunchKernelGGL((gdn_combine_kernel<E, D>), dim3(NXCD * ((groups + NXCD - 1) / NXCD) * (D / 16)),
+                       dim3(64 * combine_waves<D>()), 0,
                        stream, a);
     return (int)hipGetLastError();
 }

@@ -364,13 +364,42 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
         }
     };
 
-    auto compute = [&](const CL& cl, int c, bool prefetch) {
+    // next: the idle stage buffer, loaded with chunk cn by DMA once this chunk's V fragments are in registers. The
+    // compiler waits for every outstanding DMA before a transposing LDS read (ds_read_b64_tr_b16), so the V reads
+    // come first and the copy then overlaps phases 1 to 3 instead of phase 1 only.
+    auto compute = [&](const CL& cl, int c, bool prefetch, CL* next) {
         const int cn = c + 1 < count ? c + 1 : c;
         const char* Kb = reinterpret_cast<const char*>(cl.K);
         const char* Tb = reinterpret_cast<const char*>(cl.Tp);
         const char* Ab = reinterpret_cast<const char*>(cl.At);
         const char* Qb = reinterpret_cast<const char*>(ol.Q);
         const char* Vb = reinterpret_cast<const char*>(ol.V);
+        uint4 vf[NKC][NJ];
+        auto read_vf = [&]() {
+#pragma unroll
+        for (int ks = 0; ks < NKC; ++ks)
+#pragma unroll
+            for (int jt = 0; jt < NJ; ++jt) {
+                if constexpr (ES == 2) {
+                    const uint2 lo = lds_tr16(Vb + vtb[jt] + 32 * ks * VROWB);
+                    const uint2 hi = lds_tr16(Vb + vtb[jt] + (32 * ks + 4) * VROWB);
+                    vf[ks][jt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                } else {
+                    // element (token t, tile column cv) of the swizzled V tile
+                    const int cv = wv * WCOLS + 16 * jt + l16;
+                    uint32_t w[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int t = KF * ks + VEC * lg + e;
+                        w[e] = *reinterpret_cast<const uint32_t*>(
+                            Vb + t * VROWB + (((cv >> 2) ^ swz_v(t, VROWB / 16)) << 4) + (cv & 3) * 4);
+                    }
+                    vf[ks][jt] = make_uint4(w[0], w[1], w[2], w[3]);
+                }
+            }
+        };
+        if constexpr (DBUF) read_vf();                  // single-buffered runs read V in phase 2 (fewer live registers)
+        if (next) load_chunk(*next, cn);
         const float glast = cl.gc[SC - 1];
         const float decay = __expf(glast);
         float egc[NTC][4];                        // sc e^{gc} of the accumulator rows
@@ -440,33 +469,14 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
             }
         }
 
-        // phase 2: v_new = T' (V - e^{gc} K S) = T' V + T' (-sc e^{gc} Y). All T' and V fragments of the chunk are read
-        // first, so their LDS latency is covered by the scaling of Y.
-        uint4 tf[NKC][NTC], vf[NKC][NJ];
+        // phase 2: v_new = T' (V - e^{gc} K S) = T' V + T' (-sc e^{gc} Y). The T' fragments (and, single-buffered,
+        // the V fragments) are read first, so their LDS latency is covered by the scaling of Y.
+        uint4 tf[NKC][NTC];
 #pragma unroll
-        for (int ks = 0; ks < NKC; ++ks) {
+        for (int ks = 0; ks < NKC; ++ks)
 #pragma unroll
             for (int tt = 0; tt < NTC; ++tt) tf[ks][tt] = lds16(Tb, t_base[ks & 1] + tpart<E>(tt) * TROWB + 128 * (ks >> 1));
-#pragma unroll
-            for (int jt = 0; jt < NJ; ++jt) {
-                if constexpr (ES == 2) {
-                    const uint2 lo = lds_tr16(Vb + vtb[jt] + 32 * ks * VROWB);
-                    const uint2 hi = lds_tr16(Vb + vtb[jt] + (32 * ks + 4) * VROWB);
-                    vf[ks][jt] = make_uint4(lo.x, lo.y, hi.x, hi.y);
-                } else {
-                    // element (token t, tile column cv) of the swizzled V tile
-                    const int cv = wv * WCOLS + 16 * jt + l16;
-                    uint32_t w[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int t = KF * ks + VEC * lg + e;
-                        w[e] = *reinterpret_cast<const uint32_t*>(
-                            Vb + t * VROWB + (((cv >> 2) ^ swz_v(t, VROWB / 16)) << 4) + (cv & 3) * 4);
-                    }
-                    vf[ks][jt] = make_uint4(w[0], w[1], w[2], w[3]);
-                }
-            }
-        }
+        if constexpr (!DBUF) read_vf();
         f32x4 Vn[NTC][NJ];
 #pragma unroll
         for (int tt = 0; tt < NTC; ++tt)
@@ -627,15 +637,14 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
             wait_vmem_all();
             __syncthreads();
             for (int c = 0;;) {
-                // the next chunk's stage is loaded unconditionally (the last chunk re-loads itself into the idle
-                // buffer): a conditional load would make the wait counts drain it before the current chunk
-                load_chunk(cl1, c + 1 < count ? c + 1 : c);
-                compute(cl0, c, true);
+                // the next chunk's stage is loaded unconditionally inside compute (the last chunk re-loads itself
+                // into the idle buffer): a conditional load would make the wait counts drain it before the current
+                // chunk
+                compute(cl0, c, true, &cl1);
                 wait_vmem_all();
                 __syncthreads();
                 if (++c >= count) break;
-                load_chunk(cl0, c + 1 < count ? c + 1 : c);
-                compute(cl1, c, true);
+                compute(cl1, c, true, &cl0);
                 wait_vmem_all();
                 __syncthreads();
                 if (++c >= count) break;
@@ -646,7 +655,7 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
                 load_v(c);
                 wait_vmem_all();
                 __syncthreads();
-                compute(cl0, c, false);
+                compute(cl0, c, false, nullptr);
                 __syncthreads();
             }
         }

@@ -1,13 +1,19 @@
 #!/usr/bin/env python3
 """Benchmark of the Bifrost core on one MI355X.
 
-Headline workload (one step = one pass of the hot path over one batch of synthetic input):
-  chunked gated delta-rule prefill, B=1, T=32768, H=4 (one state per head), D_k=D_v=256, chunk 64,
-  bf16 q/k/v (k L2-normalised, q unscaled, scale 1), beta = sigmoid(N(0,1)), g ~ U[-1e-3, 0], fp32 state and
-  accumulation, zero initial state; outputs o [1, T, 4, 256] fp32 and the final 4 x 256 x 256 fp32 state.
-  Inputs are resident in HBM before the timed region. value = tokens/s.
+Headline workload (one step = one pass of the hot path over one batch of synthetic input): the converted (Bifrost)
+layer's prefill at 32K, i.e. ``_student`` over a 32768-token chunk from an empty cache: B=1, T=32768, H=24 query
+heads, G=4 KV heads, D=256, window 2048 + 4 sinks, bf16 activations, fp32 delta-rule state; per-KV-head decay
+half-lives {2048, 45255, 1e6} tokens plus one archival head, beta = sigmoid(N(0,1)), gamma = sigmoid(N(0,1)); the
+memory branch receives writes from token 2052 on. Inputs are resident in HBM before the timed region. value =
+tokens/s of the whole call (memory-branch projections and gates, delta rule, window attention with the gamma mix,
+ring and state write-back).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+roofline: the dominant kernel, the window attention (window_fa_kernel), priced on its algorithmic work
+4 D FLOP per visible (query, key) pair and query head, over its average launch duration measured with HIP events
+on the launch stream with the layer's own arguments.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra] [--only LEG]
 Prints ONE JSON line. Only one GPU is supported (--gpus > 1 exits with a message).
 """
 import argparse
@@ -201,19 +207,6 @@ def cpu_decode(B=8):
                 f"oracle layer.student decode step fp32, B={B} of 64, H=16 G=4 D=256 W=2048+4")
 
 
-def cpu_layer(T=4096):
-    """The oracle's student prefill (fp32) from an empty cache on the first T = 4096 tokens of the layer leg's
-    geometry (H=24, G=4, D=256, W=2048 + 4 sinks; the memory is active after token 2048)."""
-    H, G, D, W, S, d = 24, 4, 256, 2048, 4, 1024
-    ol, m = _oracle_layer(H, G, D, d, W, S)
-    rn = lambda *s: torch.randn(*s)
-    x, q = rn(1, T, d), rn(1, T, H, D)
-    k, v = F.normalize(rn(1, T, G, D), dim=-1), rn(1, T, G, D)
-    qr, kr = F.normalize(rn(1, H, T, D), dim=-1), F.normalize(rn(1, G, T, D), dim=-1)
-    return _cpu(T, lambda: ol.student(m, x, q, k, v, qr, kr, 0, {}), "tokens/s",
-                f"oracle layer.student prefill fp32, T={T} of the T=32768 workload, H=24 G=4 D=256 W=2048+4")
-
-
 def cpu_varlen(n=8192):
     """The oracle's per-sequence delta rule (fp32) on two packed sequences of n / 2 tokens, H=32, D=128."""
     from oracle import gdn
@@ -306,10 +299,11 @@ def run_decode(steps, warmup, dev):
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(torch.cuda.current_stream(dev))
-    for _ in range(steps):
-        lib.bf_decode_fwd(*args)
+    rcs = [lib.bf_decode_fwd(*args) for _ in range(steps)]
     e1.record(torch.cuda.current_stream(dev))
     torch.cuda.synchronize()
+    for rc in rcs:
+        _lib.check(rc, "bf_decode_fwd")
     us = e0.elapsed_time(e1) * 1e3 / steps
     # algorithmic bytes: state read + write, full ring K and V read (W slots) + sinks + new row, queries, outputs
     nbytes = (B * G * D * D * 4 * 2 + B * G * (W + S + 1) * D * 2 * 2 + B * H * D * (2 + 4 + 4)
@@ -319,11 +313,6 @@ def run_decode(steps, warmup, dev):
             "steps": steps, "roofline": {"bound": "hbm", "kernel": "decode_main_kernel+decode_combine_kernel",
                                          "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                          "frac": gbs / HBM_PEAK_GBS, "bytes_per_step": nbytes}}
-
-
-def window_pairs(T, W, S):
-    """Visible (query, key) pairs per head over positions 0..T-1: min(p + 1, W + S) each."""
-    return sum(min(p + 1, W + S) for p in range(T))
 
 
 def run_varlen(steps, warmup, dev):
@@ -643,83 +632,190 @@ def run_llama_state(steps, warmup, dev):
                          "frac": res["pack"]["frac"], "kernel": "bf_llama_state_pack (region, V plane, delta kernels)"}}
 
 
-def run_window(steps, warmup, dev, T=32768):
-    """The window kernel alone on the layer prefill's shapes (B=1, H=24, G=4, D=256, W=2048 + 4 sinks, bf16, from
-    position 0 with the first 4 tokens as sinks, no ring, no mix): bf_window_fwd timed with HIP events on the launch
-    stream. Algorithmic work: 4 D FLOP per visible (query, key) pair and query head."""
+LAYER_GEOM = dict(B=1, H=24, G=4, D=256, W=2048, S=4)
+LIVES = (2048.0, 45255.0, 1e6, None)        # decay half-lives of KV heads 0-2 in tokens; head 3 archival
+
+
+def window_pairs(T, W, S):
+    """Visible (query, key) pairs per head over positions 0..T-1: min(p + 1, W + S) each."""
+    return sum(min(p + 1, W + S) for p in range(T))
+
+
+def layer_flops(T, H, G, D, W, S):
+    """Algorithmic work of one layer prefill call from an empty cache (T tokens): the window, 4 D FLOP per visible
+    (query, key) pair and query head; the memory branch in GQA form (chunked, C = 64), G (6 C D + 4 D^2) + H (4 C D +
+    2 D^2) FLOP per token; the D x D projections of the memory inputs, (H + G) 2 D^2 FLOP per token."""
+    win = 4 * D * window_pairs(T, W, S) * H
+    mem = T * (G * (6 * C * D + 4 * D * D) + H * (4 * C * D + 2 * D * D))
+    proj = T * (H + G) * 2 * D * D
+    return {"window": win, "memory": mem, "projections": proj, "total": win + mem + proj}
+
+
+def layer_core(H, G, D, W, S, lives, dev):
+    """A converted core whose gates reproduce the workload's distributions through its own parameters: d_model =
+    G + H with x = [z_beta | z_gamma]; ab selects z_beta for the write strengths (the decay logits are 0), mix selects
+    z_gamma (mix_lse = 0), so beta = sigmoid(z_beta) and gamma = sigmoid(z_gamma); fq = fk = I; mem_scale = sqrt(D);
+    constant log-decay -ln2 / life per KV head (decay_mask 0 where life is None: the archival head)."""
+    import math
+    from heimdall_amd import hibrit
+    m = hibrit.BifrostCore(hibrit.CoreConfig(H, G, D, G + H))
+    m.convert(W, S, 0)
+    with torch.no_grad():
+        m.ab.weight.zero_()
+        m.ab.bias.zero_()
+        m.ab.weight[G:, :G] = torch.eye(G)
+        m.mix.weight.zero_()
+        m.mix.bias.zero_()
+        m.mix.weight[:, G:] = torch.eye(H)
+        sp = F.softplus(m.dt_bias)
+        for h, life in enumerate(lives):
+            if life is not None:
+                m.A_log[h] = math.log(math.log(2.0) / life) - math.log(sp[h].item())
+        m.decay_mask.copy_(torch.tensor([0.0 if life is None else 1.0 for life in lives]))
+    return m.to(dev)
+
+
+def layer_inputs(B, T, H, G, D, dev, seed=2):
+    """q, k ~ N(0,1) L2-normalised per head, v ~ N(0,1) (bf16), z_beta, z_gamma ~ N(0,1); qr = q, kr = k (the window
+    reads the same unit vectors; no rotary part)."""
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    rn = lambda *shape: torch.randn(*shape, device=dev, generator=gen)
+    q = F.normalize(rn(B, T, H, D), dim=-1).bfloat16()
+    k = F.normalize(rn(B, T, G, D), dim=-1).bfloat16()
+    v = rn(B, T, G, D).bfloat16()
+    x = torch.cat((rn(B, T, G), rn(B, T, H)), -1)
+    return x, q, k, v, q.transpose(1, 2).contiguous(), k.transpose(1, 2).contiguous()
+
+
+def time_window_in_layer(m, args, steps, warmup, dev):
+    """The window kernel with the arguments the layer call gives it (bf16 operands with their layer strides, the
+    first S tokens as sinks, the empty ring, the gamma mix against a bf16 memory read, fp32 output): the average
+    launch duration over `steps` launches, HIP events on the launch stream."""
     from heimdall_amd import _lib
     from heimdall_amd._device import stream_ptr
 
-    B, H, G, D, W, S = 1, 24, 4, 256, 2048, 4
-    gen = torch.Generator(device=dev).manual_seed(3)
-    qr = F.normalize(torch.randn(B, H, T, D, device=dev, generator=gen), dim=-1).bfloat16()
-    kr = F.normalize(torch.randn(B, G, T, D, device=dev, generator=gen), dim=-1).bfloat16()
-    v = torch.randn(B, T, G, D, device=dev, generator=gen).bfloat16()
+    x, q, k, v, qr, kr = args
+    B, T, H, D = q.shape
+    G = k.shape[2]
+    W, S = m.window, m.sinks
     sk, sv = kr[:, :, :S].contiguous(), v.transpose(1, 2)[:, :, :S].contiguous()
+    ring_k = torch.zeros(B, G, W, D, dtype=torch.bfloat16, device=dev)
+    ring_v = torch.zeros_like(ring_k)
+    ring_pos = torch.full((W,), -1, dtype=torch.long, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(9)
+    o_mem = torch.randn(B, T, H, D, device=dev, generator=gen).bfloat16()
+    z = F.linear(x, m.mix.weight, m.mix.bias).contiguous()
+    mix_lse, mem_scale = m.mix_lse.detach().float().contiguous(), m.mem_scale.detach().float().contiguous()
     o = torch.empty(B, T, H, D, dtype=torch.float32, device=dev)
-    lse = torch.empty(B, H, T, dtype=torch.float32, device=dev)
     lib = _lib.load()
     st = lambda t_, dims: tuple(int(t_.stride(i)) for i in dims)
-    args = (B, G, H // G, D, T, W, S, 0, _lib.DTYPE_BF16, qr.data_ptr(), *st(qr, (0, 1, 2)), kr.data_ptr(),
-            *st(kr, (0, 1, 2)), v.data_ptr(), *st(v, (0, 2, 1)), None, None, None, sk.data_ptr(), sv.data_ptr(), S, 0,
-            None, 0, None, None, None, o.data_ptr(), _lib.DTYPE_F32, lse.data_ptr(), stream_ptr(dev))
+    wargs = (B, G, H // G, D, T, W, S, 0, _lib.DTYPE_BF16, qr.data_ptr(), *st(qr, (0, 1, 2)), kr.data_ptr(),
+             *st(kr, (0, 1, 2)), v.data_ptr(), *st(v, (0, 2, 1)), ring_k.data_ptr(), ring_v.data_ptr(),
+             ring_pos.data_ptr(), sk.data_ptr(), sv.data_ptr(), S, 1, o_mem.data_ptr(), _lib.DTYPE_BF16, z.data_ptr(),
+             mix_lse.data_ptr(), mem_scale.data_ptr(), o.data_ptr(), _lib.DTYPE_F32, None, stream_ptr(dev))
     for _ in range(warmup):
-        _lib.check(lib.bf_window_fwd(*args), "bf_window_fwd")
+        _lib.check(lib.bf_window_fwd(*wargs), "bf_window_fwd")
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
-    for _ in range(steps):
-        lib.bf_window_fwd(*args)
+    rcs = [lib.bf_window_fwd(*wargs) for _ in range(steps)]
     e1.record(stream)
     torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / steps
-    flops = 4 * D * window_pairs(T, W, S) * H
-    tf = flops / (us * 1e-6) / 1e12
-    return {"kernel": "window_fa_kernel<256>", "us": us, "flops": flops,
-            "roofline": {"bound": "mfma", "achieved": tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                         "frac": tf / BF16_PEAK_TFLOPS}}
+    for rc in rcs:
+        _lib.check(rc, "bf_window_fwd")
+    return e0.elapsed_time(e1) * 1e3 / steps
 
 
-def run_layer(steps, warmup, dev, T=32768):
-    """Full converted-layer prefill at 32K: B=1, T=32768, H=24, G=4, D=256, W=2048 + 4 sinks, bf16 activations,
-    fp32 state; x/q/k/v/qr/kr synthetic (q, k L2-normalised), init-time gates (fq = fk = I). One step =
-    heimdall_amd.hibrit.student over the whole chunk from an empty cache (memory branch, window, mix, cache)."""
+def run_layer(steps, warmup, dev, T=32768, window_pass=True):
+    """The converted layer's prefill over T tokens from an empty cache: heimdall_amd.hibrit.student (the _student
+    drop-in), B=1, H=24, G=4, D=256, W=2048 + 4 sinks, bf16 activations, fp32 state. Timed region: `steps` whole
+    calls bracketed by device synchronisation. Then the window kernel alone with the layer's arguments for its
+    roofline."""
     from heimdall_amd import hibrit
 
-    B, H, G, D, W, S, d = 1, 24, 4, 256, 2048, 4, 1024
-    torch.manual_seed(0)
-    m = hibrit.BifrostCore(hibrit.CoreConfig(H, G, D, d))
-    m.convert(W, S, 1)
-    m = m.to(dev)
-    gen = torch.Generator(device=dev).manual_seed(2)
-    rn = lambda *shape: torch.randn(*shape, device=dev, generator=gen)
-    x = rn(B, T, d).bfloat16()
-    q = F.normalize(rn(B, T, H, D), dim=-1).bfloat16()
-    k = F.normalize(rn(B, T, G, D), dim=-1).bfloat16()
-    v = rn(B, T, G, D).bfloat16()
-    qr, kr = q.transpose(1, 2).contiguous(), k.transpose(1, 2).contiguous()
-
-    def step():
-        return hibrit.student(m, x, q, k, v, qr, kr, 0, {})
-
+    g_ = LAYER_GEOM
+    B, H, G, D, W, S = g_["B"], g_["H"], g_["G"], g_["D"], g_["W"], g_["S"]
+    m = layer_core(H, G, D, W, S, LIVES, dev)
+    args = layer_inputs(B, T, H, G, D, dev)
     with torch.no_grad():
         for _ in range(warmup):
-            step()
+            hibrit.student(m, *args, 0, {})
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(steps):
-            step()
+            hibrit.student(m, *args, 0, {})
         torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / steps
-    pairs = window_pairs(T, W, S)
-    win_flops = 4 * D * pairs * H
-    chunks = T // C
-    mem_flops = chunks * G * (8 * C * C * D + 6 * C * D * D + 2 * C * C * D) + chunks * (H - G) * (
-        4 * C * D * D + 4 * C * C * D)
-    return {"workload": f"layer prefill B=1 T={T} H=24 G=4 D=256 W=2048+4 bf16", "ms_per_step": ms,
-            "tokens_per_s": T / (ms * 1e-3), "steps": steps, "flops": {"window": win_flops, "memory": mem_flops},
-            "tflops": (win_flops + mem_flops) / (ms * 1e-3) / 1e12}
+        wall = time.perf_counter() - t0
+    ms = wall * 1e3 / steps
+    fl = layer_flops(T, H, G, D, W, S)
+    out = {"workload": f"layer prefill B={B} T={T} H={H} G={G} D={D} W={W}+{S} bf16 activations, fp32 state",
+           "T": T, "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3), "steps": steps, "flops": fl,
+           "tflops": fl["total"] / (ms * 1e-3) / 1e12,
+           "mfma_frac_whole_call": fl["total"] / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
+    if window_pass:
+        with torch.no_grad():
+            us = time_window_in_layer(m, args, max(steps, 10), max(warmup // 2, 3), dev)
+        tf = fl["window"] / (us * 1e-6) / 1e12
+        out["roofline"] = {"bound": "mfma", "kernel": "window_fa_kernel<256>", "achieved": tf,
+                           "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": tf / BF16_PEAK_TFLOPS,
+                           "traffic": traffic_from_profile("window_fa_kernel"), "launch_us": us,
+                           "flops_per_launch": fl["window"]}
+    return out, (m, args)
+
+
+def cpu_layer(m, args, budget_s=40.0):
+    """The oracle's student prefill (fp32 PyTorch restatement of _student, all host cores) on the headline's own
+    inputs and parameters (copied to the host): the whole 32768-token call when a 4096-token probe predicts it fits
+    the budget, else the longest power-of-two prefix that does."""
+    import copy
+    from oracle import layer as ol
+
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    mc = copy.deepcopy(m).cpu().float()
+    x, q, k, v, qr, kr = (z.detach().float().cpu() for z in args)
+    T = x.shape[1]
+    sl = lambda n: (x[:, :n], q[:, :n], k[:, :n], v[:, :n], qr[:, :, :n], kr[:, :, :n])
+    with torch.no_grad():
+        t = time.perf_counter()
+        ol.student(mc, *sl(4096), 0, {})
+        per_4k = time.perf_counter() - t
+        n = T
+        while n > 4096 and per_4k * n / 4096 * 1.2 > budget_s:
+            n //= 2
+        t = time.perf_counter()
+        ol.student(mc, *sl(n), 0, {})
+        dt = time.perf_counter() - t
+    return {"value": n / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle layer.student fp32 prefill from an empty cache on the first {n} of the {T} tokens of "
+                      f"the same inputs (H=24 G=4 D=256 W=2048+4), one run after a 4096-token warm-up, "
+                      f"{cpu_model()}"}
+
+
+def gdn_leg(steps, warmup, dev, cpu):
+    """Standalone chunked delta-rule prefill (B=1, T=32768, H=4, D=256, bf16 q/k/v, fp32 state and output), priced
+    as an HBM-bound pass over its algorithmic bytes (bf16 q, k, v; fp32 g, beta, o, final state) and, for its
+    contraction phases, against the reference algorithm's FLOPs on bf16 MFMA."""
+    r = run_gdn(steps, warmup, dev)
+    T, H, D = r["T"], r["H"], r["D"]
+    ms = r["wall"] * 1e3 / steps
+    nbytes, ref_f = gdn_bytes(T, H, D), reference_flops(T, H, D)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    pm = r["phase_ms"]
+    kf = gdn_kernel_flops(T, H, 1, D, r["L"])
+    out = {"workload": f"chunked gated delta rule B=1 T={T} H={H} D={D} bf16 in, fp32 state/output",
+           "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3), "steps": steps, "segment_chunks": r["L"],
+           "roofline": {"bound": "hbm", "kernel": "bf_gdn_fwd (prep, summary, combine, output)", "achieved": gbs,
+                        "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                        "algorithmic_bytes": nbytes},
+           "mfma_reference_flops": {"flops": ref_f, "achieved": ref_f / (ms * 1e-3) / 1e12, "peak": BF16_PEAK_TFLOPS,
+                                    "unit": "TFLOP/s", "frac": ref_f / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS},
+           "phases_ms": pm, "phased_step_ms": sum(pm.values()),
+           "kernel_tflops_own_flops": {k_: kf[k_] / (pm[k_] * 1e-3) / 1e12 for k_ in PHASES},
+           "traffic": {k_: traffic_from_profile("gdn_" + k_) for k_ in PHASES}}
+    if cpu:
+        out["cpu_baseline"] = cpu_baseline(r["inputs"])
+    return out
 
 
 def main():
@@ -727,11 +823,10 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--no-extra", action="store_true", help="skip the decode and layer-prefill legs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--no-extra", action="store_true", help="the headline only (no secondary legs)")
     ap.add_argument("--copy-probe", action="store_true", help="run one 256 MiB device copy first (counter scaling)")
-    ap.add_argument("--segment-chunks", type=int, default=0, help="chunks per scan segment (0 = library default)")
-    ap.add_argument("--only", choices=("decode", "layer", "layer131k", "window", "varlen", "gdn_layer", "teacher",
+    ap.add_argument("--only", choices=("layer", "layer131k", "gdn", "decode", "varlen", "gdn_layer", "teacher",
                                        "teacher_decode", "teacher_decode_full", "gdn_bwd", "llama_state"),
                     default=None,
                     help="run one secondary leg alone and print its JSON object (for per-workload profiling)")
@@ -751,10 +846,10 @@ def main():
         del src, dst
 
     if args.only:
-        leg = {"decode": lambda: run_decode(args.steps, args.warmup, dev),
-               "layer": lambda: run_layer(args.steps, args.warmup, dev),
-               "layer131k": lambda: run_layer(args.steps, args.warmup, dev, T=131072),
-               "window": lambda: run_window(args.steps, args.warmup, dev),
+        leg = {"layer": lambda: run_layer(args.steps, args.warmup, dev)[0],
+               "layer131k": lambda: run_layer(args.steps, args.warmup, dev, T=131072)[0],
+               "gdn": lambda: gdn_leg(args.steps, args.warmup, dev, not args.no_cpu),
+               "decode": lambda: run_decode(args.steps, args.warmup, dev),
                "varlen": lambda: run_varlen(args.steps, args.warmup, dev),
                "gdn_layer": lambda: run_gdn_layer(args.steps, args.warmup, dev),
                "teacher": lambda: run_teacher(args.steps, args.warmup, dev),
@@ -765,58 +860,46 @@ def main():
         print(json.dumps(leg()), flush=True)
         return
 
-    r = run_gdn(args.steps, args.warmup, dev, args.segment_chunks)
-    T, H, D, L = r["T"], r["H"], r["D"], r["L"]
-    ms = r["wall"] * 1e3 / args.steps
-    pm = r["phase_ms"]
-    kf = gdn_kernel_flops(T, H, 1, D, L)
-    dominant = max(pm, key=pm.get)                 # the kernel with the largest share of the step
-    achieved = kf[dominant] / (pm[dominant] * 1e-3) / 1e12
-    kernels = {"prep": "gdn_prep_kernel", "summary": "gdn_seg_kernel (segment summary)",
-               "combine": "gdn_combine_kernel", "output": "gdn_seg_kernel (output scan)"}
-    ref_f = reference_flops(T, H, D)
+    r, (m, inputs) = run_layer(args.steps, args.warmup, dev)
+    g_ = LAYER_GEOM
     line = {
         "metric": METRIC,
-        "value": T / (ms * 1e-3),
+        "value": r["tokens_per_s"],
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": ms,
+        "ms_per_step": r["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic",
-        "config": {"workload": "gdn_prefill", "B": 1, "T": T, "H": H, "G": H, "D": D, "chunk": C,
-                   "segment_chunks": L, "inputs": "bf16 q/k/v, fp32 g/beta/state/output",
+        "config": {"workload": "layer_prefill", "B": g_["B"], "T": r["T"], "H": g_["H"], "G": g_["G"],
+                   "D": g_["D"], "window": g_["W"], "sinks": g_["S"], "chunk": C,
+                   "inputs": "bf16 activations, fp32 delta-rule state, decay half-lives 2048/45255/1e6 + archival",
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "mfma", "kernel": kernels[dominant], "achieved": achieved,
-                     "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": achieved / BF16_PEAK_TFLOPS,
-                     "traffic": traffic_from_profile("gdn_" + dominant)},
-        "phases_ms": pm,
-        "phased_step_ms": sum(pm.values()),
-        "kernel_tflops": {k_: kf[k_] / (pm[k_] * 1e-3) / 1e12 for k_ in PHASES},
-        "operator": {"reference_flops": ref_f, "tflops": ref_f / (ms * 1e-3) / 1e12,
-                     "algorithmic_bytes": gdn_bytes(T, H, D),
-                     "achieved_GBs": gdn_bytes(T, H, D) / (ms * 1e-3) / 1e9, "peak_GBs": HBM_PEAK_GBS},
+        "roofline": r["roofline"],
+        "layer_flops": r["flops"],
+        "layer_tflops": r["tflops"],
+        "mfma_frac_whole_call": r["mfma_frac_whole_call"],
     }
     if not args.no_extra:
-        line["decode"] = run_decode(100, 50, dev)
-        line["layer_prefill_32k"] = run_layer(5, 2, dev)
-        line["layer_prefill_32k"]["window_kernel"] = run_window(10, 3, dev)
+        r131, _ = run_layer(3, 1, dev, T=131072, window_pass=False)
+        line["layer_prefill_131k"] = r131
+        line["gdn_prefill"] = gdn_leg(args.steps, args.warmup, dev, not args.no_cpu)
+        line["decode"] = run_decode(200, 100, dev)
         line["varlen_gdn"] = run_varlen(10, 3, dev)
         line["gdn_layer"] = run_gdn_layer(10, 3, dev)
         line["teacher_decode"] = run_teacher_decode(50, 10, dev)
         line["gdn_bwd"] = run_gdn_bwd(10, 2, dev, cpu=not args.no_cpu)
         line["llama_state"] = run_llama_state(5, 2, dev)
         if not args.no_cpu:
-            for leg, fn in (("decode", cpu_decode), ("layer_prefill_32k", cpu_layer), ("varlen_gdn", cpu_varlen),
-                            ("gdn_layer", cpu_gdn_layer), ("teacher_decode", cpu_teacher_decode),
-                            ("llama_state", cpu_llama_state)):
+            for leg, fn in (("decode", cpu_decode), ("varlen_gdn", cpu_varlen), ("gdn_layer", cpu_gdn_layer),
+                            ("teacher_decode", cpu_teacher_decode), ("llama_state", cpu_llama_state)):
                 line[leg]["cpu_baseline"] = fn()
     if not args.no_cpu:
-        line["cpu_baseline"] = cpu_baseline(r["inputs"])
+        line["cpu_baseline"] = cpu_layer(m, inputs)
     print(json.dumps(line), flush=True)
 
 

@@ -33,8 +33,13 @@ def require_no_grad(*tensors) -> None:
 
 
 def compute_dtype(*tensors) -> torch.dtype:
-    """bf16 if any input is a 16-bit float (bf16 MFMA operands, fp32 accumulation), else fp32."""
-    return torch.bfloat16 if any(t.dtype in (torch.bfloat16, torch.float16) for t in tensors) else torch.float32
+    """Operand dtype of the kernels: bf16 (bf16 MFMA operands, fp32 accumulation) when every input is bf16, else fp32.
+    fp16 inputs are widened to fp32, never rounded to bf16 (the reference computes in fp32 with autocast off,
+    ``kernels.py:101``, ``hibrit.py:336-339``)."""
+    for t in tensors:
+        if t.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+            raise BifrostError(f"unsupported input dtype {t.dtype}")
+    return torch.bfloat16 if all(t.dtype == torch.bfloat16 for t in tensors) else torch.float32
 
 
 def dtype_code(dt: torch.dtype) -> int:

@@ -280,9 +280,12 @@ static bool kv_aligned(const void* p, int64_t s1, int64_t s2) {
 }
 
 // workspace of bf_layer_prefill_fwd: the GDN inputs and outputs for up to B T memory queries, o_mem, the new state
-// and the GDN workspace
+// and the GDN workspace. The GDN part is laid out for B T tokens with the segment length chosen for B T tokens; the
+// inner call runs on at most B T tokens with that same segment length, and every buffer of the GDN layout grows
+// monotonically with the token count at a fixed segment length, so the reservation always suffices.
 struct LayerWs {
     size_t wq, wk, wv, wg, wb, om, o_mem, s_new, gdn, total;
+    int seg_chunks;
 };
 static LayerWs layer_ws(int B, int G, int R, int D, int T, int in_dtype) {
     LayerWs w{};
@@ -297,7 +300,9 @@ static LayerWs layer_ws(int B, int G, int R, int D, int T, int in_dtype) {
     put(w.om, BT * H * D * esz);
     put(w.o_mem, BT * H * D * esz);
     put(w.s_new, (size_t)B * G * D * D * 4);
-    put(w.gdn, gdn_layout((int64_t)B * T, B, G, R, D, in_dtype, 0).total);
+    const GdnLayout gl = gdn_layout((int64_t)B * T, B, G, R, D, in_dtype, 0);
+    w.seg_chunks = gl.seg_chunks;
+    put(w.gdn, gl.total);
     w.total = at;
     return w;
 }
@@ -366,7 +371,8 @@ int bf_layer_prefill_fwd(int B, int G, int R, int D, int T, int W, int sinks, in
         void* om = rows ? static_cast<char*>(a.o_mem) + a.qoff * H * D * esz : ws + L.om;
         a.om = om;
         rc = bf_gdn_fwd(wq, wk, wv, wg, wb, nullptr, B, (int64_t)B * a.Tq, G, R, D, in_dtype, 1.f,
-                        state_valid ? state : nullptr, om, in_dtype, reinterpret_cast<float*>(ws + L.s_new), 0, ws + L.gdn, L.total - L.gdn,
+                        state_valid ? state : nullptr, om, in_dtype, reinterpret_cast<float*>(ws + L.s_new), L.seg_chunks,
+                        ws + L.gdn, L.total - L.gdn,
                         BF_GDN_PHASE_ALL, stream);
         if (rc) return rc;
         if (!rows && (rc = bf::layer_launch(a, 1, st))) return rc;

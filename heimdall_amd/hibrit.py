@@ -23,7 +23,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from . import _lib
-from ._device import (BifrostError, check, dtype_code, require_device, require_no_grad, stream_ptr,
+from ._device import (BifrostError, check, compute_dtype, dtype_code, require_device, require_no_grad, stream_ptr,
                       workspace)
 from .teacher import set_retrieval, teacher
 
@@ -97,15 +97,27 @@ def _new_ring(b, G, w, D, kdt, vdt, dev):
                 ring_pos=torch.full((w,), -1, dtype=torch.long, device=dev))
 
 
+def _ring_to(st: dict, kvdt: torch.dtype) -> None:
+    """Bring the cache ring to the layouts the kernels read: ring_k / ring_v dense in the operand dtype, ring_km /
+    ring_g / ring_beta dense fp32, ring_pos dense int64 (a cache written by the reference keeps the activations'
+    dtype; the kernels write through these buffers in place, so they must match the dtype they are given)."""
+    for key in ("ring_k", "ring_v"):
+        if st[key].dtype != kvdt or not st[key].is_contiguous():
+            st[key] = st[key].to(kvdt).contiguous()
+    for key in ("ring_km", "ring_g", "ring_beta"):
+        if st[key].dtype != torch.float32 or not st[key].is_contiguous():
+            st[key] = st[key].float().contiguous()
+    if st["ring_pos"].dtype != torch.long or not st["ring_pos"].is_contiguous():
+        st["ring_pos"] = st["ring_pos"].long().contiguous()
+
+
 def _decode(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memory):
     """One token for every sequence: bf_decode_fwd (window, memory write on exit, read, mix, ring write)."""
     c = self.c
     b = x.shape[0]
     H, G, D, w, r = c.h, c.hkv, c.dh, self.window, c.h // c.hkv
     dev = x.device
-    kvdt = kr.dtype
-    if kvdt not in (torch.float32, torch.bfloat16) or v.dtype != kvdt:
-        raise BifrostError(f"decode needs k/v in one dtype, fp32 or bf16 (got {kr.dtype}, {v.dtype})")
+    kvdt = compute_dtype(kr, v)
     use_mem = memory and start + 1 > w
     S = None
     if use_mem:
@@ -118,15 +130,13 @@ def _decode(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memo
     ns = 0 if sink_k is None else sink_k.size(2)
     sk = sink_k.to(kvdt).contiguous() if ns else None
     sv = sink_v.to(kvdt).contiguous() if ns else None
-    for key in ("ring_k", "ring_v", "ring_km", "ring_g", "ring_beta", "ring_pos"):
-        if not st[key].is_contiguous():
-            st[key] = st[key].contiguous()
+    _ring_to(st, kvdt)
     qrd = qr.to(torch.bfloat16 if qr.dtype == torch.bfloat16 else torch.float32).contiguous()
     z = F.linear(x.float(), self.mix.weight.float(), self.mix.bias.float()).contiguous() if use_mem else None
     mix_lse = self.mix_lse.float().contiguous() if use_mem else None
     mem_scale = self.mem_scale.float().contiguous() if use_mem else None
     qm_ = qm.contiguous() if use_mem else None
-    kr_, v_ = kr.contiguous(), v.contiguous()
+    kr_, v_ = kr.to(kvdt).contiguous(), v.to(kvdt).contiguous()
     km_, g_, b_ = km.float().contiguous(), g.float().contiguous(), beta.float().contiguous()
     o = torch.empty(b, H, D, dtype=torch.float32, device=dev)
     lib = _lib.load()
@@ -147,9 +157,14 @@ def student(self, x, q, k, v, qr, kr, start: int, cache: Optional[dict], memory:
 
     x [B, t, d]; q [B, t, H, D] (normed, pre-RoPE); k, v [B, t, G, D]; qr [B, H, t, D], kr [B, G, t, D] (RoPE'd).
     cache: dict mutated in place (the reference's keys and shapes) or None. Returns o [B, t, H, D] fp32.
+
+    With autograd recording and a trainable new parameter (or a memory input that requires grad), as in the
+    conversion's stage A (``distill_pair``, ``hibrit.py:434-439``), the call is differentiable: see
+    ``_student_autograd``.
     """
     require_device(x, q, k, v, qr, kr)
-    require_no_grad(x, q, k, v, qr, kr)
+    if _needs_grad(self, x, q, k, v, qr, kr):
+        return _student_autograd(self, x, q, k, v, qr, kr, start, cache, memory)
     c = self.c
     b, t = x.shape[:2]
     w, s = self.window, self.sinks
@@ -179,6 +194,150 @@ def student(self, x, q, k, v, qr, kr, start: int, cache: Optional[dict], memory:
     return o
 
 
+def _new_params(self):
+    """The trainable tensors of the conversion (``NEW``): fq, fk, ab, mix, mix_lse, mem_scale, A_log, dt_bias."""
+    out = []
+    for n in NEW:
+        p = getattr(self, n, None)
+        if isinstance(p, nn.Module):
+            out.extend(p.parameters())
+        elif p is not None:
+            out.append(p)
+    return out
+
+
+def _needs_grad(self, *inputs) -> bool:
+    return torch.is_grad_enabled() and (any(t_ is not None and t_.requires_grad for t_ in inputs) or
+                                        any(p.requires_grad for p in _new_params(self)))
+
+
+def _window_lse(self, qr, kr, v, start, st, sink_k, sink_v):
+    """Window + sinks attention with the per-row LSE and no mix (``hibrit.py:336-361``): bf_window_fwd over the chunk
+    and, for positions before ``start``, the cache ring ``st`` (if it has one). Returns (o_win [B, t, H, D] fp32,
+    lse [B, H, t] fp32); no autograd graph (the window branch has no trainable parameter)."""
+    c = self.c
+    b, t = qr.shape[0], qr.shape[2]
+    H, G, D, w, r = c.h, c.hkv, c.dh, self.window, c.h // c.hkv
+    dev = qr.device
+    cdt = compute_dtype(qr, kr, v)
+    ring = "ring_k" in st
+    if ring:
+        _ring_to(st, cdt)
+    unit = lambda t_: t_ if t_.stride(-1) == 1 else t_.contiguous()
+    q_, k_, v_ = (unit(z.detach().to(cdt)) for z in (qr, kr, v))
+    ns = 0 if sink_k is None else sink_k.size(2)
+    sk = sink_k.detach().to(cdt).contiguous() if ns else None
+    sv = sink_v.detach().to(cdt).contiguous() if ns else None
+    o = torch.empty(b, t, H, D, dtype=torch.float32, device=dev)
+    lse = torch.empty(b, H, t, dtype=torch.float32, device=dev)
+    ptr = lambda t_: t_.data_ptr() if t_ is not None else None
+    check(_lib.load().bf_window_fwd(
+        b, G, r, D, t, w, self.sinks, start, dtype_code(cdt), ptr(q_), *_strides(q_, (0, 1, 2)), ptr(k_),
+        *_strides(k_, (0, 1, 2)), ptr(v_), *_strides(v_, (0, 2, 1)), ptr(st["ring_k"]) if ring else None,
+        ptr(st["ring_v"]) if ring else None, ptr(st["ring_pos"]) if ring else None, ptr(sk), ptr(sv), ns, 0, None, 0,
+        None, None, None, ptr(o), _lib.DTYPE_F32, ptr(lse), stream_ptr(dev)), "bf_window_fwd")
+    return o, lse
+
+
+def _student_autograd(self, x, q, k, v, qr, kr, start: int, cache: Optional[dict], memory: bool = True):
+    """``_student`` with gradients, for the conversion's training (stage A, ``distill_pair``, ``hibrit.py:434-439``):
+    the memory inputs (``_mem_inputs``), the write stream, the gamma mix and the cache update are PyTorch ops on the
+    GPU and the delta rule is ``motor.delta_rule_gqa`` (``bf_gdn_fwd`` forward, ``bf_gdn_bwd`` backward, fp32), so the
+    gradients of the new parameters (and of q, k, x) are those of the reference's autograd graph. The window branch
+    (``bf_window_fwd``) has no trainable parameter and its output and LSE enter as constants: qr, kr and v must not
+    require grad (in the reference's training they come from frozen projections, ``hibrit.py:556-561``)."""
+    from .motor import delta_rule_gqa
+    if any(t_.requires_grad for t_ in (qr, kr, v)):
+        raise BifrostError("the window branch has no backward: qr, kr and v must not require grad (the conversion "
+                           "trains only the new parameters; the projections are frozen)")
+    c = self.c
+    b, t = x.shape[:2]
+    H, G, D, w, s, r = c.h, c.hkv, c.dh, self.window, self.sinks, c.h // c.hkv
+    dev = x.device
+    st = cache if cache is not None else {}
+    pos = torch.arange(start, start + t, device=dev)
+    vt = v.transpose(1, 2)
+    sink_k, sink_v = st.get("sink_k"), st.get("sink_v")
+    n_new = max(0, min(t, s - start))
+    if n_new:
+        sink_k = kr[:, :, :n_new] if sink_k is None else torch.cat((sink_k, kr[:, :, :n_new]), 2)
+        sink_v = vt[:, :, :n_new] if sink_v is None else torch.cat((sink_v, vt[:, :, :n_new]), 2)
+    o_win, lse = _window_lse(self, qr, kr, v, start, st, sink_k, sink_v)
+    o = o_win
+    use_mem = memory and start + t > w
+    if use_mem or cache is not None:
+        qm, km, g, beta = self._mem_inputs(x, q, k, pos)
+    if use_mem:
+        s0 = st.get("S")
+        ring = "ring_k" in st
+        if start == 0 and s0 is None and not ring:
+            # empty history: the first W writes are empty (g = beta = 0) and the queries before W have gamma = 0, so
+            # the queries W .. t-1 read the state after the writes of tokens 0 .. t-W-1
+            o_tail, sm = delta_rule_gqa(qm[:, w:].reshape(b, t - w, G, r, D), km[:, :t - w], v[:, :t - w].float(),
+                                        g[:, :t - w], beta[:, :t - w], 64, None)
+            o_mem = torch.cat((o_tail.new_zeros(b, w, G, r, D), o_tail), 1).reshape(b, t, H, D)
+        else:
+            # token i - W is written before the query at position i reads: the stream is [ring ; chunk][:t]
+            pp = torch.arange(start - w, start, device=dev)
+            if ring:
+                idx = pp % w
+                rv = st["ring_v"][:, :, idx].transpose(1, 2).float()
+                rkm, rg, rb = st["ring_km"][:, idx].float(), st["ring_g"][:, idx].float(), st["ring_beta"][:, idx].float()
+                vf = (st["ring_pos"][idx] == pp).float()[None, :, None]
+            else:
+                rv = torch.zeros(b, w, G, D, device=dev)
+                rkm, rg, rb = torch.zeros_like(rv), torch.zeros(b, w, G, device=dev), torch.zeros(b, w, G, device=dev)
+                vf = torch.zeros(1, w, 1, device=dev)
+            wk = torch.cat((rkm, km.float()), 1)[:, :t]
+            wv = torch.cat((rv, v.float()), 1)[:, :t]
+            wg = torch.cat((rg * vf, g), 1)[:, :t]
+            wb = torch.cat((rb * vf, beta), 1)[:, :t]
+            o_mem, sm = delta_rule_gqa(qm.reshape(b, t, G, r, D), wk, wv, wg, wb, 64, s0)
+            o_mem = o_mem.reshape(b, t, H, D)
+        z = F.linear(x.float(), self.mix.weight.float(), self.mix.bias.float())
+        gamma = torch.sigmoid(z + self.mix_lse.float() * (lse.transpose(1, 2) - math.log(w)))
+        gamma = gamma * (pos >= w).float()[None, :, None]
+        o = o_win + gamma[..., None] * (self.mem_scale.float()[:, None] * o_mem - o_win)
+        if cache is not None:
+            cache["S"] = sm
+    if cache is not None:
+        with torch.no_grad():
+            if "ring_k" not in cache:
+                cache.update(_new_ring(b, G, w, D, compute_dtype(qr, kr, v), compute_dtype(qr, kr, v), dev))
+            m_ = min(t, w)
+            slot = pos[-m_:] % w
+            cache["ring_k"][:, :, slot] = kr[:, :, -m_:].to(cache["ring_k"].dtype)
+            cache["ring_v"][:, :, slot] = vt[:, :, -m_:].to(cache["ring_v"].dtype)
+            cache["ring_km"][:, slot], cache["ring_g"][:, slot] = km[:, -m_:].float(), g[:, -m_:].float()
+            cache["ring_beta"][:, slot], cache["ring_pos"][slot] = beta[:, -m_:].float(), pos[-m_:]
+        cache["sink_k"], cache["sink_v"] = sink_k, sink_v
+    return o
+
+
+def window(self, qr, ext_k, ext_v, ext_pos, sink_k, sink_v, pos):
+    """``HybridAttention._window`` (``hibrit.py:336-361``) on ``bf_window_fwd``: qr [B, H, t, D]; ext_k / ext_v
+    [B, G, W + t, D] = [the ring positions start - W .. start - 1 in time order ; the chunk]; ext_pos [W + t] (-1 for
+    an empty ring entry, else the position, and the chunk's positions start .. start + t - 1); sink_k / sink_v
+    [B, G, ns, D] or None; pos [t] = start .. start + t - 1. Returns (o_win [B, t, H, D] fp32, lse [B, H, t] fp32).
+
+    The kernel reads history from a ring indexed by position mod W, so the first W entries are rotated into that
+    order (position p = start - W + j goes to slot p mod W = (start + j) mod W); one host read of ``pos[0]``."""
+    dev = require_device(qr, ext_k, ext_v, ext_pos, pos)
+    require_no_grad(qr, ext_k, ext_v)
+    w = self.window
+    start = int(pos[0].item())
+    t = qr.shape[2]
+    if ext_k.shape[2] != w + t or ext_pos.numel() != w + t or pos.numel() != t:
+        raise BifrostError("ext_k / ext_v / ext_pos must hold W ring entries followed by the chunk")
+    sh = start % w
+    st = {"ring_k": torch.roll(ext_k[:, :, :w], sh, 2), "ring_v": torch.roll(ext_v[:, :, :w], sh, 2),
+          "ring_pos": torch.roll(ext_pos[:w].to(device=dev, dtype=torch.long), sh, 0).contiguous(),
+          "ring_km": torch.empty(0, device=dev), "ring_g": torch.empty(0, device=dev),
+          "ring_beta": torch.empty(0, device=dev)}
+    kr, vt = ext_k[:, :, w:], ext_v[:, :, w:]
+    return _window_lse(self, qr, kr, vt.transpose(1, 2), start, st, sink_k, sink_v)
+
+
 def _strides(t: torch.Tensor, dims):
     return tuple(int(t.stride(d)) for d in dims)
 
@@ -193,15 +352,10 @@ def _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, mem
     b, t = x.shape[:2]
     H, G, D, w, r = c.h, c.hkv, c.dh, self.window, c.h // c.hkv
     dev = x.device
-    cdt = torch.bfloat16 if qr.dtype in (torch.bfloat16, torch.float16) else torch.float32
+    cdt = compute_dtype(qr, kr, v)
     lib = _lib.load()
     use_mem = memory and start + t > w
-    for key in ("ring_k", "ring_v"):
-        if st[key].dtype != cdt or not st[key].is_contiguous():
-            st[key] = st[key].to(cdt).contiguous()
-    for key in ("ring_km", "ring_g", "ring_beta"):
-        if st[key].dtype != torch.float32 or not st[key].is_contiguous():
-            st[key] = st[key].float().contiguous()
+    _ring_to(st, cdt)
     S, valid = st.get("S"), 1
     if S is None:
         S, valid = torch.empty(b, G, D, D, dtype=torch.float32, device=dev), 0
@@ -281,6 +435,7 @@ class BifrostCore(nn.Module):
         self.converted = True
 
     _mem_inputs = mem_inputs
+    _window = window
     _student = student
     _teacher = teacher
     set_retrieval = set_retrieval

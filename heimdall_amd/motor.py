@@ -1,11 +1,13 @@
 """Drop-in GPU operators for the reference training engine (``Heimdall/heimdall/motor.py``): the GQA delta rule
-(``:70-102``) and the teacher's causal blockwise attention (``:41-67``)."""
+(``:70-102``), the window + sink attention of ``precompute`` (``window_attention``, ``:105-115``) and the teacher's
+causal blockwise attention (``:41-67``)."""
 from typing import Optional, Tuple
 
 import torch
 
 from . import _lib
-from ._device import BifrostError, check, dtype_code, gdn_forward, require_device, require_no_grad, stream_ptr
+from ._device import (BifrostError, check, compute_dtype, dtype_code, gdn_forward, require_device,
+                      require_no_grad, stream_ptr)
 
 
 def _pad_tokens(x: torch.Tensor, T: int, pad: int) -> torch.Tensor:
@@ -102,3 +104,33 @@ def blockwise_attention(qr, kr, vt, qblk: int = 2048, kblk: int = 8192) -> torch
                                     None, None, o.data_ptr(), _lib.DTYPE_F32, None, stream_ptr(dev)),
           "bf_window_fwd")
     return o
+
+
+def window_attention(a, qr, kr, v) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Window + sink attention from position 0 with an empty ring, the cache-free path of ``_student``
+    (``Heimdall/heimdall/motor.py:105-115``, called by ``precompute`` at ``:137``): ``a`` carries ``window`` and
+    ``sinks``; qr [B, H, T, D], kr [B, G, T, D] (RoPE applied), v [B, T, G, D]. The sinks are the first min(sinks, T)
+    tokens. Returns (o_win [B, T, H, D] fp32, lse [B, H, T] fp32), computed by ``bf_window_fwd`` (fp32 operands for
+    fp32 / fp16 inputs, bf16 operands with fp32 softmax and accumulation for bf16 inputs)."""
+    dev = require_device(qr, kr, v)
+    require_no_grad(qr, kr, v)
+    B, H, T, D = qr.shape
+    G = kr.shape[1]
+    if H % G or kr.shape != (B, G, T, D) or v.shape != (B, T, G, D):
+        raise BifrostError(f"inconsistent shapes qr{tuple(qr.shape)} kr{tuple(kr.shape)} v{tuple(v.shape)}")
+    cdt = compute_dtype(qr, kr, v)
+    unit = lambda t: t if t.stride(-1) == 1 else t.contiguous()
+    q_, k_, v_ = (unit(t.to(cdt)) for t in (qr, kr, v))
+    ns = min(a.sinks, T)
+    sk = k_[:, :, :ns].contiguous() if ns else None
+    sv = v_.transpose(1, 2)[:, :, :ns].contiguous() if ns else None
+    o = torch.empty(B, T, H, D, dtype=torch.float32, device=dev)
+    lse = torch.empty(B, H, T, dtype=torch.float32, device=dev)
+    st = lambda t, dims: tuple(int(t.stride(i)) for i in dims)
+    ptr = lambda t: t.data_ptr() if t is not None else None
+    check(_lib.load().bf_window_fwd(B, G, H // G, D, T, a.window, a.sinks, 0, dtype_code(cdt), q_.data_ptr(),
+                                    *st(q_, (0, 1, 2)), k_.data_ptr(), *st(k_, (0, 1, 2)), v_.data_ptr(),
+                                    *st(v_, (0, 2, 1)), None, None, None, ptr(sk), ptr(sv), ns, 0, None, 0, None, None,
+                                    None, o.data_ptr(), _lib.DTYPE_F32, lse.data_ptr(), stream_ptr(dev)),
+          "bf_window_fwd")
+    return o, lse

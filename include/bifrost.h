@@ -58,8 +58,10 @@ const char* bf_status_string(int status);
  *
  * Replaces the reference operator kernels.delta_rule(q, k, v, g, beta, chunk_size=64, initial_state)
  * (Heimdall/heimdall/kernels.py:152-155 -> delta_rule_reference, kernels.py:94-129) when R = 1, and
- * motor.delta_rule_gqa(q, k, v, g, beta, chunk=64, state) (Heimdall/heimdall/motor.py:70-102) for R > 1; it also
- * covers the native op GGML_OP_GATED_DELTA_NET at D = 256 (Heimdall/llamacpp/bifrost.patch:5-18).
+ * motor.delta_rule_gqa(q, k, v, g, beta, chunk=64, state) (Heimdall/heimdall/motor.py:70-102) for R > 1. It computes
+ * the same recurrence as the native op GGML_OP_GATED_DELTA_NET (Heimdall/llamacpp/bifrost.patch:5-18) but is not a
+ * drop-in for that op's launcher: it takes dense layouts and a [dk][dv] state, not ggml's per-tensor strides,
+ * state-slot stride, KDA variant or transposed [dv][dk] state.
  *
  * Per KV head g and token t (alpha = exp(g_t)):
  *     S_t = alpha S_{t-1} + beta_t k_t (v_t - alpha S_{t-1}^T k_t)^T,   o_{t,h} = S_t^T (scale * q_{t,h})

@@ -301,15 +301,18 @@ def _student_autograd(self, x, q, k, v, qr, kr, start: int, cache: Optional[dict
         if cache is not None:
             cache["S"] = sm
     if cache is not None:
+        if "ring_k" not in cache:
+            cache.update(_new_ring(b, G, w, D, compute_dtype(qr, kr, v), compute_dtype(qr, kr, v), dev))
+        m_ = min(t, w)
+        slot = pos[-m_:] % w
         with torch.no_grad():
-            if "ring_k" not in cache:
-                cache.update(_new_ring(b, G, w, D, compute_dtype(qr, kr, v), compute_dtype(qr, kr, v), dev))
-            m_ = min(t, w)
-            slot = pos[-m_:] % w
             cache["ring_k"][:, :, slot] = kr[:, :, -m_:].to(cache["ring_k"].dtype)
             cache["ring_v"][:, :, slot] = vt[:, :, -m_:].to(cache["ring_v"].dtype)
-            cache["ring_km"][:, slot], cache["ring_g"][:, slot] = km[:, -m_:].float(), g[:, -m_:].float()
-            cache["ring_beta"][:, slot], cache["ring_pos"][slot] = beta[:, -m_:].float(), pos[-m_:]
+            cache["ring_pos"][slot] = pos[-m_:]
+        # recorded by autograd, as the reference's slot assignments are (hibrit.py:419-420): a later chunk that reads
+        # these rows back into its write stream carries their gradient to fk, ab, A_log and dt_bias
+        cache["ring_km"][:, slot], cache["ring_g"][:, slot] = km[:, -m_:].float(), g[:, -m_:].float()
+        cache["ring_beta"][:, slot] = beta[:, -m_:].float()
         cache["sink_k"], cache["sink_v"] = sink_k, sink_v
     return o
 

@@ -1,9 +1,38 @@
 // C-ABI entry points of libbifrost_hip.so: argument checks, workspace carve-up, dispatch to the kernels.
 #include <hip/hip_runtime.h>
 
+#include <mutex>
+
 #include "bf_internal.h"
 
+// The scratch of the allocation-free decode entry point: one copy of this array on every GPU the library runs on,
+// held until the process ends. Host code never uses its name as an address: the device address comes from
+// hipGetSymbolAddress, once per device (scratch_on_current_device).
+static __device__ __align__(256) unsigned char scratch[BF_DECODE_STATIC_SCRATCH_BYTES];
+
 namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device, looked up on the first call there (with that device current).
+int scratch_on_current_device(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kMaxDevices) return BF_STATUS_UNSUPPORTED;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        if (!p) return BF_STATUS_INVALID;
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return BF_STATUS_OK;
+}
 
 constexpr int kChunk = 64;
 
@@ -77,6 +106,7 @@ const char* bf_status_string(int status) {
         case BF_STATUS_INVALID: return "invalid argument (null pointer, bad size or inconsistent shape)";
         case BF_STATUS_UNSUPPORTED: return "unsupported head dim, dtype or chunk size";
         case BF_STATUS_WORKSPACE: return "workspace missing or too small";
+        case BF_STATUS_SCRATCH: return "problem larger than the static scratch of the allocation-free entry point";
         default: break;
     }
     return status > 0 ? hipGetErrorString((hipError_t)status) : "unknown status";
@@ -198,6 +228,24 @@ int bf_decode_fwd(int B, int G, int R, int D, int W, int sinks, int64_t pos, int
     a.ws_om = reinterpret_cast<float*>(ws);
     a.ws_part = reinterpret_cast<float*>(ws + align256((size_t)B * G * R * D * sizeof(float)));
     return bf::decode_dispatch(a, static_cast<hipStream_t>(stream));
+}
+
+int bf_decode_fwd_noalloc(int B, int G, int R, int D, int W, int sinks, int64_t pos, int memory, int kv_dtype,
+                          int q_dtype, const void* qr, const float* qm, const void* kr, const void* v, const float* km,
+                          const float* g_new, const float* beta_new, const float* z, const float* mix_lse,
+                          const float* mem_scale, const void* sink_k, const void* sink_v, int n_sinks, void* ring_k,
+                          void* ring_v, float* ring_km, float* ring_g, float* ring_beta, int64_t* ring_pos,
+                          float* state, float* o, float* lse, void* stream) {
+    size_t need = 0;
+    const int st = bf_decode_workspace_size(B, G, R, D, W, &need);
+    if (st) return st;
+    if (need > sizeof(scratch)) return BF_STATUS_SCRATCH;
+    void* ws = nullptr;
+    const int rc = scratch_on_current_device(&ws);
+    if (rc) return rc;
+    return bf_decode_fwd(B, G, R, D, W, sinks, pos, memory, kv_dtype, q_dtype, qr, qm, kr, v, km, g_new, beta_new, z,
+                         mix_lse, mem_scale, sink_k, sink_v, n_sinks, ring_k, ring_v, ring_km, ring_g, ring_beta,
+                         ring_pos, state, o, lse, ws, sizeof(scratch), stream);
 }
 
 int bf_window_fwd(int B, int G, int R, int D, int T, int W, int sinks, int64_t start, int in_dtype, const void* q,

@@ -32,6 +32,7 @@ extern "C" {
 #define BF_STATUS_INVALID (-1)     /* null pointer, non-positive size, inconsistent shape */
 #define BF_STATUS_UNSUPPORTED (-2) /* head dim, dtype or chunk size outside the supported set */
 #define BF_STATUS_WORKSPACE (-3)   /* workspace missing or smaller than the size query returned */
+#define BF_STATUS_SCRATCH (-4)     /* problem needs more than the static scratch of an allocation-free entry point */
 
 /* Phases of bf_gdn_fwd (bit mask), run in the order PREP, SUMMARY, COMBINE, OUTPUT; BF_GDN_PHASE_ALL runs the whole
  * operator.
@@ -127,6 +128,25 @@ int bf_decode_fwd(int B, int G, int R, int D, int W, int sinks, int64_t pos, int
                   const void* sink_k, const void* sink_v, int n_sinks, void* ring_k, void* ring_v, float* ring_km,
                   float* ring_g, float* ring_beta, int64_t* ring_pos, float* state, float* o, float* lse,
                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * bf_decode_fwd without a workspace argument: the same kernels and results, with their scratch (the memory read and
+ * the window-split partials, bf_decode_workspace_size bytes) in a static device buffer of
+ * BF_DECODE_STATIC_SCRATCH_BYTES that the library holds on each GPU it runs on until the process ends. No counterpart
+ * in the reference: it is for callers that cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid allocation); the call allocates and frees nothing. Runs on the current device; its
+ * buffer's address is looked up once per device, on the first call there. Returns BF_STATUS_SCRATCH, launching
+ * nothing, when bf_decode_workspace_size exceeds the buffer (e.g. B = 64, H = 16, G = 4, D = 256, W = 2048 needs
+ * 5.3 MB). Every call on one GPU shares that GPU's buffer: calls that overlap in time on one GPU (other streams,
+ * other threads) race and must be serialised by the caller.
+ */
+#define BF_DECODE_STATIC_SCRATCH_BYTES (16u << 20)
+int bf_decode_fwd_noalloc(int B, int G, int R, int D, int W, int sinks, int64_t pos, int memory, int kv_dtype,
+                          int q_dtype, const void* qr, const float* qm, const void* kr, const void* v, const float* km,
+                          const float* g_new, const float* beta_new, const float* z, const float* mix_lse,
+                          const float* mem_scale, const void* sink_k, const void* sink_v, int n_sinks, void* ring_k,
+                          void* ring_v, float* ring_km, float* ring_g, float* ring_beta, int64_t* ring_pos,
+                          float* state, float* o, float* lse, void* stream);
 
 /*
  * Sliding-window + sink attention over a prefill chunk, with per-row log-sum-exp and the fused gamma mix:

@@ -96,3 +96,12 @@ def test_n_archival():
     """hibrit.py:187-190: at least one archival head for the "long" init when a fraction is asked for."""
     assert n_archival(0.5, 4) == 2 and n_archival(0.1, 4) == 1 and n_archival(0.0, 4) == 0
     assert n_archival(0.1, 4, "mamba") == 0
+
+
+def test_noalloc_decode_size_limit_without_gpu(cpu_lib):
+    """The allocation-free decode entry point refuses a problem larger than its static scratch before any device
+    call (placeholder pointers are never touched)."""
+    n = ctypes.c_size_t(0)
+    assert cpu_lib.bf_decode_workspace_size(256, 4, 8, 256, 8192, ctypes.byref(n)) == 0 and n.value > 16 << 20
+    assert cpu_lib.bf_decode_fwd_noalloc(256, 4, 8, 256, 8192, 4, 100000, 1, 1, 1, *([256] * 12), 0, *([256] * 9),
+                                         None) == -4

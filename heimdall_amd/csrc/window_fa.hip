@@ -133,41 +133,67 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
     const int slot_lo = rk ? (int)(kp_lo % a.W) : 0;               // ring slot of kp_lo (one division)
     const long start = a.start;
 
-    // copy block i's K and V rows into tile t (row r's 16-byte block pb holds the row's block pb ^ sw(r)) with
-    // buffer_load ... lds: one descriptor per source (sinks, ring, chunk), lanes of other sources masked off
+    // Copy block i's K and V rows into tile t with buffer_load ... lds (row r's 16-byte block pb holds the row's block
+    // pb ^ sw(r)). Instruction j of wave wv fills 1 KB of the tile: rows row0 + RPI j .. + RPL - 1, lane -> (row,
+    // block) fixed; the swizzle depends only on row0 (RPI is a multiple of the swizzle period), so each lane's byte
+    // offset is one clamp and one multiply-add per instruction. The source of a block is wave-uniform: the sinks, the
+    // chunk (rows past the last query are clamped to it: valid data, masked), the ring (slot kp mod W), or, for the
+    // one block that straddles the chunk start, each lane's row from its own source. Every descriptor stays uniform,
+    // so no load is serialised over distinct lane values.
+    constexpr int RPL = 64 / NBLK;                 // tile rows per 1 KB copy
+    constexpr int RPI = NW * RPL;                  // rows between a wave's consecutive copies
+    static_assert(NBLK >= 16 ? RPI % 16 == 0 : RPI % 32 == 0, "swizzle must be invariant across a wave's copies");
+    const int row0 = wv * RPL + lane / NBLK, pb0 = lane % NBLK;
+    const uint32_t kb0 = 16u * (pb0 ^ fa_swk<NBLK>(row0)), vb0 = 16u * (pb0 ^ fa_swv<NBLK>(row0));
     const rsrc_t rsk = make_rsrc(sk, (uint32_t)(ns * ROWB)), rsv = make_rsrc(sv, (uint32_t)(ns * ROWB));
     const rsrc_t rrk = make_rsrc(rk, rk ? (uint32_t)(a.W * ROWB) : 0u), rrv = make_rsrc(rv, rv ? (uint32_t)(a.W * ROWB) : 0u);
     const rsrc_t rck = make_rsrc(ck, (uint32_t)(((long)(a.T - 1) * a.k_st + D) * 2));
     const rsrc_t rcv = make_rsrc(cv, (uint32_t)(((long)(a.T - 1) * a.v_st + D) * 2));
+    const uint32_t kst_b = (uint32_t)(a.k_st * 2), vst_b = (uint32_t)(a.v_st * 2);
+    const uint32_t crow_max = (uint32_t)(p_last - start);          // chunk row of the last query
     auto dma = [](rsrc_t r, void* dst, uint32_t off) {   // 16 bytes at byte offset off (per lane) -> dst + 16 lane
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, off, 0, 0, 0);
     };
     auto stage = [&](FaTile<D>& t, int i) {
-        const bool sinkblk = has_sink && i == 0;
+        char* tk = reinterpret_cast<char*>(t.k) + wv * 1024;
+        char* tv = reinterpret_cast<char*>(t.v) + wv * 1024;
+        if (has_sink && i == 0) {
+#pragma unroll
+            for (int j = 0; j < NLD; ++j) {
+                const uint32_t r = (uint32_t)min(row0 + RPI * j, ns - 1);
+                dma(rsk, tk + NW * j * 1024, r * ROWB + kb0);
+                dma(rsv, tv + NW * j * 1024, r * ROWB + vb0);
+            }
+            return;
+        }
+        const long kpb = kp_lo + (long)(i - has_sink) * FA_KB;        // position of the block's row 0
+        if (kpb >= start || !rk) {                                     // chunk rows only
+            const uint32_t rb = (uint32_t)(kpb - start);               // wraps (huge) before the chunk: clamped
+#pragma unroll
+            for (int j = 0; j < NLD; ++j) {
+                const uint32_t cr = min(rb + (uint32_t)(row0 + RPI * j), crow_max);
+                dma(rck, tk + NW * j * 1024, __umul24(cr, kst_b) + kb0);
+                dma(rcv, tv + NW * j * 1024, __umul24(cr, vst_b) + vb0);
+            }
+            return;
+        }
+        // ring rows (position < start): slot (slot_lo + kp - kp_lo) mod W, below 2W since kp - kp_lo <= W - 2
+        int sb = slot_lo + (int)(kpb - kp_lo);
+        sb = sb >= a.W ? sb - a.W : sb;
+        const int nring = (int)min((long)FA_KB, start - kpb);          // rows before the chunk start
+        const uint32_t rb = (uint32_t)(kpb - start);
 #pragma unroll
         for (int j = 0; j < NLD; ++j) {
-            const int c = (wv + NW * j) * 64 + lane;                   // 16-byte slot of the tile
-            const int row = c / NBLK, pb = c % NBLK;
-            const uint32_t kb = 16u * (pb ^ fa_swk<NBLK>(row)), vb = 16u * (pb ^ fa_swv<NBLK>(row));
-            char* dk = reinterpret_cast<char*>(t.k) + (wv + NW * j) * 1024;
-            char* dv = reinterpret_cast<char*>(t.v) + (wv + NW * j) * 1024;
-            if (sinkblk) {
-                const uint32_t rr = row < ns ? (uint32_t)row : 0u;
-                dma(rsk, dk, rr * ROWB + kb);
-                dma(rsv, dv, rr * ROWB + vb);
-                continue;
+            const int r = row0 + RPI * j;
+            if (r < nring) {
+                const uint32_t u = (uint32_t)(sb + r), sl = min(u, u - (uint32_t)a.W);
+                dma(rrk, tk + NW * j * 1024, sl * ROWB + kb0);
+                dma(rrv, tv + NW * j * 1024, sl * ROWB + vb0);
             }
-            long kp = kp_lo + (long)(i - has_sink) * FA_KB + row;
-            kp = kp <= p_last ? kp : p_last;
-            if (kp >= start || !rk) {                  // no ring: rows before the chunk read chunk row 0 (masked)
-                const long cr = kp >= start ? kp - start : 0;
-                dma(rck, dk, (uint32_t)(cr * a.k_st * 2) + kb);
-                dma(rcv, dv, (uint32_t)(cr * a.v_st * 2) + vb);
-            } else {
-                int slot = slot_lo + (int)(kp - kp_lo);
-                slot = slot >= a.W ? slot - a.W : slot;
-                dma(rrk, dk, (uint32_t)slot * ROWB + kb);
-                dma(rrv, dv, (uint32_t)slot * ROWB + vb);
+            if (r >= nring) {                                          // the block straddles the chunk start
+                const uint32_t cr = min(rb + (uint32_t)r, crow_max);
+                dma(rck, tk + NW * j * 1024, __umul24(cr, kst_b) + kb0);
+                dma(rcv, tv + NW * j * 1024, __umul24(cr, vst_b) + vb0);
             }
         }
     };
@@ -411,6 +437,8 @@ int launch_window_fa(const WinArgs& a, hipStream_t stream) {
     // chunk K / V rows are addressed by 32-bit buffer offsets
     if (((long)(a.T - 1) * a.k_st + D) * 2 > 0xffffffffL || ((long)(a.T - 1) * a.v_st + D) * 2 > 0xffffffffL)
         return BF_ERR_UNSUPPORTED;
+    // the tile copy forms row offsets with 24-bit multiplies: chunk rows and row strides in bytes below 2^24
+    if (a.T >= (1L << 24) || a.k_st * 2 >= (1L << 24) || a.v_st * 2 >= (1L << 24)) return BF_ERR_UNSUPPORTED;
     const dim3 grid((unsigned)(FA_NXCD * per)), block(FaShape<D>::NT);
     if (a.o_dtype == DT_BF16) hipLaunchKernelGGL((window_fa_kernel<D, true>), grid, block, 0, stream, a);
     else hipLaunchKernelGGL((window_fa_kernel<D, false>), grid, block, 0, stream, a);

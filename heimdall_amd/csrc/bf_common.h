@@ -151,6 +151,19 @@ __device__ __forceinline__ void wait_vmem_all() { __builtin_amdgcn_s_waitcnt(0x0
 // from moving memory accesses across it). A DMA load whose LDS data is read after it still needs wait_vmem_all().
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Element offset of (row, col) of a 64 x 64 chunk matrix stored in MFMA A-fragment order: fragment (tt, ks) = 64
+// lanes x VEC elements, lane (lg, l16) holding row tpart(tt) + VEC*(l16/4) + l16%4 at K indices KF*ks + VEC*lg + e,
+// with tpart(tt) = KF*(tt/HP) + 4*(tt%HP) and HP = VEC/4 (the row permutation under which MFMA accumulator tiles of
+// successive products chain without data exchange). Each fragment is one contiguous 1 KB piece.
+template <class E>
+__device__ __forceinline__ int tfrag_index(int row, int col) {
+    constexpr int VEC = E::VEC, KF = E::KF, HP = VEC / 4;
+    const int tt = HP * (row / KF) + (row % VEC) / 4;
+    const int l16 = 4 * ((row % KF) / VEC) + row % 4;
+    const int ks = col / KF, lg = (col % KF) / VEC, e = col % VEC;
+    return ((ks * 4 + tt) * 64 + 16 * lg + l16) * VEC + e;
+}
+
 __device__ __forceinline__ int lane_id() { return threadIdx.x & (WAVE - 1); }
 // Wave index inside the workgroup, marked wave-uniform (readfirstlane) so that values derived from it (buffer
 // descriptors, LDS bases, loop bounds) live in SGPRs; plain threadIdx.x / 64 is treated as divergent and descriptors

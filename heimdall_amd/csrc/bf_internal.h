@@ -37,8 +37,7 @@ struct GdnArgs {
     int multi_seg;           // some sequence may span more than one segment (STATES phase needed)
     // workspace carve-up (cid = chunk id, sid = segment id; C = 64)
     float* ws_gcum;          // [cid][G][C]        in-chunk cumulative log-decay
-    void* ws_T;              // [cid][G][C][C]     (I + A)^-1 diag(beta), in_dtype
-    void* ws_attn;           // [cid][H][C][C]     scale * (q k^T masked, decayed), in_dtype
+    void* ws_T;              // [cid][G][C*C]      (I + A)^-1 diag(beta), in_dtype, MFMA A-fragment order (tfrag_index)
     void* ws_phi;            // [sid][G][D*D]      Psi = Phi - c I of each segment map (in_dtype, fragment order)
     float* ws_c;             // [sid][G]           c = e^{sum of g over the segment}
     float* ws_n;             // [sid][G][D*D]      segment state from a zero entry state (fp32, accumulator-fragment order)

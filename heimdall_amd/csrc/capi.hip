@@ -43,13 +43,13 @@ bool supported_dtype(int dt) { return dt == BF_DTYPE_F32 || dt == BF_DTYPE_BF16;
 size_t esize(int dt) { return dt == BF_DTYPE_BF16 ? 2 : 4; }
 
 struct GdnLayout {
-    size_t gcum, T, attn, phi, c, n, sin, total;
+    size_t gcum, T, phi, c, n, sin, total;
     int max_chunks, seg_chunks, max_segs;
 };
 
 // Segment length (chunks) when the caller passes 0: the L that minimises a cost model of the three sequential-part
 // kernels on an MI355X (256 CUs, one scan workgroup per CU), with per-chunk and per-step times measured at D = 256:
-//   output   ceil(segments x G x D/128 x R / 256) rounds of L chunks, ~6 us per chunk
+//   output   ceil(segments x G x D/128 / 256) rounds of L chunks, ~(4 + 2R) us per chunk (R query heads per KV head)
 //   summary  ceil((segments - 1) x G x 2D/128 / 256) rounds of L chunks, ~3.7 us per chunk
 //   combine  (segments - 1) sequential steps, ~2.6 us each
 // Times scale with D^2 for the scan kernels and D^3 for the combine, which only shifts the balance for D < 256.
@@ -57,13 +57,13 @@ constexpr int kSegMinChunks = 4;
 
 int auto_segment_chunks(int max_chunks, int G, int R, int D) {
     const double f = (double)D / 256.0;
-    const double t_out = 6.0 * f * f, t_sum = 3.7 * f * f, t_comb = 2.6 * f * f * f;
+    const double t_out = (4.0 + 2.0 * R) * f * f, t_sum = 3.7 * f * f, t_comb = 2.6 * f * f * f;
     const int cg = D >= 128 ? D / 128 : 1;
     int best_L = max_chunks > kSegMinChunks ? max_chunks : kSegMinChunks;
     double best = 1e300;
     for (int L = kSegMinChunks; L <= (max_chunks > kSegMinChunks ? max_chunks : kSegMinChunks); ++L) {
         const long nseg = (max_chunks + L - 1) / L;
-        const long out_rounds = (nseg * G * cg * R + 255) / 256;
+        const long out_rounds = (nseg * G * cg + 255) / 256;
         const long sum_rounds = ((nseg - 1) * G * 2 * cg + 255) / 256;
         const double t = out_rounds * L * t_out + sum_rounds * L * t_sum + (nseg - 1) * t_comb;
         if (t < best - 1e-9) {
@@ -85,7 +85,6 @@ GdnLayout gdn_layout(int64_t total_tokens, int num_seqs, int G, int R, int D, in
     size_t off = 0;
     L.gcum = off; off = align256(off + nc * G * kChunk * sizeof(float));
     L.T = off;    off = align256(off + nc * G * kChunk * kChunk * e);
-    L.attn = off; off = align256(off + nc * G * R * kChunk * kChunk * e);
     L.phi = off;  off = align256(off + ns * G * D * D * e);
     L.c = off;    off = align256(off + ns * G * sizeof(float));
     L.n = off;    off = align256(off + ns * G * D * D * sizeof(float));
@@ -158,7 +157,6 @@ int bf_gdn_fwd(const void* q, const void* k, const void* v, const float* g, cons
     char* ws = static_cast<char*>(workspace);
     a.ws_gcum = reinterpret_cast<float*>(ws + L.gcum);
     a.ws_T = ws + L.T;
-    a.ws_attn = ws + L.attn;
     a.ws_phi = ws + L.phi;
     a.ws_c = reinterpret_cast<float*>(ws + L.c);
     a.ws_n = reinterpret_cast<float*>(ws + L.n);

@@ -3,16 +3,16 @@
 // Algorithm (UT/WY representation; reference: Heimdall/heimdall/kernels.py:94-129, motor.py:70-102). For a chunk of
 // C = 64 tokens of KV head g with in-chunk cumulative log-decay gc:
 //   A  = strict_lower(beta_i e^{gc_i - gc_j} k_i.k_j),   T' = (I + A)^-1 diag(beta)
-//   attn_r = scale (q_r K^T * e^{gc_i - gc_j})[i >= j]           for the R query heads of the group
-// so that the reference's u - w S equals T' (V - e^{gc} K S): the scan (gdn_scan.hip) needs only T', attn and gc
-// next to the inputs q, k, v, and nothing of size C x D is written back here.
+// so that the reference's u - w S equals T' (V - e^{gc} K S): the scan (gdn_scan.hip) needs only T' and gc next to
+// the inputs q, k, v (it forms the causal q K^T block of each query head itself), and nothing of size C x D is
+// written back here.
 //
-// gdn_prep_kernel, grid (chunks, G), 4 waves: K and q tiles are staged in LDS (buffer_load ... lds); the waves compute
-// the attn tiles of the R query heads, then A, by MFMA; (I + A) is inverted in fp32 by 16 x 16 blocks (diagonal blocks
-// by forward substitution, the rest by fp32 MFMA block products, one block column per wave).
+// gdn_prep_kernel, grid (chunks, G), 4 waves: the K tile is staged in LDS (buffer_load ... lds); the waves compute A
+// by MFMA; (I + A) is inverted in fp32 by 16 x 16 blocks (diagonal blocks by forward substitution, the rest by fp32
+// MFMA block products, one block column per wave).
 //
-// Workspace written (chunk id cid, KV head g, query head h):
-//   gcum [cid][g][C] f32 | T [cid][g][C][C] in_dtype | attn [cid][h][C][C] in_dtype
+// Workspace written (chunk id cid, KV head g):
+//   gcum [cid][g][C] f32 | T [cid][g][C*C] in_dtype in MFMA A-fragment order (tfrag_index), the layout the scan reads
 #include "bf_common.h"
 #include "bf_internal.h"
 
@@ -21,8 +21,7 @@ namespace bf {
 constexpr int CH = 64;     // chunk length
 constexpr int NT = 256;    // threads per workgroup (4 waves)
 
-// LDS: the chunk's K tile and one query head's q tile (swizzled rows, staged by buffer_load ... lds); after the attn
-// tiles are done the q region holds A.
+// LDS: the chunk's K tile (swizzled rows, staged by buffer_load ... lds) and A.
 template <class E, int D>
 struct __align__(16) PrepLds {
     // the inverse X overlays K once A is built, where K is large enough
@@ -31,10 +30,7 @@ struct __align__(16) PrepLds {
         typename E::T K[CH * D];
         float XoK[XK ? CH : 1][CH + 4];
     };
-    union {
-        typename E::T Q[CH * D];
-        float A[CH][CH + 4];
-    };
+    float A[CH][CH + 4];
     float Xs[XK ? 1 : CH][CH + 4];
     float gc[CH];
     float beta[CH];
@@ -43,14 +39,14 @@ struct __align__(16) PrepLds {
 template <class E, int D>
 __global__ __launch_bounds__(NT) void gdn_prep_kernel(GdnArgs a) {
     using T = typename E::T;
-    constexpr int VEC = E::VEC, KF = E::KF, ES = (int)sizeof(T), ROWB = D * ES, NKD = D / KF;
+    constexpr int KF = E::KF, ES = (int)sizeof(T), ROWB = D * ES, NKD = D / KF;
     __shared__ PrepLds<E, D> sm;
     SeqInfo si;
     if (!locate_chunk(blockIdx.x, a.cu_seqlens, a.num_seqs, a.seq_len, CH, si)) return;
-    const int g = blockIdx.y, G = a.G, R = a.R, H = G * R;
+    const int g = blockIdx.y, G = a.G;
     const long cid = blockIdx.x;
     const int lane = lane_id(), wv = wave_id(), l16 = lane & 15, lg = lane >> 4;
-    // LDS block permutation of the K and q tiles: a fragment read covers 16 consecutive rows at one 16-byte block, so
+    // LDS block permutation of the K tile: a fragment read covers 16 consecutive rows at one 16-byte block, so
     // the block is XORed with row & 15 (rows of >= 16 blocks) or (row >> 1) & 7 (8 blocks: two rows share a 256-byte
     // bank window), putting the 16 rows on 16 distinct bank groups.
     const auto sw_row = [](int row) { return ROWB / 16 >= 16 ? (row & 15) : ((row >> 1) & 7); };
@@ -59,12 +55,6 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(GdnArgs a) {
     const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.k) + (si.tok0 * G + g) * D * ES,
                                 (uint32_t)((long)si.len * G * D * ES));
     stage_tile(rk, (uint32_t)(G * D * ES), ROWB, sm.K, CH * ROWB, wv, nw, lane, sw_row, 1 << 30);
-    auto stage_q = [&](int r) {
-        const rsrc_t rq = make_rsrc(reinterpret_cast<const char*>(a.q) + (si.tok0 * H + (long)g * R + r) * D * ES,
-                                    (uint32_t)((long)si.len * H * D * ES));
-        stage_tile(rq, (uint32_t)(H * D * ES), ROWB, sm.Q, CH * ROWB, wv, nw, lane, sw_row, 1 << 30);
-    };
-    stage_q(0);
     if (wv == 0) {
         float gv = 0.f, bv = 0.f;
         if (lane < si.len) {
@@ -88,38 +78,6 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(GdnArgs a) {
         const int row = 16 * tile + l16;
         return lds16(base, row * ROWB + (((4 * ks + lg) ^ sw_row(row)) << 4));
     };
-
-    // attn_r^T = K q_r^T (rows t' = key, cols t = query), masked to t' <= t, decayed and scaled; the 6 tiles above
-    // the diagonal are zero.
-    for (int r = 0; r < R; ++r) {
-        if (r > 0) {
-            __syncthreads();
-            stage_q(r);
-            wait_vmem_all();
-            __syncthreads();
-        }
-        for (int tile = wv; tile < 16; tile += nw) {
-            const int at = tile >> 2, bt = tile & 3;     // at: key tile (rows), bt: query tile (cols)
-            const int t = 16 * bt + l16;
-            T* dst = reinterpret_cast<T*>(a.ws_attn) + ((cid * H + (long)g * R + r) * CH + t) * CH + 16 * at + 4 * lg;
-            if (at > bt) {
-                store4<E>(dst, 0.f, 0.f, 0.f, 0.f);
-                continue;
-            }
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int ks = 0; ks < NKD; ++ks) mma<E>(acc, frag(sm.K, at, ks), frag(sm.Q, bt, ks));
-            float o[4];
-            const float gt = sm.gc[t];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int tk = 16 * at + 4 * lg + i;
-                o[i] = tk <= t ? a.scale * __expf(gt - sm.gc[tk]) * acc[i] : 0.f;
-            }
-            store4<E>(dst, o[0], o[1], o[2], o[3]);
-        }
-    }
-    __syncthreads();                                     // the q region becomes A
 
     // A = strict_lower(beta_r e^{gc_r - gc_c} (K K^T)_{rc}). K K^T is symmetric: tile (rt, ct) with rt <= ct read
     // in transposed form fills rows 16ct.., columns 16rt.. of A.
@@ -167,7 +125,7 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(GdnArgs a) {
         const float bj = sm.beta[16 * j + l16];
         auto put = [&](int i, const f32x4& v) {            // block (i, j) of T' from an accumulator tile
 #pragma unroll
-            for (int e = 0; e < 4; ++e) Tg[(16 * i + 4 * lg + e) * CH + 16 * j + l16] = E::from_f(v[e] * bj);
+            for (int e = 0; e < 4; ++e) Tg[tfrag_index<E>(16 * i + 4 * lg + e, 16 * j + l16)] = E::from_f(v[e] * bj);
         };
         // A fragment of a 16 x 16 fp32 block of an LDS matrix M (rows r0.., columns c0..): lane row l16, k = 4 lg ..
         auto afrag = [&](const float (*M)[CH + 4], int r0, int c0) {

@@ -11,14 +11,15 @@
 //   gdn_combine_kernel  per (sequence, KV head, 16-column strip): X_0 = S0, X_{p+1} = Phi_p X_p + N_p in fp32
 //                       (bf16 runs: Psi = Phi - cI in bf16 times X split into bf16 high and low parts, plus the exact
 //                       c X term), the entry state of every segment.
-//   gdn_seg_kernel<.., OUT=true>   (output) per (segment, KV head, column group, query head): the chunk map with
-//                       outputs from the segment's entry state; the last segment of a sequence writes the final state.
-//
+//   gdn_seg_kernel<.., OUT=true>   (output) per (segment, KV head, column group): the chunk map with outputs of all R
+//                       query heads of the KV head from the segment's entry state; the last segment of a sequence
+//                       writes the final state.
 // Inside a workgroup each wave owns 16 state columns (one 16-column MFMA tile) for all D rows, held in registers as
 // MFMA accumulators, so the per-chunk chain runs inside the wave with no exchange between waves:
 //   K S, q S      A = K / q rows (LDS),     B = S packed from the accumulators
-//   T' y          A = T' rows (LDS),        B = the Y accumulators after y = V - e^{gc} Y
-//   attn v_new    A = attn rows (LDS),      B = the v_new accumulators
+//   T' y          A = T' fragments (LDS),   B = the Y accumulators after y = V - e^{gc} Y
+//   attn_r        A = K rows, B = q_r rows (LDS): attn_r^T tiles, masked and decayed into attn_r's A fragments
+//   attn_r v_new  A = attn_r fragments (LDS, written by the waves),  B = the v_new accumulators
 //   K^T v'        A = K^T through transposing reads of the K tile in LDS,  B = the v_new accumulators scaled by
 //                 e^{gc_last - gc}
 // An accumulator tile holds rows 4g..4g+3 of its 16 rows in lane group g, while an MFMA operand fragment holds VEC
@@ -26,10 +27,15 @@
 // permutation prow(tile, m): rows 4g..4g+3 of the HP = VEC/4 tiles of one K fragment are that fragment's VEC values
 // of group g, so accumulators feed the next product directly. A rows are read through the same permutation.
 //
-// The chunk operands all waves share (K, q of the workgroup's query head, T', attn, gc, V) are staged in LDS with
-// buffer_load ... lds (no registers, out-of-range rows read as zero); bf16 runs double-buffer the stage so chunk c+1
-// is in flight while chunk c is computed. LDS rows are swizzled by 16-byte blocks (swz) so that the fragment reads
-// of 16 rows hit distinct banks.
+// The chunk operands all waves share (K, q, T', gc, V) are staged in LDS with buffer_load ... lds (no registers,
+// out-of-range rows read as zero); bf16 runs double-buffer the stage so chunk c+1 is in flight while chunk c is
+// computed. K, q and V rows are swizzled by 16-byte blocks (swz) so that the fragment reads of 16 rows hit distinct
+// banks; T' and attn are kept in fragment order (tfrag_index), one contiguous 1 KB per fragment.
+//
+// The output scan runs the R query heads of a KV head inside one workgroup: the chunk's K S, T' y and K^T v' products
+// are shared, and per query head the waves form the causal block attn_r = scale (q_r K^T e^{gc_i - gc_j})[i >= j]
+// (its nonzero A fragments, one per wave) into LDS, then o_r = scale e^{gc} q_r S + attn_r v_new. bf16 runs double
+// buffer q so that head r + 1 loads while head r is computed, and write o_r while head r + 1 is computed.
 #include <type_traits>
 
 #include "bf_common.h"
@@ -49,15 +55,22 @@ constexpr int WG_COLS = 128;
 constexpr int SEG_THREADS = WG_COLS / WCOLS * 64;
 constexpr int SEG_WAVES_PER_EU = SEG_THREADS / 256;
 
-// 16-byte block permutation of the 64 x 64 T' and attn tiles. bf16 rows are 128 bytes (8 blocks, two rows per 256-byte
-// bank window); a fragment read covers the 16 rows tp + {0..3, 8..11, 16..19, 24..27} at one block, and bits 1, 3
-// and 4 of those rows tell apart the 8 rows of each row parity, so each half-window gets 8 distinct blocks. The value
-// does not change with the tile offsets tp (multiples of 4 and 32 only touch bits 2 and 5+). fp32 rows (16 blocks)
-// keep swz.
+// Nonzero A fragments (token tile b, K step ks) of the causal 64 x 64 attn block: K step ks covers tokens KF*ks ..
+// KF*ks + KF - 1, which reach the tile's last token 16b + 15 for ks <= (16b + 15) / KF. Fragments are numbered tile by
+// tile (attn_fidx); the others are all zero and skipped.
 template <class E>
-__device__ __forceinline__ int swz_t(int row, int nblk) {
-    if constexpr (E::VEC == 8) return ((row >> 1) & 1) | (((row >> 3) & 1) << 1) | (((row >> 4) & 1) << 2);
-    else return swz<E>(row, nblk);
+__device__ __forceinline__ constexpr int attn_nks(int b) { return (16 * b + 15) / E::KF + 1; }
+template <class E>
+__device__ __forceinline__ constexpr int attn_fidx(int b, int ks) {
+    int n = 0;
+    for (int bb = 0; bb < b; ++bb) n += attn_nks<E>(bb);
+    return n + ks;
+}
+template <class E>
+constexpr int attn_frags() {
+    int n = 0;
+    for (int b = 0; b < SC / 16; ++b) n += (16 * b + 15) / E::KF + 1;
+    return n;
 }
 
 template <class E>
@@ -66,19 +79,22 @@ __device__ __forceinline__ int prow(int tile, int m) {
     return KF * (tile / HP) + VEC * (m >> 2) + 4 * (tile % HP) + (m & 3);
 }
 
-template <class E, int D, bool OUT>
+// Per-chunk stage: K, gc and (TP) T'.
+template <class E, int D, bool TP>
 struct __align__(16) ChunkLds {
     typename E::T K[SC * D];
-    typename E::T Tp[SC * SC];
-    typename E::T At[OUT ? SC * SC : 8];
+    typename E::T Tp[TP ? SC * SC : 8];
     float gc[SC];
 };
-// Single-buffered operands: q of the workgroup's query head (bf16 output scan) and the V columns of the workgroup;
-// each is reloaded for the next chunk as soon as the current chunk has consumed it.
-template <class E, int D, bool QL, int VW>
+// Operands outside the chunk stage: NQ q buffers (bf16 output scan), the V columns of the workgroup, the attn
+// fragments of one query head (NAT elements, output scan) and (TP) a single T' buffer (bf16 output scan). V and T' are
+// reloaded for the next chunk as soon as the current chunk has consumed them.
+template <class E, int D, int NQ, int VW, int NAT, bool TP>
 struct __align__(16) OnceLds {
-    typename E::T Q[QL ? SC * D : 8];
+    typename E::T Q[NQ > 0 ? NQ : 1][NQ > 0 ? SC * D : 8];
     typename E::T V[SC * VW];
+    typename E::T At[NAT > 0 ? NAT : 8];
+    typename E::T Tp[TP ? SC * SC : 8];
 };
 struct __align__(16) NoLds {
     float pad[4];
@@ -179,6 +195,7 @@ struct SegCfg {
     static constexpr int NW = (COLS < WG_COLS ? COLS : WG_COLS) / WCOLS;  // waves per workgroup
     static constexpr int NCG = COLS / (NW * WCOLS);                 // column groups (workgroups per head)
     static constexpr bool DBUF = E::VEC == 8;                       // bf16: double-buffered stage
+    static constexpr bool TPS = !(OUT && DBUF);                      // T' in the chunk stage (else single-buffered)
 };
 
 }  // namespace
@@ -210,22 +227,21 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
     constexpr int NTD = D / 16, NTC = SC / 16, NKD = D / KF, NKC = SC / KF;
     constexpr int ROWB = D * ES, TROWB = SC * ES;
     constexpr int NW = Cfg::NW, NCG = Cfg::NCG;
-    constexpr bool DBUF = Cfg::DBUF;
-    constexpr bool QL = OUT && ES == 2;                  // q staged in LDS (bf16); fp32 reads it from global
+    constexpr bool DBUF = Cfg::DBUF, TPS = Cfg::TPS;
+    constexpr bool QL = OUT && DBUF;                     // q staged in LDS, two buffers (bf16); fp32 reads it from global
     constexpr int VW = NW * WCOLS, VROWB = VW * ES;      // V tile: the workgroup's columns
-    using CL = ChunkLds<E, D, OUT>;
-    using OL = OnceLds<E, D, QL, VW>;
+    constexpr int NFR = OUT ? attn_frags<E>() : 0;       // nonzero attn fragments of one query head
+    using CL = ChunkLds<E, D, TPS>;
+    using OL = OnceLds<E, D, QL ? 2 : 0, VW, NFR * 64 * VEC, !TPS>;
     __shared__ CL cl0;
     __shared__ typename std::conditional<DBUF, CL, NoLds>::type cl1;
     __shared__ OL ol;
 
     const int G = a.G, R = a.R, H = G * R;
-    const int per = NCG * (OUT ? R : 1);
     const int xcd = blockIdx.x % NXCD, local = blockIdx.x / NXCD;
-    const int grp = xcd + NXCD * (local / per), sub = local % per;
+    const int grp = xcd + NXCD * (local / NCG), cg = local % NCG;
     if (grp >= a.max_segs * G) return;
     const int g = grp % G, sid = grp / G;
-    const int cg = sub % NCG, r = sub / NCG;
     SegInfo sg;
     if (!locate_segment(a, sid, sg)) return;
     if (!OUT && sg.p == sg.nseg - 1) return;
@@ -235,23 +251,21 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
     const int j0 = cb + wv * WCOLS;                      // first of this wave's columns
     const bool phi_part = !OUT && j0 >= D;
     const int jc = phi_part ? j0 - D : j0;               // column inside the D x D block
-    const int h = g * R + r;
     const int n = sg.n;
     const int v_blk = OUT ? VROWB / 16 : (cb < D ? ((D - cb < VW ? D - cb : VW) * ES) / 16 : 0);  // loaded V blocks
 
     // per-lane address parts
-    constexpr int NBLK = ROWB / 16, TNBLK = TROWB / 16;
+    constexpr int NBLK = ROWB / 16;
     constexpr bool FAST = ES == 2 && NBLK >= 16;           // 4-bit swizzle of the K / q tiles
     constexpr int NX = FAST ? 4 : 2;
     const int lt = VEC * (l16 >> 2) + (l16 & 3);         // fragment row offset inside a tile
     // K / q fragment of K index group (ks, lg) at row tp(tile) + lt: block (4ks + lg) ^ swz(row), and the swizzle of
     // those rows depends on the lane only, so the block is 4*NX*(ks / NX) + xb[ks % NX]
-    const int sl = swz<E>(lt, NBLK), tsl = swz_t<E>(lt, TNBLK);
-    int kq_base[NX], t_base[2];
+    const int sl = swz<E>(lt, NBLK);
+    int kq_base[NX];
 #pragma unroll
     for (int c = 0; c < NX; ++c) kq_base[c] = lt * ROWB + 16 * (4 * (c ^ (sl >> 2)) + (lg ^ (sl & 3)));
-#pragma unroll
-    for (int c = 0; c < 2; ++c) t_base[c] = lt * TROWB + 16 * (4 * (c ^ (tsl >> 2)) + (lg ^ (tsl & 3)));
+    const int fo = lane * 16;                            // lane offset inside a 1 KB fragment-order piece
     // K^T A fragments (rows tp(td) + lt, K index = tokens KF*ks + VEC*lg + e).
     // bf16: two transposing reads per fragment; lane (e, q) = (l16/4, l16%4) of group lg reads the 4 state rows
     // tp(td) + 8q .. +3 of token 32ks + 8lg + 4h + e, so lane 4q + r collects tokens 8lg + 4h + 0..3 of row
@@ -324,35 +338,34 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
         return (int)(rem < SC ? rem : SC);
     };
     const auto sw_row = [](int row) { return swz<E>(row, ROWB / 16); };
-    const auto sw_t = [](int row) { return swz_t<E>(row, TROWB / 16); };
     const auto sw_v = [](int row) { return swz_v(row, VROWB / 16); };
-    auto load_chunk = [&](auto& cl, int c) {
+    const auto sw_lin = [](int) { return 0; };
+    auto load_tp = [&](T* dst, int c) {                  // T' of chunk c: a linear copy of its fragment-order block
+        const long cid = sg.cid0 + c;
+        const rsrc_t rt = make_rsrc(reinterpret_cast<const char*>(a.ws_T) + (cid * G + g) * SC * SC * ES,
+                                    (uint32_t)(SC * SC * ES));
+        stage_tile(rt, (uint32_t)TROWB, TROWB, dst, SC * TROWB, wv, NW, lane, sw_lin, 1 << 30);
+    };
+    auto load_chunk = [&](CL& cl, int c) {
         const long t0 = chunk_tok0(c);
         const int len = chunk_len(c);
         const long cid = sg.cid0 + c;
         const rsrc_t rk = make_rsrc(reinterpret_cast<const char*>(a.k) + (t0 * G + g) * D * ES,
                                     (uint32_t)((long)len * G * D * ES));
         stage_tile(rk, (uint32_t)(G * D * ES), ROWB, cl.K, SC * ROWB, wv, NW, lane, sw_row, 1 << 30);
-        const rsrc_t rt = make_rsrc(reinterpret_cast<const char*>(a.ws_T) + (cid * G + g) * SC * SC * ES,
-                                    (uint32_t)(SC * SC * ES));
-        stage_tile(rt, (uint32_t)TROWB, TROWB, cl.Tp, SC * TROWB, wv, NW, lane, sw_t, 1 << 30);
-        if constexpr (OUT) {
-            const rsrc_t ra = make_rsrc(reinterpret_cast<const char*>(a.ws_attn) + (cid * H + h) * SC * SC * ES,
-                                        (uint32_t)(SC * SC * ES));
-            stage_tile(ra, (uint32_t)TROWB, TROWB, cl.At, SC * TROWB, wv, NW, lane, sw_t, 1 << 30);
-        }
+        if constexpr (TPS) load_tp(cl.Tp, c);
         if (wv == 0 && lane < SC / 4) {
             const rsrc_t rg = make_rsrc(a.ws_gcum + (cid * G + g) * SC, SC * 4);
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rg, (__attribute__((address_space(3))) void*)cl.gc, 16,
                                                      lane * 16, 0, 0, 0);
         }
     };
-    auto load_q = [&](int c) {
+    auto load_q = [&](int buf, int c, int r) {           // q of query head r of chunk c into buffer buf (bf16)
         if constexpr (QL) {
             const long t0 = chunk_tok0(c);
-            const rsrc_t rq = make_rsrc(reinterpret_cast<const char*>(a.q) + (t0 * H + h) * D * ES,
+            const rsrc_t rq = make_rsrc(reinterpret_cast<const char*>(a.q) + (t0 * H + (long)g * R + r) * D * ES,
                                         (uint32_t)((long)chunk_len(c) * H * D * ES));
-            stage_tile(rq, (uint32_t)(H * D * ES), ROWB, ol.Q, SC * ROWB, wv, NW, lane, sw_row, 1 << 30);
+            stage_tile(rq, (uint32_t)(H * D * ES), ROWB, ol.Q[buf], SC * ROWB, wv, NW, lane, sw_row, 1 << 30);
         }
     };
     auto load_v = [&](int c) {
@@ -364,15 +377,199 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
         }
     };
 
+    // acc = X S_stored over the D state rows for the 64 x D operand X whose A fragment (K step ks, token tile tt)
+    // frag(ks, tt) returns; the fragments of step ks + 1 are read while step ks multiplies, and the scheduling
+    // barrier keeps the compiler from hoisting every step's reads (and their registers) to the front.
+    auto times_s = [&](auto&& frag, f32x4 (&acc)[NTC][NJ]) {
+#pragma unroll
+        for (int tt = 0; tt < NTC; ++tt)
+#pragma unroll
+            for (int jt = 0; jt < NJ; ++jt) acc[tt][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        uint4 af[NTC];
+#pragma unroll
+        for (int tt = 0; tt < NTC; ++tt) af[tt] = frag(0, tt);
+#pragma unroll
+        for (int ks = 0; ks < NKD; ++ks) {
+            uint4 nf[NTC];
+            if (ks + 1 < NKD) {
+#pragma unroll
+                for (int tt = 0; tt < NTC; ++tt) nf[tt] = frag(ks + 1, tt);
+            }
+            uint4 sb[NJ];
+#pragma unroll
+            for (int jt = 0; jt < NJ; ++jt) sb[jt] = pack_b<E>(S[ks * HP][jt], S[ks * HP + HP - 1][jt]);
+#pragma unroll
+            for (int tt = 0; tt < NTC; ++tt)
+#pragma unroll
+                for (int jt = 0; jt < NJ; ++jt) mma<E>(acc[tt][jt], af[tt], sb[jt]);
+            if (ks + 1 < NKD) {
+#pragma unroll
+                for (int tt = 0; tt < NTC; ++tt) af[tt] = nf[tt];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    auto kq_off = [&](int ks, int row0) { return kq_base[ks % NX] + row0 * ROWB + 64 * NX * (ks / NX); };
+
+    // o tiles of query head h for chunk rows t0 .. t0 + len - 1. With bf16 inputs each 16 x 16 tile is transposed
+    // inside every quad of lanes (l16 = 4qa + qb holds rows VEC*lg + 0..3 of column 4qa + qb and gets row VEC*lg + qb
+    // of columns 4qa .. 4qa + 3): a lane-dependent rotation, a rotation across the quad (DPP quad_perm: register k read
+    // from lane (qb - k) mod 4) and the inverse lane-dependent rotation. A lane then writes 4 consecutive columns with
+    // one store (8 bytes bf16, 16 bytes fp32) instead of four 2- or 4-byte stores. fp32-input scans (register-bound at
+    // D = 256) store the accumulator layout directly.
+    constexpr int OS = BO ? 2 : 4;
+    using OPk = typename std::conditional<BO, uint2, uint4>::type;   // one lane's 4 columns of one row
+    auto pack_o = [&](const f32x4 (&O)[NTC][NJ], OPk (&P)[NTC][NJ]) {
+        const int qb4 = l16 & 3;
+        auto pick = [&](const float (&x)[4], int idx) {
+            const float lo = (idx & 1) ? x[1] : x[0], hi = (idx & 1) ? x[3] : x[2];
+            return (idx & 2) ? hi : lo;
+        };
+        auto dpp = [](float x, auto ctrl) {
+            return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), decltype(ctrl)::value, 0xF, 0xF, true));
+        };
+#pragma unroll
+        for (int tt = 0; tt < NTC; ++tt)
+#pragma unroll
+            for (int jt = 0; jt < NJ; ++jt) {
+                const float x[4] = {O[tt][jt][0], O[tt][jt][1], O[tt][jt][2], O[tt][jt][3]};
+                float u[4], z[4], w[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) u[k] = pick(x, (k + qb4) & 3);
+                z[0] = u[0];
+                z[1] = dpp(u[1], std::integral_constant<int, 0x93>());   // quad_perm [3, 0, 1, 2]
+                z[2] = dpp(u[2], std::integral_constant<int, 0x4E>());   // quad_perm [2, 3, 0, 1]
+                z[3] = dpp(u[3], std::integral_constant<int, 0x39>());   // quad_perm [1, 2, 3, 0]
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) w[jj] = pick(z, (qb4 - jj) & 3);
+                if constexpr (BO) P[tt][jt] = make_uint2(pack_bf16x2(w[0], w[1]), pack_bf16x2(w[2], w[3]));
+                else P[tt][jt] = make_uint4(__float_as_uint(w[0]), __float_as_uint(w[1]), __float_as_uint(w[2]),
+                                            __float_as_uint(w[3]));
+            }
+    };
+    auto write_o = [&](const OPk (&P)[NTC][NJ], long t0, int len, int h) {
+        const rsrc_t ro = make_rsrc(reinterpret_cast<char*>(a.o) + (t0 * H + h) * (long)D * OS,
+                                    (uint32_t)((long)len * H * D * OS));
+        const int row_l = VEC * lg + (l16 & 3);          // the lane's row inside a tile after the transpose
+#pragma unroll
+        for (int tt = 0; tt < NTC; ++tt)
+#pragma unroll
+            for (int jt = 0; jt < NJ; ++jt) {
+                const int row = tpart<E>(tt) + row_l;
+                // rows past the end of a partial chunk get an offset past the descriptor's range and are dropped
+                const uint32_t off = row < len ? (uint32_t)((row * H * D + jc + 16 * jt + 4 * (l16 >> 2)) * OS)
+                                               : 0xFFFFFFF0u;
+                if constexpr (BO) {
+                    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+                    const u32x2 v2 = {P[tt][jt].x, P[tt][jt].y};
+                    __builtin_amdgcn_raw_buffer_store_b64(v2, ro, off, 0, 0);
+                } else {
+                    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+                    const u32x4 v4 = {P[tt][jt].x, P[tt][jt].y, P[tt][jt].z, P[tt][jt].w};
+                    __builtin_amdgcn_raw_buffer_store_b128(v4, ro, off, 0, 0);
+                }
+            }
+    };
+    auto store_o = [&](const f32x4 (&O)[NTC][NJ], long t0, int len, int h) {
+        if constexpr (ES == 4) {
+            const uint32_t o_lane = (uint32_t)((VEC * lg * H * D + l16) * OS);
+#pragma unroll
+            for (int tt = 0; tt < NTC; ++tt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int row = tpart<E>(tt) + i;
+                    const int nrow = len > row ? len - row : 0;
+                    const rsrc_t ro = make_rsrc(reinterpret_cast<char*>(a.o) + ((t0 + row) * H + h) * (long)D * OS,
+                                                (uint32_t)(nrow * H * D * OS));
+#pragma unroll
+                    for (int jt = 0; jt < NJ; ++jt) {
+                        const uint32_t voff = o_lane + (uint32_t)((jc + 16 * jt) * OS);
+                        if constexpr (BO) __builtin_amdgcn_raw_buffer_store_b16(f2bf(O[tt][jt][i]), ro, voff, 0u, 0);
+                        else __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(O[tt][jt][i]), ro, voff, 0u, 0);
+                    }
+                }
+        } else {
+            OPk P[NTC][NJ];
+            pack_o(O, P);
+            write_o(P, t0, len, h);
+        }
+    };
+
+    // attn fragment f of one query head: the accumulators of K tiles ks*HP + h (rows = keys t') times q tile b
+    // (columns = queries t) are attn^T, and lane l16 of group lg holds query t = tp(b) + lt with keys
+    // t' = KF*ks + VEC*lg + 4h + i, i.e. the A fragment (b, ks) of o = attn v_new once masked to t' <= t and scaled by
+    // scale e^{gc_t - gc_t'}. q: LDS (bf16) or global (fp32).
+    auto attn_frag = [&](int f, const char* Kb, const char* Qb, const rsrc_t& rq, const float* gcl, char* Atb) {
+        int b = 0, ks = f;
+#pragma unroll
+        for (int i = 0; i < NTC - 1; ++i)
+            if (ks >= attn_nks<E>(b)) {
+                ks -= attn_nks<E>(b);
+                ++b;
+            }
+        const int qrow = tpart<E>(b), krow = KF * ks;
+        f32x4 acc[HP];
+#pragma unroll
+        for (int hh = 0; hh < HP; ++hh) acc[hh] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < NKD; ++kk) {
+            uint4 qf;
+            if constexpr (QL) qf = lds16(Qb, kq_off(kk, qrow));
+            else qf = buf_ld16(rq, (uint32_t)(((qrow + lt) * H * D + KF * kk + VEC * lg) * ES));
+#pragma unroll
+            for (int hh = 0; hh < HP; ++hh) mma<E>(acc[hh], lds16(Kb, kq_off(kk, krow + 4 * hh)), qf);
+        }
+        const int t = qrow + lt;
+        const float gt = gcl[t];
+        f32x4 m[HP];
+#pragma unroll
+        for (int hh = 0; hh < HP; ++hh) {
+            const float4 gk = *reinterpret_cast<const float4*>(&gcl[krow + VEC * lg + 4 * hh]);
+            const float gkv[4] = {gk.x, gk.y, gk.z, gk.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int tk = krow + VEC * lg + 4 * hh + i;
+                m[hh][i] = tk <= t ? a.scale * __expf(gt - gkv[i]) * acc[hh][i] : 0.f;
+            }
+        }
+        *reinterpret_cast<uint4*>(Atb + f * 1024 + fo) = pack_b<E>(m[0], m[HP - 1]);
+    };
+
+    int qb = 0;                                          // q buffer of the current query head (bf16)
+    // bf16: the o tiles of the last DEP query heads (pk), written DEP heads later so that the stores
+    // complete under the MFMAs of the heads in between (pq_h < 0: empty entry). One head of delay measured best at
+    // T = 32768, G = 4, R = 6 (364 us per output launch; two heads: 390 us).
+    constexpr int DEP = 1;
+    f32x4 pk[DEP][NTC][NJ];
+    long pq_t0[DEP];
+    int pq_len[DEP], pq_h[DEP];
+#pragma unroll
+    for (int d = 0; d < DEP; ++d) {
+        pq_t0[d] = 0;
+        pq_len[d] = 0;
+        pq_h[d] = -1;
+    }
+    auto flush_oldest = [&]() {                          // write entry 0 and move the others down
+        if (pq_h[0] >= 0) store_o(pk[0], pq_t0[0], pq_len[0], pq_h[0]);
+#pragma unroll
+        for (int d = 0; d + 1 < DEP; ++d) {
+#pragma unroll
+            for (int tt = 0; tt < NTC; ++tt)
+#pragma unroll
+                for (int jt = 0; jt < NJ; ++jt) pk[d][tt][jt] = pk[d + 1][tt][jt];
+            pq_t0[d] = pq_t0[d + 1];
+            pq_len[d] = pq_len[d + 1];
+            pq_h[d] = pq_h[d + 1];
+        }
+        pq_h[DEP - 1] = -1;
+    };
     // next: the idle stage buffer, loaded with chunk cn by DMA once this chunk's V fragments are in registers. The
     // compiler waits for every outstanding DMA before a transposing LDS read (ds_read_b64_tr_b16), so the V reads
     // come first and the copy then overlaps phases 1 to 3 instead of phase 1 only.
     auto compute = [&](const CL& cl, int c, bool prefetch, CL* next) {
         const int cn = c + 1 < count ? c + 1 : c;
         const char* Kb = reinterpret_cast<const char*>(cl.K);
-        const char* Tb = reinterpret_cast<const char*>(cl.Tp);
-        const char* Ab = reinterpret_cast<const char*>(cl.At);
-        const char* Qb = reinterpret_cast<const char*>(ol.Q);
+        const char* Tb = reinterpret_cast<const char*>(TPS ? cl.Tp : ol.Tp);
         const char* Vb = reinterpret_cast<const char*>(ol.V);
         uint4 vf[NKC][NJ];
         auto read_vf = [&]() {
@@ -412,62 +609,9 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
             egc[tt][3] = sc * __expf(gq.w);
         }
 
-        // phase 1: Y = K S_stored, O = q S_stored. A fragments of step ks + 1 are read while step ks multiplies; the
-        // scheduling barrier keeps the compiler from hoisting every step's reads (and their registers) to the front.
-        f32x4 Y[NTC][NJ], O[OUT ? NTC : 1][NJ];
-#pragma unroll
-        for (int tt = 0; tt < NTC; ++tt)
-#pragma unroll
-            for (int jt = 0; jt < NJ; ++jt) {
-                Y[tt][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
-                if constexpr (OUT) O[tt][jt] = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
-        // fp32 output scan: q fragments straight from global memory (rows past the end read as zero)
-        const rsrc_t rqg = make_rsrc(reinterpret_cast<const char*>(a.q) + (chunk_tok0(c) * H + h) * D * ES,
-                                     (uint32_t)(OUT && !QL ? (long)chunk_len(c) * H * D * ES : 0));
-        auto read_kq = [&](int ks, uint4 (&ak)[NTC], uint4 (&aq)[NTC]) {
-#pragma unroll
-            for (int tt = 0; tt < NTC; ++tt) {
-                const int off = kq_base[ks % NX] + tpart<E>(tt) * ROWB + 64 * NX * (ks / NX);
-                ak[tt] = lds16(Kb, off);
-                if constexpr (QL) aq[tt] = lds16(Qb, off);
-                else if constexpr (OUT)
-                    aq[tt] = buf_ld16(rqg, (uint32_t)(((tpart<E>(tt) + lt) * H * D + KF * ks + VEC * lg) * ES));
-            }
-        };
-        uint4 ak[NTC], aq[NTC];
-        read_kq(0, ak, aq);
-#pragma unroll
-        for (int ks = 0; ks < NKD; ++ks) {
-            uint4 nk[NTC], nq[NTC];
-            if (ks + 1 < NKD) read_kq(ks + 1, nk, nq);
-            uint4 sb[NJ];
-#pragma unroll
-            for (int jt = 0; jt < NJ; ++jt) sb[jt] = pack_b<E>(S[ks * HP][jt], S[ks * HP + HP - 1][jt]);
-#pragma unroll
-            for (int tt = 0; tt < NTC; ++tt) {
-#pragma unroll
-                for (int jt = 0; jt < NJ; ++jt) mma<E>(Y[tt][jt], ak[tt], sb[jt]);
-                if constexpr (OUT) {
-#pragma unroll
-                    for (int jt = 0; jt < NJ; ++jt) mma<E>(O[tt][jt], aq[tt], sb[jt]);
-                }
-            }
-            if (ks + 1 < NKD) {
-#pragma unroll
-                for (int tt = 0; tt < NTC; ++tt) {
-                    ak[tt] = nk[tt];
-                    aq[tt] = nq[tt];
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if constexpr (QL) {
-            if (prefetch) {
-                lds_barrier();                     // every wave is done with q of this chunk (its LDS reads)
-                load_q(cn);
-            }
-        }
+        // phase 1: Y = K S_stored
+        f32x4 Y[NTC][NJ];
+        times_s([&](int ks, int tt) { return lds16(Kb, kq_off(ks, tpart<E>(tt))); }, Y);
 
         // phase 2: v_new = T' (V - e^{gc} K S) = T' V + T' (-sc e^{gc} Y). The T' fragments (and, single-buffered,
         // the V fragments) are read first, so their LDS latency is covered by the scaling of Y.
@@ -475,7 +619,7 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
 #pragma unroll
         for (int ks = 0; ks < NKC; ++ks)
 #pragma unroll
-            for (int tt = 0; tt < NTC; ++tt) tf[ks][tt] = lds16(Tb, t_base[ks & 1] + tpart<E>(tt) * TROWB + 128 * (ks >> 1));
+            for (int tt = 0; tt < NTC; ++tt) tf[ks][tt] = lds16(Tb, (ks * NTC + tt) * 1024 + fo);
         if constexpr (!DBUF) read_vf();
         f32x4 Vn[NTC][NJ];
 #pragma unroll
@@ -500,72 +644,86 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (prefetch) {
-            lds_barrier();                         // every wave is done with V of this chunk (its LDS reads)
-            load_v(cn);
+        if constexpr (!OUT) {
+            if (prefetch) {
+                lds_barrier();                     // every wave is done with V of this chunk (its LDS reads)
+                load_v(cn);
+            }
         }
 
-        // phase 3: o = scale e^{gc} (q S) + attn v_new (attn fragments read before the scaling of O)
+        // phase 3, per query head r: o_r = scale e^{gc} (q_r S) + attn_r v_new
         if constexpr (OUT) {
-            uint4 af[NKC][NTC];
+            const long t0 = chunk_tok0(c);
+            const int len = chunk_len(c);
+            char* Atb = reinterpret_cast<char*>(ol.At);
+            uint4 vb[NKC][NJ];
 #pragma unroll
             for (int ks = 0; ks < NKC; ++ks)
 #pragma unroll
-                for (int tt = 0; tt < NTC; ++tt)
-                    af[ks][tt] = lds16(Ab, t_base[ks & 1] + tpart<E>(tt) * TROWB + 128 * (ks >> 1));
-#pragma unroll
-            for (int tt = 0; tt < NTC; ++tt)
-#pragma unroll
-                for (int jt = 0; jt < NJ; ++jt)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) O[tt][jt][i] *= a.scale * egc[tt][i];   // egc carries sc
-#pragma unroll
-            for (int ks = 0; ks < NKC; ++ks) {
-                uint4 vb[NJ];
-#pragma unroll
-                for (int jt = 0; jt < NJ; ++jt) vb[jt] = pack_b<E>(Vn[ks * HP][jt], Vn[ks * HP + HP - 1][jt]);
-#pragma unroll
-                for (int tt = 0; tt < NTC; ++tt)
-#pragma unroll
-                    for (int jt = 0; jt < NJ; ++jt) mma<E>(O[tt][jt], af[ks][tt], vb[jt]);
-            }
-            constexpr int OS = BO ? 2 : 4;
-            const long t0 = chunk_tok0(c);
-            const int len = chunk_len(c);
-            const uint32_t o_lane = (uint32_t)((VEC * lg * H * D + l16) * OS);
-            auto put = [&](rsrc_t ro, uint32_t voff, uint32_t soff, float x) {
-                if constexpr (BO) __builtin_amdgcn_raw_buffer_store_b16(f2bf(x), ro, voff, soff, 0);
-                else __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(x), ro, voff, soff, 0);
-            };
-            if (len == SC) {
-                // whole chunk: one descriptor, the row and column parts go to the scalar offset
-                const rsrc_t ro = make_rsrc(reinterpret_cast<char*>(a.o) + (t0 * H + h) * (long)D * OS,
-                                            (uint32_t)((long)SC * H * D * OS));
-#pragma unroll
-                for (int tt = 0; tt < NTC; ++tt)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i)
-#pragma unroll
-                        for (int jt = 0; jt < NJ; ++jt)
-                            put(ro, o_lane, (uint32_t)(((tpart<E>(tt) + i) * H * D + jc + 16 * jt) * OS),
-                                O[tt][jt][i]);
-            } else {
-                // last chunk of a sequence: one descriptor per row offset, so rows past the end are dropped
-#pragma unroll
-                for (int tt = 0; tt < NTC; ++tt)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int row = tpart<E>(tt) + i;
-                        const int nrow = len > row ? len - row : 0;
-                        const rsrc_t ro = make_rsrc(
-                            reinterpret_cast<char*>(a.o) + ((t0 + row) * H + h) * (long)D * OS,
-                            (uint32_t)(nrow * H * D * OS));
-#pragma unroll
-                        for (int jt = 0; jt < NJ; ++jt)
-                            put(ro, o_lane + (uint32_t)((jc + 16 * jt) * OS), 0u, O[tt][jt][i]);
+                for (int jt = 0; jt < NJ; ++jt) vb[ks][jt] = pack_b<E>(Vn[ks * HP][jt], Vn[ks * HP + HP - 1][jt]);
+            for (int r = 0; r < R; ++r) {
+                const int h = g * R + r;
+                const char* Qb = reinterpret_cast<const char*>(ol.Q[QL ? qb : 0]);
+                const rsrc_t rq = make_rsrc(reinterpret_cast<const char*>(a.q) + (t0 * H + h) * D * ES,
+                                            (uint32_t)(QL ? 0 : (long)len * H * D * ES));
+                if constexpr (DBUF) {
+                    if (r == 0) {
+                        lds_barrier();             // q_0 landed before the chunk; every wave is done with T' and V
+                    } else {
+                        wait_vmem_all();
+                        __syncthreads();           // q_r has landed; every wave is done with head r - 1
                     }
+                    if (prefetch) {
+                        if (r == 0) {              // T' and V of this chunk were consumed in phase 2
+                            load_tp(ol.Tp, cn);
+                            load_v(cn);
+                        }
+                        if (r + 1 < R) load_q(qb ^ 1, c, r + 1);
+                        else load_q(qb ^ 1, cn, 0);
+                    }
+                    flush_oldest();
+                } else if (r > 0) {
+                    lds_barrier();                 // every wave is done with the attn fragments of head r - 1
+                }
+                for (int f = wv; f < NFR; f += NW) attn_frag(f, Kb, Qb, rq, cl.gc, Atb);
+                f32x4 O[NTC][NJ];
+                if constexpr (QL) times_s([&](int ks, int tt) { return lds16(Qb, kq_off(ks, tpart<E>(tt))); }, O);
+                else
+                    times_s([&](int ks, int tt) {
+                        return buf_ld16(rq, (uint32_t)(((tpart<E>(tt) + lt) * H * D + KF * ks + VEC * lg) * ES));
+                    }, O);
+                lds_barrier();                     // the attn fragments of head r are complete
+                uint4 af[NFR];
+#pragma unroll
+                for (int f = 0; f < NFR; ++f) af[f] = lds16(Atb, f * 1024 + fo);
+#pragma unroll
+                for (int tt = 0; tt < NTC; ++tt)
+#pragma unroll
+                    for (int jt = 0; jt < NJ; ++jt)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) O[tt][jt][i] *= a.scale * egc[tt][i];   // egc carries sc
+#pragma unroll
+                for (int ks = 0; ks < NKC; ++ks)
+#pragma unroll
+                    for (int tt = 0; tt < NTC; ++tt)
+                        if (ks < attn_nks<E>(tt)) {
+#pragma unroll
+                            for (int jt = 0; jt < NJ; ++jt) mma<E>(O[tt][jt], af[attn_fidx<E>(tt, ks)], vb[ks][jt]);
+                        }
+                if constexpr (DBUF) {
+#pragma unroll
+                    for (int tt = 0; tt < NTC; ++tt)
+#pragma unroll
+                        for (int jt = 0; jt < NJ; ++jt) pk[DEP - 1][tt][jt] = O[tt][jt];
+                    pq_t0[DEP - 1] = t0;
+                    pq_len[DEP - 1] = len;
+                    pq_h[DEP - 1] = h;
+                    qb ^= 1;
+                } else {
+                    store_o(O, t0, len, h);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
-            __builtin_amdgcn_sched_barrier(0);
         }
 
         // phase 4: S = e^{gc_last} S + K^T (e^{gc_last - gc} v_new), as S_stored += K^T (e^{gc_last - gc} v_new / sc')
@@ -632,7 +790,8 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
     if (count > 0) {
         if constexpr (DBUF) {
             load_chunk(cl0, 0);
-            load_q(0);
+            if constexpr (!TPS) load_tp(ol.Tp, 0);
+            load_q(0, 0, 0);
             load_v(0);
             wait_vmem_all();
             __syncthreads();
@@ -662,7 +821,9 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
     }
 
     if constexpr (OUT) {
-        if (sg.p == sg.nseg - 1 && r == 0 && a.s_out) {
+#pragma unroll
+        for (int d = 0; d < DEP; ++d) flush_oldest();
+        if (sg.p == sg.nseg - 1 && a.s_out) {
             float* dst = a.s_out + ((long)n * G + g) * D * D;
 #pragma unroll
             for (int td = 0; td < NTD; ++td)
@@ -897,7 +1058,7 @@ namespace {
 template <class E, int D, bool OUT>
 dim3 seg_grid(const GdnArgs& a) {
     using Cfg = SegCfg<E, D, OUT>;
-    const int per = Cfg::NCG * (OUT ? a.R : 1);
+    const int per = Cfg::NCG;
     const int groups = a.max_segs * a.G;
     return dim3(NXCD * ((groups + NXCD - 1) / NXCD) * per);
 }

@@ -126,13 +126,24 @@ struct WinArgs {
 int window_dispatch(const WinArgs& a, hipStream_t stream);
 
 // 4 consecutive elements of the memory read (fp32 or bf16) at element index i (a multiple of 4) as fp32.
-__device__ __forceinline__ float4 load_om4(const WinArgs& a, long i) {
+// om[j] = o_mem elements i + 16 j .. + 3 as fp32. The N reads are issued back to back under one dtype branch: with
+// the dtype tested per read, each read sat in its own basic block and the compiler waited for it before the next.
+template <int N>
+__device__ __forceinline__ void load_om(const WinArgs& a, long i, float4 (&om)[N]) {
     if (a.o_mem_dtype == DT_BF16) {
-        const uint2 v = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(a.o_mem) + i);
-        return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xffff0000u), __uint_as_float(v.y << 16),
-                           __uint_as_float(v.y & 0xffff0000u));
+        const uint16_t* p = reinterpret_cast<const uint16_t*>(a.o_mem) + i;
+        uint2 raw[N];
+#pragma unroll
+        for (int j = 0; j < N; ++j) raw[j] = *reinterpret_cast<const uint2*>(p + 16 * j);
+#pragma unroll
+        for (int j = 0; j < N; ++j)
+            om[j] = make_float4(__uint_as_float(raw[j].x << 16), __uint_as_float(raw[j].x & 0xffff0000u),
+                                __uint_as_float(raw[j].y << 16), __uint_as_float(raw[j].y & 0xffff0000u));
+    } else {
+        const float* p = reinterpret_cast<const float*>(a.o_mem) + i;
+#pragma unroll
+        for (int j = 0; j < N; ++j) om[j] = *reinterpret_cast<const float4*>(p + 16 * j);
     }
-    return *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(a.o_mem) + i);
 }
 
 struct MemProjArgs {

@@ -330,18 +330,21 @@ __global__ __launch_bounds__(NT_WIN) void window_kernel(WinArgs a) {
             gam = 1.f / (1.f + __expf(-(a.z[((long)b * a.T + tq) * H + h] + a.mix_lse[h] * (lse - lnW))));
         const float ms = a.mix_on ? a.mem_scale[h] : 0.f;
         const long orow = (((long)b * a.T + tq) * H + h) * D;
+        // memory reads issued together (every row of o_mem exists); rows with gam = 0 keep the window output by
+        // selection, so rows the delta rule never wrote cannot leak in
+        const bool on = gam != 0.f;
+        float4 om[NDT];
+        if (a.mix_on) load_om<NDT>(a, orow + 4 * lg, om);
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
             const int d0 = 16 * dt + 4 * lg;
             float r4[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) r4[e] = o[dt][qt][e] * inv;
-            if (gam != 0.f) {
-                const float4 om = load_om4(a, orow + d0);
-                r4[0] += gam * (ms * om.x - r4[0]);
-                r4[1] += gam * (ms * om.y - r4[1]);
-                r4[2] += gam * (ms * om.z - r4[2]);
-                r4[3] += gam * (ms * om.w - r4[3]);
+            if (a.mix_on) {
+                const float mv[4] = {om[dt].x, om[dt].y, om[dt].z, om[dt].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) r4[e] = on ? r4[e] + gam * (ms * mv[e] - r4[e]) : r4[e];
             }
             if constexpr (BO) store4<BF16>(reinterpret_cast<uint16_t*>(a.o) + orow + d0, r4[0], r4[1], r4[2], r4[3]);
             else store4<F32>(reinterpret_cast<float*>(a.o) + orow + d0, r4[0], r4[1], r4[2], r4[3]);

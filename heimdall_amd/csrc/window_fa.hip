@@ -407,28 +407,11 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
             gam = 1.f / (1.f + __expf(-(a.z[((long)b * a.T + tq) * H + h] + a.mix_lse[h] * (lse - lnW))));
         const float ms = a.mix_on ? a.mem_scale[h] : 0.f;
         const long orow = (((long)b * a.T + tq) * H + h) * D;
-        // The memory reads are issued together (every row of o_mem exists), with the dtype branch outside the loop:
-        // a branch per element put every load in its own basic block, and the compiler waited for each before the
-        // next. Lanes before the first memory query (gam = 0) keep the window output by selection, so rows the delta
-        // rule never wrote cannot leak in.
+        // The memory reads are issued together (every row of o_mem exists); lanes before the first memory query
+        // (gam = 0) keep the window output by selection, so rows the delta rule never wrote cannot leak in.
         const bool on = gam != 0.f;
         float4 om[NDT];
-        if (a.mix_on) {
-            if (a.o_mem_dtype == DT_BF16) {
-                const uint16_t* pm = reinterpret_cast<const uint16_t*>(a.o_mem) + orow + 4 * lg;
-                uint2 raw[NDT];
-#pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) raw[dt] = *reinterpret_cast<const uint2*>(pm + 16 * dt);
-#pragma unroll
-                for (int dt = 0; dt < NDT; ++dt)
-                    om[dt] = make_float4(__uint_as_float(raw[dt].x << 16), __uint_as_float(raw[dt].x & 0xffff0000u),
-                                         __uint_as_float(raw[dt].y << 16), __uint_as_float(raw[dt].y & 0xffff0000u));
-            } else {
-                const float* pm = reinterpret_cast<const float*>(a.o_mem) + orow + 4 * lg;
-#pragma unroll
-                for (int dt = 0; dt < NDT; ++dt) om[dt] = *reinterpret_cast<const float4*>(pm + 16 * dt);
-            }
-        }
+        if (a.mix_on) load_om<NDT>(a, orow + 4 * lg, om);
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
             const int d0 = 16 * dt + 4 * lg;

@@ -609,9 +609,16 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
             egc[tt][3] = sc * __expf(gq.w);
         }
 
-        // phase 1: Y = K S_stored
+        // phase 1: Y = K S_stored; output scan: then the attn fragments of the chunk's first query head (their LDS
+        // writes are ordered by the barrier that starts head 0, which saves that head its own barrier)
         f32x4 Y[NTC][NJ];
         times_s([&](int ks, int tt) { return lds16(Kb, kq_off(ks, tpart<E>(tt))); }, Y);
+        if constexpr (OUT) {
+            const char* Q0b = reinterpret_cast<const char*>(ol.Q[QL ? qb : 0]);
+            const rsrc_t rq0 = make_rsrc(reinterpret_cast<const char*>(a.q) + (chunk_tok0(c) * H + (long)g * R) * D * ES,
+                                         (uint32_t)(QL ? 0 : (long)chunk_len(c) * H * D * ES));
+            for (int f = wv; f < NFR; f += NW) attn_frag(f, Kb, Q0b, rq0, cl.gc, reinterpret_cast<char*>(ol.At));
+        }
 
         // phase 2: v_new = T' (V - e^{gc} K S) = T' V + T' (-sc e^{gc} Y). The T' fragments (and, single-buffered,
         // the V fragments) are read first, so their LDS latency is covered by the scaling of Y.
@@ -682,17 +689,17 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
                         else load_q(qb ^ 1, cn, 0);
                     }
                     flush_oldest();
-                } else if (r > 0) {
-                    lds_barrier();                 // every wave is done with the attn fragments of head r - 1
-                }
-                for (int f = wv; f < NFR; f += NW) attn_frag(f, Kb, Qb, rq, cl.gc, Atb);
+                } else {
+                    lds_barrier();                 // head 0: its attn fragments are complete; later heads: every
+                }                                  // wave is done with the attn fragments of head r - 1
+                if (r > 0) for (int f = wv; f < NFR; f += NW) attn_frag(f, Kb, Qb, rq, cl.gc, Atb);
                 f32x4 O[NTC][NJ];
                 if constexpr (QL) times_s([&](int ks, int tt) { return lds16(Qb, kq_off(ks, tpart<E>(tt))); }, O);
                 else
                     times_s([&](int ks, int tt) {
                         return buf_ld16(rq, (uint32_t)(((tpart<E>(tt) + lt) * H * D + KF * ks + VEC * lg) * ES));
                     }, O);
-                lds_barrier();                     // the attn fragments of head r are complete
+                if (r > 0) lds_barrier();          // the attn fragments of head r are complete (head 0: above)
                 uint4 af[NFR];
 #pragma unroll
                 for (int f = 0; f < NFR; ++f) af[f] = lds16(Atb, f * 1024 + fo);

@@ -49,15 +49,21 @@ struct GdnLayout {
 
 // Segment length (chunks) when the caller passes 0: the L that minimises a cost model of the three sequential-part
 // kernels on an MI355X (256 CUs, one scan workgroup per CU), with per-chunk and per-step times measured at D = 256:
-//   output   ceil(segments x G x D/128 / 256) rounds of L chunks, ~(4 + 2R) us per chunk (R query heads per KV head)
+//   output   ceil(segments x G x D/128 / 256) rounds of L chunks, ~(4.6 + 2.8 R) us per chunk (R query heads per KV
+//            head; 7.4 us at R = 1, 21.5 us at R = 6)
 //   summary  ceil((segments - 1) x G x 2D/128 / 256) rounds of L chunks, ~3.7 us per chunk
-//   combine  (segments - 1) sequential steps, ~2.6 us each
+//   combine  (segments - 1) sequential steps, ~2.1 us each
 // Times scale with D^2 for the scan kernels and D^3 for the combine, which only shifts the balance for D < 256.
+// The chunk count of the model is ceil(tokens / 64) + sequences - 1 (exact for one sequence; each further sequence
+// adds at most one partial chunk), so that e.g. one sequence of 32768 tokens gets 32 segments of 16 chunks: one
+// round of 256 output workgroups at G = 4.
 constexpr int kSegMinChunks = 4;
+
+int model_chunks(int64_t total_tokens, int num_seqs) { return (int)((total_tokens + kChunk - 1) / kChunk) + num_seqs - 1; }
 
 int auto_segment_chunks(int max_chunks, int G, int R, int D) {
     const double f = (double)D / 256.0;
-    const double t_out = (4.0 + 2.0 * R) * f * f, t_sum = 3.7 * f * f, t_comb = 2.6 * f * f * f;
+    const double t_out = (4.6 + 2.8 * R) * f * f, t_sum = 3.7 * f * f, t_comb = 2.1 * f * f * f;
     const int cg = D >= 128 ? D / 128 : 1;
     int best_L = max_chunks > kSegMinChunks ? max_chunks : kSegMinChunks;
     double best = 1e300;
@@ -78,7 +84,8 @@ GdnLayout gdn_layout(int64_t total_tokens, int num_seqs, int G, int R, int D, in
     GdnLayout L;
     // every sequence contributes ceil(len / C) chunks: at most total/C + num_seqs overall
     L.max_chunks = (int)(total_tokens / kChunk) + num_seqs;
-    L.seg_chunks = segment_chunks > 0 ? segment_chunks : auto_segment_chunks(L.max_chunks, G, R, D);
+    L.seg_chunks = segment_chunks > 0 ? segment_chunks
+                                      : auto_segment_chunks(model_chunks(total_tokens, num_seqs), G, R, D);
     // every sequence contributes max(1, ceil(chunks / L)) segments
     L.max_segs = (L.max_chunks + L.seg_chunks - 1) / L.seg_chunks + num_seqs;
     const size_t nc = (size_t)L.max_chunks, ns = (size_t)L.max_segs, e = esize(in_dtype);
@@ -114,7 +121,7 @@ const char* bf_status_string(int status) {
 int bf_gdn_segment_chunks(int64_t total_tokens, int num_seqs, int G, int R, int D) {
     if (total_tokens < 0 || num_seqs <= 0 || G <= 0 || R <= 0) return BF_STATUS_INVALID;
     if (!supported_dim(D)) return BF_STATUS_UNSUPPORTED;
-    return auto_segment_chunks((int)(total_tokens / kChunk) + num_seqs, G, R, D);
+    return auto_segment_chunks(model_chunks(total_tokens, num_seqs), G, R, D);
 }
 
 int bf_gdn_workspace_size(int64_t total_tokens, int num_seqs, int G, int R, int D, int in_dtype,

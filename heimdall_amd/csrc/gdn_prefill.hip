@@ -7,7 +7,7 @@
 // the inputs q, k, v (it forms the causal q K^T block of each query head itself), and nothing of size C x D is
 // written back here.
 //
-// gdn_prep_kernel, grid (chunks, G), 4 waves: the K tile is staged in LDS (buffer_load ... lds); the waves compute A
+// gdn_prep_kernel, grid G x chunks (head fastest), 4 waves: the K tile is staged in LDS (buffer_load ... lds); the waves compute A
 // by MFMA; (I + A) is inverted in fp32 by 16 x 16 blocks (diagonal blocks by forward substitution, the rest by fp32
 // MFMA block products, one block column per wave).
 //
@@ -41,10 +41,12 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(GdnArgs a) {
     using T = typename E::T;
     constexpr int KF = E::KF, ES = (int)sizeof(T), ROWB = D * ES, NKD = D / KF;
     __shared__ PrepLds<E, D> sm;
+    // 1D grid, KV head fastest: the G workgroups of one chunk are dispatched together, so the cache lines of g and
+    // beta ([token][G], one line holds the values of all heads) are fetched from HBM once per XCD, not once per head
+    const int G = a.G, g = (int)(blockIdx.x % G);
+    const long cid = blockIdx.x / G;
     SeqInfo si;
-    if (!locate_chunk(blockIdx.x, a.cu_seqlens, a.num_seqs, a.seq_len, CH, si)) return;
-    const int g = blockIdx.y, G = a.G;
-    const long cid = blockIdx.x;
+    if (!locate_chunk(cid, a.cu_seqlens, a.num_seqs, a.seq_len, CH, si)) return;
     const int lane = lane_id(), wv = wave_id(), l16 = lane & 15, lg = lane >> 4;
     // LDS block permutation of the K tile: a fragment read covers 16 consecutive rows at one 16-byte block, so
     // the block is XORed with row & 15 (rows of >= 16 blocks) or (row >> 1) & 7 (8 blocks: two rows share a 256-byte
@@ -161,7 +163,7 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(GdnArgs a) {
 
 template <class E, int D>
 static int launch_prep(const GdnArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL((gdn_prep_kernel<E, D>), dim3(a.max_chunks, a.G), dim3(NT), 0, stream, a);
+    hipLaunchKernelGGL((gdn_prep_kernel<E, D>), dim3((unsigned)((long)a.G * a.max_chunks)), dim3(NT), 0, stream, a);
     return (int)hipGetLastError();
 }
 

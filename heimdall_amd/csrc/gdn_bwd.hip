@@ -228,21 +228,30 @@ __global__ __launch_bounds__(64) void unit_lower_inverse_kernel(const float* Am,
 }
 
 // ------------------------------------------------------------------------------------ state walks
-// Grid (sequences, G, D / 16): a workgroup owns 16 state columns and walks the chunks in order, the strip held in
-// fp32 MFMA accumulators (wave w: rows [w D/4, (w + 1) D/4)); per chunk two products on v_mfma_f32_16x16x4f32 with the
-// strip (and v_new) passed through LDS transposed, so every operand fragment is one 16-byte read. The next chunk's
-// operands are fetched into registers at the end of the current chunk, and the barriers order LDS only
-// (lds_barrier). (A second register set fetched a whole chunk ahead measured slower: 964 against 844 us per launch
-// at T = 8192, G = 4, D = 256.)
+// Grid (sequences, G, 2 D / 16): a workgroup owns 16 state columns of one KV head and walks the chunks in order (the
+// first D / 16 strips forward, the others backward), the strip held in fp32 MFMA accumulators; per chunk two products on
+// v_mfma_f32_16x16x4f32 with the strip (and v_new / dvn) passed through LDS transposed, so every operand fragment is
+// one 16-byte read. WALK_NW<D> waves: 8 at D >= 128 (two per SIMD, so one wave's loads and LDS exchange overlap the
+// other's MFMAs), 4 at D = 64. Wave w owns row tiles [w RT, (w + 1) RT) of the strip; for the 64-token product the
+// waves split into KH = NW / 4 parts of the D-long reduction, each part's partial sums go to LDS and the reader adds
+// them. The next chunk's operands are fetched into registers at the end of the current chunk, and the barriers order
+// LDS only (lds_barrier), so the fetch stays in flight across them. (At 4 waves per workgroup the walks took 845 us per
+// launch at T = 8192, G = 4, D = 256, at 8 waves 819 us; a second register set fetched a whole chunk ahead measured
+// slower at either count: 964 and 904-917 us.)
+template <int D>
+constexpr int walk_nw() { return D >= 128 ? 8 : 4; }
+
 template <int D>
 __device__ __forceinline__ void walk_fwd(const GdnBwdArgs& a, int strip) {
-    constexpr int RT = D / 64;                            // 16-row tiles of the strip per wave
-    constexpr int KD = D / 16, KC = BC / 16;              // 16-wide k steps over D and over the chunk
+    constexpr int NW = walk_nw<D>(), NTD = D / 16, RT = NTD / NW;   // row tiles per wave
+    constexpr int KH = NW / 4;                                       // parts of the D-long reduction of v_new
+    constexpr int KD = D / 16 / KH, KC = BC / 16;                    // 16-wide k steps per part / over the chunk
     const int b = blockIdx.x, g = blockIdx.y, col0 = strip * 16;
     const int lane = lane_id(), wv = wave_id(), i16 = lane & 15, q = lane >> 4;
+    const int tq = wv & 3, kh = wv >> 2;                             // v_new token tile and reduction part
     const int G = a.G, n = a.n_chunks;
     __shared__ float ST[16][D + 4];                       // strip transposed: ST[col][row]
-    __shared__ float VT[16][BC + 4];                      // v_new strip transposed: VT[col][token]
+    __shared__ float VT[KH][16][BC + 4];                  // v_new partial sums transposed: VT[part][col][token]
     f32x4 S[RT];
 #pragma unroll
     for (int t = 0; t < RT; ++t) S[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -255,12 +264,13 @@ __device__ __forceinline__ void walk_fwd(const GdnBwdArgs& a, int strip) {
                 S[t][v] = a.s0[(((long)b * G + g) * D + row) * D + col0 + i16];
             }
     }
-    // one chunk's operands, loaded a chunk ahead: w row fragments, kt^T fragments, the u strip, the chunk decay
+    // one chunk's operands, loaded a chunk ahead: w row fragments of this wave's reduction part, kt^T fragments of its
+    // row tiles, the u strip (part 0), the chunk decay
     float4 wf[KD], kf[RT][KC];
     float uf[4], gl;
     auto fetch = [&](int c) {
         const long cg = ((long)b * n + c) * G + g;
-        const float* wr = a.w + (cg * BC + 16 * wv + i16) * D + 4 * q;
+        const float* wr = a.w + (cg * BC + 16 * tq + i16) * D + kh * (D / KH) + 4 * q;
 #pragma unroll
         for (int k = 0; k < KD; ++k) wf[k] = *reinterpret_cast<const float4*>(wr + 16 * k);
 #pragma unroll
@@ -270,7 +280,7 @@ __device__ __forceinline__ void walk_fwd(const GdnBwdArgs& a, int strip) {
             for (int k = 0; k < KC; ++k) kf[t][k] = *reinterpret_cast<const float4*>(kr + 16 * k);
         }
 #pragma unroll
-        for (int v = 0; v < 4; ++v) uf[v] = a.u[(cg * BC + 16 * wv + 4 * q + v) * D + col0 + i16];
+        for (int v = 0; v < 4; ++v) uf[v] = kh == 0 ? a.u[(cg * BC + 16 * tq + 4 * q + v) * D + col0 + i16] : 0.f;
         gl = a.gam[cg * BC + BC - 1];
     };
     fetch(0);
@@ -285,21 +295,22 @@ __device__ __forceinline__ void walk_fwd(const GdnBwdArgs& a, int strip) {
                 ST[i16][row] = S[t][v];
             }
         lds_barrier();
-        // v_new rows [16 wv, 16 wv + 16) = u - w S (four partial accumulators: shorter MFMA dependency chains)
+        // v_new rows [16 tq, 16 tq + 16) = u - w S, this wave's part of the reduction (four partial accumulators:
+        // shorter MFMA dependency chains)
         f32x4 part[4] = {f32x4{uf[0], uf[1], uf[2], uf[3]}, f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f},
                          f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int k = 0; k < KD; ++k) {
             const uint4 af = make_uint4(__float_as_uint(-wf[k].x), __float_as_uint(-wf[k].y), __float_as_uint(-wf[k].z),
                                         __float_as_uint(-wf[k].w));
-            const uint4 bf = *reinterpret_cast<const uint4*>(&ST[i16][16 * k + 4 * q]);
+            const uint4 bf = *reinterpret_cast<const uint4*>(&ST[i16][kh * (D / KH) + 16 * k + 4 * q]);
             mma<F32>(part[k & 3], af, bf);
         }
         const f32x4 acc = (part[0] + part[1]) + (part[2] + part[3]);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) VT[i16][16 * wv + 4 * q + v] = acc[v];
+        for (int v = 0; v < 4; ++v) VT[kh][i16][16 * tq + 4 * q + v] = acc[v];
         lds_barrier();
-        // S = e^(gc_C') S + kt^T v_new
+        // S = e^(gc_C') S + kt^T v_new (v_new = the sum of the parts)
         const float ec = expf(gl);
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
@@ -307,8 +318,13 @@ __device__ __forceinline__ void walk_fwd(const GdnBwdArgs& a, int strip) {
             for (int v = 0; v < 4; ++v) S[t][v] *= ec;
 #pragma unroll
             for (int k = 0; k < KC; ++k) {
-                const uint4 bf = *reinterpret_cast<const uint4*>(&VT[i16][16 * k + 4 * q]);
-                mma<F32>(S[t], __builtin_bit_cast(uint4, kf[t][k]), bf);
+                float4 vs = *reinterpret_cast<const float4*>(&VT[0][i16][16 * k + 4 * q]);
+#pragma unroll
+                for (int p = 1; p < KH; ++p) {
+                    const float4 x = *reinterpret_cast<const float4*>(&VT[p][i16][16 * k + 4 * q]);
+                    vs.x += x.x; vs.y += x.y; vs.z += x.z; vs.w += x.w;
+                }
+                mma<F32>(S[t], __builtin_bit_cast(uint4, kf[t][k]), __builtin_bit_cast(uint4, vs));
             }
         }
         fetch(c + 1 < n ? c + 1 : c);   // unconditional: a conditional load is drained where the branches join
@@ -319,13 +335,15 @@ __device__ __forceinline__ void walk_fwd(const GdnBwdArgs& a, int strip) {
 // reverse: every chunk's exit-state gradient dS' and dvn, and ds0; same grid and layout
 template <int D>
 __device__ __forceinline__ void walk_bwd(const GdnBwdArgs& a, int strip) {
-    constexpr int RT = D / 64;
-    constexpr int KD = D / 16, KC = BC / 16;
+    constexpr int NW = walk_nw<D>(), NTD = D / 16, RT = NTD / NW;
+    constexpr int KH = NW / 4;
+    constexpr int KD = D / 16 / KH, KC = BC / 16;
     const int b = blockIdx.x, g = blockIdx.y, col0 = strip * 16;
     const int lane = lane_id(), wv = wave_id(), i16 = lane & 15, q = lane >> 4;
+    const int tq = wv & 3, kh = wv >> 2;
     const int G = a.G, n = a.n_chunks;
     __shared__ float LT[16][D + 4];
-    __shared__ float VT[16][BC + 4];
+    __shared__ float VT[KH][16][BC + 4];
     f32x4 L[RT];
 #pragma unroll
     for (int t = 0; t < RT; ++t) L[t] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -338,12 +356,13 @@ __device__ __forceinline__ void walk_bwd(const GdnBwdArgs& a, int strip) {
                 L[t][v] = a.dsf[(((long)b * G + g) * D + row) * D + col0 + i16];
             }
     }
-    // one chunk's operands, a chunk ahead: kt row fragments, w^T fragments, the E1 and E2 strips, the chunk decay
+    // one chunk's operands, a chunk ahead: kt row fragments of this wave's reduction part, w^T fragments of its row
+    // tiles, the E1 strip (part 0) and E2 rows, the chunk decay
     float4 kf[KD], wf[RT][KC];
     float e1[4], e2[RT][4], gl;
     auto fetch = [&](int c) {
         const long cg = ((long)b * n + c) * G + g;
-        const float* kr = a.ktl + (cg * BC + 16 * wv + i16) * D + 4 * q;
+        const float* kr = a.ktl + (cg * BC + 16 * tq + i16) * D + kh * (D / KH) + 4 * q;
 #pragma unroll
         for (int k = 0; k < KD; ++k) kf[k] = *reinterpret_cast<const float4*>(kr + 16 * k);
 #pragma unroll
@@ -356,7 +375,7 @@ __device__ __forceinline__ void walk_bwd(const GdnBwdArgs& a, int strip) {
                 e2[t][v] = a.E2[(cg * D + (wv * RT + t) * 16 + 4 * q + v) * D + col0 + i16];
         }
 #pragma unroll
-        for (int v = 0; v < 4; ++v) e1[v] = a.E1[(cg * BC + 16 * wv + 4 * q + v) * D + col0 + i16];
+        for (int v = 0; v < 4; ++v) e1[v] = kh == 0 ? a.E1[(cg * BC + 16 * tq + 4 * q + v) * D + col0 + i16] : 0.f;
         gl = a.gam[cg * BC + BC - 1];
     };
     fetch(n - 1);
@@ -371,22 +390,28 @@ __device__ __forceinline__ void walk_bwd(const GdnBwdArgs& a, int strip) {
                 LT[i16][row] = L[t][v];
             }
         lds_barrier();
-        // dvn rows [16 wv, 16 wv + 16) = E1 + kt dS' (four partial accumulators)
+        // dvn rows [16 tq, 16 tq + 16) = E1 + kt dS', this wave's part of the reduction
         f32x4 part[4] = {f32x4{e1[0], e1[1], e1[2], e1[3]}, f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f},
                          f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
         for (int k = 0; k < KD; ++k) {
-            const uint4 bf = *reinterpret_cast<const uint4*>(&LT[i16][16 * k + 4 * q]);
+            const uint4 bf = *reinterpret_cast<const uint4*>(&LT[i16][kh * (D / KH) + 16 * k + 4 * q]);
             mma<F32>(part[k & 3], __builtin_bit_cast(uint4, kf[k]), bf);
         }
         const f32x4 acc = (part[0] + part[1]) + (part[2] + part[3]);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            a.dvn[(cg * BC + 16 * wv + 4 * q + v) * D + col0 + i16] = acc[v];
-            VT[i16][16 * wv + 4 * q + v] = acc[v];
-        }
+        for (int v = 0; v < 4; ++v) VT[kh][i16][16 * tq + 4 * q + v] = acc[v];
         lds_barrier();
-        // dS = e^(gc_C') dS' + E2 - w^T dvn
+        // dvn (the sum of the parts) out; dS = e^(gc_C') dS' + E2 - w^T dvn
+        if (kh == 0) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                float x = VT[0][i16][16 * tq + 4 * q + v];
+#pragma unroll
+                for (int p = 1; p < KH; ++p) x += VT[p][i16][16 * tq + 4 * q + v];
+                a.dvn[(cg * BC + 16 * tq + 4 * q + v) * D + col0 + i16] = x;
+            }
+        }
         const float ec = expf(gl);
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
@@ -396,8 +421,13 @@ __device__ __forceinline__ void walk_bwd(const GdnBwdArgs& a, int strip) {
             for (int k = 0; k < KC; ++k) {
                 const uint4 af = make_uint4(__float_as_uint(-wf[t][k].x), __float_as_uint(-wf[t][k].y),
                                             __float_as_uint(-wf[t][k].z), __float_as_uint(-wf[t][k].w));
-                const uint4 bf = *reinterpret_cast<const uint4*>(&VT[i16][16 * k + 4 * q]);
-                mma<F32>(L[t], af, bf);
+                float4 vs = *reinterpret_cast<const float4*>(&VT[0][i16][16 * k + 4 * q]);
+#pragma unroll
+                for (int p = 1; p < KH; ++p) {
+                    const float4 x = *reinterpret_cast<const float4*>(&VT[p][i16][16 * k + 4 * q]);
+                    vs.x += x.x; vs.y += x.y; vs.z += x.z; vs.w += x.w;
+                }
+                mma<F32>(L[t], af, __builtin_bit_cast(uint4, vs));
             }
         }
         fetch(c > 0 ? c - 1 : c);       // unconditional, as in the forward walk
@@ -413,10 +443,9 @@ __device__ __forceinline__ void walk_bwd(const GdnBwdArgs& a, int strip) {
             }
 }
 
-// the two walks are independent (the reverse one needs E1, E2, kt, w, not the entry states): one launch, grid
-// (sequences, G, 2 D / 16), the first D / 16 strips walk forward, the others backward
+// the two walks are independent (the reverse one needs E1, E2, kt, w, not the entry states): one launch
 template <int D>
-__global__ __launch_bounds__(BW_NT) void walk_kernel(GdnBwdArgs a) {
+__global__ __launch_bounds__(64 * walk_nw<D>()) void walk_kernel(GdnBwdArgs a) {
     if ((int)blockIdx.z < D / 16) walk_fwd<D>(a, blockIdx.z);
     else walk_bwd<D>(a, blockIdx.z - D / 16);
 }
@@ -653,9 +682,9 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
             D, 1, 1.f, 0, 0, nullptr, s));
     // walks
     const dim3 wgrid(a.num_seqs, G, 2 * D / 16);
-    if (D == 64) hipLaunchKernelGGL(walk_kernel<64>, wgrid, dim3(BW_NT), 0, s, a);
-    else if (D == 128) hipLaunchKernelGGL(walk_kernel<128>, wgrid, dim3(BW_NT), 0, s, a);
-    else hipLaunchKernelGGL(walk_kernel<256>, wgrid, dim3(BW_NT), 0, s, a);
+    if (D == 64) hipLaunchKernelGGL(walk_kernel<64>, wgrid, dim3(64 * walk_nw<64>()), 0, s, a);
+    else if (D == 128) hipLaunchKernelGGL(walk_kernel<128>, wgrid, dim3(64 * walk_nw<128>()), 0, s, a);
+    else hipLaunchKernelGGL(walk_kernel<256>, wgrid, dim3(64 * walk_nw<256>()), 0, s, a);
     ok((int)hipGetLastError());
     // v_new = u - w S
     ok(gemm(BC, D, D, nzg, G, 1, W(a.w, BC, D), W(a.Sc, D, D), a.vn, (long)G * cd, cd, 0, D, 1, -1.f, 0, 0, a.u, s));

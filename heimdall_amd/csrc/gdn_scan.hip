@@ -419,6 +419,8 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
     // D = 256) store the accumulator layout directly.
     constexpr int OS = BO ? 2 : 4;
     using OPk = typename std::conditional<BO, uint2, uint4>::type;   // one lane's 4 columns of one row
+    // bf16 output scans whose o block (64 rows x the workgroup's columns) fits a q buffer stage o through it
+    constexpr bool STG = OUT && DBUF && SC * VW * OS <= SC * D * ES;
     auto pack_o = [&](const f32x4 (&O)[NTC][NJ], OPk (&P)[NTC][NJ]) {
         const int qb4 = l16 & 3;
         auto pick = [&](const float (&x)[4], int idx) {
@@ -717,7 +719,36 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
 #pragma unroll
                             for (int jt = 0; jt < NJ; ++jt) mma<E>(O[tt][jt], af[attn_fidx<E>(tt, ks)], vb[ks][jt]);
                         }
-                if constexpr (DBUF) {
+                if constexpr (DBUF && STG) {
+                    // o through the q buffer this head has consumed (its q reads are ordered before this barrier; the
+                    // next head's copy into it waits for the top barrier of head r + 1), then whole-row stores
+                    if (r == 0) lds_barrier();
+                    char* stg = reinterpret_cast<char*>(ol.Q[qb]);
+                    OPk P[NTC][NJ];
+                    pack_o(O, P);
+#pragma unroll
+                    for (int tt = 0; tt < NTC; ++tt)
+#pragma unroll
+                        for (int jt = 0; jt < NJ; ++jt) {
+                            const int row = tpart<E>(tt) + VEC * lg + (l16 & 3);
+                            *reinterpret_cast<OPk*>(stg + (row * VW + wv * WCOLS + 16 * jt + 4 * (l16 >> 2)) * OS) =
+                                P[tt][jt];
+                        }
+                    lds_barrier();
+                    constexpr int RB = VW * OS, LPR = RB / 16, RPI = 64 / LPR;   // row bytes, lanes per row, rows
+                    const rsrc_t ro = make_rsrc(reinterpret_cast<char*>(a.o) + (t0 * H + h) * (long)D * OS,
+                                                (uint32_t)((long)len * H * D * OS));
+#pragma unroll
+                    for (int k = 0; k < SC / NW / RPI; ++k) {
+                        const int row = (SC / NW) * wv + RPI * k + lane / LPR, ch = lane % LPR;
+                        const uint4 v4 = lds16(stg, row * RB + 16 * ch);
+                        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+                        const u32x4 w4 = {v4.x, v4.y, v4.z, v4.w};
+                        __builtin_amdgcn_raw_buffer_store_b128(
+                            w4, ro, (uint32_t)((row * H * D + cb) * OS + 16 * ch), 0, 0);
+                    }
+                    qb ^= 1;
+                } else if constexpr (DBUF) {
 #pragma unroll
                     for (int tt = 0; tt < NTC; ++tt)
 #pragma unroll

@@ -27,120 +27,244 @@ constexpr int BC = 64;                  // chunk length
 constexpr int BW_NT = 256;
 
 // ------------------------------------------------------------------------------------ batched strided fp32 GEMM
-// C[z] (M x N) = add[z] + alpha * A[z] (M x K) B[z] (K x N)   (or C += alpha A B when acc), z = (z0, z1, z2);
-// element (m, k) of A at A + z0 sa0 + z1 sa1 + z2 sa2 + m am + k ak (B, C, add likewise). M, N multiples of 64,
-// K of 16, each operand contiguous along one dimension, 16-byte aligned. mask 1 keeps m >= n, mask 2 keeps m > n (the
-// rest is written 0, or left unchanged when accumulating).
+// C[z] (M x N) = add[z] + alpha * A[z] diag(ksc) (M x K) B[z] (K x N)   (or C += ... when acc), z = (z0, z1, z2);
+// element (m, k) of A at A + z0 sa0 + z1 sa1 + z2 sa2 + m am + (k >> kshift) sak + (k & (2^kshift - 1)) ak (B, C,
+// add likewise): the reduction index may run over two strides, e.g. (query head, token) pairs of a token-major
+// [token][head][D] tensor. M, N multiples of 64, K of 16 (and 2^kshift a multiple of 16 when it splits K), each
+// operand contiguous along one dimension, 16-byte aligned. ksc (or null) scales A's column k by
+// ksc[z0 ks0 + z1 ks1 + (k & (2^kshift - 1))], msc (or null) the product's row m by msc[z0 ms0 + z1 ms1 + m]. mask 1
+// keeps m >= n, mask 2 keeps m > n (the rest is written 0, or left unchanged when accumulating). With rdo (C
+// contiguous along n only), the unscaled product's row dots with rdx (addressed like C) go to
+// rdo[(z N/64 + n/64) M + m], one partial per 64 columns (z = blockIdx.x).
 struct BgArgs {
-    int M, N, K, n1, n2, nz;
-    const float* A; long sa0, sa1, sa2, am, ak;
-    const float* B; long sb0, sb1, sb2, bk, bn;
+    int M, N, K, n1, n2, nz, kshift;
+    const float* A; long sa0, sa1, sa2, am, ak, sak;
+    const float* B; long sb0, sb1, sb2, bk, bn, sbk;
     float* C; long sc0, sc1, sc2, cm, cn;
     const float* add;                   // same strides as C, or null
+    const float* ksc; long ks0, ks1;
+    const float* msc; long ms0, ms1;
+    const float* rdx; float* rdo;
     float alpha;
     int acc, mask;
 };
 
-// Operand tiles go through LDS: per K step of 16, a 64 x 16 tile of A and a 16 x 64 tile of B are read with one
-// 16-byte load per thread each, along whichever dimension is contiguous (AK: A's k, else its m; BK: B's k, else its n),
-// stored k-contiguous per row (As[m][k], Bs[n][k]) so every MFMA fragment is one 16-byte LDS read; the next step's
-// loads are issued before the current step's MFMAs.
-template <bool AK, bool BK>
+// Tiles of 64 x BN (BN = 64 or 128; 4 waves of 32 x BN/2) over K steps of 32. Each step's 64 x 32 tile of A and
+// 32 x BN tile of B are read with 16-byte loads along whichever dimension is contiguous (AK: A's k, else its m; BK:
+// B's k, else its n) and stored in LDS in the same orientation with 16-byte writes: a k-contiguous operand as
+// [row][k] (pitch 36 floats: the 16 rows of a fragment hit distinct banks; a fragment is one 16-byte read), the other
+// as [k][row] (pitch 4 mod 16 floats: the four k rows a fragment read spans fall 16 banks apart; a fragment is four
+// 4-byte reads). Fragment value j of lane (i, q) is k = 16 kh + 4 q + j for both operands. The LDS tiles are double
+// buffered: step s computes from one buffer, then writes step s + 1's operands (loaded from global during step s - 1)
+// into the other and issues step s + 2's loads, with one barrier per step.
+template <bool AK, bool BK, int BN>
 __global__ __launch_bounds__(BW_NT) void bgemm_kernel(BgArgs a) {
+    constexpr int KS = 32, LDK = KS + 4;        // k per step, LDS row pitch (floats)
+    constexpr int WN = BN / 2, TU = WN / 16;    // wave tile 32 x WN: 2 x TU MFMA tiles
+    constexpr int NA = 2, NB = BN / 32;         // 16-byte global loads per thread per step
     const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
     const long z = blockIdx.x;
     const long z2 = z % a.n2, z1 = (z / a.n2) % a.n1, z0 = z / ((long)a.n1 * a.n2);
     const float* A = a.A + z0 * a.sa0 + z1 * a.sa1 + z2 * a.sa2;
     const float* B = a.B + z0 * a.sb0 + z1 * a.sb1 + z2 * a.sb2;
+    const float* ksc = a.ksc ? a.ksc + z0 * a.ks0 + z1 * a.ks1 : nullptr;
+    const int ksh = a.kshift, klo = (1 << ksh) - 1;
     const long coff = z0 * a.sc0 + z1 * a.sc1 + z2 * a.sc2;
-    const int tm = blockIdx.y * 64, tn = blockIdx.z * 64;
-    const int m0 = (wv >> 1) * 32, n0 = (wv & 1) * 32;      // the wave's 32 x 32 block inside the tile
+    const int tm = blockIdx.y * 64, tn = blockIdx.z * BN;
+    const int m0 = (wv >> 1) * 32, n0 = (wv & 1) * WN;      // the wave's 32 x WN block inside the tile
     const int i = lane & 15, q = lane >> 4;
-    __shared__ float As[64][20];
-    __shared__ float Bs[64][20];
-    f32x4 acc[2][2];
+    constexpr int AR = AK ? 64 : KS, AP = AK ? LDK : 64 + 4;     // LDS rows and pitch of A
+    constexpr int BR = BK ? BN : KS, BP = BK ? LDK : BN + 4;     // and of B
+    constexpr int ASZ = 2 * AR * AP, BSZ = 2 * BR * BP, CSZ = 64 * (BN + 4);
+    __shared__ __align__(16) float lds[ASZ + BSZ > CSZ ? ASZ + BSZ : CSZ];   // operand tiles, then the output tile
+    float (*As)[AR][AP] = reinterpret_cast<float (*)[AR][AP]>(lds);
+    float (*Bs)[BR][BP] = reinterpret_cast<float (*)[BR][BP]>(lds + ASZ);
+    f32x4 acc[2][TU];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int u = 0; u < 2; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int u = 0; u < TU; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
     // the block-level skip of a masked tile wholly outside the kept triangle
     const bool skip = (a.mask == 1 && tm + 63 < tn) || (a.mask == 2 && tm + 63 <= tn);
-    // load slots: k-contiguous operand: row t / 4, k (t % 4) * 4; otherwise k t / 16, rows (t % 16) * 4 .. + 3
-    const int ra = AK ? tid / 4 : (tid % 16) * 4, ka = AK ? (tid % 4) * 4 : tid / 16;
-    const int rb = BK ? tid / 4 : (tid % 16) * 4, kb = BK ? (tid % 4) * 4 : tid / 16;
-    auto load_a = [&](int k0) {
-        return AK ? *reinterpret_cast<const float4*>(A + (long)(tm + ra) * a.am + k0 + ka)
-                  : *reinterpret_cast<const float4*>(A + (long)(k0 + ka) * a.ak + tm + ra);
+    // Load slot h of a thread. k-contiguous operand: row tid / 8 + 32 h, k (tid % 8) * 4 .. + 3; otherwise k
+    // tid / 16 + 16 (h & 1), rows (tid % 16) * 4 + 64 (h >> 1) .. + 3. A step starts at a multiple of 32 and 2^kshift
+    // is a multiple of 16, so the 4 k of a k-contiguous slot share their high part.
+    auto koff = [&](int k, long shi, long slo) { return (long)(k >> ksh) * shi + (long)(k & klo) * slo; };
+    auto load_a = [&](int k0, int h) {
+        float4 x;
+        if (AK) {
+            const int k = k0 + (tid % 8) * 4;
+            x = *reinterpret_cast<const float4*>(A + (long)(tm + tid / 8 + 32 * h) * a.am + koff(k, a.sak, a.ak));
+            if (ksc) {
+                const float4 sv = *reinterpret_cast<const float4*>(ksc + (k & klo));
+                x.x *= sv.x; x.y *= sv.y; x.z *= sv.z; x.w *= sv.w;
+            }
+        } else {
+            const int k = k0 + tid / 16 + 16 * h;
+            x = *reinterpret_cast<const float4*>(A + koff(k, a.sak, a.ak) + tm + (tid % 16) * 4);
+            if (ksc) {
+                const float sv = ksc[k & klo];
+                x.x *= sv; x.y *= sv; x.z *= sv; x.w *= sv;
+            }
+        }
+        return x;
     };
-    auto load_b = [&](int k0) {
-        return BK ? *reinterpret_cast<const float4*>(B + (long)(tn + rb) * a.bn + k0 + kb)
-                  : *reinterpret_cast<const float4*>(B + (long)(k0 + kb) * a.bk + tn + rb);
+    auto load_b = [&](int k0, int h) {
+        if (BK) {
+            const int k = k0 + (tid % 8) * 4;
+            return *reinterpret_cast<const float4*>(B + (long)(tn + tid / 8 + 32 * h) * a.bn + koff(k, a.sbk, a.bk));
+        }
+        const int k = k0 + tid / 16 + 16 * (h & 1);
+        return *reinterpret_cast<const float4*>(B + koff(k, a.sbk, a.bk) + tn + (tid % 16) * 4 + 64 * (h >> 1));
     };
-    if (!skip) {
-        float4 xa = load_a(0), xb = load_b(0);
-        for (int k0 = 0; k0 < a.K; k0 += 16) {
-            __syncthreads();
-            if (AK) {
-                *reinterpret_cast<float4*>(&As[ra][ka]) = xa;
-            } else {
-                As[ra][ka] = xa.x; As[ra + 1][ka] = xa.y; As[ra + 2][ka] = xa.z; As[ra + 3][ka] = xa.w;
-            }
-            if (BK) {
-                *reinterpret_cast<float4*>(&Bs[rb][kb]) = xb;
-            } else {
-                Bs[rb][kb] = xb.x; Bs[rb + 1][kb] = xb.y; Bs[rb + 2][kb] = xb.z; Bs[rb + 3][kb] = xb.w;
-            }
-            __syncthreads();
-            if (k0 + 16 < a.K) {
-                xa = load_a(k0 + 16);
-                xb = load_b(k0 + 16);
-            }
-            uint4 af[2], bf[2];
+    auto store = [&](int buf, const float4 (&xa)[NA], const float4 (&xb)[NB]) {
+#pragma unroll
+        for (int h = 0; h < NA; ++h) {
+            if (AK) *reinterpret_cast<float4*>(&As[buf][tid / 8 + 32 * h][(tid % 8) * 4]) = xa[h];
+            else *reinterpret_cast<float4*>(&As[buf][tid / 16 + 16 * h][(tid % 16) * 4]) = xa[h];
+        }
+#pragma unroll
+        for (int h = 0; h < NB; ++h) {
+            if (BK) *reinterpret_cast<float4*>(&Bs[buf][tid / 8 + 32 * h][(tid % 8) * 4]) = xb[h];
+            else *reinterpret_cast<float4*>(&Bs[buf][tid / 16 + 16 * (h & 1)][(tid % 16) * 4 + 64 * (h >> 1)]) = xb[h];
+        }
+    };
+    auto compute = [&](int buf) {
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+            uint4 af[2], bf[TU];
+            const int kr = 16 * kh + 4 * q;
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                af[t] = *reinterpret_cast<const uint4*>(&As[m0 + 16 * t + i][4 * q]);
-                bf[t] = *reinterpret_cast<const uint4*>(&Bs[n0 + 16 * t + i][4 * q]);
+                const int r = m0 + 16 * t + i;
+                af[t] = AK ? *reinterpret_cast<const uint4*>(&As[buf][r][kr])
+                           : make_uint4(__float_as_uint(As[buf][kr][r]), __float_as_uint(As[buf][kr + 1][r]),
+                                        __float_as_uint(As[buf][kr + 2][r]), __float_as_uint(As[buf][kr + 3][r]));
+            }
+#pragma unroll
+            for (int u = 0; u < TU; ++u) {
+                const int r = n0 + 16 * u + i;
+                bf[u] = BK ? *reinterpret_cast<const uint4*>(&Bs[buf][r][kr])
+                           : make_uint4(__float_as_uint(Bs[buf][kr][r]), __float_as_uint(Bs[buf][kr + 1][r]),
+                                        __float_as_uint(Bs[buf][kr + 2][r]), __float_as_uint(Bs[buf][kr + 3][r]));
             }
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int u = 0; u < 2; ++u) mma<F32>(acc[t][u], af[t], bf[u]);
+                for (int u = 0; u < TU; ++u) mma<F32>(acc[t][u], af[t], bf[u]);
+        }
+    };
+    if (!skip) {
+        const int ns = a.K / KS;
+        float4 xa[NA], xb[NB];
+        auto fetch = [&](int s) {
+#pragma unroll
+            for (int h = 0; h < NA; ++h) xa[h] = load_a(s * KS, h);
+#pragma unroll
+            for (int h = 0; h < NB; ++h) xb[h] = load_b(s * KS, h);
+        };
+        fetch(0);
+        store(0, xa, xb);
+        if (ns > 1) fetch(1);
+        __syncthreads();
+        for (int s = 0; s < ns; ++s) {
+            compute(s & 1);
+            if (s + 1 < ns) {
+                store((s + 1) & 1, xa, xb);
+                if (s + 2 < ns) fetch(s + 2);
+            }
+            __syncthreads();
         }
     }
-    // The prior values (C when accumulating, else the addend) are read first, all 16 under one branch: tested per
-    // element, each read sat in its own basic block and was waited for before the next one was issued. The tiles
-    // cover M x N exactly (both are multiples of 64), so every address is in range.
+    const float* msc = a.msc ? a.msc + z0 * a.ms0 + z1 * a.ms1 : nullptr;
+    if (a.cn == 1) {
+        // Row-contiguous output: the tile goes through LDS (free after the last step's barrier) and each thread then
+        // handles 16-byte row pieces, so C, the addend and rdx move as whole rows. All reads of a thread are issued
+        // before the first use. Out = prev + (kept ? alpha msc[m] x : 0), prev = C when accumulating, else the
+        // addend or 0 (a masked element keeps its C).
+        float (*Cs)[BN + 4] = reinterpret_cast<float (*)[BN + 4]>(lds);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int u = 0; u < TU; ++u)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) Cs[m0 + 16 * t + 4 * q + v][n0 + 16 * u + i] = acc[t][u][v];
+        __syncthreads();
+        constexpr int RW = BN / 4, NP = 64 * RW / BW_NT;    // pieces per row, per thread
+        const int c4 = tid % RW;
+        const int n = tn + 4 * c4;
+        auto row = [&](int j) { return tid / RW + (BW_NT / RW) * j; };
+        auto at = [&](int j) { return coff + (long)(tm + row(j)) * a.cm + n; };
+        float4 prev[NP], rx[NP];
+        if (a.acc || a.add) {
+            const float* src = a.acc ? a.C : a.add;
+#pragma unroll
+            for (int j = 0; j < NP; ++j) prev[j] = *reinterpret_cast<const float4*>(src + at(j));
+        } else {
+#pragma unroll
+            for (int j = 0; j < NP; ++j) prev[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        if (a.rdo) {
+#pragma unroll
+            for (int j = 0; j < NP; ++j) rx[j] = *reinterpret_cast<const float4*>(a.rdx + at(j));
+        }
+#pragma unroll
+        for (int j = 0; j < NP; ++j) {
+            const int m = tm + row(j);
+            const float4 x = *reinterpret_cast<const float4*>(&Cs[row(j)][4 * c4]);
+            if (a.rdo) {                                   // one partial per 64 columns: 16 pieces of the row
+                float d = x.x * rx[j].x + x.y * rx[j].y + x.z * rx[j].z + x.w * rx[j].w;
+#pragma unroll
+                for (int off = 1; off < 16; off <<= 1) d += __shfl_xor(d, off);
+                if (c4 % 16 == 0) a.rdo[((long)z * (a.N / 64) + (tn + 4 * c4) / 64) * a.M + m] = d;
+            }
+            const float al = msc ? a.alpha * msc[m] : a.alpha;
+            const float xv[4] = {x.x, x.y, x.z, x.w};
+            float ov[4] = {prev[j].x, prev[j].y, prev[j].z, prev[j].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const bool keep = a.mask == 0 || (a.mask == 1 && m >= n + e) || (a.mask == 2 && m > n + e);
+                if (keep) ov[e] += al * xv[e];
+            }
+            *reinterpret_cast<float4*>(a.C + at(j)) = make_float4(ov[0], ov[1], ov[2], ov[3]);
+        }
+        return;
+    }
+    // Column-strided output: per lane. The prior values are read first, all under one branch: tested per element, each
+    // read sat in its own basic block and was waited for before the next one was issued. The tiles cover M x N
+    // exactly (multiples of 64 and BN), so every address is in range.
     auto at_of = [&](int t, int u, int v) {
         const int m = tm + m0 + 16 * t + 4 * q + v, n = tn + n0 + 16 * u + i;
         return coff + (long)m * a.cm + (long)n * a.cn;
     };
-    float prev[2][2][4];
+    float prev[2][TU][4];
     if (a.acc || a.add) {
         const float* src = a.acc ? a.C : a.add;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int u = 0; u < 2; ++u)
+            for (int u = 0; u < TU; ++u)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) prev[t][u][v] = src[at_of(t, u, v)];
     } else {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-            for (int u = 0; u < 2; ++u)
+            for (int u = 0; u < TU; ++u)
 #pragma unroll
                 for (int v = 0; v < 4; ++v) prev[t][u][v] = 0.f;
     }
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < TU; ++u)
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 const int m = tm + m0 + 16 * t + 4 * q + v, n = tn + n0 + 16 * u + i;
                 const bool keep = a.mask == 0 || (a.mask == 1 && m >= n) || (a.mask == 2 && m > n);
                 const long at = at_of(t, u, v);
-                const float val = keep ? a.alpha * acc[t][u][v] : 0.f;
+                const float al = msc ? a.alpha * msc[m] : a.alpha;
+                const float val = keep ? al * acc[t][u][v] : 0.f;
                 if (a.acc) {
                     if (keep) a.C[at] = prev[t][u][v] + val;
                 } else {
@@ -150,11 +274,11 @@ __global__ __launch_bounds__(BW_NT) void bgemm_kernel(BgArgs a) {
 }
 
 // ------------------------------------------------------------------------------------ per-chunk elementwise prep
-// one workgroup per (chunk, KV head): gc, k b, v b, k b e^gc, kt, and qd_r = s q_r e^gc for the R query heads
+// one workgroup per (chunk, KV head, row quarter): gc, e^gc, k b, v b, k b e^gc, kt (and transposed)
 __global__ __launch_bounds__(BW_NT) void chunk_prep_kernel(GdnBwdArgs a) {
     const long bc = blockIdx.x;
     const int g = blockIdx.y, r0 = blockIdx.z * 16, tid = threadIdx.x;   // rows r0 .. r0 + 15 of the chunk
-    const int D = a.D, G = a.G, R = a.R, H = G * R;
+    const int D = a.D, G = a.G;
     __shared__ float gc[BC], eg[BC];
     const long cg = bc * G + g;
     if (tid < 64) {
@@ -167,7 +291,10 @@ __global__ __launch_bounds__(BW_NT) void chunk_prep_kernel(GdnBwdArgs a) {
         }
         gc[tid] = x;
         eg[tid] = expf(x);
-        if (blockIdx.z == 0) a.gam[cg * BC + tid] = x;
+        if (blockIdx.z == 0) {
+            a.gam[cg * BC + tid] = x;
+            a.eg[cg * BC + tid] = eg[tid];
+        }
     }
     __syncthreads();
     const float gl = gc[BC - 1];
@@ -181,13 +308,6 @@ __global__ __launch_bounds__(BW_NT) void chunk_prep_kernel(GdnBwdArgs a) {
         a.vb[o] = vx * be;
         a.kbe[o] = kx * be * eg[i];
         a.ktl[o] = kx * expf(gl - gc[i]);
-        for (int r = 0; r < R; ++r) {
-            const long oc = ((cg * R + r) * BC + i) * D + d;
-            const float qx = a.q[(tok * H + g * R + r) * D + d];
-            a.qd[oc] = a.scale * qx * eg[i];
-            a.qc[oc] = qx;
-            a.dOc[oc] = a.dO[(tok * H + g * R + r) * D + d];
-        }
     }
     for (int e = tid; e < 16 * D; e += BW_NT) {              // kt transposed [D][C], token index fastest
         const int d = e / 16, i = r0 + e % 16;
@@ -491,13 +611,13 @@ __global__ __launch_bounds__(BW_NT) void decay_grad_kernel(GdnBwdArgs a) {
 }
 
 // ------------------------------------------------------------------------------------ final assembly
-// grid (chunks, G, 4): rows r0 .. r0 + 15 of (chunk, KV head): dq += s dqd e^gc, dk, dv, d beta, and each row's share
+// grid (chunks, G, 4): rows r0 .. r0 + 15 of (chunk, KV head): dk, dv, d beta, and each row's share
 // of d gc (into dgz, which holds the decay's share); the last row's extra terms (sum dkt kt and e^(gc_C') <S, dS'>,
 // the latter over a quarter of the D x D entries) into part[cg][z]
 __global__ __launch_bounds__(BW_NT) void chunk_final_kernel(GdnBwdArgs a) {
     const long bc = blockIdx.x;
     const int g = blockIdx.y, z = blockIdx.z, r0 = z * 16, tid = threadIdx.x, lane = lane_id(), wv = wave_id();
-    const int D = a.D, G = a.G, R = a.R, H = G * R;
+    const int D = a.D, G = a.G, R = a.R;
     const long cg = bc * G + g;
     __shared__ float gc[BC], red[BW_NT / 64];
     if (tid < BC) gc[tid] = a.gam[cg * BC + tid];
@@ -511,22 +631,18 @@ __global__ __launch_bounds__(BW_NT) void chunk_final_kernel(GdnBwdArgs a) {
         const long tok = bc * BC + i;
         const float egi = expf(gc[i]), eti = expf(gl - gc[i]);
         const float be = a.beta[tok * G + g];
+        // the query path's share: s e^gc sum_r dqd_r . q_r, from the row-dot partials of the dqd products
         float dgi = 0.f, dbi = 0.f;
+        for (int e = lane; e < R * (D / 64); e += 64) dgi += a.qdot[(cg * R * (D / 64) + e) * BC + i];
+        dgi *= a.scale * egi;
         for (int d = lane; d < D; d += 64) {
             const long o = (cg * BC + i) * D + d;
-            float dqsum = 0.f;
-            for (int r = 0; r < R; ++r) {
-                const long orr = ((cg * R + r) * BC + i) * D + d;
-                const float dqd = a.dqd[orr];
-                dqsum += dqd * a.qd[orr];
-                a.dq[(tok * H + g * R + r) * D + d] += a.scale * dqd * egi;
-            }
             const float dkt = a.dkt[o], kt = a.ktl[o];
             const float dkbe = a.dkbe[o];
             const float dkbt = a.dkb[o] + dkbe * egi;
             const float kx = a.k[(tok * G + g) * D + d], vx = a.v[(tok * G + g) * D + d];
             const float dvb = a.dvb[o];
-            dgi += dqsum + dkbe * a.kbe[o] - dkt * kt;
+            dgi += dkbe * a.kbe[o] - dkt * kt;
             ktsum += dkt * kt;
             dbi += dkbt * kx + dvb * vx;
             a.dk[(tok * G + g) * D + d] = a.dkacc[o] + dkt * eti + dkbt * be;
@@ -574,12 +690,23 @@ __global__ __launch_bounds__(64) void dg_scan_kernel(GdnBwdArgs a) {
 int bgemm(const BgArgs& a, hipStream_t s) {
     // each operand must be contiguous along k or along its other dimension (16-byte tile loads)
     if ((a.ak != 1 && a.am != 1) || (a.bk != 1 && a.bn != 1)) return BF_ERR_UNSUPPORTED;
-    const dim3 grid((unsigned)a.nz, a.M / 64, a.N / 64);
+    if (a.M % 64 || a.N % 64 || a.K % 32 || a.K <= 0 || (a.rdo && a.cn != 1)) return BF_ERR_UNSUPPORTED;
+    // 16-byte row pieces of C, the addend and rdx when C is contiguous along n
+    if (a.cn == 1 && ((a.cm | a.sc0 | a.sc1 | a.sc2) % 4)) return BF_ERR_UNSUPPORTED;
     const bool ak = a.ak == 1, bk = a.bk == 1;
-    if (ak && bk) hipLaunchKernelGGL((bgemm_kernel<true, true>), grid, dim3(BW_NT), 0, s, a);
-    else if (ak) hipLaunchKernelGGL((bgemm_kernel<true, false>), grid, dim3(BW_NT), 0, s, a);
-    else if (bk) hipLaunchKernelGGL((bgemm_kernel<false, true>), grid, dim3(BW_NT), 0, s, a);
-    else hipLaunchKernelGGL((bgemm_kernel<false, false>), grid, dim3(BW_NT), 0, s, a);
+    if (a.N % 128 == 0) {
+        const dim3 grid((unsigned)a.nz, a.M / 64, a.N / 128);
+        if (ak && bk) hipLaunchKernelGGL((bgemm_kernel<true, true, 128>), grid, dim3(BW_NT), 0, s, a);
+        else if (ak) hipLaunchKernelGGL((bgemm_kernel<true, false, 128>), grid, dim3(BW_NT), 0, s, a);
+        else if (bk) hipLaunchKernelGGL((bgemm_kernel<false, true, 128>), grid, dim3(BW_NT), 0, s, a);
+        else hipLaunchKernelGGL((bgemm_kernel<false, false, 128>), grid, dim3(BW_NT), 0, s, a);
+    } else {
+        const dim3 grid((unsigned)a.nz, a.M / 64, a.N / 64);
+        if (ak && bk) hipLaunchKernelGGL((bgemm_kernel<true, true, 64>), grid, dim3(BW_NT), 0, s, a);
+        else if (ak) hipLaunchKernelGGL((bgemm_kernel<true, false, 64>), grid, dim3(BW_NT), 0, s, a);
+        else if (bk) hipLaunchKernelGGL((bgemm_kernel<false, true, 64>), grid, dim3(BW_NT), 0, s, a);
+        else hipLaunchKernelGGL((bgemm_kernel<false, false, 64>), grid, dim3(BW_NT), 0, s, a);
+    }
     return (int)hipGetLastError();
 }
 
@@ -589,15 +716,36 @@ struct Op {
     long s0, s1, s2, rs, cs;
 };
 
+// a split reduction index k = (kh, kl), kl < 2^shift: the operands' strides of kh, and the optional column scale
+// of A (ksc[z0 s0 + z1 s1 + kl])
+struct KSplit {
+    int shift = 30;
+    long a = 0, b = 0;
+    const float* ksc = nullptr;
+    long s0 = 0, s1 = 0;
+};
+
+// epilogue extras: a row scale msc[z0 s0 + z1 s1 + m] and row dots with rdx into rdo
+struct Epi {
+    const float* msc = nullptr;
+    long s0 = 0, s1 = 0;
+    const float* rdx = nullptr;
+    float* rdo = nullptr;
+};
+
 // C (M x N) per (chunk, g[, r]) = add + alpha * A B, with A, B given as Op (transposes by swapping strides)
 int gemm(int M, int N, int K, int nz, int n1, int n2, Op A, Op B, float* C, long c0, long c1, long c2, long cm,
-         long cn, float alpha, int acc, int mask, const float* add, hipStream_t s) {
+         long cn, float alpha, int acc, int mask, const float* add, hipStream_t s, const KSplit& ks = KSplit{},
+         const Epi& ep = Epi{}) {
     BgArgs g{};
-    g.M = M; g.N = N; g.K = K; g.n1 = n1; g.n2 = n2; g.nz = nz;
-    g.A = A.p; g.sa0 = A.s0; g.sa1 = A.s1; g.sa2 = A.s2; g.am = A.rs; g.ak = A.cs;
-    g.B = B.p; g.sb0 = B.s0; g.sb1 = B.s1; g.sb2 = B.s2; g.bk = B.rs; g.bn = B.cs;
+    g.M = M; g.N = N; g.K = K; g.n1 = n1; g.n2 = n2; g.nz = nz; g.kshift = ks.shift;
+    g.A = A.p; g.sa0 = A.s0; g.sa1 = A.s1; g.sa2 = A.s2; g.am = A.rs; g.ak = A.cs; g.sak = ks.a;
+    g.B = B.p; g.sb0 = B.s0; g.sb1 = B.s1; g.sb2 = B.s2; g.bk = B.rs; g.bn = B.cs; g.sbk = ks.b;
     g.C = C; g.sc0 = c0; g.sc1 = c1; g.sc2 = c2; g.cm = cm; g.cn = cn;
+    g.ksc = ks.ksc; g.ks0 = ks.s0; g.ks1 = ks.s1;
+    g.msc = ep.msc; g.ms0 = ep.s0; g.ms1 = ep.s1; g.rdx = ep.rdx; g.rdo = ep.rdo;
     g.alpha = alpha; g.acc = acc; g.mask = mask; g.add = add;
+    if (ks.shift < 30 && ((1 << ks.shift) % 16 != 0 || K % (1 << ks.shift) != 0)) return BF_ERR_UNSUPPORTED;
     return bgemm(g, s);
 }
 
@@ -608,10 +756,10 @@ Op tr(Op o) { std::swap(o.rs, o.cs); return o; }
 size_t gdn_bwd_workspace(int num_seqs, long T, int G, int R, int D) {
     const long n = T / BC, NC = (long)num_seqs * n * G;             // chunk-heads
     const long cc = BC * BC, cd = (long)BC * D, dd = (long)D * D;
-    const long floats = NC * (BC * 2 + 4                             // gam, dgz, part
+    const long floats = NC * (BC * 3 + 4                             // gam, eg, dgz, part
                               + cc * 4                               // P, Am, M, dA
                               + cd * 8                               // kb, vb, kbe, ktl, u, w, ktlT, wT
-                              + (long)R * (cc * 3 + cd * 4)          // QK, attn, dattn; qd, dqd, qc, dOc
+                              + (long)R * (cc * 3 + (D / 64) * BC)   // QK, attn, dattn; qdot
                               + dd * 3                               // Sc, E2, dSx
                               + cd * 9                               // E1, dvn, vn, dkt, dw, dvb, dkbe, dkb, dkacc
                               + cc * 2);                             // dM, T1
@@ -628,12 +776,12 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
         p += ((count * (long)sizeof(float) + 255) / 256) * 256;
         return r;
     };
-    a.gam = take(NC * BC); a.dgz = take(NC * BC); a.part = take(NC * 4);
+    a.gam = take(NC * BC); a.eg = take(NC * BC); a.dgz = take(NC * BC); a.part = take(NC * 4);
     a.P = take(NC * cc); a.Am = take(NC * cc); a.Mi = take(NC * cc); a.dA = take(NC * cc);
     a.kb = take(NC * cd); a.vb = take(NC * cd); a.kbe = take(NC * cd); a.ktl = take(NC * cd);
     a.u = take(NC * cd); a.w = take(NC * cd); a.ktlT = take(NC * cd); a.wT = take(NC * cd);
     a.QK = take(NC * R * cc); a.attn = take(NC * R * cc); a.dattn = take(NC * R * cc);
-    a.qd = take(NC * R * cd); a.dqd = take(NC * R * cd); a.qc = take(NC * R * cd); a.dOc = take(NC * R * cd);
+    a.qdot = take(NC * R * (D / 64) * BC);
     a.Sc = take(NC * dd); a.E2 = take(NC * dd); a.dSx = take(NC * dd);
     a.E1 = take(NC * cd); a.dvn = take(NC * cd); a.vn = take(NC * cd); a.dkt = take(NC * cd); a.dw = take(NC * cd);
     a.dvb = take(NC * cd); a.dkbe = take(NC * cd); a.dkb = take(NC * cd); a.dkacc = take(NC * cd);
@@ -673,13 +821,18 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
             (long)R * cc, cc, BC, 1, a.scale, 0, 1, nullptr, s));
     hipLaunchKernelGGL(decay_mask_kernel, dim3((unsigned)NC), dim3(BW_NT), 0, s, a.QK, a.attn, a.gam, R, 1);
     ok((int)hipGetLastError());
-    // E1 = sum_r attn_r^T dO_r [C x D], E2 = sum_r qd_r^T dO_r [D x D]: one product each over K = R C, the (r, token)
-    // pairs of the chunk-major copies [cg][r C + i][...]
-    const Op dOc{a.dOc, (long)G * R * cd, (long)R * cd, 0, D, 1};
-    ok(gemm(BC, D, R * BC, nzg, G, 1, tr(Op{a.attn, (long)G * R * cc, (long)R * cc, 0, BC, 1}), dOc, a.E1, (long)G * cd,
-            cd, 0, D, 1, 1.f, 0, 0, nullptr, s));
-    ok(gemm(D, D, R * BC, nzg, G, 1, tr(Op{a.qd, (long)G * R * cd, (long)R * cd, 0, D, 1}), dOc, a.E2, (long)G * dd, dd, 0,
-            D, 1, 1.f, 0, 0, nullptr, s));
+    // E1 = sum_r attn_r^T dO_r [C x D], E2 = sum_r qd_r^T dO_r = s sum_r q_r^T diag(e^gc) dO_r [D x D]: one product
+    // each over K = R C, the (r, token) pairs, read from the token-major q and dO (k = 64 r + i: token stride H D,
+    // head stride D)
+    const Op dOk{a.dO, (long)BC * H * D, (long)R * D, 0, (long)H * D, 1};
+    const Op qk{a.q, (long)BC * H * D, (long)R * D, 0, (long)H * D, 1};
+    KSplit rk;
+    rk.shift = 6; rk.a = cc; rk.b = D;                    // attn^T / dattn^T (chunk-major [r][i][j]) against dO or q
+    ok(gemm(BC, D, R * BC, nzg, G, 1, tr(Op{a.attn, (long)G * R * cc, (long)R * cc, 0, BC, 1}), dOk, a.E1, (long)G * cd,
+            cd, 0, D, 1, 1.f, 0, 0, nullptr, s, rk));
+    KSplit rq;
+    rq.shift = 6; rq.a = D; rq.b = D; rq.ksc = a.eg; rq.s0 = (long)G * BC; rq.s1 = BC;   // A = q^T, columns e^gc
+    ok(gemm(D, D, R * BC, nzg, G, 1, tr(qk), dOk, a.E2, (long)G * dd, dd, 0, D, 1, a.scale, 0, 0, nullptr, s, rq));
     // walks
     const dim3 wgrid(a.num_seqs, G, 2 * D / 16);
     if (D == 64) hipLaunchKernelGGL(walk_kernel<64>, wgrid, dim3(64 * walk_nw<64>()), 0, s, a);
@@ -688,11 +841,14 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
     ok((int)hipGetLastError());
     // v_new = u - w S
     ok(gemm(BC, D, D, nzg, G, 1, W(a.w, BC, D), W(a.Sc, D, D), a.vn, (long)G * cd, cd, 0, D, 1, -1.f, 0, 0, a.u, s));
-    // dattn_r = tril(dO_r v_new^T), dqd_r = dO_r S^T
+    // dattn_r = tril(dO_r v_new^T); dqd_r = dO_r S^T goes straight into dq_r = s e^gc dqd_r (token-major; the attn
+    // share is added below), with each row's dot with q_r (the query path's d gc share) as partials in qdot
     ok(gemm(BC, BC, D, nzr, G, R, dOR(), tr(Op{a.vn, (long)G * cd, cd, 0, D, 1}), a.dattn, (long)G * R * cc,
             (long)R * cc, cc, BC, 1, 1.f, 0, 1, nullptr, s));
-    ok(gemm(BC, D, D, nzr, G, R, dOR(), tr(Op{a.Sc, (long)G * dd, dd, 0, D, 1}), a.dqd, (long)G * R * cd, (long)R * cd,
-            cd, D, 1, 1.f, 0, 0, nullptr, s));
+    Epi eq;
+    eq.msc = a.eg; eq.s0 = (long)G * BC; eq.s1 = BC; eq.rdx = a.q; eq.rdo = a.qdot;
+    ok(gemm(BC, D, D, nzr, G, R, dOR(), tr(Op{a.Sc, (long)G * dd, dd, 0, D, 1}), a.dq, (long)BC * H * D, (long)R * D, D,
+            (long)H * D, 1, a.scale, 0, 0, nullptr, s, KSplit{}, eq));
     // dkt = v_new dS'^T, dw = -dvn S^T
     ok(gemm(BC, D, D, nzg, G, 1, W(a.vn, BC, D), tr(W(a.dSx, D, D)), a.dkt, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0,
             nullptr, s));
@@ -719,11 +875,10 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
     ok(gemm(BC, D, BC, nzg, G, 1, W(a.dA, BC, BC), kT(), a.dkb, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0, nullptr, s));
     ok(gemm(BC, D, BC, nzg, G, 1, tr(W(a.dA, BC, BC)), W(a.kb, BC, D), a.dkacc, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0,
             nullptr, s));
-    ok(gemm(BC, D, R * BC, nzg, G, 1, tr(Op{a.dattn, (long)G * R * cc, (long)R * cc, 0, BC, 1}),
-            Op{a.qc, (long)G * R * cd, (long)R * cd, 0, D, 1}, a.dkacc, (long)G * cd, cd, 0, D, 1, a.scale, 1, 0, nullptr,
-            s));                                          // sum_r dattn_r^T (s q_r), K = R C
+    ok(gemm(BC, D, R * BC, nzg, G, 1, tr(Op{a.dattn, (long)G * R * cc, (long)R * cc, 0, BC, 1}), qk, a.dkacc,
+            (long)G * cd, cd, 0, D, 1, a.scale, 1, 0, nullptr, s, rk));   // sum_r dattn_r^T (s q_r), K = R C
     ok(gemm(BC, D, BC, nzr, G, R, WR(a.dattn, BC, BC), Op{a.k, (long)BC * G * D, D, 0, (long)G * D, 1}, a.dq,
-            (long)BC * H * D, (long)R * D, D, (long)H * D, 1, a.scale, 0, 0, nullptr, s));
+            (long)BC * H * D, (long)R * D, D, (long)H * D, 1, a.scale, 1, 0, nullptr, s));
     hipLaunchKernelGGL(chunk_final_kernel, dim3((unsigned)NB, G, 4), dim3(BW_NT), 0, s, a);
     hipLaunchKernelGGL(dg_scan_kernel, dim3((unsigned)NC), dim3(64), 0, s, a);
     ok((int)hipGetLastError());

@@ -14,8 +14,8 @@
 // followed by the decay, gate and cumulative-sum chains (chunk_final_kernel).
 //
 // Kernels: bgemm_kernel (batched strided fp32 GEMM on v_mfma_f32_16x16x4f32, optional triangular mask, addend and
-// accumulate), chunk_prep_kernel, decay_mask_kernel, unit_lower_inverse_kernel, walk_kernel (both state walks in one
-// launch), decay_grad_kernel, chunk_final_kernel, dg_scan_kernel.
+// accumulate, in-chunk decay, row scale and row / column dots in the epilogue), chunk_prep_kernel,
+// unit_lower_inverse_kernel, walk_kernel (both state walks in one launch), chunk_final_kernel, dg_scan_kernel.
 #include "bf_common.h"
 #include "bf_internal.h"
 
@@ -32,10 +32,12 @@ constexpr int BW_NT = 256;
 // add likewise): the reduction index may run over two strides, e.g. (query head, token) pairs of a token-major
 // [token][head][D] tensor. M, N multiples of 64, K of 16 (and 2^kshift a multiple of 16 when it splits K), each
 // operand contiguous along one dimension, 16-byte aligned. ksc (or null) scales A's column k by
-// ksc[z0 ks0 + z1 ks1 + (k & (2^kshift - 1))], msc (or null) the product's row m by msc[z0 ms0 + z1 ms1 + m]. mask 1
-// keeps m >= n, mask 2 keeps m > n (the rest is written 0, or left unchanged when accumulating). With rdo (C
-// contiguous along n only), the unscaled product's row dots with rdx (addressed like C) go to
-// rdo[(z N/64 + n/64) M + m], one partial per 64 columns (z = blockIdx.x).
+// ksc[z0 ks0 + z1 ks1 + (k & (2^kshift - 1))], msc (or null) the product's row m by msc[z0 ms0 + z1 ms1 + m]; with
+// P = alpha msc A B so scaled, dgc (or null) multiplies kept element (m, n) by e^(gc[m] - gc[n]), gc = dgc + z0 dg0 +
+// z1 dg1 (the in-chunk decay). mask 1 keeps m >= n, mask 2 keeps m > n (the rest is written 0, or left unchanged when
+// accumulating). C contiguous along n only: with rdo, the row dots of P with rdx (addressed like C) go to
+// rdo[(z N/64 + n/64) M + m], one partial per 64 columns, and with cdo the column dots to cdo[(z M/64 + m/64) N + n]
+// (z = blockIdx.x).
 struct BgArgs {
     int M, N, K, n1, n2, nz, kshift;
     const float* A; long sa0, sa1, sa2, am, ak, sak;
@@ -44,7 +46,8 @@ struct BgArgs {
     const float* add;                   // same strides as C, or null
     const float* ksc; long ks0, ks1;
     const float* msc; long ms0, ms1;
-    const float* rdx; float* rdo;
+    const float* dgc; long dg0, dg1;
+    const float* rdx; float* rdo; float* cdo;
     float alpha;
     int acc, mask;
 };
@@ -57,7 +60,9 @@ struct BgArgs {
 // 4-byte reads). Fragment value j of lane (i, q) is k = 16 kh + 4 q + j for both operands. The LDS tiles are double
 // buffered: step s computes from one buffer, then writes step s + 1's operands (loaded from global during step s - 1)
 // into the other and issues step s + 2's loads, with one barrier per step.
-template <bool AK, bool BK, int BN>
+// EX: the epilogue extras compiled in: 0 none, 1 msc and rdo, 2 also dgc and cdo. The plain products measurably need
+// the small epilogue, and the row-scaled ones one without the per-element decay.
+template <bool AK, bool BK, int BN, int EX>
 __global__ __launch_bounds__(BW_NT) void bgemm_kernel(BgArgs a) {
     constexpr int KS = 32, LDK = KS + 4;        // k per step, LDS row pitch (floats)
     constexpr int WN = BN / 2, TU = WN / 16;    // wave tile 32 x WN: 2 x TU MFMA tiles
@@ -176,7 +181,7 @@ __global__ __launch_bounds__(BW_NT) void bgemm_kernel(BgArgs a) {
             __syncthreads();
         }
     }
-    const float* msc = a.msc ? a.msc + z0 * a.ms0 + z1 * a.ms1 : nullptr;
+    const float* msc = EX >= 1 && a.msc ? a.msc + z0 * a.ms0 + z1 * a.ms1 : nullptr;
     if (a.cn == 1) {
         // Row-contiguous output: the tile goes through LDS (free after the last step's barrier) and each thread then
         // handles 16-byte row pieces, so C, the addend and rdx move as whole rows. All reads of a thread are issued
@@ -195,7 +200,9 @@ __global__ __launch_bounds__(BW_NT) void bgemm_kernel(BgArgs a) {
         const int n = tn + 4 * c4;
         auto row = [&](int j) { return tid / RW + (BW_NT / RW) * j; };
         auto at = [&](int j) { return coff + (long)(tm + row(j)) * a.cm + n; };
-        float4 prev[NP], rx[NP];
+        const bool dots = (EX >= 1 && a.rdo) || (EX == 2 && a.cdo);
+        const float* gc = EX == 2 && a.dgc ? a.dgc + z0 * a.dg0 + z1 * a.dg1 : nullptr;
+        float4 prev[NP], rx[NP], gn = make_float4(0.f, 0.f, 0.f, 0.f);
         if (a.acc || a.add) {
             const float* src = a.acc ? a.C : a.add;
 #pragma unroll
@@ -204,29 +211,46 @@ __global__ __launch_bounds__(BW_NT) void bgemm_kernel(BgArgs a) {
 #pragma unroll
             for (int j = 0; j < NP; ++j) prev[j] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
-        if (a.rdo) {
+        if (dots) {
 #pragma unroll
             for (int j = 0; j < NP; ++j) rx[j] = *reinterpret_cast<const float4*>(a.rdx + at(j));
         }
+        if (gc) gn = *reinterpret_cast<const float4*>(gc + n);
 #pragma unroll
         for (int j = 0; j < NP; ++j) {
             const int m = tm + row(j);
             const float4 x = *reinterpret_cast<const float4*>(&Cs[row(j)][4 * c4]);
-            if (a.rdo) {                                   // one partial per 64 columns: 16 pieces of the row
-                float d = x.x * rx[j].x + x.y * rx[j].y + x.z * rx[j].z + x.w * rx[j].w;
-#pragma unroll
-                for (int off = 1; off < 16; off <<= 1) d += __shfl_xor(d, off);
-                if (c4 % 16 == 0) a.rdo[((long)z * (a.N / 64) + (tn + 4 * c4) / 64) * a.M + m] = d;
-            }
             const float al = msc ? a.alpha * msc[m] : a.alpha;
-            const float xv[4] = {x.x, x.y, x.z, x.w};
+            const float pv[4] = {al * x.x, al * x.y, al * x.z, al * x.w};
+            if (dots) {
+                const float zv[4] = {pv[0] * rx[j].x, pv[1] * rx[j].y, pv[2] * rx[j].z, pv[3] * rx[j].w};
+                if (a.rdo) {                              // one partial per 64 columns: 16 pieces of the row
+                    float d = (zv[0] + zv[1]) + (zv[2] + zv[3]);
+#pragma unroll
+                    for (int off = 1; off < 16; off <<= 1) d += __shfl_xor(d, off);
+                    if (c4 % 16 == 0) a.rdo[((long)z * (a.N / 64) + (tn + 4 * c4) / 64) * a.M + m] = d;
+                }
+                if (EX == 2 && a.cdo)                      // the piece's own slot: only this thread reads it
+                    *reinterpret_cast<float4*>(&Cs[row(j)][4 * c4]) = make_float4(zv[0], zv[1], zv[2], zv[3]);
+            }
+            const float gm = gc ? gc[m] : 0.f;
+            const float gv[4] = {gn.x, gn.y, gn.z, gn.w};
             float ov[4] = {prev[j].x, prev[j].y, prev[j].z, prev[j].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const bool keep = a.mask == 0 || (a.mask == 1 && m >= n + e) || (a.mask == 2 && m > n + e);
-                if (keep) ov[e] += al * xv[e];
+                if (keep) ov[e] += gc ? pv[e] * expf(gm - gv[e]) : pv[e];
             }
             *reinterpret_cast<float4*>(a.C + at(j)) = make_float4(ov[0], ov[1], ov[2], ov[3]);
+        }
+        if (EX == 2 && a.cdo) {                            // column sums of the tile's row dots
+            __syncthreads();
+            if (tid < BN) {
+                float cs = 0.f;
+#pragma unroll 8
+                for (int r = 0; r < 64; ++r) cs += Cs[r][tid];
+                a.cdo[((long)z * (a.M / 64) + tm / 64) * a.N + tn + tid] = cs;
+            }
         }
         return;
     }
@@ -315,21 +339,6 @@ __global__ __launch_bounds__(BW_NT) void chunk_prep_kernel(GdnBwdArgs a) {
     }
 }
 
-// dst = src * e^(gc_i - gc_j) on the kept triangle (mask 1: i >= j, 2: i > j), 0 elsewhere; nmat matrices per
-// (chunk, KV head), C x C each
-__global__ __launch_bounds__(BW_NT) void decay_mask_kernel(const float* src, float* dst, const float* gam, int nmat,
-                                                           int mask) {
-    const long cg = blockIdx.x;
-    __shared__ float gc[BC];
-    if (threadIdx.x < BC) gc[threadIdx.x] = gam[cg * BC + threadIdx.x];
-    __syncthreads();
-    for (int e = threadIdx.x; e < nmat * BC * BC; e += BW_NT) {
-        const int ij = e % (BC * BC), i = ij / BC, j = ij % BC;
-        const bool keep = mask == 1 ? i >= j : i > j;
-        const long at = cg * nmat * BC * BC + e;
-        dst[at] = keep ? src[at] * expf(gc[i] - gc[j]) : 0.f;
-    }
-}
 
 // M = (I + A)^-1 for a strictly lower A (C x C): forward substitution, lane j owns column j
 __global__ __launch_bounds__(64) void unit_lower_inverse_kernel(const float* Am, float* Mi) {
@@ -570,45 +579,6 @@ __global__ __launch_bounds__(64 * walk_nw<D>()) void walk_kernel(GdnBwdArgs a) {
     else walk_bwd<D>(a, blockIdx.z - D / 16);
 }
 
-// ------------------------------------------------------------------------------------ decay gradients
-// dAd = dA * decay (in place), dattn_r *= decay (in place), and the decay's share of d gc:
-// Z = dAd * P + sum_r dattn_r * QK_r, dgz_i = sum_j Z_ij - sum_j Z_ji
-__global__ __launch_bounds__(BW_NT) void decay_grad_kernel(GdnBwdArgs a) {
-    const long cg = blockIdx.x;
-    const int tid = threadIdx.x, R = a.R;
-    __shared__ float gc[BC];
-    __shared__ float Z[BC][BC + 1];
-    if (tid < BC) gc[tid] = a.gam[cg * BC + tid];
-    __syncthreads();
-    for (int e = tid; e < BC * BC; e += BW_NT) {
-        const int i = e / BC, j = e % BC;
-        float z = 0.f;
-        if (i >= j) {
-            const float dec = expf(gc[i] - gc[j]);
-            const long at = cg * BC * BC + e;
-            if (i > j) {
-                const float d = a.dA[at] * dec;
-                a.dA[at] = d;
-                z = d * a.P[at];
-            } else {
-                a.dA[at] = 0.f;
-            }
-            for (int r = 0; r < R; ++r) {
-                const long ar = (cg * R + r) * BC * BC + e;
-                const float d = a.dattn[ar] * dec;
-                a.dattn[ar] = d;
-                z += d * a.QK[ar];
-            }
-        }
-        Z[i][j] = z;
-    }
-    __syncthreads();
-    if (tid < BC) {
-        float s = 0.f;
-        for (int j = 0; j < BC; ++j) s += Z[tid][j] - Z[j][tid];
-        a.dgz[cg * BC + tid] = s;
-    }
-}
 
 // ------------------------------------------------------------------------------------ final assembly
 // grid (chunks, G, 4): rows r0 .. r0 + 15 of (chunk, KV head): dk, dv, d beta, and each row's share
@@ -634,7 +604,10 @@ __global__ __launch_bounds__(BW_NT) void chunk_final_kernel(GdnBwdArgs a) {
         // the query path's share: s e^gc sum_r dqd_r . q_r, from the row-dot partials of the dqd products
         float dgi = 0.f, dbi = 0.f;
         for (int e = lane; e < R * (D / 64); e += 64) dgi += a.qdot[(cg * R * (D / 64) + e) * BC + i];
-        dgi *= a.scale * egi;
+        // the decay's share: row minus column sums of dP . P and of dQK_r . QK_r (dP = the gradient of the
+        // decayed strict-lower A, dQK_r of attn_r), from the epilogues of the dA and dattn products
+        if (lane == 0) dgi += a.zrA[cg * BC + i] - a.zcA[cg * BC + i];
+        for (int r = lane; r < R; r += 64) dgi += a.zr[(cg * R + r) * BC + i] - a.zc[(cg * R + r) * BC + i];
         for (int d = lane; d < D; d += 64) {
             const long o = (cg * BC + i) * D + d;
             const float dkt = a.dkt[o], kt = a.ktl[o];
@@ -654,7 +627,7 @@ __global__ __launch_bounds__(BW_NT) void chunk_final_kernel(GdnBwdArgs a) {
             dbi += __shfl_xor(dbi, off);
         }
         if (lane == 0) {
-            a.dgz[cg * BC + i] += dgi;
+            a.dgz[cg * BC + i] = dgi;
             a.dbeta[tok * G + g] = dbi;
         }
     }
@@ -690,23 +663,32 @@ __global__ __launch_bounds__(64) void dg_scan_kernel(GdnBwdArgs a) {
 int bgemm(const BgArgs& a, hipStream_t s) {
     // each operand must be contiguous along k or along its other dimension (16-byte tile loads)
     if ((a.ak != 1 && a.am != 1) || (a.bk != 1 && a.bn != 1)) return BF_ERR_UNSUPPORTED;
-    if (a.M % 64 || a.N % 64 || a.K % 32 || a.K <= 0 || (a.rdo && a.cn != 1)) return BF_ERR_UNSUPPORTED;
+    if (a.M % 64 || a.N % 64 || a.K % 32 || a.K <= 0) return BF_ERR_UNSUPPORTED;
+    if ((a.rdo || a.cdo || a.dgc) && a.cn != 1) return BF_ERR_UNSUPPORTED;
     // 16-byte row pieces of C, the addend and rdx when C is contiguous along n
     if (a.cn == 1 && ((a.cm | a.sc0 | a.sc1 | a.sc2) % 4)) return BF_ERR_UNSUPPORTED;
     const bool ak = a.ak == 1, bk = a.bk == 1;
+    const int ex = a.dgc || a.cdo ? 2 : a.msc || a.rdo ? 1 : 0;
+    auto go = [&](auto kern, int bn) {
+        hipLaunchKernelGGL(kern, dim3((unsigned)a.nz, a.M / 64, a.N / bn), dim3(BW_NT), 0, s, a);
+    };
+#define BG_GO(BN, EX)                                                                         \
+    do {                                                                                      \
+        if (ak && bk) go(bgemm_kernel<true, true, BN, EX>, BN);                               \
+        else if (ak) go(bgemm_kernel<true, false, BN, EX>, BN);                               \
+        else if (bk) go(bgemm_kernel<false, true, BN, EX>, BN);                               \
+        else go(bgemm_kernel<false, false, BN, EX>, BN);                                      \
+    } while (0)
     if (a.N % 128 == 0) {
-        const dim3 grid((unsigned)a.nz, a.M / 64, a.N / 128);
-        if (ak && bk) hipLaunchKernelGGL((bgemm_kernel<true, true, 128>), grid, dim3(BW_NT), 0, s, a);
-        else if (ak) hipLaunchKernelGGL((bgemm_kernel<true, false, 128>), grid, dim3(BW_NT), 0, s, a);
-        else if (bk) hipLaunchKernelGGL((bgemm_kernel<false, true, 128>), grid, dim3(BW_NT), 0, s, a);
-        else hipLaunchKernelGGL((bgemm_kernel<false, false, 128>), grid, dim3(BW_NT), 0, s, a);
+        if (ex == 2) BG_GO(128, 2);
+        else if (ex == 1) BG_GO(128, 1);
+        else BG_GO(128, 0);
     } else {
-        const dim3 grid((unsigned)a.nz, a.M / 64, a.N / 64);
-        if (ak && bk) hipLaunchKernelGGL((bgemm_kernel<true, true, 64>), grid, dim3(BW_NT), 0, s, a);
-        else if (ak) hipLaunchKernelGGL((bgemm_kernel<true, false, 64>), grid, dim3(BW_NT), 0, s, a);
-        else if (bk) hipLaunchKernelGGL((bgemm_kernel<false, true, 64>), grid, dim3(BW_NT), 0, s, a);
-        else hipLaunchKernelGGL((bgemm_kernel<false, false, 64>), grid, dim3(BW_NT), 0, s, a);
+        if (ex == 2) BG_GO(64, 2);
+        else if (ex == 1) BG_GO(64, 1);
+        else BG_GO(64, 0);
     }
+#undef BG_GO
     return (int)hipGetLastError();
 }
 
@@ -725,12 +707,16 @@ struct KSplit {
     long s0 = 0, s1 = 0;
 };
 
-// epilogue extras: a row scale msc[z0 s0 + z1 s1 + m] and row dots with rdx into rdo
+// epilogue extras: a row scale msc[z0 s0 + z1 s1 + m], the in-chunk decay from dgc[z0 g0 + z1 g1 + .], and the row /
+// column dots with rdx into rdo / cdo
 struct Epi {
     const float* msc = nullptr;
     long s0 = 0, s1 = 0;
+    const float* dgc = nullptr;
+    long g0 = 0, g1 = 0;
     const float* rdx = nullptr;
     float* rdo = nullptr;
+    float* cdo = nullptr;
 };
 
 // C (M x N) per (chunk, g[, r]) = add + alpha * A B, with A, B given as Op (transposes by swapping strides)
@@ -743,7 +729,8 @@ int gemm(int M, int N, int K, int nz, int n1, int n2, Op A, Op B, float* C, long
     g.B = B.p; g.sb0 = B.s0; g.sb1 = B.s1; g.sb2 = B.s2; g.bk = B.rs; g.bn = B.cs; g.sbk = ks.b;
     g.C = C; g.sc0 = c0; g.sc1 = c1; g.sc2 = c2; g.cm = cm; g.cn = cn;
     g.ksc = ks.ksc; g.ks0 = ks.s0; g.ks1 = ks.s1;
-    g.msc = ep.msc; g.ms0 = ep.s0; g.ms1 = ep.s1; g.rdx = ep.rdx; g.rdo = ep.rdo;
+    g.msc = ep.msc; g.ms0 = ep.s0; g.ms1 = ep.s1; g.dgc = ep.dgc; g.dg0 = ep.g0; g.dg1 = ep.g1;
+    g.rdx = ep.rdx; g.rdo = ep.rdo; g.cdo = ep.cdo;
     g.alpha = alpha; g.acc = acc; g.mask = mask; g.add = add;
     if (ks.shift < 30 && ((1 << ks.shift) % 16 != 0 || K % (1 << ks.shift) != 0)) return BF_ERR_UNSUPPORTED;
     return bgemm(g, s);
@@ -756,10 +743,10 @@ Op tr(Op o) { std::swap(o.rs, o.cs); return o; }
 size_t gdn_bwd_workspace(int num_seqs, long T, int G, int R, int D) {
     const long n = T / BC, NC = (long)num_seqs * n * G;             // chunk-heads
     const long cc = BC * BC, cd = (long)BC * D, dd = (long)D * D;
-    const long floats = NC * (BC * 3 + 4                             // gam, eg, dgz, part
-                              + cc * 4                               // P, Am, M, dA
+    const long floats = NC * (BC * 5 + 4                             // gam, eg, dgz, zrA, zcA, part
+                              + cc * 3                               // Am, M, dA
                               + cd * 8                               // kb, vb, kbe, ktl, u, w, ktlT, wT
-                              + (long)R * (cc * 3 + (D / 64) * BC)   // QK, attn, dattn; qdot
+                              + (long)R * (cc * 2 + (D / 64 + 2) * BC)   // attn, dattn; qdot, zr, zc
                               + dd * 3                               // Sc, E2, dSx
                               + cd * 9                               // E1, dvn, vn, dkt, dw, dvb, dkbe, dkb, dkacc
                               + cc * 2);                             // dM, T1
@@ -777,10 +764,11 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
         return r;
     };
     a.gam = take(NC * BC); a.eg = take(NC * BC); a.dgz = take(NC * BC); a.part = take(NC * 4);
-    a.P = take(NC * cc); a.Am = take(NC * cc); a.Mi = take(NC * cc); a.dA = take(NC * cc);
+    a.Am = take(NC * cc); a.Mi = take(NC * cc); a.dA = take(NC * cc);
+    a.zrA = take(NC * BC); a.zcA = take(NC * BC); a.zr = take(NC * R * BC); a.zc = take(NC * R * BC);
     a.kb = take(NC * cd); a.vb = take(NC * cd); a.kbe = take(NC * cd); a.ktl = take(NC * cd);
     a.u = take(NC * cd); a.w = take(NC * cd); a.ktlT = take(NC * cd); a.wT = take(NC * cd);
-    a.QK = take(NC * R * cc); a.attn = take(NC * R * cc); a.dattn = take(NC * R * cc);
+    a.attn = take(NC * R * cc); a.dattn = take(NC * R * cc);
     a.qdot = take(NC * R * (D / 64) * BC);
     a.Sc = take(NC * dd); a.E2 = take(NC * dd); a.dSx = take(NC * dd);
     a.E1 = take(NC * cd); a.dvn = take(NC * cd); a.vn = take(NC * cd); a.dkt = take(NC * cd); a.dw = take(NC * cd);
@@ -805,10 +793,11 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
     // prep
     hipLaunchKernelGGL(chunk_prep_kernel, dim3((unsigned)NB, G, 4), dim3(BW_NT), 0, s, a);
     ok((int)hipGetLastError());
-    // P = (k b) k^T ; Am = strict_lower(P * decay)
-    ok(gemm(BC, BC, D, nzg, G, 1, W(a.kb, BC, D), tr(kT()), a.P, (long)G * cc, cc, 0, BC, 1, 1.f, 0, 0, nullptr, s));
-    hipLaunchKernelGGL(decay_mask_kernel, dim3((unsigned)NC), dim3(BW_NT), 0, s, a.P, a.Am, a.gam, 1, 2);
-    ok((int)hipGetLastError());
+    // Am = strict_lower((k b) k^T * decay)
+    Epi dec;
+    dec.dgc = a.gam; dec.g0 = (long)G * BC; dec.g1 = BC;
+    ok(gemm(BC, BC, D, nzg, G, 1, W(a.kb, BC, D), tr(kT()), a.Am, (long)G * cc, cc, 0, BC, 1, 1.f, 0, 2, nullptr, s,
+            KSplit{}, dec));
     hipLaunchKernelGGL(unit_lower_inverse_kernel, dim3((unsigned)NC), dim3(64), 0, s, a.Am, a.Mi);
     ok((int)hipGetLastError());
     // u = M (v b), w = M (k b e^gc)
@@ -816,11 +805,9 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
     ok(gemm(BC, D, BC, nzg, G, 1, W(a.Mi, BC, BC), W(a.kbe, BC, D), a.w, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0, nullptr, s));
     ok(gemm(BC, D, BC, nzg, G, 1, W(a.Mi, BC, BC), W(a.kbe, BC, D), a.wT, (long)G * cd, cd, 0, 1, BC, 1.f, 0, 0, nullptr,
             s));                                          // the same product stored transposed [D][C]
-    // QK_r = s q_r k^T (lower incl.), attn_r = tril(QK_r * decay)
-    ok(gemm(BC, BC, D, nzr, G, R, qR(), tr(Op{a.k, (long)BC * G * D, D, 0, (long)G * D, 1}), a.QK, (long)G * R * cc,
-            (long)R * cc, cc, BC, 1, a.scale, 0, 1, nullptr, s));
-    hipLaunchKernelGGL(decay_mask_kernel, dim3((unsigned)NC), dim3(BW_NT), 0, s, a.QK, a.attn, a.gam, R, 1);
-    ok((int)hipGetLastError());
+    // attn_r = tril(s q_r k^T * decay)
+    ok(gemm(BC, BC, D, nzr, G, R, qR(), tr(Op{a.k, (long)BC * G * D, D, 0, (long)G * D, 1}), a.attn, (long)G * R * cc,
+            (long)R * cc, cc, BC, 1, a.scale, 0, 1, nullptr, s, KSplit{}, dec));
     // E1 = sum_r attn_r^T dO_r [C x D], E2 = sum_r qd_r^T dO_r = s sum_r q_r^T diag(e^gc) dO_r [D x D]: one product
     // each over K = R C, the (r, token) pairs, read from the token-major q and dO (k = 64 r + i: token stride H D,
     // head stride D)
@@ -843,8 +830,12 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
     ok(gemm(BC, D, D, nzg, G, 1, W(a.w, BC, D), W(a.Sc, D, D), a.vn, (long)G * cd, cd, 0, D, 1, -1.f, 0, 0, a.u, s));
     // dattn_r = tril(dO_r v_new^T); dqd_r = dO_r S^T goes straight into dq_r = s e^gc dqd_r (token-major; the attn
     // share is added below), with each row's dot with q_r (the query path's d gc share) as partials in qdot
+    // (the decayed dattn_r; the decay's d gc share from dQK_r . QK_r = dattn_r(undecayed) . attn_r as row and column
+    // sums)
+    Epi da = dec;
+    da.rdx = a.attn; da.rdo = a.zr; da.cdo = a.zc;
     ok(gemm(BC, BC, D, nzr, G, R, dOR(), tr(Op{a.vn, (long)G * cd, cd, 0, D, 1}), a.dattn, (long)G * R * cc,
-            (long)R * cc, cc, BC, 1, 1.f, 0, 1, nullptr, s));
+            (long)R * cc, cc, BC, 1, 1.f, 0, 1, nullptr, s, KSplit{}, da));
     Epi eq;
     eq.msc = a.eg; eq.s0 = (long)G * BC; eq.s1 = BC; eq.rdx = a.q; eq.rdo = a.qdot;
     ok(gemm(BC, D, D, nzr, G, R, dOR(), tr(Op{a.Sc, (long)G * dd, dd, 0, D, 1}), a.dq, (long)BC * H * D, (long)R * D, D,
@@ -866,11 +857,11 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
             nullptr, s));
     ok(gemm(BC, BC, BC, nzg, G, 1, tr(W(a.Mi, BC, BC)), W(dM, BC, BC), T1, (long)G * cc, cc, 0, BC, 1, 1.f, 0, 0,
             nullptr, s));
+    // (written decayed, the decay's d gc share from dP . P = dA(undecayed) . Am as row and column sums)
+    Epi dd_ = dec;
+    dd_.rdx = a.Am; dd_.rdo = a.zrA; dd_.cdo = a.zcA;
     ok(gemm(BC, BC, BC, nzg, G, 1, W(T1, BC, BC), tr(W(a.Mi, BC, BC)), a.dA, (long)G * cc, cc, 0, BC, 1, -1.f, 0, 2,
-            nullptr, s));
-    // decay: dA *= decay, dattn_r *= decay, d gc share
-    hipLaunchKernelGGL(decay_grad_kernel, dim3((unsigned)NC), dim3(BW_NT), 0, s, a);
-    ok((int)hipGetLastError());
+            nullptr, s, KSplit{}, dd_));
     // d(k b) from A: dAd k ; dk from A: dAd^T (k b) ; from attn: sum_r dattn_r^T (s q_r) ; dq_r = s dattn_r k
     ok(gemm(BC, D, BC, nzg, G, 1, W(a.dA, BC, BC), kT(), a.dkb, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0, nullptr, s));
     ok(gemm(BC, D, BC, nzg, G, 1, tr(W(a.dA, BC, BC)), W(a.kb, BC, D), a.dkacc, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0,

@@ -363,101 +363,138 @@ __global__ __launch_bounds__(64) void unit_lower_inverse_kernel(const float* Am,
 // one 16-byte read. WALK_NW<D> waves: 8 at D >= 128 (two per SIMD, so one wave's loads and LDS exchange overlap the
 // other's MFMAs), 4 at D = 64. Wave w owns row tiles [w RT, (w + 1) RT) of the strip; for the 64-token product the
 // waves split into KH = NW / 4 parts of the D-long reduction, each part's partial sums go to LDS and the reader adds
-// them. The next chunk's operands are fetched into registers at the end of the current chunk, and the barriers order
-// LDS only (lds_barrier), so the fetch stays in flight across them. (At 4 waves per workgroup the walks took 845 us per
-// launch at T = 8192, G = 4, D = 256, at 8 waves 819 us; a second register set fetched a whole chunk ahead measured
-// slower at either count: 964 and 904-917 us.)
+// them. The next chunk's operands go into a second register set, their loads (and the chunk's own stores) issued one
+// per MFMA step; the barriers order LDS only (lds_barrier), so the loads stay in flight across them.
 template <int D>
 constexpr int walk_nw() { return D >= 128 ? 8 : 4; }
+// 16-column strips per workgroup. Every workgroup streams all of w and kt each chunk whatever its width; two strips
+// per workgroup halve that traffic but measured slower (978 against 756 us per launch at T = 8192, G = 4, D = 256).
+template <int D>
+constexpr int walk_sw() { return 1; }
 
 template <int D>
 __device__ __forceinline__ void walk_fwd(const GdnBwdArgs& a, int strip) {
     constexpr int NW = walk_nw<D>(), NTD = D / 16, RT = NTD / NW;   // row tiles per wave
     constexpr int KH = NW / 4;                                       // parts of the D-long reduction of v_new
     constexpr int KD = D / 16 / KH, KC = BC / 16;                    // 16-wide k steps per part / over the chunk
-    const int b = blockIdx.x, g = blockIdx.y, col0 = strip * 16;
+    constexpr int SW = walk_sw<D>(), NE = SW * RT * 4;              // strips; state elements per lane
+    const int b = blockIdx.x, g = blockIdx.y, col0 = strip * 16 * SW;
     const int lane = lane_id(), wv = wave_id(), i16 = lane & 15, q = lane >> 4;
     const int tq = wv & 3, kh = wv >> 2;                             // v_new token tile and reduction part
     const int G = a.G, n = a.n_chunks;
-    __shared__ float ST[16][D + 4];                       // strip transposed: ST[col][row]
-    __shared__ float VT[KH][16][BC + 4];                  // v_new partial sums transposed: VT[part][col][token]
-    f32x4 S[RT];
+    __shared__ float ST[16 * SW][D + 4];                  // strips transposed: ST[col][row]
+    __shared__ float VT[KH][16 * SW][BC + 4];             // v_new partial sums transposed: VT[part][col][token]
+    // element e of a lane: strip e / (4 RT), row tile (e / 4) % RT, accumulator row e % 4
+    auto erow = [&](int e) { return (wv * RT + (e / 4) % RT) * 16 + 4 * q + e % 4; };
+    auto ecol = [&](int e) { return col0 + 16 * (e / (4 * RT)) + i16; };
+    f32x4 S[SW][RT];
 #pragma unroll
-    for (int t = 0; t < RT; ++t) S[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (a.s0) {
-#pragma unroll
-        for (int t = 0; t < RT; ++t)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int row = (wv * RT + t) * 16 + 4 * q + v;
-                S[t][v] = a.s0[(((long)b * G + g) * D + row) * D + col0 + i16];
-            }
-    }
-    // one chunk's operands, loaded a chunk ahead: w row fragments of this wave's reduction part, kt^T fragments of its
-    // row tiles, the u strip (part 0), the chunk decay
-    float4 wf[KD], kf[RT][KC];
-    float uf[4], gl;
-    auto fetch = [&](int c) {
-        const long cg = ((long)b * n + c) * G + g;
-        const float* wr = a.w + (cg * BC + 16 * tq + i16) * D + kh * (D / KH) + 4 * q;
-#pragma unroll
-        for (int k = 0; k < KD; ++k) wf[k] = *reinterpret_cast<const float4*>(wr + 16 * k);
-#pragma unroll
-        for (int t = 0; t < RT; ++t) {
-            const float* kr = a.ktlT + (cg * D + (wv * RT + t) * 16 + i16) * BC + 4 * q;
-#pragma unroll
-            for (int k = 0; k < KC; ++k) kf[t][k] = *reinterpret_cast<const float4*>(kr + 16 * k);
-        }
-#pragma unroll
-        for (int v = 0; v < 4; ++v) uf[v] = kh == 0 ? a.u[(cg * BC + 16 * tq + 4 * q + v) * D + col0 + i16] : 0.f;
-        gl = a.gam[cg * BC + BC - 1];
+    for (int e = 0; e < NE; ++e) S[e / (4 * RT)][(e / 4) % RT][e % 4] = a.s0 ? a.s0[(((long)b * G + g) * D + erow(e)) * D + ecol(e)] : 0.f;
+    // One chunk's operands: w row fragments of this wave's reduction part, kt^T fragments of its row tiles, the u strip
+    // (part 0), the chunk decay. Each workgroup streams all of w and kt (128 KB at D = 256) per chunk, more than the
+    // CU's vector memory path takes in the chunk's MFMA time, so a wave issuing them back to back stalls on the full
+    // queue (3.6-6.4 K cycles a chunk, measured) with its MFMAs behind it. Two register sets: chunk c + 1's loads
+    // (and chunk c's state stores) are issued one per MFMA step of chunk c, after chunk c's operands have been waited
+    // for, so they queue while the MFMAs run and have the rest of the chunk to land.
+    struct Ops {
+        float4 wf[KD], kf[RT][KC];
+        float uf[SW][4], gl;
     };
-    fetch(0);
-    for (int c = 0; c < n; ++c) {
-        const long cg = ((long)b * n + c) * G + g;
+    auto ld_w = [&](Ops& o, long cg, int k) {
+        o.wf[k] = *reinterpret_cast<const float4*>(a.w + (cg * BC + 16 * tq + i16) * D + kh * (D / KH) + 4 * q + 16 * k);
+    };
+    auto ld_k = [&](Ops& o, long cg, int t, int k) {
+        o.kf[t][k] = *reinterpret_cast<const float4*>(a.ktlT + (cg * D + (wv * RT + t) * 16 + i16) * BC + 4 * q + 16 * k);
+    };
+    auto ld_rest = [&](Ops& o, long cg) {
+#pragma unroll
+        for (int c2 = 0; c2 < SW; ++c2)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                o.uf[c2][v] = kh == 0 ? a.u[(cg * BC + 16 * tq + 4 * q + v) * D + col0 + 16 * c2 + i16] : 0.f;
+        o.gl = a.gam[cg * BC + BC - 1];
+    };
+    Ops o0, o1;
+    {
+        const long cg = (long)b * n * G + g;
+#pragma unroll
+        for (int k = 0; k < KD; ++k) ld_w(o0, cg, k);
 #pragma unroll
         for (int t = 0; t < RT; ++t)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int row = (wv * RT + t) * 16 + 4 * q + v;
-                a.Sc[(cg * D + row) * D + col0 + i16] = S[t][v];     // entry state of chunk c
-                ST[i16][row] = S[t][v];
-            }
+            for (int k = 0; k < KC; ++k) ld_k(o0, cg, t, k);
+        ld_rest(o0, cg);
+    }
+    auto chunk = [&](int c, const Ops& cur, Ops& nxt) {
+        const long cg = ((long)b * n + c) * G + g;
+        const long cn = ((long)b * n + (c + 1 < n ? c + 1 : c)) * G + g;   // the next chunk (the last one refetches)
+#pragma unroll
+        for (int e = 0; e < NE; ++e) ST[16 * (e / (4 * RT)) + i16][erow(e)] = S[e / (4 * RT)][(e / 4) % RT][e % 4];
         lds_barrier();
+        wait_vmem_all();                                   // this chunk's operands (and the last chunk's stores)
         // v_new rows [16 tq, 16 tq + 16) = u - w S, this wave's part of the reduction (four partial accumulators:
-        // shorter MFMA dependency chains)
-        f32x4 part[4] = {f32x4{uf[0], uf[1], uf[2], uf[3]}, f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f},
-                         f32x4{0.f, 0.f, 0.f, 0.f}};
+        // shorter MFMA dependency chains); the next chunk's w and this chunk's entry-state stores ride along
+        f32x4 part[SW][4];
+#pragma unroll
+        for (int c2 = 0; c2 < SW; ++c2) {
+            part[c2][0] = f32x4{cur.uf[c2][0], cur.uf[c2][1], cur.uf[c2][2], cur.uf[c2][3]};
+#pragma unroll
+            for (int p = 1; p < 4; ++p) part[c2][p] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
 #pragma unroll
         for (int k = 0; k < KD; ++k) {
-            const uint4 af = make_uint4(__float_as_uint(-wf[k].x), __float_as_uint(-wf[k].y), __float_as_uint(-wf[k].z),
-                                        __float_as_uint(-wf[k].w));
-            const uint4 bf = *reinterpret_cast<const uint4*>(&ST[i16][kh * (D / KH) + 16 * k + 4 * q]);
-            mma<F32>(part[k & 3], af, bf);
-        }
-        const f32x4 acc = (part[0] + part[1]) + (part[2] + part[3]);
+            const uint4 af = make_uint4(__float_as_uint(-cur.wf[k].x), __float_as_uint(-cur.wf[k].y),
+                                        __float_as_uint(-cur.wf[k].z), __float_as_uint(-cur.wf[k].w));
 #pragma unroll
-        for (int v = 0; v < 4; ++v) VT[kh][i16][16 * tq + 4 * q + v] = acc[v];
+            for (int c2 = 0; c2 < SW; ++c2) {
+                const uint4 bf = *reinterpret_cast<const uint4*>(&ST[16 * c2 + i16][kh * (D / KH) + 16 * k + 4 * q]);
+                mma<F32>(part[c2][k & 3], af, bf);
+            }
+            ld_w(nxt, cn, k);
+#pragma unroll
+            for (int e = k * NE / KD; e < (k + 1) * NE / KD; ++e)              // entry state of chunk c
+                a.Sc[(cg * D + erow(e)) * D + ecol(e)] = S[e / (4 * RT)][(e / 4) % RT][e % 4];
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int c2 = 0; c2 < SW; ++c2) {
+            const f32x4 acc = (part[c2][0] + part[c2][1]) + (part[c2][2] + part[c2][3]);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) VT[kh][16 * c2 + i16][16 * tq + 4 * q + v] = acc[v];
+        }
         lds_barrier();
-        // S = e^(gc_C') S + kt^T v_new (v_new = the sum of the parts)
-        const float ec = expf(gl);
+        // S = e^(gc_C') S + kt^T v_new (v_new = the sum of the parts); the next chunk's kt^T rides along
+        const float ec = expf(cur.gl);
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) S[t][v] *= ec;
+            for (int c2 = 0; c2 < SW; ++c2)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) S[c2][t][v] *= ec;
 #pragma unroll
             for (int k = 0; k < KC; ++k) {
-                float4 vs = *reinterpret_cast<const float4*>(&VT[0][i16][16 * k + 4 * q]);
 #pragma unroll
-                for (int p = 1; p < KH; ++p) {
-                    const float4 x = *reinterpret_cast<const float4*>(&VT[p][i16][16 * k + 4 * q]);
-                    vs.x += x.x; vs.y += x.y; vs.z += x.z; vs.w += x.w;
+                for (int c2 = 0; c2 < SW; ++c2) {
+                    float4 vs = *reinterpret_cast<const float4*>(&VT[0][16 * c2 + i16][16 * k + 4 * q]);
+#pragma unroll
+                    for (int p = 1; p < KH; ++p) {
+                        const float4 x = *reinterpret_cast<const float4*>(&VT[p][16 * c2 + i16][16 * k + 4 * q]);
+                        vs.x += x.x; vs.y += x.y; vs.z += x.z; vs.w += x.w;
+                    }
+                    mma<F32>(S[c2][t], __builtin_bit_cast(uint4, cur.kf[t][k]), __builtin_bit_cast(uint4, vs));
                 }
-                mma<F32>(S[t], __builtin_bit_cast(uint4, kf[t][k]), __builtin_bit_cast(uint4, vs));
+                ld_k(nxt, cn, t, k);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-        fetch(c + 1 < n ? c + 1 : c);   // unconditional: a conditional load is drained where the branches join
+        ld_rest(nxt, cn);
         lds_barrier();
+    };
+    for (int c = 0;;) {
+        chunk(c, o0, o1);
+        if (++c >= n) break;
+        chunk(c, o1, o0);
+        if (++c >= n) break;
     }
 }
 
@@ -467,116 +504,146 @@ __device__ __forceinline__ void walk_bwd(const GdnBwdArgs& a, int strip) {
     constexpr int NW = walk_nw<D>(), NTD = D / 16, RT = NTD / NW;
     constexpr int KH = NW / 4;
     constexpr int KD = D / 16 / KH, KC = BC / 16;
-    const int b = blockIdx.x, g = blockIdx.y, col0 = strip * 16;
+    constexpr int SW = walk_sw<D>(), NE = SW * RT * 4;
+    const int b = blockIdx.x, g = blockIdx.y, col0 = strip * 16 * SW;
     const int lane = lane_id(), wv = wave_id(), i16 = lane & 15, q = lane >> 4;
     const int tq = wv & 3, kh = wv >> 2;
     const int G = a.G, n = a.n_chunks;
-    __shared__ float LT[16][D + 4];
-    __shared__ float VT[KH][16][BC + 4];
-    f32x4 L[RT];
+    __shared__ float LT[16 * SW][D + 4];
+    __shared__ float VT[KH][16 * SW][BC + 4];
+    auto erow = [&](int e) { return (wv * RT + (e / 4) % RT) * 16 + 4 * q + e % 4; };
+    auto ecol = [&](int e) { return col0 + 16 * (e / (4 * RT)) + i16; };
+    f32x4 L[SW][RT];
 #pragma unroll
-    for (int t = 0; t < RT; ++t) L[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (a.dsf) {
+    for (int e = 0; e < NE; ++e) L[e / (4 * RT)][(e / 4) % RT][e % 4] = a.dsf ? a.dsf[(((long)b * G + g) * D + erow(e)) * D + ecol(e)] : 0.f;
+    // one chunk's operands: kt row fragments of this wave's reduction part, w^T fragments of its row tiles, the E1
+    // strip (part 0) and E2 rows, the chunk decay; two register sets, the next chunk's loads and this chunk's stores
+    // issued one per MFMA step as in the forward walk
+    struct Ops {
+        float4 kf[KD], wf[RT][KC];
+        float e1[SW][4], e2[SW][RT][4], gl;
+    };
+    auto ld_k = [&](Ops& o, long cg, int k) {
+        o.kf[k] = *reinterpret_cast<const float4*>(a.ktl + (cg * BC + 16 * tq + i16) * D + kh * (D / KH) + 4 * q + 16 * k);
+    };
+    auto ld_w = [&](Ops& o, long cg, int t, int k) {
+        o.wf[t][k] = *reinterpret_cast<const float4*>(a.wT + (cg * D + (wv * RT + t) * 16 + i16) * BC + 4 * q + 16 * k);
+    };
+    auto ld_rest = [&](Ops& o, long cg) {
 #pragma unroll
-        for (int t = 0; t < RT; ++t)
+        for (int e = 0; e < NE; ++e) o.e2[e / (4 * RT)][(e / 4) % RT][e % 4] = a.E2[(cg * D + erow(e)) * D + ecol(e)];
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int row = (wv * RT + t) * 16 + 4 * q + v;
-                L[t][v] = a.dsf[(((long)b * G + g) * D + row) * D + col0 + i16];
-            }
-    }
-    // one chunk's operands, a chunk ahead: kt row fragments of this wave's reduction part, w^T fragments of its row
-    // tiles, the E1 strip (part 0) and E2 rows, the chunk decay
-    float4 kf[KD], wf[RT][KC];
-    float e1[4], e2[RT][4], gl;
-    auto fetch = [&](int c) {
-        const long cg = ((long)b * n + c) * G + g;
-        const float* kr = a.ktl + (cg * BC + 16 * tq + i16) * D + kh * (D / KH) + 4 * q;
-#pragma unroll
-        for (int k = 0; k < KD; ++k) kf[k] = *reinterpret_cast<const float4*>(kr + 16 * k);
-#pragma unroll
-        for (int t = 0; t < RT; ++t) {
-            const float* wr = a.wT + (cg * D + (wv * RT + t) * 16 + i16) * BC + 4 * q;
-#pragma unroll
-            for (int k = 0; k < KC; ++k) wf[t][k] = *reinterpret_cast<const float4*>(wr + 16 * k);
+        for (int c2 = 0; c2 < SW; ++c2)
 #pragma unroll
             for (int v = 0; v < 4; ++v)
-                e2[t][v] = a.E2[(cg * D + (wv * RT + t) * 16 + 4 * q + v) * D + col0 + i16];
-        }
-#pragma unroll
-        for (int v = 0; v < 4; ++v) e1[v] = kh == 0 ? a.E1[(cg * BC + 16 * tq + 4 * q + v) * D + col0 + i16] : 0.f;
-        gl = a.gam[cg * BC + BC - 1];
+                o.e1[c2][v] = kh == 0 ? a.E1[(cg * BC + 16 * tq + 4 * q + v) * D + col0 + 16 * c2 + i16] : 0.f;
+        o.gl = a.gam[cg * BC + BC - 1];
     };
-    fetch(n - 1);
-    for (int c = n - 1; c >= 0; --c) {
-        const long cg = ((long)b * n + c) * G + g;
+    Ops o0, o1;
+    {
+        const long cg = ((long)b * n + n - 1) * G + g;
+#pragma unroll
+        for (int k = 0; k < KD; ++k) ld_k(o0, cg, k);
 #pragma unroll
         for (int t = 0; t < RT; ++t)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int row = (wv * RT + t) * 16 + 4 * q + v;
-                a.dSx[(cg * D + row) * D + col0 + i16] = L[t][v];    // exit-state gradient of chunk c
-                LT[i16][row] = L[t][v];
-            }
+            for (int k = 0; k < KC; ++k) ld_w(o0, cg, t, k);
+        ld_rest(o0, cg);
+    }
+    auto chunk = [&](int c, const Ops& cur, Ops& nxt) {
+        const long cg = ((long)b * n + c) * G + g;
+        const long cn = ((long)b * n + (c > 0 ? c - 1 : c)) * G + g;       // the next chunk down (0 refetches)
+#pragma unroll
+        for (int e = 0; e < NE; ++e) LT[16 * (e / (4 * RT)) + i16][erow(e)] = L[e / (4 * RT)][(e / 4) % RT][e % 4];
         lds_barrier();
-        // dvn rows [16 tq, 16 tq + 16) = E1 + kt dS', this wave's part of the reduction
-        f32x4 part[4] = {f32x4{e1[0], e1[1], e1[2], e1[3]}, f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f},
-                         f32x4{0.f, 0.f, 0.f, 0.f}};
+        wait_vmem_all();                                   // this chunk's operands (and the last chunk's stores)
+        // dvn rows [16 tq, 16 tq + 16) = E1 + kt dS', this wave's part of the reduction; the next chunk's kt rows and
+        // this chunk's exit-state gradient stores ride along
+        f32x4 part[SW][4];
+#pragma unroll
+        for (int c2 = 0; c2 < SW; ++c2) {
+            part[c2][0] = f32x4{cur.e1[c2][0], cur.e1[c2][1], cur.e1[c2][2], cur.e1[c2][3]};
+#pragma unroll
+            for (int p = 1; p < 4; ++p) part[c2][p] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
 #pragma unroll
         for (int k = 0; k < KD; ++k) {
-            const uint4 bf = *reinterpret_cast<const uint4*>(&LT[i16][kh * (D / KH) + 16 * k + 4 * q]);
-            mma<F32>(part[k & 3], __builtin_bit_cast(uint4, kf[k]), bf);
-        }
-        const f32x4 acc = (part[0] + part[1]) + (part[2] + part[3]);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) VT[kh][i16][16 * tq + 4 * q + v] = acc[v];
+            for (int c2 = 0; c2 < SW; ++c2) {
+                const uint4 bf = *reinterpret_cast<const uint4*>(&LT[16 * c2 + i16][kh * (D / KH) + 16 * k + 4 * q]);
+                mma<F32>(part[c2][k & 3], __builtin_bit_cast(uint4, cur.kf[k]), bf);
+            }
+            ld_k(nxt, cn, k);
+#pragma unroll
+            for (int e = k * NE / KD; e < (k + 1) * NE / KD; ++e)              // exit-state gradient of chunk c
+                a.dSx[(cg * D + erow(e)) * D + ecol(e)] = L[e / (4 * RT)][(e / 4) % RT][e % 4];
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int c2 = 0; c2 < SW; ++c2) {
+            const f32x4 acc = (part[c2][0] + part[c2][1]) + (part[c2][2] + part[c2][3]);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) VT[kh][16 * c2 + i16][16 * tq + 4 * q + v] = acc[v];
+        }
         lds_barrier();
-        // dvn (the sum of the parts) out; dS = e^(gc_C') dS' + E2 - w^T dvn
+        // dvn (the sum of the parts) out; dS = e^(gc_C') dS' + E2 - w^T dvn; the next chunk's w^T rides along
         if (kh == 0) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                float x = VT[0][i16][16 * tq + 4 * q + v];
+            for (int c2 = 0; c2 < SW; ++c2)
 #pragma unroll
-                for (int p = 1; p < KH; ++p) x += VT[p][i16][16 * tq + 4 * q + v];
-                a.dvn[(cg * BC + 16 * tq + 4 * q + v) * D + col0 + i16] = x;
-            }
+                for (int v = 0; v < 4; ++v) {
+                    float x = VT[0][16 * c2 + i16][16 * tq + 4 * q + v];
+#pragma unroll
+                    for (int p = 1; p < KH; ++p) x += VT[p][16 * c2 + i16][16 * tq + 4 * q + v];
+                    a.dvn[(cg * BC + 16 * tq + 4 * q + v) * D + col0 + 16 * c2 + i16] = x;
+                }
         }
-        const float ec = expf(gl);
+        const float ec = expf(cur.gl);
 #pragma unroll
         for (int t = 0; t < RT; ++t) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) L[t][v] = ec * L[t][v] + e2[t][v];
+            for (int c2 = 0; c2 < SW; ++c2)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) L[c2][t][v] = ec * L[c2][t][v] + cur.e2[c2][t][v];
 #pragma unroll
             for (int k = 0; k < KC; ++k) {
-                const uint4 af = make_uint4(__float_as_uint(-wf[t][k].x), __float_as_uint(-wf[t][k].y),
-                                            __float_as_uint(-wf[t][k].z), __float_as_uint(-wf[t][k].w));
-                float4 vs = *reinterpret_cast<const float4*>(&VT[0][i16][16 * k + 4 * q]);
+                const uint4 af = make_uint4(__float_as_uint(-cur.wf[t][k].x), __float_as_uint(-cur.wf[t][k].y),
+                                            __float_as_uint(-cur.wf[t][k].z), __float_as_uint(-cur.wf[t][k].w));
 #pragma unroll
-                for (int p = 1; p < KH; ++p) {
-                    const float4 x = *reinterpret_cast<const float4*>(&VT[p][i16][16 * k + 4 * q]);
-                    vs.x += x.x; vs.y += x.y; vs.z += x.z; vs.w += x.w;
+                for (int c2 = 0; c2 < SW; ++c2) {
+                    float4 vs = *reinterpret_cast<const float4*>(&VT[0][16 * c2 + i16][16 * k + 4 * q]);
+#pragma unroll
+                    for (int p = 1; p < KH; ++p) {
+                        const float4 x = *reinterpret_cast<const float4*>(&VT[p][16 * c2 + i16][16 * k + 4 * q]);
+                        vs.x += x.x; vs.y += x.y; vs.z += x.z; vs.w += x.w;
+                    }
+                    mma<F32>(L[c2][t], af, __builtin_bit_cast(uint4, vs));
                 }
-                mma<F32>(L[t], af, __builtin_bit_cast(uint4, vs));
+                ld_w(nxt, cn, t, k);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-        fetch(c > 0 ? c - 1 : c);       // unconditional, as in the forward walk
+        ld_rest(nxt, cn);
         lds_barrier();
+    };
+    for (int c = n - 1;;) {
+        chunk(c, o0, o1);
+        if (--c < 0) break;
+        chunk(c, o1, o0);
+        if (--c < 0) break;
     }
     if (a.ds0)
 #pragma unroll
-        for (int t = 0; t < RT; ++t)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int row = (wv * RT + t) * 16 + 4 * q + v;
-                a.ds0[(((long)b * G + g) * D + row) * D + col0 + i16] = L[t][v];
-            }
+        for (int e = 0; e < NE; ++e)
+            a.ds0[(((long)b * G + g) * D + erow(e)) * D + ecol(e)] = L[e / (4 * RT)][(e / 4) % RT][e % 4];
 }
 
 // the two walks are independent (the reverse one needs E1, E2, kt, w, not the entry states): one launch
 template <int D>
 __global__ __launch_bounds__(64 * walk_nw<D>()) void walk_kernel(GdnBwdArgs a) {
-    if ((int)blockIdx.z < D / 16) walk_fwd<D>(a, blockIdx.z);
-    else walk_bwd<D>(a, blockIdx.z - D / 16);
+    constexpr int NS = D / 16 / walk_sw<D>();              // strips each way
+    if ((int)blockIdx.z < NS) walk_fwd<D>(a, blockIdx.z);
+    else walk_bwd<D>(a, blockIdx.z - NS);
 }
 
 
@@ -821,7 +888,7 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
     rq.shift = 6; rq.a = D; rq.b = D; rq.ksc = a.eg; rq.s0 = (long)G * BC; rq.s1 = BC;   // A = q^T, columns e^gc
     ok(gemm(D, D, R * BC, nzg, G, 1, tr(qk), dOk, a.E2, (long)G * dd, dd, 0, D, 1, a.scale, 0, 0, nullptr, s, rq));
     // walks
-    const dim3 wgrid(a.num_seqs, G, 2 * D / 16);
+    const dim3 wgrid(a.num_seqs, G, 2 * D / 16);          // walk_sw<D>() == 1
     if (D == 64) hipLaunchKernelGGL(walk_kernel<64>, wgrid, dim3(64 * walk_nw<64>()), 0, s, a);
     else if (D == 128) hipLaunchKernelGGL(walk_kernel<128>, wgrid, dim3(64 * walk_nw<128>()), 0, s, a);
     else hipLaunchKernelGGL(walk_kernel<256>, wgrid, dim3(64 * walk_nw<256>()), 0, s, a);

@@ -194,7 +194,7 @@ struct GdnBwdArgs {
     // outputs (same layouts); ds0 may be null
     float *dq, *dk, *dv, *dg, *dbeta, *ds0;
     // workspace, chunk-major [chunk][g][...] (cg = chunk * G + g)
-    float *gam, *eg, *dgz, *Am, *Mi, *dA, *kb, *vb, *kbe, *ktl, *ktlT, *u, *w, *wT, *attn, *dattn, *qdot, *zr, *zc, *zrA, *zcA;
+    float *gam, *eg, *dgz, *Am, *Mi, *dA, *kb, *vb, *kbe, *ktl, *ktlF, *ktlTF, *u, *w, *wF, *wTF, *attn, *dattn, *qdot, *zr, *zc, *zrA, *zcA;
     float *Sc, *E2, *dSx, *part;
     float *E1, *dvn, *vn, *dkt, *dw, *dvb, *dkbe, *dkb, *dkacc;
 };

@@ -26,6 +26,13 @@ namespace {
 constexpr int BC = 64;                  // chunk length
 constexpr int BW_NT = 256;
 
+// Fragment order of an R x C fp32 matrix (C a multiple of 16): its 16 x 16 tiles one after another, row-major over
+// tiles, each as 64 lanes x 4 floats with lane 16 q + i holding row i, columns 4 q .. 4 q + 3 of the tile, so a wave
+// reads a tile (the operand fragment of v_mfma_f32_16x16x4f32 over 4 k steps) as one contiguous 1 KB.
+__device__ __forceinline__ long frag16(int r, int c, int C) {
+    return ((long)((r >> 4) * (C >> 4) + (c >> 4)) * 64 + ((c & 15) >> 2) * 16 + (r & 15)) * 4 + (c & 3);
+}
+
 // ------------------------------------------------------------------------------------ batched strided fp32 GEMM
 // C[z] (M x N) = add[z] + alpha * A[z] diag(ksc) (M x K) B[z] (K x N)   (or C += ... when acc), z = (z0, z1, z2);
 // element (m, k) of A at A + z0 sa0 + z1 sa1 + z2 sa2 + m am + (k >> kshift) sak + (k & (2^kshift - 1)) ak (B, C,
@@ -37,7 +44,7 @@ constexpr int BW_NT = 256;
 // z1 dg1 (the in-chunk decay). mask 1 keeps m >= n, mask 2 keeps m > n (the rest is written 0, or left unchanged when
 // accumulating). C contiguous along n only: with rdo, the row dots of P with rdx (addressed like C) go to
 // rdo[(z N/64 + n/64) M + m], one partial per 64 columns, and with cdo the column dots to cdo[(z M/64 + m/64) N + n]
-// (z = blockIdx.x).
+// (z = blockIdx.x). With cfrag, C is written in fragment order (frag16) at its batch offset.
 struct BgArgs {
     int M, N, K, n1, n2, nz, kshift;
     const float* A; long sa0, sa1, sa2, am, ak, sak;
@@ -49,7 +56,7 @@ struct BgArgs {
     const float* dgc; long dg0, dg1;
     const float* rdx; float* rdo; float* cdo;
     float alpha;
-    int acc, mask;
+    int acc, mask, cfrag;               // cfrag: C (per z at its batch offset) in fragment order, cm / cn unused
 };
 
 // Tiles of 64 x BN (BN = 64 or 128; 4 waves of 32 x BN/2) over K steps of 32. Each step's 64 x 32 tile of A and
@@ -199,7 +206,8 @@ __global__ __launch_bounds__(BW_NT) void bgemm_kernel(BgArgs a) {
         const int c4 = tid % RW;
         const int n = tn + 4 * c4;
         auto row = [&](int j) { return tid / RW + (BW_NT / RW) * j; };
-        auto at = [&](int j) { return coff + (long)(tm + row(j)) * a.cm + n; };
+        const bool cf = EX >= 1 && a.cfrag;
+        auto at = [&](int j) { return cf ? coff + frag16(tm + row(j), n, a.N) : coff + (long)(tm + row(j)) * a.cm + n; };
         const bool dots = (EX >= 1 && a.rdo) || (EX == 2 && a.cdo);
         const float* gc = EX == 2 && a.dgc ? a.dgc + z0 * a.dg0 + z1 * a.dg1 : nullptr;
         float4 prev[NP], rx[NP], gn = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -331,11 +339,13 @@ __global__ __launch_bounds__(BW_NT) void chunk_prep_kernel(GdnBwdArgs a) {
         a.kb[o] = kx * be;
         a.vb[o] = vx * be;
         a.kbe[o] = kx * be * eg[i];
-        a.ktl[o] = kx * expf(gl - gc[i]);
+        const float kt = kx * expf(gl - gc[i]);
+        a.ktl[o] = kt;
+        a.ktlF[cg * BC * D + frag16(i, d, D)] = kt;                 // fragment order, for the reverse walk
     }
-    for (int e = tid; e < 16 * D; e += BW_NT) {              // kt transposed [D][C], token index fastest
+    for (int e = tid; e < 16 * D; e += BW_NT) {              // kt transposed [D][C] in fragment order, forward walk
         const int d = e / 16, i = r0 + e % 16;
-        a.ktlT[(cg * D + d) * BC + i] = a.k[((bc * BC + i) * G + g) * D + d] * expf(gl - gc[i]);
+        a.ktlTF[cg * D * BC + frag16(d, i, BC)] = a.k[((bc * BC + i) * G + g) * D + d] * expf(gl - gc[i]);
     }
 }
 
@@ -400,11 +410,12 @@ __device__ __forceinline__ void walk_fwd(const GdnBwdArgs& a, int strip) {
         float4 wf[KD], kf[RT][KC];
         float uf[SW][4], gl;
     };
+    // (w and kt^T in fragment order: each load is one contiguous 1 KB tile)
     auto ld_w = [&](Ops& o, long cg, int k) {
-        o.wf[k] = *reinterpret_cast<const float4*>(a.w + (cg * BC + 16 * tq + i16) * D + kh * (D / KH) + 4 * q + 16 * k);
+        o.wf[k] = *reinterpret_cast<const float4*>(a.wF + cg * BC * D + (long)(tq * (D / 16) + kh * (D / KH / 16) + k) * 256 + 4 * lane);
     };
     auto ld_k = [&](Ops& o, long cg, int t, int k) {
-        o.kf[t][k] = *reinterpret_cast<const float4*>(a.ktlT + (cg * D + (wv * RT + t) * 16 + i16) * BC + 4 * q + 16 * k);
+        o.kf[t][k] = *reinterpret_cast<const float4*>(a.ktlTF + cg * D * BC + (long)((wv * RT + t) * (BC / 16) + k) * 256 + 4 * lane);
     };
     auto ld_rest = [&](Ops& o, long cg) {
 #pragma unroll
@@ -524,10 +535,10 @@ __device__ __forceinline__ void walk_bwd(const GdnBwdArgs& a, int strip) {
         float e1[SW][4], e2[SW][RT][4], gl;
     };
     auto ld_k = [&](Ops& o, long cg, int k) {
-        o.kf[k] = *reinterpret_cast<const float4*>(a.ktl + (cg * BC + 16 * tq + i16) * D + kh * (D / KH) + 4 * q + 16 * k);
+        o.kf[k] = *reinterpret_cast<const float4*>(a.ktlF + cg * BC * D + (long)(tq * (D / 16) + kh * (D / KH / 16) + k) * 256 + 4 * lane);
     };
     auto ld_w = [&](Ops& o, long cg, int t, int k) {
-        o.wf[t][k] = *reinterpret_cast<const float4*>(a.wT + (cg * D + (wv * RT + t) * 16 + i16) * BC + 4 * q + 16 * k);
+        o.wf[t][k] = *reinterpret_cast<const float4*>(a.wTF + cg * D * BC + (long)((wv * RT + t) * (BC / 16) + k) * 256 + 4 * lane);
     };
     auto ld_rest = [&](Ops& o, long cg) {
 #pragma unroll
@@ -731,11 +742,12 @@ int bgemm(const BgArgs& a, hipStream_t s) {
     // each operand must be contiguous along k or along its other dimension (16-byte tile loads)
     if ((a.ak != 1 && a.am != 1) || (a.bk != 1 && a.bn != 1)) return BF_ERR_UNSUPPORTED;
     if (a.M % 64 || a.N % 64 || a.K % 32 || a.K <= 0) return BF_ERR_UNSUPPORTED;
-    if ((a.rdo || a.cdo || a.dgc) && a.cn != 1) return BF_ERR_UNSUPPORTED;
+    if ((a.rdo || a.cdo || a.dgc || a.cfrag) && a.cn != 1) return BF_ERR_UNSUPPORTED;
+    if (a.cfrag && (a.acc || a.add || a.rdo || a.cdo)) return BF_ERR_UNSUPPORTED;
     // 16-byte row pieces of C, the addend and rdx when C is contiguous along n
     if (a.cn == 1 && ((a.cm | a.sc0 | a.sc1 | a.sc2) % 4)) return BF_ERR_UNSUPPORTED;
     const bool ak = a.ak == 1, bk = a.bk == 1;
-    const int ex = a.dgc || a.cdo ? 2 : a.msc || a.rdo ? 1 : 0;
+    const int ex = a.dgc || a.cdo ? 2 : a.msc || a.rdo || a.cfrag ? 1 : 0;
     auto go = [&](auto kern, int bn) {
         hipLaunchKernelGGL(kern, dim3((unsigned)a.nz, a.M / 64, a.N / bn), dim3(BW_NT), 0, s, a);
     };
@@ -784,6 +796,7 @@ struct Epi {
     const float* rdx = nullptr;
     float* rdo = nullptr;
     float* cdo = nullptr;
+    int frag = 0;
 };
 
 // C (M x N) per (chunk, g[, r]) = add + alpha * A B, with A, B given as Op (transposes by swapping strides)
@@ -797,7 +810,7 @@ int gemm(int M, int N, int K, int nz, int n1, int n2, Op A, Op B, float* C, long
     g.C = C; g.sc0 = c0; g.sc1 = c1; g.sc2 = c2; g.cm = cm; g.cn = cn;
     g.ksc = ks.ksc; g.ks0 = ks.s0; g.ks1 = ks.s1;
     g.msc = ep.msc; g.ms0 = ep.s0; g.ms1 = ep.s1; g.dgc = ep.dgc; g.dg0 = ep.g0; g.dg1 = ep.g1;
-    g.rdx = ep.rdx; g.rdo = ep.rdo; g.cdo = ep.cdo;
+    g.rdx = ep.rdx; g.rdo = ep.rdo; g.cdo = ep.cdo; g.cfrag = ep.frag;
     g.alpha = alpha; g.acc = acc; g.mask = mask; g.add = add;
     if (ks.shift < 30 && ((1 << ks.shift) % 16 != 0 || K % (1 << ks.shift) != 0)) return BF_ERR_UNSUPPORTED;
     return bgemm(g, s);
@@ -812,7 +825,7 @@ size_t gdn_bwd_workspace(int num_seqs, long T, int G, int R, int D) {
     const long cc = BC * BC, cd = (long)BC * D, dd = (long)D * D;
     const long floats = NC * (BC * 5 + 4                             // gam, eg, dgz, zrA, zcA, part
                               + cc * 3                               // Am, M, dA
-                              + cd * 8                               // kb, vb, kbe, ktl, u, w, ktlT, wT
+                              + cd * 10                              // kb, vb, kbe, ktl, u, w; ktl, kt^T, w, w^T in fragment order
                               + (long)R * (cc * 2 + (D / 64 + 2) * BC)   // attn, dattn; qdot, zr, zc
                               + dd * 3                               // Sc, E2, dSx
                               + cd * 9                               // E1, dvn, vn, dkt, dw, dvb, dkbe, dkb, dkacc
@@ -834,7 +847,8 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
     a.Am = take(NC * cc); a.Mi = take(NC * cc); a.dA = take(NC * cc);
     a.zrA = take(NC * BC); a.zcA = take(NC * BC); a.zr = take(NC * R * BC); a.zc = take(NC * R * BC);
     a.kb = take(NC * cd); a.vb = take(NC * cd); a.kbe = take(NC * cd); a.ktl = take(NC * cd);
-    a.u = take(NC * cd); a.w = take(NC * cd); a.ktlT = take(NC * cd); a.wT = take(NC * cd);
+    a.u = take(NC * cd); a.w = take(NC * cd);
+    a.ktlF = take(NC * cd); a.ktlTF = take(NC * cd); a.wF = take(NC * cd); a.wTF = take(NC * cd);
     a.attn = take(NC * R * cc); a.dattn = take(NC * R * cc);
     a.qdot = take(NC * R * (D / 64) * BC);
     a.Sc = take(NC * dd); a.E2 = take(NC * dd); a.dSx = take(NC * dd);
@@ -870,8 +884,12 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
     // u = M (v b), w = M (k b e^gc)
     ok(gemm(BC, D, BC, nzg, G, 1, W(a.Mi, BC, BC), W(a.vb, BC, D), a.u, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0, nullptr, s));
     ok(gemm(BC, D, BC, nzg, G, 1, W(a.Mi, BC, BC), W(a.kbe, BC, D), a.w, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0, nullptr, s));
-    ok(gemm(BC, D, BC, nzg, G, 1, W(a.Mi, BC, BC), W(a.kbe, BC, D), a.wT, (long)G * cd, cd, 0, 1, BC, 1.f, 0, 0, nullptr,
-            s));                                          // the same product stored transposed [D][C]
+    Epi fr;
+    fr.frag = 1;                                          // w and w^T in fragment order for the state walks
+    ok(gemm(BC, D, BC, nzg, G, 1, W(a.Mi, BC, BC), W(a.kbe, BC, D), a.wF, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0, nullptr,
+            s, KSplit{}, fr));
+    ok(gemm(D, BC, BC, nzg, G, 1, tr(W(a.kbe, BC, D)), tr(W(a.Mi, BC, BC)), a.wTF, (long)G * cd, cd, 0, BC, 1, 1.f, 0, 0,
+            nullptr, s, KSplit{}, fr));                   // w^T = (k b e^gc)^T M^T
     // attn_r = tril(s q_r k^T * decay)
     ok(gemm(BC, BC, D, nzr, G, R, qR(), tr(Op{a.k, (long)BC * G * D, D, 0, (long)G * D, 1}), a.attn, (long)G * R * cc,
             (long)R * cc, cc, BC, 1, a.scale, 0, 1, nullptr, s, KSplit{}, dec));

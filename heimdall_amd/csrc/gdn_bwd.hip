@@ -16,6 +16,8 @@
 // Kernels: bgemm_kernel (batched strided fp32 GEMM on v_mfma_f32_16x16x4f32, optional triangular mask, addend and
 // accumulate, in-chunk decay, row scale and row / column dots in the epilogue), chunk_prep_kernel,
 // unit_lower_inverse_kernel, walk_kernel (both state walks in one launch), chunk_final_kernel, dg_scan_kernel.
+#include <array>
+
 #include "bf_common.h"
 #include "bf_internal.h"
 
@@ -73,7 +75,8 @@ template <bool AK, bool BK, int BN, int EX>
 __global__ __launch_bounds__(BW_NT) void bgemm_kernel(BgArgs a) {
     constexpr int KS = 32, LDK = KS + 4;        // k per step, LDS row pitch (floats)
     constexpr int WN = BN / 2, TU = WN / 16;    // wave tile 32 x WN: 2 x TU MFMA tiles
-    constexpr int NA = 2, NB = BN / 32;         // 16-byte global loads per thread per step
+    constexpr int KQ = KS / 4, KG = KS / 16;    // 16-byte slots along k per row; 16-k groups per step
+    constexpr int NA = 64 * KS / 1024, NB = BN * KS / 1024;   // 16-byte global loads per thread per step
     const int lane = lane_id(), wv = wave_id(), tid = threadIdx.x;
     const long z = blockIdx.x;
     const long z2 = z % a.n2, z1 = (z / a.n2) % a.n1, z0 = z / ((long)a.n1 * a.n2);
@@ -98,22 +101,22 @@ __global__ __launch_bounds__(BW_NT) void bgemm_kernel(BgArgs a) {
         for (int u = 0; u < TU; ++u) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
     // the block-level skip of a masked tile wholly outside the kept triangle
     const bool skip = (a.mask == 1 && tm + 63 < tn) || (a.mask == 2 && tm + 63 <= tn);
-    // Load slot h of a thread. k-contiguous operand: row tid / 8 + 32 h, k (tid % 8) * 4 .. + 3; otherwise k
-    // tid / 16 + 16 (h & 1), rows (tid % 16) * 4 + 64 (h >> 1) .. + 3. A step starts at a multiple of 32 and 2^kshift
-    // is a multiple of 16, so the 4 k of a k-contiguous slot share their high part.
+    // Load slot h of a thread. k-contiguous operand: row tid / KQ + (256 / KQ) h, k (tid % KQ) * 4 .. + 3; otherwise
+    // k tid / 16 + 16 (h % KG), rows (tid % 16) * 4 + 64 (h / KG) .. + 3. A step starts at a multiple of 16 and
+    // 2^kshift is a multiple of 16, so the 4 k of a k-contiguous slot share their high part.
     auto koff = [&](int k, long shi, long slo) { return (long)(k >> ksh) * shi + (long)(k & klo) * slo; };
     auto load_a = [&](int k0, int h) {
         float4 x;
         if (AK) {
-            const int k = k0 + (tid % 8) * 4;
-            x = *reinterpret_cast<const float4*>(A + (long)(tm + tid / 8 + 32 * h) * a.am + koff(k, a.sak, a.ak));
+            const int k = k0 + (tid % KQ) * 4;
+            x = *reinterpret_cast<const float4*>(A + (long)(tm + tid / KQ + (256 / KQ) * h) * a.am + koff(k, a.sak, a.ak));
             if (ksc) {
                 const float4 sv = *reinterpret_cast<const float4*>(ksc + (k & klo));
                 x.x *= sv.x; x.y *= sv.y; x.z *= sv.z; x.w *= sv.w;
             }
         } else {
-            const int k = k0 + tid / 16 + 16 * h;
-            x = *reinterpret_cast<const float4*>(A + koff(k, a.sak, a.ak) + tm + (tid % 16) * 4);
+            const int k = k0 + tid / 16 + 16 * (h % KG);
+            x = *reinterpret_cast<const float4*>(A + koff(k, a.sak, a.ak) + tm + (tid % 16) * 4 + 64 * (h / KG));
             if (ksc) {
                 const float sv = ksc[k & klo];
                 x.x *= sv; x.y *= sv; x.z *= sv; x.w *= sv;
@@ -123,27 +126,27 @@ __global__ __launch_bounds__(BW_NT) void bgemm_kernel(BgArgs a) {
     };
     auto load_b = [&](int k0, int h) {
         if (BK) {
-            const int k = k0 + (tid % 8) * 4;
-            return *reinterpret_cast<const float4*>(B + (long)(tn + tid / 8 + 32 * h) * a.bn + koff(k, a.sbk, a.bk));
+            const int k = k0 + (tid % KQ) * 4;
+            return *reinterpret_cast<const float4*>(B + (long)(tn + tid / KQ + (256 / KQ) * h) * a.bn + koff(k, a.sbk, a.bk));
         }
-        const int k = k0 + tid / 16 + 16 * (h & 1);
-        return *reinterpret_cast<const float4*>(B + koff(k, a.sbk, a.bk) + tn + (tid % 16) * 4 + 64 * (h >> 1));
+        const int k = k0 + tid / 16 + 16 * (h % KG);
+        return *reinterpret_cast<const float4*>(B + koff(k, a.sbk, a.bk) + tn + (tid % 16) * 4 + 64 * (h / KG));
     };
     auto store = [&](int buf, const float4 (&xa)[NA], const float4 (&xb)[NB]) {
 #pragma unroll
         for (int h = 0; h < NA; ++h) {
-            if (AK) *reinterpret_cast<float4*>(&As[buf][tid / 8 + 32 * h][(tid % 8) * 4]) = xa[h];
-            else *reinterpret_cast<float4*>(&As[buf][tid / 16 + 16 * h][(tid % 16) * 4]) = xa[h];
+            if (AK) *reinterpret_cast<float4*>(&As[buf][tid / KQ + (256 / KQ) * h][(tid % KQ) * 4]) = xa[h];
+            else *reinterpret_cast<float4*>(&As[buf][tid / 16 + 16 * (h % KG)][(tid % 16) * 4 + 64 * (h / KG)]) = xa[h];
         }
 #pragma unroll
         for (int h = 0; h < NB; ++h) {
-            if (BK) *reinterpret_cast<float4*>(&Bs[buf][tid / 8 + 32 * h][(tid % 8) * 4]) = xb[h];
-            else *reinterpret_cast<float4*>(&Bs[buf][tid / 16 + 16 * (h & 1)][(tid % 16) * 4 + 64 * (h >> 1)]) = xb[h];
+            if (BK) *reinterpret_cast<float4*>(&Bs[buf][tid / KQ + (256 / KQ) * h][(tid % KQ) * 4]) = xb[h];
+            else *reinterpret_cast<float4*>(&Bs[buf][tid / 16 + 16 * (h % KG)][(tid % 16) * 4 + 64 * (h / KG)]) = xb[h];
         }
     };
     auto compute = [&](int buf) {
 #pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
+        for (int kh = 0; kh < KG; ++kh) {
             uint4 af[2], bf[TU];
             const int kr = 16 * kh + 4 * q;
 #pragma unroll
@@ -330,22 +333,30 @@ __global__ __launch_bounds__(BW_NT) void chunk_prep_kernel(GdnBwdArgs a) {
     }
     __syncthreads();
     const float gl = gc[BC - 1];
-    for (int e = tid; e < 16 * D; e += BW_NT) {
-        const int i = r0 + e / D, d = e % D;
+    // 16-byte pieces: rows r0 .. r0 + 15, four dims each (every output row-contiguous or a fragment-order float4)
+    const int D4 = D / 4;
+    for (int e = tid; e < 16 * D4; e += BW_NT) {
+        const int i = r0 + e / D4, d = 4 * (e % D4);
         const long tok = bc * BC + i;
-        const float be = a.beta[tok * G + g];
-        const float kx = a.k[(tok * G + g) * D + d], vx = a.v[(tok * G + g) * D + d];
+        const float be = a.beta[tok * G + g], ei = eg[i], et = expf(gl - gc[i]);
+        const float4 kx = *reinterpret_cast<const float4*>(a.k + (tok * G + g) * D + d);
+        const float4 vx = *reinterpret_cast<const float4*>(a.v + (tok * G + g) * D + d);
         const long o = (cg * BC + i) * D + d;
-        a.kb[o] = kx * be;
-        a.vb[o] = vx * be;
-        a.kbe[o] = kx * be * eg[i];
-        const float kt = kx * expf(gl - gc[i]);
-        a.ktl[o] = kt;
-        a.ktlF[cg * BC * D + frag16(i, d, D)] = kt;                 // fragment order, for the reverse walk
+        const float4 kb = make_float4(kx.x * be, kx.y * be, kx.z * be, kx.w * be);
+        const float4 kt = make_float4(kx.x * et, kx.y * et, kx.z * et, kx.w * et);
+        *reinterpret_cast<float4*>(a.kb + o) = kb;
+        *reinterpret_cast<float4*>(a.vb + o) = make_float4(vx.x * be, vx.y * be, vx.z * be, vx.w * be);
+        *reinterpret_cast<float4*>(a.kbe + o) = make_float4(kb.x * ei, kb.y * ei, kb.z * ei, kb.w * ei);
+        *reinterpret_cast<float4*>(a.ktl + o) = kt;
+        *reinterpret_cast<float4*>(a.ktlF + cg * BC * D + frag16(i, d, D)) = kt;   // fragment order, reverse walk
     }
-    for (int e = tid; e < 16 * D; e += BW_NT) {              // kt transposed [D][C] in fragment order, forward walk
-        const int d = e / 16, i = r0 + e % 16;
-        a.ktlTF[cg * D * BC + frag16(d, i, BC)] = a.k[((bc * BC + i) * G + g) * D + d] * expf(gl - gc[i]);
+    // kt transposed [D][C] in fragment order (forward walk): dim d, tokens i .. i + 3 of the quarter per piece
+    for (int e = tid; e < 4 * D; e += BW_NT) {
+        const int d = e % D, i = r0 + 4 * (e / D);
+        float x[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) x[u] = a.k[((bc * BC + i + u) * G + g) * D + d] * expf(gl - gc[i + u]);
+        *reinterpret_cast<float4*>(a.ktlTF + cg * D * BC + frag16(d, i, BC)) = make_float4(x[0], x[1], x[2], x[3]);
     }
 }
 
@@ -672,8 +683,13 @@ __global__ __launch_bounds__(BW_NT) void chunk_final_kernel(GdnBwdArgs a) {
     __syncthreads();
     const float gl = gc[BC - 1], ec = expf(gl);
     float sdot = 0.f;
-    const long q4 = (long)D * D / 4;
-    for (long e = z * q4 + tid; e < (z + 1) * q4; e += BW_NT) sdot += a.Sc[cg * D * D + e] * a.dSx[cg * D * D + e];
+    const long q4 = (long)D * D / 16;                     // this quarter's 16-byte pieces of S and dS'
+    const float4* S4 = reinterpret_cast<const float4*>(a.Sc + cg * D * D) + z * q4;
+    const float4* X4 = reinterpret_cast<const float4*>(a.dSx + cg * D * D) + z * q4;
+    for (long e = tid; e < q4; e += BW_NT) {
+        const float4 x = S4[e], y = X4[e];
+        sdot += (x.x * y.x + x.y * y.y) + (x.z * y.z + x.w * y.w);
+    }
     float ktsum = 0.f;
     for (int i = r0 + wv; i < r0 + 16; i += BW_NT / 64) {
         const long tok = bc * BC + i;
@@ -686,18 +702,27 @@ __global__ __launch_bounds__(BW_NT) void chunk_final_kernel(GdnBwdArgs a) {
         // decayed strict-lower A, dQK_r of attn_r), from the epilogues of the dA and dattn products
         if (lane == 0) dgi += a.zrA[cg * BC + i] - a.zcA[cg * BC + i];
         for (int r = lane; r < R; r += 64) dgi += a.zr[(cg * R + r) * BC + i] - a.zc[(cg * R + r) * BC + i];
-        for (int d = lane; d < D; d += 64) {
-            const long o = (cg * BC + i) * D + d;
-            const float dkt = a.dkt[o], kt = a.ktl[o];
-            const float dkbe = a.dkbe[o];
-            const float dkbt = a.dkb[o] + dkbe * egi;
-            const float kx = a.k[(tok * G + g) * D + d], vx = a.v[(tok * G + g) * D + d];
-            const float dvb = a.dvb[o];
-            dgi += dkbe * a.kbe[o] - dkt * kt;
-            ktsum += dkt * kt;
-            dbi += dkbt * kx + dvb * vx;
-            a.dk[(tok * G + g) * D + d] = a.dkacc[o] + dkt * eti + dkbt * be;
-            a.dv[(tok * G + g) * D + d] = dvb * be;
+        for (int d = 4 * lane; d < D; d += 256) {          // four dims per lane, 16-byte accesses
+            const long o = (cg * BC + i) * D + d, ot = (tok * G + g) * D + d;
+            auto ld = [&](const float* p) {
+                const float4 x = *reinterpret_cast<const float4*>(p);
+                return std::array<float, 4>{x.x, x.y, x.z, x.w};
+            };
+            const auto dkt = ld(a.dkt + o), kt = ld(a.ktl + o), dkbe = ld(a.dkbe + o), dkb = ld(a.dkb + o);
+            const auto kx = ld(a.k + ot), vx = ld(a.v + ot), dvb = ld(a.dvb + o), kbe = ld(a.kbe + o);
+            const auto dka = ld(a.dkacc + o);
+            float dk[4], dv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const float dkbt = dkb[u] + dkbe[u] * egi;
+                dgi += dkbe[u] * kbe[u] - dkt[u] * kt[u];
+                ktsum += dkt[u] * kt[u];
+                dbi += dkbt * kx[u] + dvb[u] * vx[u];
+                dk[u] = dka[u] + dkt[u] * eti + dkbt * be;
+                dv[u] = dvb[u] * be;
+            }
+            *reinterpret_cast<float4*>(a.dk + ot) = make_float4(dk[0], dk[1], dk[2], dk[3]);
+            *reinterpret_cast<float4*>(a.dv + ot) = make_float4(dv[0], dv[1], dv[2], dv[3]);
         }
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) {

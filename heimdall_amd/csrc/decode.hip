@@ -13,12 +13,12 @@
 // ring_g, ring_beta [B][W][G] f32; ring_pos [W] int64; sinks [B][G][ns][D]; qr, qm, o [B][H][D]; kr, v, km [B][G][D].
 //
 // Kernels:
-//   decode_slab    grid (D/32, G, B): state slab x (32 columns): memory write of the evicted row, memory read
+//   decode_slab    grid (D/64, G, B): state slab x (64 columns): memory write of the evicted row, memory read
 //   decode_main    grid (W/256, G, B): window split x (256 ring slots; split 0 also takes the sinks and new token)
 //   decode_combine grid (R, G, B): merge the window splits, gamma mix, ring write
 // The slab and window kernels are launched one after the other: run as one grid, their mixed workgroups took
 // longer than the two launches together.
-//   gdn_step       grid (D/32, G, B): the state slab pass alone (delta_rule_step)
+//   gdn_step       grid (D/64, G, B): the state slab pass alone (delta_rule_step)
 #include "bf_common.h"
 #include "bf_internal.h"
 
@@ -26,7 +26,9 @@ namespace bf {
 
 constexpr int NT_DEC = 256;
 constexpr int SLOTS = 512;       // ring slots per window split (512: 132 us at B=64 against 141 us with 256)
-constexpr int SCOL = 32;         // state columns per slab
+constexpr int SCG = 16;          // 4-column groups per state slab (64 columns: 1024 slab workgroups at B = 64, G = 4
+                                 // fit one round; 16 / 32 / 128 columns measured 150 / 133 / 134 us per step, 64 131)
+constexpr int SCOL = 4 * SCG;    // state columns per slab
 constexpr int RMAX = 8;          // query heads per KV head supported by the decode kernels
 
 template <class KV>
@@ -54,52 +56,51 @@ __device__ __forceinline__ void ld16f<F32>(const float* p, float (&out)[16]) {
     }
 }
 
-// Sum over the 32 threads of a block that share (tid % 8): lanes l, l+8, .., l+56 of each wave, then the 4 waves.
-// red: shared scratch of 4 * 8 * NV floats. Returns the total in every thread of the group (tid % 8).
+// Sum over the threads of a block that share (tid % SCG): lanes l, l + SCG, .. of each wave, then the 4 waves.
+// red: shared scratch of 4 * SCG * NV floats. Returns the total in every thread of the group (tid % SCG).
 template <int NV>
 __device__ __forceinline__ void reduce_colgroups(float (&v)[NV], float* red) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         float x = v[i];
-        x += __shfl_xor(x, 8);
-        x += __shfl_xor(x, 16);
-        x += __shfl_xor(x, 32);
+#pragma unroll
+        for (int off = SCG; off < 64; off <<= 1) x += __shfl_xor(x, off);
         v[i] = x;
     }
-    if (lane < 8) {
+    if (lane < SCG) {
 #pragma unroll
-        for (int i = 0; i < NV; ++i) red[(wv * 8 + lane) * NV + i] = v[i];
+        for (int i = 0; i < NV; ++i) red[(wv * SCG + lane) * NV + i] = v[i];
     }
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-        const int c = tid & 7;
-        v[i] = red[(0 * 8 + c) * NV + i] + red[(1 * 8 + c) * NV + i] + red[(2 * 8 + c) * NV + i] +
-               red[(3 * 8 + c) * NV + i];
+        const int c = tid & (SCG - 1);
+        v[i] = red[(0 * SCG + c) * NV + i] + red[(1 * SCG + c) * NV + i] + red[(2 * SCG + c) * NV + i] +
+               red[(3 * SCG + c) * NV + i];
     }
     __syncthreads();
 }
 
-// State slab pass for one (b, g): columns [j0, j0 + 32). Thread tid owns columns j0 + 4 (tid % 8) .. +3 of rows
-// tid / 8 + 32 i. Applies S <- e^{wg} S; delta = wb (wv - S^T wk); S <- S + wk delta^T (skipped when !write), then
+// State slab pass for one (b, g): columns [j0, j0 + SCOL). Thread tid owns columns j0 + 4 (tid % SCG) .. +3 of rows
+// tid / SCG + (256 / SCG) i. Applies S <- e^{wg} S; delta = wb (wv - S^T wk); S <- S + wk delta^T (skipped when !write), then
 // writes o[r][j] = sum_d qm_r[d] S[d][j] for the R query heads. S is updated in place (s_in == s_out allowed).
 template <int D, int RMAX>
 __device__ __forceinline__ void state_slab(const float* s_in, float* s_out, const float* wk, const float* wv,
                                            float wg, float wb, bool write, const float* qm, int R, long q_stride,
                                            float* om, long o_stride, int j0, float* red) {
-    constexpr int RPT = D / 32;                      // rows per thread
-    const int tid = threadIdx.x, cg = tid & 7, r0 = tid >> 3;
+    constexpr int RSTEP = 256 / SCG, RPT = D / RSTEP;   // row step, rows per thread
+    const int tid = threadIdx.x, cg = tid & (SCG - 1), r0 = tid / SCG;
     const int jc = j0 + 4 * cg;
     float4 s[RPT];
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) s[i] = nt_ldf4(s_in + (long)(r0 + 32 * i) * D + jc);    // streamed: read once
+    for (int i = 0; i < RPT; ++i) s[i] = nt_ldf4(s_in + (long)(r0 + RSTEP * i) * D + jc);    // streamed: read once
     if (write) {
         const float a = __expf(wg);
         float rc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i = 0; i < RPT; ++i) {
-            const float k = wk[r0 + 32 * i];
+            const float k = wk[r0 + RSTEP * i];
             rc[0] += k * s[i].x; rc[1] += k * s[i].y; rc[2] += k * s[i].z; rc[3] += k * s[i].w;
         }
         reduce_colgroups<4>(rc, red);
@@ -108,7 +109,7 @@ __device__ __forceinline__ void state_slab(const float* s_in, float* s_out, cons
                              wb * (v4.w - a * rc[3])};
 #pragma unroll
         for (int i = 0; i < RPT; ++i) {
-            const float k = wk[r0 + 32 * i];
+            const float k = wk[r0 + RSTEP * i];
             s[i].x = a * s[i].x + k * dl[0];
             s[i].y = a * s[i].y + k * dl[1];
             s[i].z = a * s[i].z + k * dl[2];
@@ -116,7 +117,7 @@ __device__ __forceinline__ void state_slab(const float* s_in, float* s_out, cons
         }
     }
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) nt_stf4(s_out + (long)(r0 + 32 * i) * D + jc, s[i]);
+    for (int i = 0; i < RPT; ++i) nt_stf4(s_out + (long)(r0 + RSTEP * i) * D + jc, s[i]);
     if (!om) return;
     float acc[RMAX * 4];
 #pragma unroll
@@ -125,7 +126,7 @@ __device__ __forceinline__ void state_slab(const float* s_in, float* s_out, cons
         if (r < R) {
 #pragma unroll
             for (int i = 0; i < RPT; ++i) {
-                const float qv = qm[r * q_stride + r0 + 32 * i];
+                const float qv = qm[r * q_stride + r0 + RSTEP * i];
                 a0 += qv * s[i].x; a1 += qv * s[i].y; a2 += qv * s[i].z; a3 += qv * s[i].w;
             }
         }
@@ -428,7 +429,7 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
 template <class KV, int D, int RM>
 __global__ __launch_bounds__(NT_DEC) void decode_slab_kernel(DecodeArgs a) {
     using T = typename KV::T;
-    __shared__ float red[4 * 8 * RM * 4];
+    __shared__ float red[4 * SCG * RM * 4];
     __shared__ float vrow[D];
     const int x = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
     const int G = a.G, R = a.R, H = G * R, W = a.W;
@@ -517,7 +518,7 @@ __global__ __launch_bounds__(NT_DEC) void decode_combine_kernel(DecodeArgs a) {
 // ----------------------------------------------------------------------------------------------- single-token GDN
 template <int D>
 __global__ __launch_bounds__(NT_DEC) void gdn_step_kernel(StepArgs a) {
-    __shared__ float red[4 * 8 * RMAX * 4];
+    __shared__ float red[4 * SCG * RMAX * 4];
     const int x = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
     const int G = a.G, R = a.R, H = G * R;
     const long bg = (long)b * G + g;

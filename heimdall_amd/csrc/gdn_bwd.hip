@@ -28,6 +28,9 @@ namespace {
 constexpr int BC = 64;                  // chunk length
 constexpr int BW_NT = 256;
 
+// Column scale of a GEMM's A operand when it has none (loaded like a real scale, so no branch drains the prefetch).
+__device__ const float kOnes[4] = {1.f, 1.f, 1.f, 1.f};
+
 // Fragment order of an R x C fp32 matrix (C a multiple of 16): its 16 x 16 tiles one after another, row-major over
 // tiles, each as 64 lanes x 4 floats with lane 16 q + i holding row i, columns 4 q .. 4 q + 3 of the tile, so a wave
 // reads a tile (the operand fragment of v_mfma_f32_16x16x4f32 over 4 k steps) as one contiguous 1 KB.
@@ -82,7 +85,10 @@ __global__ __launch_bounds__(BW_NT) void bgemm_kernel(BgArgs a) {
     const long z2 = z % a.n2, z1 = (z / a.n2) % a.n1, z0 = z / ((long)a.n1 * a.n2);
     const float* A = a.A + z0 * a.sa0 + z1 * a.sa1 + z2 * a.sa2;
     const float* B = a.B + z0 * a.sb0 + z1 * a.sb1 + z2 * a.sb2;
-    const float* ksc = a.ksc ? a.ksc + z0 * a.ks0 + z1 * a.ks1 : nullptr;
+    // A's column scale (ones without one): loaded with the tile and applied when the tile is stored to LDS a step
+    // later, since a multiply right after the loads would wait for them
+    const float* ksc = a.ksc ? a.ksc + z0 * a.ks0 + z1 * a.ks1 : kOnes;
+    const int kscm = a.ksc ? -1 : 0;                      // index mask: every k, or element 0 of kOnes
     const int ksh = a.kshift, klo = (1 << ksh) - 1;
     const long coff = z0 * a.sc0 + z1 * a.sc1 + z2 * a.sc2;
     const int tm = blockIdx.y * 64, tn = blockIdx.z * BN;
@@ -105,24 +111,16 @@ __global__ __launch_bounds__(BW_NT) void bgemm_kernel(BgArgs a) {
     // k tid / 16 + 16 (h % KG), rows (tid % 16) * 4 + 64 (h / KG) .. + 3. A step starts at a multiple of 16 and
     // 2^kshift is a multiple of 16, so the 4 k of a k-contiguous slot share their high part.
     auto koff = [&](int k, long shi, long slo) { return (long)(k >> ksh) * shi + (long)(k & klo) * slo; };
-    auto load_a = [&](int k0, int h) {
-        float4 x;
+    auto load_a = [&](int k0, int h, float4& sv) {
         if (AK) {
             const int k = k0 + (tid % KQ) * 4;
-            x = *reinterpret_cast<const float4*>(A + (long)(tm + tid / KQ + (256 / KQ) * h) * a.am + koff(k, a.sak, a.ak));
-            if (ksc) {
-                const float4 sv = *reinterpret_cast<const float4*>(ksc + (k & klo));
-                x.x *= sv.x; x.y *= sv.y; x.z *= sv.z; x.w *= sv.w;
-            }
-        } else {
-            const int k = k0 + tid / 16 + 16 * (h % KG);
-            x = *reinterpret_cast<const float4*>(A + koff(k, a.sak, a.ak) + tm + (tid % 16) * 4 + 64 * (h / KG));
-            if (ksc) {
-                const float sv = ksc[k & klo];
-                x.x *= sv; x.y *= sv; x.z *= sv; x.w *= sv;
-            }
+            sv = *reinterpret_cast<const float4*>(ksc + (k & klo & kscm));
+            return *reinterpret_cast<const float4*>(A + (long)(tm + tid / KQ + (256 / KQ) * h) * a.am + koff(k, a.sak, a.ak));
         }
-        return x;
+        const int k = k0 + tid / 16 + 16 * (h % KG);
+        const float c = ksc[k & klo & kscm];
+        sv = make_float4(c, c, c, c);
+        return *reinterpret_cast<const float4*>(A + koff(k, a.sak, a.ak) + tm + (tid % 16) * 4 + 64 * (h / KG));
     };
     auto load_b = [&](int k0, int h) {
         if (BK) {
@@ -132,11 +130,12 @@ __global__ __launch_bounds__(BW_NT) void bgemm_kernel(BgArgs a) {
         const int k = k0 + tid / 16 + 16 * (h % KG);
         return *reinterpret_cast<const float4*>(B + koff(k, a.sbk, a.bk) + tn + (tid % 16) * 4 + 64 * (h / KG));
     };
-    auto store = [&](int buf, const float4 (&xa)[NA], const float4 (&xb)[NB]) {
+    auto store = [&](int buf, const float4 (&xa)[NA], const float4 (&sa)[NA], const float4 (&xb)[NB]) {
 #pragma unroll
         for (int h = 0; h < NA; ++h) {
-            if (AK) *reinterpret_cast<float4*>(&As[buf][tid / KQ + (256 / KQ) * h][(tid % KQ) * 4]) = xa[h];
-            else *reinterpret_cast<float4*>(&As[buf][tid / 16 + 16 * (h % KG)][(tid % 16) * 4 + 64 * (h / KG)]) = xa[h];
+            const float4 x = make_float4(xa[h].x * sa[h].x, xa[h].y * sa[h].y, xa[h].z * sa[h].z, xa[h].w * sa[h].w);
+            if (AK) *reinterpret_cast<float4*>(&As[buf][tid / KQ + (256 / KQ) * h][(tid % KQ) * 4]) = x;
+            else *reinterpret_cast<float4*>(&As[buf][tid / 16 + 16 * (h % KG)][(tid % 16) * 4 + 64 * (h / KG)]) = x;
         }
 #pragma unroll
         for (int h = 0; h < NB; ++h) {
@@ -171,21 +170,21 @@ __global__ __launch_bounds__(BW_NT) void bgemm_kernel(BgArgs a) {
     };
     if (!skip) {
         const int ns = a.K / KS;
-        float4 xa[NA], xb[NB];
+        float4 xa[NA], sa[NA], xb[NB];
         auto fetch = [&](int s) {
 #pragma unroll
-            for (int h = 0; h < NA; ++h) xa[h] = load_a(s * KS, h);
+            for (int h = 0; h < NA; ++h) xa[h] = load_a(s * KS, h, sa[h]);
 #pragma unroll
             for (int h = 0; h < NB; ++h) xb[h] = load_b(s * KS, h);
         };
         fetch(0);
-        store(0, xa, xb);
+        store(0, xa, sa, xb);
         if (ns > 1) fetch(1);
         __syncthreads();
         for (int s = 0; s < ns; ++s) {
             compute(s & 1);
             if (s + 1 < ns) {
-                store((s + 1) & 1, xa, xb);
+                store((s + 1) & 1, xa, sa, xb);
                 if (s + 2 < ns) fetch(s + 2);
             }
             __syncthreads();

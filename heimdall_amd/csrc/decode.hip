@@ -180,16 +180,23 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
         if (k < nring + a.n_sinks) return sink + (long)(k - nring) * D;
         return nw;
     };
-    // visibility of every key of the split, read once into LDS (its ring_pos loads overlap the first K loads)
-    for (int k = tid; k < nkeys; k += NT_DEC) {
-        bool v_;
-        if (k < nring) {
-            const long p = a.ring_pos[s0 + k];
-            v_ = p >= lo && p <= a.pos - 1;
-        } else {
-            v_ = k < nring + a.n_sinks ? true : a.pos >= a.sinks;
+    // visibility of every key of the split, read once into LDS (its ring_pos loads overlap the first K loads). The
+    // loads are issued together, unconditionally (indices clamped to the split): a load under a per-key branch is
+    // waited for before the next one.
+    {
+        constexpr int VI = (SLOTS + 64 + NT_DEC - 1) / NT_DEC;
+        long rpv[VI];
+#pragma unroll
+        for (int u = 0; u < VI; ++u) rpv[u] = a.ring_pos[s0 + min(tid + u * NT_DEC, nring - 1)];
+#pragma unroll
+        for (int u = 0; u < VI; ++u) {
+            const int k = tid + u * NT_DEC;
+            if (k < nkeys) {
+                const bool v_ = k < nring ? rpv[u] >= lo && rpv[u] <= a.pos - 1
+                                          : (k < nring + a.n_sinks ? true : a.pos >= a.sinks);
+                vis[k] = v_;
+            }
         }
-        vis[k] = v_;
     }
     __syncthreads();
     auto visible = [&](int k) -> bool { return vis[k] != 0; };
@@ -202,21 +209,29 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
         const int l16 = lane & 15, lg = lane >> 4;
         uint4 qf[NKD];
         {
+            // all NKD loads issued before any is used, under one dtype branch (lanes past R read head 0, then zero)
             const int r = l16 < R ? l16 : 0;
             const long qrow = ((long)b * H + g * R + r) * D;
+            if (a.q_dtype == DT_BF16) {
+                const uint16_t* qp = reinterpret_cast<const uint16_t*>(a.qr) + qrow + 8 * lg;
 #pragma unroll
-            for (int ks = 0; ks < NKD; ++ks) {
-                uint4 v = zero16();
-                if (l16 < R) {
-                    if (a.q_dtype == DT_BF16) {
-                        v = ld16(reinterpret_cast<const uint16_t*>(a.qr) + qrow + 32 * ks + 8 * lg);
-                    } else {
-                        const float* qp = reinterpret_cast<const float*>(a.qr) + qrow + 32 * ks + 8 * lg;
-                        v = make_uint4(pack_bf16x2(qp[0], qp[1]), pack_bf16x2(qp[2], qp[3]),
-                                       pack_bf16x2(qp[4], qp[5]), pack_bf16x2(qp[6], qp[7]));
-                    }
+                for (int ks = 0; ks < NKD; ++ks) qf[ks] = ld16(qp + 32 * ks);
+            } else {
+                const float* qp = reinterpret_cast<const float*>(a.qr) + qrow + 8 * lg;
+                float4 q0[NKD], q1[NKD];
+#pragma unroll
+                for (int ks = 0; ks < NKD; ++ks) {
+                    q0[ks] = *reinterpret_cast<const float4*>(qp + 32 * ks);
+                    q1[ks] = *reinterpret_cast<const float4*>(qp + 32 * ks + 4);
                 }
-                qf[ks] = v;
+#pragma unroll
+                for (int ks = 0; ks < NKD; ++ks)
+                    qf[ks] = make_uint4(pack_bf16x2(q0[ks].x, q0[ks].y), pack_bf16x2(q0[ks].z, q0[ks].w),
+                                        pack_bf16x2(q1[ks].x, q1[ks].y), pack_bf16x2(q1[ks].z, q1[ks].w));
+            }
+            if (l16 >= R) {
+#pragma unroll
+                for (int ks = 0; ks < NKD; ++ks) qf[ks] = zero16();
             }
         }
         // ring keys: two 16-key groups per wave iteration (addresses past the last ring key clamped to it)

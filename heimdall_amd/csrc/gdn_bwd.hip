@@ -15,8 +15,11 @@
 //
 // Kernels: bgemm_kernel (batched strided fp32 GEMM on v_mfma_f32_16x16x4f32, optional triangular mask, addend and
 // accumulate, in-chunk decay, row scale and row / column dots in the epilogue), chunk_prep_kernel,
-// unit_lower_inverse_kernel, walk_kernel (both state walks in one launch), chunk_final_kernel, dg_scan_kernel.
+// unit_lower_inverse_kernel, walk_fwd_kernel / walk_bwd_kernel (the two state walks), chunk_final_kernel,
+// dg_scan_kernel. The host side runs the forward walk and the products that need only its states on a second stream,
+// beside the reverse walk and its products.
 #include <array>
+#include <mutex>
 
 #include "bf_common.h"
 #include "bf_internal.h"
@@ -377,8 +380,8 @@ __global__ __launch_bounds__(64) void unit_lower_inverse_kernel(const float* Am,
 }
 
 // ------------------------------------------------------------------------------------ state walks
-// Grid (sequences, G, 2 D / 16): a workgroup owns 16 state columns of one KV head and walks the chunks in order (the
-// first D / 16 strips forward, the others backward), the strip held in fp32 MFMA accumulators; per chunk two products on
+// Grid (sequences, G, D / 16) per walk: a workgroup owns 16 state columns of one KV head and walks the chunks in order
+// (forward, or backward in the reverse walk), the strip held in fp32 MFMA accumulators; per chunk two products on
 // v_mfma_f32_16x16x4f32 with the strip (and v_new / dvn) passed through LDS transposed, so every operand fragment is
 // one 16-byte read. WALK_NW<D> waves: 8 at D >= 128 (two per SIMD, so one wave's loads and LDS exchange overlap the
 // other's MFMAs), 4 at D = 64. Wave w owns row tiles [w RT, (w + 1) RT) of the strip; for the 64-token product the
@@ -659,13 +662,12 @@ __device__ __forceinline__ void walk_bwd(const GdnBwdArgs& a, int strip) {
             a.ds0[(((long)b * G + g) * D + erow(e)) * D + ecol(e)] = L[e / (4 * RT)][(e / 4) % RT][e % 4];
 }
 
-// the two walks are independent (the reverse one needs E1, E2, kt, w, not the entry states): one launch
+// the two walks are independent (the reverse one needs E1, E2, kt, w, not the entry states): separate launches, so
+// each starts as soon as its own operands exist and the products around it fill the CUs the walks leave idle
 template <int D>
-__global__ __launch_bounds__(64 * walk_nw<D>()) void walk_kernel(GdnBwdArgs a) {
-    constexpr int NS = D / 16 / walk_sw<D>();              // strips each way
-    if ((int)blockIdx.z < NS) walk_fwd<D>(a, blockIdx.z);
-    else walk_bwd<D>(a, blockIdx.z - NS);
-}
+__global__ __launch_bounds__(64 * walk_nw<D>()) void walk_fwd_kernel(GdnBwdArgs a) { walk_fwd<D>(a, blockIdx.z); }
+template <int D>
+__global__ __launch_bounds__(64 * walk_nw<D>()) void walk_bwd_kernel(GdnBwdArgs a) { walk_bwd<D>(a, blockIdx.z); }
 
 
 // ------------------------------------------------------------------------------------ final assembly
@@ -842,6 +844,31 @@ int gemm(int M, int N, int K, int nz, int n1, int n2, Op A, Op B, float* C, long
 
 Op tr(Op o) { std::swap(o.rs, o.cs); return o; }
 
+// The backward's second stream on each device (default priority, created on a device's first call) and the events
+// that order it against the caller's stream. The caller holds g_bwd_mu over a call's whole enqueue, so the records and
+// waits of concurrent calls from several host threads do not interleave.
+constexpr int kBwdMaxDevices = 64;
+struct BwdSide {
+    hipStream_t s = nullptr;
+    hipEvent_t ev[6] = {};
+};
+std::mutex g_bwd_mu;
+BwdSide g_bwd_side[kBwdMaxDevices];
+
+int side_stream(hipStream_t& s2, hipEvent_t (&ev)[6]) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kBwdMaxDevices) return BF_ERR_UNSUPPORTED;
+    BwdSide& sd = g_bwd_side[dev];
+    for (hipEvent_t& x : sd.ev)
+        if (!x && (e = hipEventCreateWithFlags(&x, hipEventDisableTiming)) != hipSuccess) return (int)e;
+    if (!sd.s && (e = hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking)) != hipSuccess) return (int)e;
+    s2 = sd.s;
+    for (int i = 0; i < 6; ++i) ev[i] = sd.ev[i];
+    return 0;
+}
+
 }  // namespace
 
 size_t gdn_bwd_workspace(int num_seqs, long T, int G, int R, int D) {
@@ -858,6 +885,7 @@ size_t gdn_bwd_workspace(int num_seqs, long T, int G, int R, int D) {
 }
 
 int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
+    std::lock_guard<std::mutex> lock(g_bwd_mu);
     const int D = a.D, G = a.G, R = a.R, H = G * R;
     const long n = a.n_chunks, NB = (long)a.num_seqs * n, NC = NB * G;
     const long cc = BC * BC, cd = (long)BC * D, dd = (long)D * D;
@@ -895,6 +923,10 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
     };
     const int nzg = (int)NC, nzr = (int)(NC * R);
 
+    hipStream_t s2 = nullptr;
+    hipEvent_t ev[6] = {};
+    ok(side_stream(s2, ev));
+    if (e) return e;
     // prep
     hipLaunchKernelGGL(chunk_prep_kernel, dim3((unsigned)NB, G, 4), dim3(BW_NT), 0, s, a);
     ok((int)hipGetLastError());
@@ -914,48 +946,73 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
             s, KSplit{}, fr));
     ok(gemm(D, BC, BC, nzg, G, 1, tr(W(a.kbe, BC, D)), tr(W(a.Mi, BC, BC)), a.wTF, (long)G * cd, cd, 0, BC, 1, 1.f, 0, 0,
             nullptr, s, KSplit{}, fr));                   // w^T = (k b e^gc)^T M^T
+    // Side stream: the forward walk, then what needs only the entry states (v_new, dattn, dq). Main stream: attn, E1,
+    // E2, the reverse walk, then what needs dS' and dvn, joining the side stream where its results are read.
+    ok((int)hipEventRecord(ev[0], s));
+    ok((int)hipStreamWaitEvent(s2, ev[0], 0));
+    const dim3 wgrid(a.num_seqs, G, D / 16);               // walk_sw<D>() == 1: one workgroup per 16-column strip
+    // The walks are the call's critical path on few workgroups: each asks for LDS up to 128 KB of the CU's 160 KB,
+    // so no product workgroup (34-55 KB) shares its CU and slows it (2.11 -> 2.06 ms with the attn product after the
+    // fork, T = 8192, G = 4, R = 6, D = 256)
+    auto walk = [&](bool fwd, hipStream_t st) {
+        const dim3 blk(64 * (D >= 128 ? 8 : 4));
+        const int kh = D >= 128 ? 2 : 1;
+        const size_t res = 128 * 1024 - (size_t)(16 * (D + 4) + kh * 16 * (BC + 4)) * sizeof(float);
+        if (D == 64) hipLaunchKernelGGL(fwd ? walk_fwd_kernel<64> : walk_bwd_kernel<64>, wgrid, blk, res, st, a);
+        else if (D == 128) hipLaunchKernelGGL(fwd ? walk_fwd_kernel<128> : walk_bwd_kernel<128>, wgrid, blk, res, st, a);
+        else hipLaunchKernelGGL(fwd ? walk_fwd_kernel<256> : walk_bwd_kernel<256>, wgrid, blk, res, st, a);
+        ok((int)hipGetLastError());
+    };
     // attn_r = tril(s q_r k^T * decay)
     ok(gemm(BC, BC, D, nzr, G, R, qR(), tr(Op{a.k, (long)BC * G * D, D, 0, (long)G * D, 1}), a.attn, (long)G * R * cc,
             (long)R * cc, cc, BC, 1, a.scale, 0, 1, nullptr, s, KSplit{}, dec));
+    ok((int)hipEventRecord(ev[4], s));                     // attn
+    walk(true, s2);
+    ok((int)hipEventRecord(ev[1], s2));                    // entry states Sc
+    // v_new = u - w S
+    ok(gemm(BC, D, D, nzg, G, 1, W(a.w, BC, D), W(a.Sc, D, D), a.vn, (long)G * cd, cd, 0, D, 1, -1.f, 0, 0, a.u, s2));
+    ok((int)hipEventRecord(ev[2], s2));                    // v_new
+    // dattn_r = tril(dO_r v_new^T); dqd_r = dO_r S^T goes straight into dq_r = s e^gc dqd_r (token-major; the attn
+    // share is added below), with each row's dot with q_r (the query path's d gc share) as partials in qdot
+    // (the decayed dattn_r; the decay's d gc share from dQK_r . QK_r = dattn_r(undecayed) . attn_r as row and column
+    // sums)
+    ok((int)hipStreamWaitEvent(s2, ev[4], 0));
+    Epi da = dec;
+    da.rdx = a.attn; da.rdo = a.zr; da.cdo = a.zc;
+    ok(gemm(BC, BC, D, nzr, G, R, dOR(), tr(Op{a.vn, (long)G * cd, cd, 0, D, 1}), a.dattn, (long)G * R * cc,
+            (long)R * cc, cc, BC, 1, 1.f, 0, 1, nullptr, s2, KSplit{}, da));
+    // dk from attn: sum_r dattn_r^T (s q_r), K = R C (the share from A is added on the main stream)
+    KSplit rk;
+    rk.shift = 6; rk.a = cc; rk.b = D;                    // attn^T / dattn^T (chunk-major [r][i][j]) against dO or q
+    const Op qk{a.q, (long)BC * H * D, (long)R * D, 0, (long)H * D, 1};
+    ok(gemm(BC, D, R * BC, nzg, G, 1, tr(Op{a.dattn, (long)G * R * cc, (long)R * cc, 0, BC, 1}), qk, a.dkacc,
+            (long)G * cd, cd, 0, D, 1, a.scale, 0, 0, nullptr, s2, rk));
+    ok((int)hipEventRecord(ev[5], s2));                    // dkacc (attn share)
+    Epi eq;
+    eq.msc = a.eg; eq.s0 = (long)G * BC; eq.s1 = BC; eq.rdx = a.q; eq.rdo = a.qdot;
+    ok(gemm(BC, D, D, nzr, G, R, dOR(), tr(Op{a.Sc, (long)G * dd, dd, 0, D, 1}), a.dq, (long)BC * H * D, (long)R * D, D,
+            (long)H * D, 1, a.scale, 0, 0, nullptr, s2, KSplit{}, eq));
+    // dq_r += s dattn_r k
+    ok(gemm(BC, D, BC, nzr, G, R, WR(a.dattn, BC, BC), Op{a.k, (long)BC * G * D, D, 0, (long)G * D, 1}, a.dq,
+            (long)BC * H * D, (long)R * D, D, (long)H * D, 1, a.scale, 1, 0, nullptr, s2));
+    ok((int)hipEventRecord(ev[3], s2));                    // dattn, dq, qdot, zr, zc
+
     // E1 = sum_r attn_r^T dO_r [C x D], E2 = sum_r qd_r^T dO_r = s sum_r q_r^T diag(e^gc) dO_r [D x D]: one product
     // each over K = R C, the (r, token) pairs, read from the token-major q and dO (k = 64 r + i: token stride H D,
     // head stride D)
     const Op dOk{a.dO, (long)BC * H * D, (long)R * D, 0, (long)H * D, 1};
-    const Op qk{a.q, (long)BC * H * D, (long)R * D, 0, (long)H * D, 1};
-    KSplit rk;
-    rk.shift = 6; rk.a = cc; rk.b = D;                    // attn^T / dattn^T (chunk-major [r][i][j]) against dO or q
     ok(gemm(BC, D, R * BC, nzg, G, 1, tr(Op{a.attn, (long)G * R * cc, (long)R * cc, 0, BC, 1}), dOk, a.E1, (long)G * cd,
             cd, 0, D, 1, 1.f, 0, 0, nullptr, s, rk));
     KSplit rq;
     rq.shift = 6; rq.a = D; rq.b = D; rq.ksc = a.eg; rq.s0 = (long)G * BC; rq.s1 = BC;   // A = q^T, columns e^gc
     ok(gemm(D, D, R * BC, nzg, G, 1, tr(qk), dOk, a.E2, (long)G * dd, dd, 0, D, 1, a.scale, 0, 0, nullptr, s, rq));
-    // walks
-    const dim3 wgrid(a.num_seqs, G, 2 * D / 16);          // walk_sw<D>() == 1
-    if (D == 64) hipLaunchKernelGGL(walk_kernel<64>, wgrid, dim3(64 * walk_nw<64>()), 0, s, a);
-    else if (D == 128) hipLaunchKernelGGL(walk_kernel<128>, wgrid, dim3(64 * walk_nw<128>()), 0, s, a);
-    else hipLaunchKernelGGL(walk_kernel<256>, wgrid, dim3(64 * walk_nw<256>()), 0, s, a);
-    ok((int)hipGetLastError());
-    // v_new = u - w S
-    ok(gemm(BC, D, D, nzg, G, 1, W(a.w, BC, D), W(a.Sc, D, D), a.vn, (long)G * cd, cd, 0, D, 1, -1.f, 0, 0, a.u, s));
-    // dattn_r = tril(dO_r v_new^T); dqd_r = dO_r S^T goes straight into dq_r = s e^gc dqd_r (token-major; the attn
-    // share is added below), with each row's dot with q_r (the query path's d gc share) as partials in qdot
-    // (the decayed dattn_r; the decay's d gc share from dQK_r . QK_r = dattn_r(undecayed) . attn_r as row and column
-    // sums)
-    Epi da = dec;
-    da.rdx = a.attn; da.rdo = a.zr; da.cdo = a.zc;
-    ok(gemm(BC, BC, D, nzr, G, R, dOR(), tr(Op{a.vn, (long)G * cd, cd, 0, D, 1}), a.dattn, (long)G * R * cc,
-            (long)R * cc, cc, BC, 1, 1.f, 0, 1, nullptr, s, KSplit{}, da));
-    Epi eq;
-    eq.msc = a.eg; eq.s0 = (long)G * BC; eq.s1 = BC; eq.rdx = a.q; eq.rdo = a.qdot;
-    ok(gemm(BC, D, D, nzr, G, R, dOR(), tr(Op{a.Sc, (long)G * dd, dd, 0, D, 1}), a.dq, (long)BC * H * D, (long)R * D, D,
-            (long)H * D, 1, a.scale, 0, 0, nullptr, s, KSplit{}, eq));
-    // dkt = v_new dS'^T, dw = -dvn S^T
-    ok(gemm(BC, D, D, nzg, G, 1, W(a.vn, BC, D), tr(W(a.dSx, D, D)), a.dkt, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0,
-            nullptr, s));
-    ok(gemm(BC, D, D, nzg, G, 1, W(a.dvn, BC, D), tr(W(a.Sc, D, D)), a.dw, (long)G * cd, cd, 0, D, 1, -1.f, 0, 0,
-            nullptr, s));
-    // d(v b) = M^T dvn, d(k b e^gc) = M^T dw
+    walk(false, s);
+    // d(v b) = M^T dvn
     ok(gemm(BC, D, BC, nzg, G, 1, tr(W(a.Mi, BC, BC)), W(a.dvn, BC, D), a.dvb, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0,
+            nullptr, s));
+    // dw = -dvn S^T, d(k b e^gc) = M^T dw
+    ok((int)hipStreamWaitEvent(s, ev[1], 0));
+    ok(gemm(BC, D, D, nzg, G, 1, W(a.dvn, BC, D), tr(W(a.Sc, D, D)), a.dw, (long)G * cd, cd, 0, D, 1, -1.f, 0, 0,
             nullptr, s));
     ok(gemm(BC, D, BC, nzg, G, 1, tr(W(a.Mi, BC, BC)), W(a.dw, BC, D), a.dkbe, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0,
             nullptr, s));
@@ -971,14 +1028,16 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
     dd_.rdx = a.Am; dd_.rdo = a.zrA; dd_.cdo = a.zcA;
     ok(gemm(BC, BC, BC, nzg, G, 1, W(T1, BC, BC), tr(W(a.Mi, BC, BC)), a.dA, (long)G * cc, cc, 0, BC, 1, -1.f, 0, 2,
             nullptr, s, KSplit{}, dd_));
-    // d(k b) from A: dAd k ; dk from A: dAd^T (k b) ; from attn: sum_r dattn_r^T (s q_r) ; dq_r = s dattn_r k
+    // d(k b) from A: dAd k ; dk from A: dAd^T (k b), added to the attn share
     ok(gemm(BC, D, BC, nzg, G, 1, W(a.dA, BC, BC), kT(), a.dkb, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0, nullptr, s));
-    ok(gemm(BC, D, BC, nzg, G, 1, tr(W(a.dA, BC, BC)), W(a.kb, BC, D), a.dkacc, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0,
+    ok((int)hipStreamWaitEvent(s, ev[5], 0));
+    ok(gemm(BC, D, BC, nzg, G, 1, tr(W(a.dA, BC, BC)), W(a.kb, BC, D), a.dkacc, (long)G * cd, cd, 0, D, 1, 1.f, 1, 0,
             nullptr, s));
-    ok(gemm(BC, D, R * BC, nzg, G, 1, tr(Op{a.dattn, (long)G * R * cc, (long)R * cc, 0, BC, 1}), qk, a.dkacc,
-            (long)G * cd, cd, 0, D, 1, a.scale, 1, 0, nullptr, s, rk));   // sum_r dattn_r^T (s q_r), K = R C
-    ok(gemm(BC, D, BC, nzr, G, R, WR(a.dattn, BC, BC), Op{a.k, (long)BC * G * D, D, 0, (long)G * D, 1}, a.dq,
-            (long)BC * H * D, (long)R * D, D, (long)H * D, 1, a.scale, 1, 0, nullptr, s));
+    // dkt = v_new dS'^T
+    ok((int)hipStreamWaitEvent(s, ev[2], 0));
+    ok(gemm(BC, D, D, nzg, G, 1, W(a.vn, BC, D), tr(W(a.dSx, D, D)), a.dkt, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0,
+            nullptr, s));
+    ok((int)hipStreamWaitEvent(s, ev[3], 0));             // the side stream's dq, qdot, zr, zc
     hipLaunchKernelGGL(chunk_final_kernel, dim3((unsigned)NB, G, 4), dim3(BW_NT), 0, s, a);
     hipLaunchKernelGGL(dg_scan_kernel, dim3((unsigned)NC), dim3(64), 0, s, a);
     ok((int)hipGetLastError());

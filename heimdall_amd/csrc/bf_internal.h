@@ -8,6 +8,10 @@
 
 namespace bf {
 
+// Ring slots per window split of the decode step (at B = 64, G = 4, W = 2048: 1024 slots 129.1 us per step, 512 130.4,
+// 2048 134.0, 256 141).
+constexpr int DECODE_SLOTS = 1024;
+
 constexpr int DT_F32 = BF_DTYPE_F32;
 constexpr int DT_BF16 = BF_DTYPE_BF16;
 constexpr int BF_ERR_UNSUPPORTED = BF_STATUS_UNSUPPORTED;
@@ -76,7 +80,7 @@ struct DecodeArgs {
     float* state;             // [B][G][D][D]
     float* o;                 // [B][H][D]
     float* lse;               // [B][H] or null
-    int nsplit;               // window splits of 512 ring slots
+    int nsplit;               // window splits of DECODE_SLOTS ring slots
     float* ws_om;             // [B][H][D] memory read
     float* ws_part;           // [B][G][nsplit][R][D + 2] window partials
 };

@@ -194,7 +194,7 @@ int bf_gdn_step(const float* q, const float* k, const float* v, const float* g, 
 int bf_decode_workspace_size(int B, int G, int R, int D, int W, size_t* bytes) {
     if (!bytes || B <= 0 || G <= 0 || R <= 0 || W <= 0) return BF_STATUS_INVALID;
     if (!supported_dim(D) || R > 8) return BF_STATUS_UNSUPPORTED;
-    const size_t nsplit = (size_t)(W + 511) / 512;
+    const size_t nsplit = (size_t)(W + bf::DECODE_SLOTS - 1) / bf::DECODE_SLOTS;
     *bytes = align256((size_t)B * G * R * D * sizeof(float)) +
              align256((size_t)B * G * nsplit * R * (D + 2) * sizeof(float));
     return BF_STATUS_OK;
@@ -228,7 +228,7 @@ int bf_decode_fwd(int B, int G, int R, int D, int W, int sinks, int64_t pos, int
     a.sink_k = sink_k; a.sink_v = sink_v; a.n_sinks = n_sinks;
     a.ring_k = ring_k; a.ring_v = ring_v; a.ring_km = ring_km; a.ring_g = ring_g; a.ring_beta = ring_beta;
     a.ring_pos = ring_pos; a.state = state; a.o = o; a.lse = lse;
-    a.nsplit = (W + 511) / 512;
+    a.nsplit = (W + bf::DECODE_SLOTS - 1) / bf::DECODE_SLOTS;
     char* ws = static_cast<char*>(workspace);
     a.ws_om = reinterpret_cast<float*>(ws);
     a.ws_part = reinterpret_cast<float*>(ws + align256((size_t)B * G * R * D * sizeof(float)));

@@ -14,7 +14,7 @@
 //
 // Kernels:
 //   decode_slab    grid (D/64, G, B): state slab x (64 columns): memory write of the evicted row, memory read
-//   decode_main    grid (W/256, G, B): window split x (256 ring slots; split 0 also takes the sinks and new token)
+//   decode_main    grid (W/1024, G, B): window split x (1024 ring slots; split 0 also takes the sinks and new token)
 //   decode_combine grid (R, G, B): merge the window splits, gamma mix, ring write
 // The slab and window kernels are launched one after the other: run as one grid, their mixed workgroups took
 // longer than the two launches together.
@@ -25,7 +25,7 @@
 namespace bf {
 
 constexpr int NT_DEC = 256;
-constexpr int SLOTS = 512;       // ring slots per window split (512: 132 us at B=64 against 141 us with 256)
+constexpr int SLOTS = DECODE_SLOTS;   // ring slots per window split
 constexpr int SCG = 16;          // 4-column groups per state slab (64 columns: 1024 slab workgroups at B = 64, G = 4
                                  // fit one round; 16 / 32 / 128 columns measured 150 / 133 / 134 us per step, 64 131)
 constexpr int SCOL = 4 * SCG;    // state columns per slab

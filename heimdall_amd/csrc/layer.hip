@@ -103,6 +103,45 @@ __global__ __launch_bounds__(LT) void layer_writeback_kernel(LayerArgs a) {
     }
 }
 
+// The write-back with 4 consecutive dims per thread (8-byte bf16 or 16-byte fp32 accesses); strides multiples of 4.
+__device__ __forceinline__ float4 ldx4(const void* p, long i, int dt) {
+    if (dt == DT_BF16) {
+        const uint2 u = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p) + i);
+        return make_float4(__uint_as_float(u.x << 16), __uint_as_float(u.x & 0xffff0000u), __uint_as_float(u.y << 16),
+                           __uint_as_float(u.y & 0xffff0000u));
+    }
+    return *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(p) + i);
+}
+__device__ __forceinline__ void stx4(void* p, long i, float4 v, int dt) {
+    if (dt == DT_BF16)
+        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p) + i) =
+            make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+    else *reinterpret_cast<float4*>(reinterpret_cast<float*>(p) + i) = v;
+}
+
+__global__ __launch_bounds__(LT) void layer_writeback4_kernel(LayerArgs a) {
+    const int G = a.G, D4 = a.D / 4, W = a.W;
+    const int n = a.T < W ? a.T : W;
+    const long total = (long)a.B * n * G * D4, e = (long)blockIdx.x * LT + threadIdx.x;
+    if (e >= total) return;
+    const int d = 4 * (int)(e % D4), g = (int)((e / D4) % G);
+    const long bi = e / ((long)G * D4);
+    const int b = (int)(bi / n), j = (int)(bi % n);
+    const long t = a.T - n + j, p = a.start + t;
+    const int s = (int)(p % W);
+    const float4 kx = ldx4(a.kr, b * a.k_sb + g * a.k_sh + t * a.k_st + d, a.in_dtype);
+    const float4 vx = ldx4(a.v, b * a.v_sb + g * a.v_sh + t * a.v_st + d, a.in_dtype);
+    const float4 mx = ldx4(a.km, (((long)b * a.T + t) * G + g) * a.D + d, a.km_dtype);
+    stx4(a.ring_k_w, (((long)b * G + g) * W + s) * a.D + d, kx, a.in_dtype);
+    stx4(a.ring_v_w, (((long)b * G + g) * W + s) * a.D + d, vx, a.in_dtype);
+    *reinterpret_cast<float4*>(a.ring_km_w + (((long)b * W + s) * G + g) * a.D + d) = mx;
+    if (d == 0) {
+        a.ring_g_w[((long)b * W + s) * G + g] = a.g[((long)b * a.T + t) * G + g];
+        a.ring_beta_w[((long)b * W + s) * G + g] = a.beta[((long)b * a.T + t) * G + g];
+        if (b == 0 && g == 0) a.ring_pos_w[s] = p;
+    }
+}
+
 __global__ __launch_bounds__(LT) void layer_copy_kernel(const float* src, float* dst, long n) {
     const long e = ((long)blockIdx.x * LT + threadIdx.x) * 4;
     if (e + 3 < n) {
@@ -130,7 +169,16 @@ int layer_launch(const LayerArgs& a, int what, hipStream_t s) {
             break;
         case 2: {
             const long n = a.T < a.W ? a.T : a.W;
-            hipLaunchKernelGGL(layer_writeback_kernel, dim3(blocks_for((long)a.B * n * a.G * a.D)), dim3(LT), 0, s, a);
+            // 4 dims per thread when every row start is 4-element aligned
+            const uintptr_t ain = a.in_dtype == DT_BF16 ? 7 : 15, akm = a.km_dtype == DT_BF16 ? 7 : 15;
+            const bool al = !(((uintptr_t)a.kr | (uintptr_t)a.v | (uintptr_t)a.ring_k_w | (uintptr_t)a.ring_v_w) & ain) &&
+                            !((uintptr_t)a.km & akm) && !((uintptr_t)a.ring_km_w & 15);
+            if (al && ((a.k_sb | a.k_sh | a.k_st | a.v_sb | a.v_sh | a.v_st) & 3) == 0)
+                hipLaunchKernelGGL(layer_writeback4_kernel, dim3(blocks_for((long)a.B * n * a.G * a.D / 4)), dim3(LT), 0,
+                                   s, a);
+            else
+                hipLaunchKernelGGL(layer_writeback_kernel, dim3(blocks_for((long)a.B * n * a.G * a.D)), dim3(LT), 0, s,
+                                   a);
             break;
         }
         default: {

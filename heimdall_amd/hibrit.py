@@ -88,7 +88,16 @@ def _mem_inputs_bf16(self, xf, q, k, pos):
     return qm, km, g, beta
 
 
-def _new_ring(b, G, w, D, kdt, vdt, dev):
+def _new_ring(b, G, w, D, kdt, vdt, dev, overwritten: bool = False):
+    """An empty ring (no valid slot). ``overwritten``: the caller's next write fills every slot before anything reads
+    the ring (a prefill of at least W tokens from position 0), so the tensors are left uninitialised."""
+    if overwritten:
+        return dict(ring_k=torch.empty(b, G, w, D, dtype=kdt, device=dev),
+                    ring_v=torch.empty(b, G, w, D, dtype=vdt, device=dev),
+                    ring_km=torch.empty(b, w, G, D, dtype=torch.float32, device=dev),
+                    ring_g=torch.empty(b, w, G, dtype=torch.float32, device=dev),
+                    ring_beta=torch.empty(b, w, G, dtype=torch.float32, device=dev),
+                    ring_pos=torch.empty(w, dtype=torch.long, device=dev))
     return dict(ring_k=torch.zeros(b, G, w, D, dtype=kdt, device=dev),
                 ring_v=torch.zeros(b, G, w, D, dtype=vdt, device=dev),
                 ring_km=torch.zeros(b, w, G, D, dtype=torch.float32, device=dev),
@@ -184,7 +193,10 @@ def student(self, x, q, k, v, qr, kr, start: int, cache: Optional[dict], memory:
     else:
         qm, km, g, beta = self._mem_inputs(x, q, k, pos)
     if "ring_k" not in st:
-        st.update(_new_ring(b, c.hkv, w, c.dh, kr.dtype, vt.dtype, dev))
+        # a prefill of t >= W tokens from position 0 writes every ring slot (bf_layer_prefill_fwd's write-back) and
+        # reads none before that
+        full = t >= w and start == 0
+        st.update(_new_ring(b, c.hkv, w, c.dh, kr.dtype, vt.dtype, dev, overwritten=full))
     if t == 1:
         o = _decode(self, x, qr, kr[:, :, 0], v[:, 0], qm[:, 0], km[:, 0], g[:, 0], beta[:, 0], start, st, sink_k,
                     sink_v, memory)

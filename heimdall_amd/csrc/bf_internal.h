@@ -160,6 +160,15 @@ struct MemProjArgs {
     void* out;                // [n_tok][nh][D] bf16
 };
 
+struct MemGatesArgs {
+    const float* ab;                // [n_tok][ab_st]: columns [a (G) | b (G)]
+    long n_tok, T, ab_st;           // tokens, tokens per sequence, row stride
+    int G, sinks;
+    long start;                     // position of each sequence's first token
+    const float *A_log, *dt_bias, *decay_mask;
+    float *g, *beta;                // [n_tok][G]
+};
+int mem_gates_dispatch(const MemGatesArgs& a, hipStream_t stream);
 int mem_project_dispatch(const MemProjArgs& a, hipStream_t stream);
 int window_fa_dispatch(const WinArgs& a, hipStream_t stream);
 

@@ -292,6 +292,18 @@ int bf_mem_project(const void* x, int64_t n_tok, int nh, int D, int64_t x_st, in
     return bf::mem_project_dispatch(a, static_cast<hipStream_t>(stream));
 }
 
+int bf_mem_gates(const float* ab, int64_t n_tok, int64_t T, int G, int64_t ab_st, const float* A_log,
+                 const float* dt_bias, const float* decay_mask, int64_t start, int sinks, float* g, float* beta,
+                 void* stream) {
+    if (n_tok < 0 || T <= 0 || G <= 0 || ab_st < 2 * G || start < 0 || sinks < 0 || (n_tok % T)) return BF_STATUS_INVALID;
+    if (n_tok == 0) return BF_STATUS_OK;
+    if (!ab || !A_log || !dt_bias || !decay_mask || !g || !beta) return BF_STATUS_INVALID;
+    bf::MemGatesArgs a{};
+    a.ab = ab; a.n_tok = n_tok; a.T = T; a.ab_st = ab_st; a.G = G; a.sinks = sinks; a.start = start;
+    a.A_log = A_log; a.dt_bias = dt_bias; a.decay_mask = decay_mask; a.g = g; a.beta = beta;
+    return bf::mem_gates_dispatch(a, static_cast<hipStream_t>(stream));
+}
+
 int bf_gdn_conv_inputs(const void* z, int64_t z_st, const void* prefix, int in_dtype, const float* conv_w, int K,
                        const float* a, const float* b, const float* A_log, const float* dt_bias,
                        const int32_t* cu_seqlens, int num_seqs, int64_t n_tok, int HK, int HV, int D, float eps,

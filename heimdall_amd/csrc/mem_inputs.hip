@@ -133,4 +133,25 @@ int mem_project_dispatch(const MemProjArgs& a, hipStream_t stream) {
     return (int)hipGetLastError();
 }
 
+// Gates of the memory branch (reference: HybridAttention._mem_inputs, Heimdall/heimdall/hibrit.py:331-333), one
+// thread per (token, KV head): g = -exp(A_log) softplus(a + dt_bias) decay_mask, beta = sigmoid(b) [pos >= sinks].
+__global__ __launch_bounds__(256) void mem_gates_kernel(MemGatesArgs a) {
+    const long e = (long)blockIdx.x * 256 + threadIdx.x;
+    if (e >= a.n_tok * a.G) return;
+    const long t = e / a.G;
+    const int j = (int)(e % a.G);
+    const float* row = a.ab + t * a.ab_st;
+    const float x = row[j] + a.dt_bias[j];
+    const float sp = x > 20.f ? x : log1pf(expf(x));            // softplus, torch's default threshold
+    a.g[e] = -expf(a.A_log[j]) * sp * a.decay_mask[j];
+    const long pos = a.start + t % a.T;
+    a.beta[e] = pos >= a.sinks ? 1.f / (1.f + expf(-row[a.G + j])) : 0.f;
+}
+
+int mem_gates_dispatch(const MemGatesArgs& a, hipStream_t stream) {
+    const long n = a.n_tok * a.G;
+    hipLaunchKernelGGL(mem_gates_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a);
+    return (int)hipGetLastError();
+}
+
 }  // namespace bf

@@ -64,27 +64,48 @@ def mem_inputs(self, x, q, k, pos):
     return qm, km, g, beta
 
 
-def _project_bf16(x: torch.Tensor, f: torch.Tensor, scale: float) -> torch.Tensor:
-    """bf16 x [B, t, nh, D] -> scale * normalize(x_h f_h) as bf16 [B, t, nh, D] on bf_mem_project."""
+def _ft_bf16(self, name: str) -> torch.Tensor:
+    """The projection ``name`` (fq or fk, [nh, D, D]) transposed in bf16, as bf_mem_project reads it; kept between
+    calls and rebuilt when the parameter changes (its storage or its version counter)."""
+    f = getattr(self, name)
+    cache = self.__dict__.setdefault("_ft_cache", {})
+    key = (f.data_ptr(), f._version, f.dtype, f.shape)
+    hit = cache.get(name)
+    if hit is None or hit[0] != key:
+        hit = (key, f.detach().transpose(1, 2).to(torch.bfloat16).contiguous())
+        cache[name] = hit
+    return hit[1]
+
+
+def _project_bf16(x: torch.Tensor, ft: torch.Tensor, scale: float) -> torch.Tensor:
+    """bf16 x [B, t, nh, D] -> scale * normalize(x_h f_h) as bf16 [B, t, nh, D] on bf_mem_project (ft = f_h^T in
+    bf16, [nh, D, D])."""
     b, t, nh, d = x.shape
     if x.stride(-1) != 1 or (b > 1 and x.stride(0) != t * x.stride(1)):
         x = x.contiguous()
-    ft = f.detach().transpose(1, 2).to(torch.bfloat16).contiguous()
     out = torch.empty(b, t, nh, d, dtype=torch.bfloat16, device=x.device)
     check(_lib.load().bf_mem_project(x.data_ptr(), b * t, nh, d, x.stride(1), x.stride(2), ft.data_ptr(), float(scale),
                                      out.data_ptr(), _lib.DTYPE_BF16, stream_ptr(x.device)), "bf_mem_project")
     return out
 
 
-def _mem_inputs_bf16(self, xf, q, k, pos):
-    """mem_inputs for bf16 activations: qm, km from the fused projection kernel (bf16 out, fp32 accumulation and
-    norm), the gates g, beta in fp32 from xf = x in fp32 (``hibrit.py:327-334``)."""
-    dh = self.c.dh
-    qm = _project_bf16(q, self.fq, dh ** -0.5)
-    km = _project_bf16(k, self.fk, 1.0)
-    a, bb = F.linear(xf, self.ab.weight.float(), self.ab.bias.float()).chunk(2, dim=-1)
-    g = -self.A_log.float().exp() * F.softplus(a + self.dt_bias.float()) * self.decay_mask.float()
-    beta = torch.sigmoid(bb) * (pos >= self.sinks).float()[None, :, None]
+def _mem_inputs_bf16(self, xf, q, k, start: int):
+    """mem_inputs for bf16 activations (no autograd): qm, km from the fused projection kernel (bf16 out, fp32
+    accumulation and norm), the gates g, beta in fp32 from xf = x in fp32 by bf_mem_gates (``hibrit.py:327-334``)."""
+    dh, G = self.c.dh, self.c.hkv
+    qm = _project_bf16(q, _ft_bf16(self, "fq"), dh ** -0.5)
+    km = _project_bf16(k, _ft_bf16(self, "fk"), 1.0)
+    ab = F.linear(xf, self.ab.weight.float(), self.ab.bias.float())
+    if not ab.is_contiguous():
+        ab = ab.contiguous()
+    b, t = ab.shape[:2]
+    g = torch.empty(b, t, G, dtype=torch.float32, device=xf.device)
+    beta = torch.empty_like(g)
+    f32 = lambda p: p if p.dtype == torch.float32 and p.is_contiguous() else p.float().contiguous()
+    A_log, dt_bias, mask = f32(self.A_log.detach()), f32(self.dt_bias.detach()), f32(self.decay_mask)
+    check(_lib.load().bf_mem_gates(ab.data_ptr(), b * t, t, G, 2 * G, A_log.data_ptr(), dt_bias.data_ptr(),
+                                   mask.data_ptr(), start, self.sinks, g.data_ptr(), beta.data_ptr(),
+                                   stream_ptr(xf.device)), "bf_mem_gates")
     return qm, km, g, beta
 
 
@@ -189,7 +210,7 @@ def student(self, x, q, k, v, qr, kr, start: int, cache: Optional[dict], memory:
     xf = None
     if t > 1 and all(z.dtype == torch.bfloat16 for z in (q, k, qr, kr)):
         xf = x.float()
-        qm, km, g, beta = _mem_inputs_bf16(self, xf, q, k, pos)
+        qm, km, g, beta = _mem_inputs_bf16(self, xf, q, k, start)
     else:
         qm, km, g, beta = self._mem_inputs(x, q, k, pos)
     if "ring_k" not in st:

@@ -188,6 +188,18 @@ int bf_mem_project(const void* x, int64_t n_tok, int nh, int D, int64_t x_st, in
                    float scale, void* out, int in_dtype, void* stream);
 
 /*
+ * Memory-branch gates of the converted layer, replacing the gate lines of HybridAttention._mem_inputs
+ * (Heimdall/heimdall/hibrit.py:331-333):
+ *     g[i][j]    = -exp(A_log[j]) * softplus(ab[i][j] + dt_bias[j]) * decay_mask[j]     (softplus threshold 20)
+ *     beta[i][j] = sigmoid(ab[i][G + j]) * [pos_i >= sinks],   pos_i = start + i mod T
+ *   ab: f32 rows of the ab projection (x W_ab^T + b_ab, columns [a | b], 2G wide) at ab + i * ab_st for the
+ *   n_tok = B * T tokens (T tokens per sequence); A_log, dt_bias, decay_mask [G] f32; g, beta [n_tok][G] f32.
+ */
+int bf_mem_gates(const float* ab, int64_t n_tok, int64_t T, int G, int64_t ab_st, const float* A_log,
+                 const float* dt_bias, const float* decay_mask, int64_t start, int sinks, float* g, float* beta,
+                 void* stream);
+
+/*
  * Native Gated DeltaNet layer, the pass before the delta rule: GatedDeltaNet.forward up to delta_rule
  * (Heimdall/heimdall/hibrit.py:159-179) with causal_conv (Heimdall/heimdall/kernels.py:29-37) and l2norm
  * (hibrit.py:132-133), for packed sequences.

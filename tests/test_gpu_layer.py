@@ -87,7 +87,7 @@ def test_mem_inputs_bf16_fused_projection(dev, d):
     pos = torch.arange(t)
     qm_ref, km_ref, g_ref, b_ref = olayer.mem_inputs(m, x, q.float(), k.float(), pos)
     with torch.no_grad():
-        qm, km, g, beta = hibrit._mem_inputs_bf16(mg, x.to(dev), q.to(dev), k.to(dev), pos.to(dev))
+        qm, km, g, beta = hibrit._mem_inputs_bf16(mg, x.to(dev), q.to(dev), k.to(dev), 0)
     assert qm.dtype == km.dtype == torch.bfloat16
     for got, ref in ((qm, qm_ref), (km, km_ref), (g, g_ref), (beta, b_ref)):
         assert rel(got, ref) < TOL_BF16, rel(got, ref)
@@ -95,6 +95,40 @@ def test_mem_inputs_bf16_fused_projection(dev, d):
     # rows are unit vectors times the scale
     nq = qm.float().norm(dim=-1).cpu()
     assert torch.allclose(nq, torch.full_like(nq, d ** -0.5), rtol=1e-2)
+
+
+def test_mem_gates_and_projection_cache(dev):
+    """bf_mem_gates (the gates of _mem_inputs for bf16 activations) against the oracle's fp32 gates for B = 2
+    sequences starting at position 1 with 2 sinks (beta is zero at position 1), relative error <= 1e-5; then an
+    in-place change of fq (as an optimizer step makes) reaches the next projection through the cached bf16 F^T."""
+    from heimdall_amd import hibrit
+    print("mem_inputs bf16 gates and F^T cache, D=64", flush=True)
+    m = make_core(6, 2, 64, 32, window=16, sinks=2)
+    mg = make_core(6, 2, 64, 32, window=16, sinks=2).to(dev)
+    with torch.no_grad():                                  # non-trivial gates: trained-like ab, one archival head
+        gen0 = torch.Generator().manual_seed(5)
+        w_ab, b_ab = torch.randn(4, 32, generator=gen0), torch.randn(4, generator=gen0)
+        for mm in (m, mg):
+            mm.ab.weight.copy_(w_ab)
+            mm.ab.bias.copy_(b_ab)
+    b, t, start = 2, 70, 1
+    gen = torch.Generator().manual_seed(22)
+    x = torch.randn(b, t, 32, generator=gen)
+    q = torch.randn(b, t, 6, 64, generator=gen).bfloat16()
+    k = torch.randn(b, t, 2, 64, generator=gen).bfloat16()
+    pos = torch.arange(start, start + t)
+    _, _, g_ref, b_ref = olayer.mem_inputs(m, x, q.float(), k.float(), pos)
+    with torch.no_grad():
+        qm0, _, g, beta = hibrit._mem_inputs_bf16(mg, x.to(dev), q.to(dev), k.to(dev), start)
+    assert rel(g, g_ref) < 1e-5 and rel(beta, b_ref) < 1e-5, (rel(g, g_ref), rel(beta, b_ref))
+    assert beta[:, 0].abs().max().item() == 0.0
+    noise = torch.randn(m.fq.shape, generator=gen) * 0.3
+    with torch.no_grad():
+        m.fq.add_(noise)
+        mg.fq.add_(noise.to(dev))
+        qm1, _, _, _ = hibrit._mem_inputs_bf16(mg, x.to(dev), q.to(dev), k.to(dev), start)
+    qm_ref, _, _, _ = olayer.mem_inputs(m, x, q.float(), k.float(), pos)
+    assert rel(qm1, qm_ref) < TOL_BF16 and rel(qm1, qm0) > 10 * TOL_BF16, (rel(qm1, qm_ref), rel(qm1, qm0))
 
 
 @pytest.mark.parametrize("b", [1, 3])

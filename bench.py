@@ -310,7 +310,7 @@ def run_decode(steps, warmup, dev):
               + B * G * D * (4 + 2 + 2 + 4))
     gbs = nbytes / (us * 1e-6) / 1e9
     return {"workload": "decode B=64 H=16 G=4 D=256 W=2048+4 bf16 ring, fp32 state", "us_per_step": us,
-            "steps": steps, "roofline": {"bound": "hbm", "kernel": "decode_main_kernel+decode_combine_kernel",
+            "steps": steps, "roofline": {"bound": "hbm", "kernel": "decode_main_kernel+decode_tail_kernel",
                                          "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                          "frac": gbs / HBM_PEAK_GBS, "bytes_per_step": nbytes}}
 

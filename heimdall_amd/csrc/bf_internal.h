@@ -83,6 +83,7 @@ struct DecodeArgs {
     int nsplit;               // window splits of DECODE_SLOTS ring slots
     float* ws_om;             // [B][H][D] memory read
     float* ws_part;           // [B][G][nsplit][R][D + 2] window partials
+    float* ws_ev;             // [B][G][2 D + 4] the ring row leaving the window: v, km, g, beta, valid
 };
 
 int decode_dispatch(const DecodeArgs& a, hipStream_t stream);

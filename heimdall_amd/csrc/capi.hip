@@ -196,7 +196,8 @@ int bf_decode_workspace_size(int B, int G, int R, int D, int W, size_t* bytes) {
     if (!supported_dim(D) || R > 8) return BF_STATUS_UNSUPPORTED;
     const size_t nsplit = (size_t)(W + bf::DECODE_SLOTS - 1) / bf::DECODE_SLOTS;
     *bytes = align256((size_t)B * G * R * D * sizeof(float)) +
-             align256((size_t)B * G * nsplit * R * (D + 2) * sizeof(float));
+             align256((size_t)B * G * nsplit * R * (D + 2) * sizeof(float)) +
+             align256((size_t)B * G * (2 * D + 4) * sizeof(float));
     return BF_STATUS_OK;
 }
 
@@ -232,6 +233,8 @@ int bf_decode_fwd(int B, int G, int R, int D, int W, int sinks, int64_t pos, int
     char* ws = static_cast<char*>(workspace);
     a.ws_om = reinterpret_cast<float*>(ws);
     a.ws_part = reinterpret_cast<float*>(ws + align256((size_t)B * G * R * D * sizeof(float)));
+    a.ws_ev = reinterpret_cast<float*>(reinterpret_cast<char*>(a.ws_part) +
+                                       align256((size_t)B * G * a.nsplit * R * (D + 2) * sizeof(float)));
     return bf::decode_dispatch(a, static_cast<hipStream_t>(stream));
 }
 

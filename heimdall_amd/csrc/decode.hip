@@ -12,12 +12,11 @@
 // Layout (row-major): state [B][G][D][D] f32; ring_k, ring_v [B][G][W][D]; ring_km [B][W][G][D] f32;
 // ring_g, ring_beta [B][W][G] f32; ring_pos [W] int64; sinks [B][G][ns][D]; qr, qm, o [B][H][D]; kr, v, km [B][G][D].
 //
-// Kernels:
-//   decode_slab    grid (D/64, G, B): state slab x (64 columns): memory write of the evicted row, memory read
-//   decode_main    grid (W/1024, G, B): window split x (1024 ring slots; split 0 also takes the sinks and new token)
-//   decode_combine grid (R, G, B): merge the window splits, gamma mix, ring write
-// The slab and window kernels are launched one after the other: run as one grid, their mixed workgroups took
-// longer than the two launches together.
+// Kernels (two launches per step):
+//   decode_main    grid (W/1024, G, B): window split x (1024 ring slots; split 0 also takes the sinks and the new
+//                  token, saves the ring row leaving the window and writes the new token's values into its slot)
+//   decode_tail    grid (D/64, G, B): state slab x (64 columns): memory write of the saved row, memory read; then
+//                  the merge of the window splits, the gamma mix and o for the slab's 64 dims; the new ring_pos entry
 //   gdn_step       grid (D/64, G, B): the state slab pass alone (delta_rule_step)
 #include "bf_common.h"
 #include "bf_internal.h"
@@ -437,52 +436,63 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
         out[tid * (D + 2)] = mx[tid];
         out[tid * (D + 2) + 1] = sm[tid];
     }
-}
-
-// State slab x (32 columns) of (b, g): the write of the ring row leaving the window, then the memory read of the
-// R query heads into ws_om.
-template <class KV, int D, int RM>
-__global__ __launch_bounds__(NT_DEC) void decode_slab_kernel(DecodeArgs a) {
-    using T = typename KV::T;
-    __shared__ float red[4 * SCG * RM * 4];
-    __shared__ float vrow[D];
-    const int x = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-    const int G = a.G, R = a.R, H = G * R, W = a.W;
-    const int tid = threadIdx.x;
-    const long bg = (long)b * G + g;
+    if (x != 0) return;
+    // Split 0: the ring row of slot pos mod W (position pos - W, leaving the window) into ws_ev for the state update
+    // of decode_tail_kernel, then the new token into that slot. No split reads the slot's values: its ring_pos
+    // (pos - W or older, rewritten by the tail) keeps it out of every window, so its scores are masked.
     const int slot = (int)(a.pos % W);
-    const long pe = a.pos - W;
-    const bool valid = pe >= 0 && a.ring_pos[slot] == pe;
-    const float* wk = a.ring_km + (((long)b * W + slot) * G + g) * D;
-    // evicted value row (kv dtype) -> fp32 in shared scratch
-    const T* rv = reinterpret_cast<const T*>(a.ring_v) + (bg * W + slot) * D;
-    for (int d = tid; d < D; d += NT_DEC) vrow[d] = KV::to_f(rv[d]);
-    __syncthreads();
-    const float wg = valid ? a.ring_g[((long)b * W + slot) * G + g] : 0.f;
-    const float wb = valid ? a.ring_beta[((long)b * W + slot) * G + g] : 0.f;
-    float* S = a.state + bg * D * D;
-    state_slab<D, RM>(S, S, wk, vrow, wg, wb, valid, a.qm + ((long)b * H + g * R) * D, R, D,
-                      a.ws_om + ((long)b * H + g * R) * D, D, x * SCOL, red);
+    const long pe = a.pos - W, rg = ((long)b * W + slot) * G + g;
+    T* RKs = reinterpret_cast<T*>(a.ring_k) + (bg * W + slot) * D;
+    T* RVs = reinterpret_cast<T*>(a.ring_v) + (bg * W + slot) * D;
+    float* KM = a.ring_km + rg * D;
+    float* ev = a.ws_ev + bg * (2 * D + 4);
+    for (int d = tid; d < D; d += NT_DEC) {
+        const float vv = KV::to_f(RVs[d]), kk = KM[d];
+        ev[d] = vv;
+        ev[D + d] = kk;
+        RKs[d] = NK[d];
+        RVs[d] = NV[d];
+        KM[d] = a.km[bg * D + d];
+    }
+    if (tid == 0) {
+        const bool valid = pe >= 0 && a.ring_pos[slot] == pe;
+        ev[2 * D] = a.ring_g[rg];
+        ev[2 * D + 1] = a.ring_beta[rg];
+        ev[2 * D + 2] = valid ? 1.f : 0.f;
+        a.ring_g[rg] = a.g_new[bg];
+        a.ring_beta[rg] = a.beta_new[bg];
+    }
 }
 
-// Merge of the window splits for query head r of (b, g): one output dimension per thread; the split statistics are
-// read once into LDS. Then the gamma mix and, by the r == 0 block, the ring write of the new token.
-template <class KV, int D>
-__global__ __launch_bounds__(NT_DEC) void decode_combine_kernel(DecodeArgs a) {
-    using T = typename KV::T;
-    constexpr int MAXS = 64;                            // window splits held in LDS (W <= 32768)
-    __shared__ float fs[MAXS];
-    __shared__ float stat[2];
-    const int r = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+// After the window splits: state slab x (SCOL columns) of (b, g) and the output dims of those columns.
+//  - memory on: the write of the ring row that left the window (from ws_ev), then the memory read of the R query
+//    heads for the slab's columns (into ws_om);
+//  - the merge of the window splits for the slab's dims and every query head, the gamma mix, o and lse;
+//  - the ring_pos entry of the new token (its values were written by split 0 of the window kernel).
+template <class KV, int D, int RM>
+__global__ __launch_bounds__(NT_DEC) void decode_tail_kernel(DecodeArgs a) {
+    constexpr int MAXS = 64;                            // window splits held in LDS (W <= 65536)
+    __shared__ float red[4 * SCG * RM * 4];
+    __shared__ float fs[RM][MAXS];
+    __shared__ float st2[RM][2];
+    const int x = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
     const int G = a.G, R = a.R, H = G * R, W = a.W, NS = a.nsplit;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const long bg = (long)b * G + g;
-    const int h = g * R + r;
+    const int j0 = x * SCOL;
+    float* om = a.ws_om + ((long)b * H + g * R) * D;
+    if (a.mem_on) {
+        const float* ev = a.ws_ev + bg * (2 * D + 4);
+        const bool valid = ev[2 * D + 2] != 0.f;
+        const float wg = valid ? ev[2 * D] : 0.f, wb = valid ? ev[2 * D + 1] : 0.f;
+        float* S = a.state + bg * D * D;
+        state_slab<D, RM>(S, S, ev + D, ev, wg, wb, valid, a.qm + ((long)b * H + g * R) * D, R, D, om, D, j0, red);
+    }
+    // split statistics per head (wave w takes heads w, w + 4): M = max m_s, f_s = e^{m_s - M}, L = sum f_s l_s
     const float* part = a.ws_part + bg * NS * R * (D + 2);
-    if (tid < 64) {
-        // wave 0: M = max over splits, f_s = e^{m_s - M}, L = sum f_s l_s
-        const float ms = tid < NS ? part[(tid * R + r) * (D + 2)] : -INFINITY;
-        const float ls = tid < NS ? part[(tid * R + r) * (D + 2) + 1] : 0.f;
+    for (int r = wv; r < R; r += NT_DEC / 64) {
+        const float ms = lane < NS ? part[(lane * R + r) * (D + 2)] : -INFINITY;
+        const float ls = lane < NS ? part[(lane * R + r) * (D + 2) + 1] : 0.f;
         float M = ms;
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, __shfl_xor(M, off));
@@ -490,44 +500,27 @@ __global__ __launch_bounds__(NT_DEC) void decode_combine_kernel(DecodeArgs a) {
         float L = f * ls;
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) L += __shfl_xor(L, off);
-        if (tid < NS) fs[tid] = f;
-        if (tid == 0) { stat[0] = M; stat[1] = L; }
+        if (lane < NS) fs[r][lane] = f;
+        if (lane == 0) { st2[r][0] = M; st2[r][1] = L; }
     }
-    __syncthreads();
-    const float M = stat[0], L = stat[1];
-    const float lse = M + logf(L);
+    __syncthreads();                                    // also orders the slab's om stores before their reads below
     const float lnW = logf((float)W);
-    for (int d = tid; d < D; d += NT_DEC) {
+    for (int i = tid; i < R * SCOL; i += NT_DEC) {
+        const int r = i / SCOL, d = j0 + i % SCOL, h = g * R + r;
+        const float M = st2[r][0], L = st2[r][1];
         float ow = 0.f;
-        for (int s_ = 0; s_ < NS; ++s_) ow += fs[s_] * part[(s_ * R + r) * (D + 2) + 2 + d];
+        for (int s_ = 0; s_ < NS; ++s_) ow += fs[r][s_] * part[(s_ * R + r) * (D + 2) + 2 + d];
         ow /= L;
+        const float lse = M + logf(L);
         float o = ow;
         if (a.mem_on) {
             const float gam = 1.f / (1.f + __expf(-(a.z[(long)b * H + h] + a.mix_lse[h] * (lse - lnW))));
-            const float om = a.ws_om[((long)b * H + h) * D + d];
-            o = ow + gam * (a.mem_scale[h] * om - ow);
+            o = ow + gam * (a.mem_scale[h] * om[r * D + d] - ow);
         }
         a.o[((long)b * H + h) * D + d] = o;
+        if (x == 0 && i % SCOL == 0 && a.lse) a.lse[(long)b * H + h] = lse;
     }
-    if (tid == 0 && a.lse) a.lse[(long)b * H + h] = lse;
-    if (r != 0) return;
-    // cache write: slot pos mod W <- (kr, v, km, g, beta, pos)
-    const int slot = (int)(a.pos % W);
-    T* RK = reinterpret_cast<T*>(a.ring_k) + (bg * W + slot) * D;
-    T* RV = reinterpret_cast<T*>(a.ring_v) + (bg * W + slot) * D;
-    const T* NK = reinterpret_cast<const T*>(a.kr) + bg * D;
-    const T* NV = reinterpret_cast<const T*>(a.v) + bg * D;
-    float* KM = a.ring_km + (((long)b * W + slot) * G + g) * D;
-    for (int d = tid; d < D; d += NT_DEC) {
-        RK[d] = NK[d];
-        RV[d] = NV[d];
-        KM[d] = a.km[bg * D + d];
-    }
-    if (tid == 0) {
-        a.ring_g[((long)b * W + slot) * G + g] = a.g_new[bg];
-        a.ring_beta[((long)b * W + slot) * G + g] = a.beta_new[bg];
-        if (b == 0 && g == 0) a.ring_pos[slot] = a.pos;
-    }
+    if (x == 0 && b == 0 && g == 0 && tid == 0) a.ring_pos[(int)(a.pos % W)] = a.pos;
 }
 
 // ----------------------------------------------------------------------------------------------- single-token GDN
@@ -546,15 +539,11 @@ template <class KV, int D>
 static int launch_decode(const DecodeArgs& a, hipStream_t stream) {
     if (a.nsplit > 64) return BF_STATUS_UNSUPPORTED;
     hipError_t e;
-    if (a.mem_on) {
-        if (a.R <= 4) hipLaunchKernelGGL((decode_slab_kernel<KV, D, 4>), dim3(D / SCOL, a.G, a.B), dim3(NT_DEC), 0, stream, a);
-        else hipLaunchKernelGGL((decode_slab_kernel<KV, D, 8>), dim3(D / SCOL, a.G, a.B), dim3(NT_DEC), 0, stream, a);
-        if ((e = hipGetLastError()) != hipSuccess) return (int)e;
-    }
     if (a.R <= 4) hipLaunchKernelGGL((decode_main_kernel<KV, D, 4>), dim3(a.nsplit, a.G, a.B), dim3(NT_DEC), 0, stream, a);
     else hipLaunchKernelGGL((decode_main_kernel<KV, D, 8>), dim3(a.nsplit, a.G, a.B), dim3(NT_DEC), 0, stream, a);
     if ((e = hipGetLastError()) != hipSuccess) return (int)e;
-    hipLaunchKernelGGL((decode_combine_kernel<KV, D>), dim3(a.R, a.G, a.B), dim3(NT_DEC), 0, stream, a);
+    if (a.R <= 4) hipLaunchKernelGGL((decode_tail_kernel<KV, D, 4>), dim3(D / SCOL, a.G, a.B), dim3(NT_DEC), 0, stream, a);
+    else hipLaunchKernelGGL((decode_tail_kernel<KV, D, 8>), dim3(D / SCOL, a.G, a.B), dim3(NT_DEC), 0, stream, a);
     e = hipGetLastError();
     return e == hipSuccess ? 0 : (int)e;
 }

@@ -687,7 +687,19 @@ __global__ __launch_bounds__(BW_NT) void chunk_final_kernel(GdnBwdArgs a) {
     const long q4 = (long)D * D / 16;                     // this quarter's 16-byte pieces of S and dS'
     const float4* S4 = reinterpret_cast<const float4*>(a.Sc + cg * D * D) + z * q4;
     const float4* X4 = reinterpret_cast<const float4*>(a.dSx + cg * D * D) + z * q4;
-    for (long e = tid; e < q4; e += BW_NT) {
+    // four iterations' loads issued together over the whole multiples of 4 BW_NT, then the rest one at a time
+    const long q4u = q4 - q4 % (4 * BW_NT);
+    for (long e = tid; e < q4u; e += 4 * BW_NT) {
+        float4 x[4], y[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            x[u] = S4[e + u * BW_NT];
+            y[u] = X4[e + u * BW_NT];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) sdot += (x[u].x * y[u].x + x[u].y * y[u].y) + (x[u].z * y[u].z + x[u].w * y[u].w);
+    }
+    for (long e = q4u + tid; e < q4; e += BW_NT) {
         const float4 x = S4[e], y = X4[e];
         sdot += (x.x * y.x + x.y * y.y) + (x.z * y.z + x.w * y.w);
     }

@@ -105,6 +105,27 @@ def test_decode_steps_match_oracle_fp32(dev, prefill):
     compare_caches(c_ref, c_gpu, TOL_F32)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_decode_steps_eight_heads_per_kv_D128(dev, dtype):
+    """Eight query heads per KV head (the R > 4 instance of the decode kernels), D = 128, two sequences: 40 steps from
+    an empty cache (the memory switches on at the window, the ring wraps twice) against the oracle; outputs and the
+    whole cache must agree (fp32 to 1e-4; bf16 activations against the fp32 oracle on the same bf16 values)."""
+    from heimdall_amd import hibrit
+    print(f"decode {dtype} B=2 H=16 G=2 D=128 W=16 S=2, 40 steps", flush=True)
+    m = make_core(16, 2, 128, 32, window=16, sinks=2)
+    mg = make_core(16, 2, 128, 32, window=16, sinks=2).to(dev)
+    args = make_inputs(m, 2, 40, seed=9, dtype=dtype)
+    ref_args = tuple(z.float() for z in args)
+    tol = TOL_F32 if dtype == torch.float32 else TOL_BF16
+    c_ref, c_gpu = {}, {}
+    with torch.no_grad():
+        for p in range(40):
+            o_ref = olayer.student(m, *split(ref_args, p, p + 1), p, c_ref)
+            o = hibrit.student(mg, *to_dev(split(args, p, p + 1), dev), p, c_gpu)
+            assert rel(o, o_ref) < tol, (p, rel(o, o_ref))
+    compare_caches(c_ref, c_gpu, tol)
+
+
 def test_decode_full_size_bf16(dev):
     """B=64 sequences, H=16, G=4, D=256, W=2048 + 4 sinks, bf16 ring, fp32 state ~ N(0, 0.02), one step at a
     position far past the window (memory active, ring full)."""

@@ -209,7 +209,7 @@ struct GdnBwdArgs {
     float *dq, *dk, *dv, *dg, *dbeta, *ds0;
     // workspace, chunk-major [chunk][g][...] (cg = chunk * G + g)
     float *gam, *eg, *dgz, *Am, *Mi, *dA, *kb, *vb, *kbe, *ktl, *ktlF, *ktlTF, *u, *w, *wF, *wTF, *attn, *dattn, *qdot, *zr, *zc, *zrA, *zcA;
-    float *Sc, *E2, *dSx, *part;
+    float *Sc, *E2, *dSx, *part, *psd;
     float *E1, *dvn, *vn, *dkt, *dw, *dvb, *dkbe, *dkb, *dkacc;
 };
 size_t gdn_bwd_workspace(int num_seqs, long T, int G, int R, int D);

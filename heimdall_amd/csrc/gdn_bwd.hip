@@ -15,9 +15,9 @@
 //
 // Kernels: bgemm_kernel (batched strided fp32 GEMM on v_mfma_f32_16x16x4f32, optional triangular mask, addend and
 // accumulate, in-chunk decay, row scale and row / column dots in the epilogue), chunk_prep_kernel,
-// unit_lower_inverse_kernel, walk_fwd_kernel / walk_bwd_kernel (the two state walks), chunk_final_kernel,
-// dg_scan_kernel. The host side runs the forward walk and the products that need only its states on a second stream,
-// beside the reverse walk and its products.
+// unit_lower_inverse_kernel, walk_fwd_kernel / walk_bwd_kernel (the two state walks), state_dot_kernel,
+// chunk_final_kernel, dg_scan_kernel. The host side runs the forward walk, the products that need only its states and
+// the state dot on a second stream, beside the reverse walk and its products.
 #include <array>
 #include <mutex>
 
@@ -682,27 +682,7 @@ __global__ __launch_bounds__(BW_NT) void chunk_final_kernel(GdnBwdArgs a) {
     __shared__ float gc[BC], red[BW_NT / 64];
     if (tid < BC) gc[tid] = a.gam[cg * BC + tid];
     __syncthreads();
-    const float gl = gc[BC - 1], ec = expf(gl);
-    float sdot = 0.f;
-    const long q4 = (long)D * D / 16;                     // this quarter's 16-byte pieces of S and dS'
-    const float4* S4 = reinterpret_cast<const float4*>(a.Sc + cg * D * D) + z * q4;
-    const float4* X4 = reinterpret_cast<const float4*>(a.dSx + cg * D * D) + z * q4;
-    // four iterations' loads issued together over the whole multiples of 4 BW_NT, then the rest one at a time
-    const long q4u = q4 - q4 % (4 * BW_NT);
-    for (long e = tid; e < q4u; e += 4 * BW_NT) {
-        float4 x[4], y[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            x[u] = S4[e + u * BW_NT];
-            y[u] = X4[e + u * BW_NT];
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) sdot += (x[u].x * y[u].x + x[u].y * y[u].y) + (x[u].z * y[u].z + x[u].w * y[u].w);
-    }
-    for (long e = q4u + tid; e < q4; e += BW_NT) {
-        const float4 x = S4[e], y = X4[e];
-        sdot += (x.x * y.x + x.y * y.y) + (x.z * y.z + x.w * y.w);
-    }
+    const float gl = gc[BC - 1];
     float ktsum = 0.f;
     for (int i = r0 + wv; i < r0 + 16; i += BW_NT / 64) {
         const long tok = bc * BC + i;
@@ -747,7 +727,7 @@ __global__ __launch_bounds__(BW_NT) void chunk_final_kernel(GdnBwdArgs a) {
             a.dbeta[tok * G + g] = dbi;
         }
     }
-    float t = sdot * ec + ktsum;
+    float t = ktsum;
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) t += __shfl_xor(t, off);
     if (lane == 0) red[wv] = t;
@@ -759,6 +739,45 @@ __global__ __launch_bounds__(BW_NT) void chunk_final_kernel(GdnBwdArgs a) {
     }
 }
 
+// grid (chunks, G, 4): the state path's share of the last row's d gc, e^(gc_C') <S, dS'>, over a quarter of the D x D
+// entries into psd[cg][z] (it needs only the two walks, so it runs beside the products that follow them)
+__global__ __launch_bounds__(BW_NT) void state_dot_kernel(GdnBwdArgs a) {
+    const long bc = blockIdx.x;
+    const int g = blockIdx.y, z = blockIdx.z, tid = threadIdx.x, lane = lane_id(), wv = wave_id();
+    const int D = a.D, G = a.G;
+    const long cg = bc * G + g;
+    __shared__ float red[BW_NT / 64];
+    float sdot = 0.f;
+    const long q4 = (long)D * D / 16;                     // this quarter's 16-byte pieces of S and dS'
+    const float4* S4 = reinterpret_cast<const float4*>(a.Sc + cg * D * D) + z * q4;
+    const float4* X4 = reinterpret_cast<const float4*>(a.dSx + cg * D * D) + z * q4;
+    // four iterations' loads issued together over the whole multiples of 4 BW_NT, then the rest one at a time
+    const long q4u = q4 - q4 % (4 * BW_NT);
+    for (long e = tid; e < q4u; e += 4 * BW_NT) {
+        float4 x[4], y[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            x[u] = S4[e + u * BW_NT];
+            y[u] = X4[e + u * BW_NT];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) sdot += (x[u].x * y[u].x + x[u].y * y[u].y) + (x[u].z * y[u].z + x[u].w * y[u].w);
+    }
+    for (long e = q4u + tid; e < q4; e += BW_NT) {
+        const float4 x = S4[e], y = X4[e];
+        sdot += (x.x * y.x + x.y * y.y) + (x.z * y.z + x.w * y.w);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sdot += __shfl_xor(sdot, off);
+    if (lane == 0) red[wv] = sdot;
+    __syncthreads();
+    if (tid == 0) {
+        float s_ = 0.f;
+        for (int w = 0; w < BW_NT / 64; ++w) s_ += red[w];
+        a.psd[cg * 4 + z] = s_ * expf(a.gam[cg * BC + BC - 1]);
+    }
+}
+
 // per (chunk, KV head), one wave: dg_j = sum_{i >= j} d gc_i (the last row with its extra terms)
 __global__ __launch_bounds__(64) void dg_scan_kernel(GdnBwdArgs a) {
     const long cg = blockIdx.x;
@@ -766,7 +785,9 @@ __global__ __launch_bounds__(64) void dg_scan_kernel(GdnBwdArgs a) {
     const long bc = cg / G;
     const int g = (int)(cg % G);
     float x = a.dgz[cg * BC + BC - 1 - tid];
-    if (tid == 0) x += a.part[cg * 4] + a.part[cg * 4 + 1] + a.part[cg * 4 + 2] + a.part[cg * 4 + 3];
+    if (tid == 0)
+        x += (a.part[cg * 4] + a.part[cg * 4 + 1]) + (a.part[cg * 4 + 2] + a.part[cg * 4 + 3]) +
+             (a.psd[cg * 4] + a.psd[cg * 4 + 1]) + (a.psd[cg * 4 + 2] + a.psd[cg * 4 + 3]);
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
         const float y = __shfl_up(x, off);
@@ -862,12 +883,12 @@ Op tr(Op o) { std::swap(o.rs, o.cs); return o; }
 constexpr int kBwdMaxDevices = 64;
 struct BwdSide {
     hipStream_t s = nullptr;
-    hipEvent_t ev[6] = {};
+    hipEvent_t ev[7] = {};
 };
 std::mutex g_bwd_mu;
 BwdSide g_bwd_side[kBwdMaxDevices];
 
-int side_stream(hipStream_t& s2, hipEvent_t (&ev)[6]) {
+int side_stream(hipStream_t& s2, hipEvent_t (&ev)[7]) {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return (int)e;
@@ -877,7 +898,7 @@ int side_stream(hipStream_t& s2, hipEvent_t (&ev)[6]) {
         if (!x && (e = hipEventCreateWithFlags(&x, hipEventDisableTiming)) != hipSuccess) return (int)e;
     if (!sd.s && (e = hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking)) != hipSuccess) return (int)e;
     s2 = sd.s;
-    for (int i = 0; i < 6; ++i) ev[i] = sd.ev[i];
+    for (int i = 0; i < 7; ++i) ev[i] = sd.ev[i];
     return 0;
 }
 
@@ -886,14 +907,14 @@ int side_stream(hipStream_t& s2, hipEvent_t (&ev)[6]) {
 size_t gdn_bwd_workspace(int num_seqs, long T, int G, int R, int D) {
     const long n = T / BC, NC = (long)num_seqs * n * G;             // chunk-heads
     const long cc = BC * BC, cd = (long)BC * D, dd = (long)D * D;
-    const long floats = NC * (BC * 5 + 4                             // gam, eg, dgz, zrA, zcA, part
+    const long floats = NC * (BC * 5 + 8                             // gam, eg, dgz, zrA, zcA, part, psd
                               + cc * 3                               // Am, M, dA
                               + cd * 10                              // kb, vb, kbe, ktl, u, w; ktl, kt^T, w, w^T in fragment order
                               + (long)R * (cc * 2 + (D / 64 + 2) * BC)   // attn, dattn; qdot, zr, zc
                               + dd * 3                               // Sc, E2, dSx
                               + cd * 9                               // E1, dvn, vn, dkt, dw, dvb, dkbe, dkb, dkacc
                               + cc * 2);                             // dM, T1
-    return (size_t)floats * sizeof(float) + 256 * 48;                // each buffer rounded up to 256 bytes
+    return (size_t)floats * sizeof(float) + 256 * 49;                // each buffer rounded up to 256 bytes
 }
 
 int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
@@ -907,7 +928,7 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
         p += ((count * (long)sizeof(float) + 255) / 256) * 256;
         return r;
     };
-    a.gam = take(NC * BC); a.eg = take(NC * BC); a.dgz = take(NC * BC); a.part = take(NC * 4);
+    a.gam = take(NC * BC); a.eg = take(NC * BC); a.dgz = take(NC * BC); a.part = take(NC * 4); a.psd = take(NC * 4);
     a.Am = take(NC * cc); a.Mi = take(NC * cc); a.dA = take(NC * cc);
     a.zrA = take(NC * BC); a.zcA = take(NC * BC); a.zr = take(NC * R * BC); a.zc = take(NC * R * BC);
     a.kb = take(NC * cd); a.vb = take(NC * cd); a.kbe = take(NC * cd); a.ktl = take(NC * cd);
@@ -936,7 +957,7 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
     const int nzg = (int)NC, nzr = (int)(NC * R);
 
     hipStream_t s2 = nullptr;
-    hipEvent_t ev[6] = {};
+    hipEvent_t ev[7] = {};
     ok(side_stream(s2, ev));
     if (e) return e;
     // prep
@@ -1007,7 +1028,6 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
     // dq_r += s dattn_r k
     ok(gemm(BC, D, BC, nzr, G, R, WR(a.dattn, BC, BC), Op{a.k, (long)BC * G * D, D, 0, (long)G * D, 1}, a.dq,
             (long)BC * H * D, (long)R * D, D, (long)H * D, 1, a.scale, 1, 0, nullptr, s2));
-    ok((int)hipEventRecord(ev[3], s2));                    // dattn, dq, qdot, zr, zc
 
     // E1 = sum_r attn_r^T dO_r [C x D], E2 = sum_r qd_r^T dO_r = s sum_r q_r^T diag(e^gc) dO_r [D x D]: one product
     // each over K = R C, the (r, token) pairs, read from the token-major q and dO (k = 64 r + i: token stride H D,
@@ -1019,6 +1039,13 @@ int gdn_bwd(GdnBwdArgs a, void* ws, hipStream_t s) {
     rq.shift = 6; rq.a = D; rq.b = D; rq.ksc = a.eg; rq.s0 = (long)G * BC; rq.s1 = BC;   // A = q^T, columns e^gc
     ok(gemm(D, D, R * BC, nzg, G, 1, tr(qk), dOk, a.E2, (long)G * dd, dd, 0, D, 1, a.scale, 0, 0, nullptr, s, rq));
     walk(false, s);
+    // Side stream, after its products: the state path's d gc share, e^(gc_C') <S, dS'>, once the reverse walk has
+    // written dS' (enqueued here, after that walk's record, so the wait binds to this call's walk)
+    ok((int)hipEventRecord(ev[6], s));                     // dS'
+    ok((int)hipStreamWaitEvent(s2, ev[6], 0));
+    hipLaunchKernelGGL(state_dot_kernel, dim3((unsigned)NB, G, 4), dim3(BW_NT), 0, s2, a);
+    ok((int)hipGetLastError());
+    ok((int)hipEventRecord(ev[3], s2));                    // dattn, dq, qdot, zr, zc, psd
     // d(v b) = M^T dvn
     ok(gemm(BC, D, BC, nzg, G, 1, tr(W(a.Mi, BC, BC)), W(a.dvn, BC, D), a.dvb, (long)G * cd, cd, 0, D, 1, 1.f, 0, 0,
             nullptr, s));

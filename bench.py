@@ -345,9 +345,13 @@ def run_varlen(steps, warmup, dev):
     ms = e0.elapsed_time(e1) / steps
     flops = reference_flops(N, H, D)
     nbytes = gdn_bytes(N, H, D) - H * D * D * 4 + len(lens) * H * D * D * 4
+    gbs = nbytes / (ms * 1e-3) / 1e9
     return {"workload": "varlen gated delta rule, 4 seqs {8192,16384,24576,16384}, H=32, D=128, bf16",
             "ms_per_step": ms, "tokens_per_s": N / (ms * 1e-3), "steps": steps,
-            "tflops_reference": flops / (ms * 1e-3) / 1e12, "GBs": nbytes / (ms * 1e-3) / 1e9}
+            "tflops_reference": flops / (ms * 1e-3) / 1e12, "GBs": gbs,
+            "roofline": {"bound": "hbm", "kernel": "bf_gdn_fwd varlen (prep, summary, combine, output)",
+                         "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS,
+                         "algorithmic_bytes": nbytes}}
 
 
 def run_gdn_layer(steps, warmup, dev):
@@ -632,7 +636,7 @@ def run_llama_state(steps, warmup, dev):
                          "frac": res["pack"]["frac"], "kernel": "bf_llama_state_pack (region, V plane, delta kernels)"}}
 
 
-LAYER_GEOM = dict(B=1, H=24, G=4, D=256, W=2048, S=4)
+LAYER_GEOM = dict(B=1, H=24, G=4, D=256, W=2048, S=4, d=5120)   # d: the target model's hidden size
 LIVES = (2048.0, 45255.0, 1e6, None)        # decay half-lives of KV heads 0-2 in tokens; head 3 archival
 
 
@@ -651,14 +655,15 @@ def layer_flops(T, H, G, D, W, S):
     return {"window": win, "memory": mem, "projections": proj, "total": win + mem + proj}
 
 
-def layer_core(H, G, D, W, S, lives, dev):
-    """A converted core whose gates reproduce the workload's distributions through its own parameters: d_model =
-    G + H with x = [z_beta | z_gamma]; ab selects z_beta for the write strengths (the decay logits are 0), mix selects
-    z_gamma (mix_lse = 0), so beta = sigmoid(z_beta) and gamma = sigmoid(z_gamma); fq = fk = I; mem_scale = sqrt(D);
+def layer_core(H, G, D, W, S, lives, dev, d=None):
+    """A converted core whose gates reproduce the workload's distributions through its own parameters: x [.., d] with
+    columns [z_beta (G) | z_gamma (H) | the rest]; ab selects z_beta for the write strengths (the decay logits are 0),
+    mix selects z_gamma (mix_lse = 0), so beta = sigmoid(z_beta) and gamma = sigmoid(z_gamma), with zero weights on
+    the other d - G - H columns (the projections still read all d of them); fq = fk = I; mem_scale = sqrt(D);
     constant log-decay -ln2 / life per KV head (decay_mask 0 where life is None: the archival head)."""
     import math
     from heimdall_amd import hibrit
-    m = hibrit.BifrostCore(hibrit.CoreConfig(H, G, D, G + H))
+    m = hibrit.BifrostCore(hibrit.CoreConfig(H, G, D, d if d else G + H))
     m.convert(W, S, 0)
     with torch.no_grad():
         m.ab.weight.zero_()
@@ -666,7 +671,7 @@ def layer_core(H, G, D, W, S, lives, dev):
         m.ab.weight[G:, :G] = torch.eye(G)
         m.mix.weight.zero_()
         m.mix.bias.zero_()
-        m.mix.weight[:, G:] = torch.eye(H)
+        m.mix.weight[:, G:G + H] = torch.eye(H)
         sp = F.softplus(m.dt_bias)
         for h, life in enumerate(lives):
             if life is not None:
@@ -675,22 +680,24 @@ def layer_core(H, G, D, W, S, lives, dev):
     return m.to(dev)
 
 
-def layer_inputs(B, T, H, G, D, dev, seed=2):
-    """q, k ~ N(0,1) L2-normalised per head, v ~ N(0,1) (bf16), z_beta, z_gamma ~ N(0,1); qr = q, kr = k (the window
-    reads the same unit vectors; no rotary part)."""
+def layer_inputs(B, T, H, G, D, dev, seed=2, d=None):
+    """q, k ~ N(0,1) L2-normalised per head, v ~ N(0,1) (bf16); x ~ N(0,1) [B, T, d] in bf16, whose first G + H
+    columns are z_beta, z_gamma (d = G + H without the rest, fp32, when d is None); qr = q, kr = k (the window reads
+    the same unit vectors; no rotary part)."""
     gen = torch.Generator(device=dev).manual_seed(seed)
     rn = lambda *shape: torch.randn(*shape, device=dev, generator=gen)
     q = F.normalize(rn(B, T, H, D), dim=-1).bfloat16()
     k = F.normalize(rn(B, T, G, D), dim=-1).bfloat16()
     v = rn(B, T, G, D).bfloat16()
-    x = torch.cat((rn(B, T, G), rn(B, T, H)), -1)
+    x = rn(B, T, d).bfloat16() if d else torch.cat((rn(B, T, G), rn(B, T, H)), -1)
     return x, q, k, v, q.transpose(1, 2).contiguous(), k.transpose(1, 2).contiguous()
 
 
-def time_window_in_layer(m, args, steps, warmup, dev):
+def time_window_in_layer(m, args, steps, warmup, dev, start=0, cache=None):
     """The window kernel with the arguments the layer call gives it (bf16 operands with their layer strides, the
-    first S tokens as sinks, the empty ring, the gamma mix against a bf16 memory read, fp32 output): the average
-    launch duration over `steps` launches, HIP events on the launch stream."""
+    first S tokens as sinks, the ring, the gamma mix against a bf16 memory read, fp32 output): the average launch
+    duration over `steps` launches, HIP events on the launch stream. From an empty cache (start 0) the ring is empty;
+    otherwise `args` is the chunk at position `start` and `cache` the student cache before it (ring and sinks)."""
     from heimdall_amd import _lib
     from heimdall_amd._device import stream_ptr
 
@@ -698,18 +705,23 @@ def time_window_in_layer(m, args, steps, warmup, dev):
     B, T, H, D = q.shape
     G = k.shape[2]
     W, S = m.window, m.sinks
-    sk, sv = kr[:, :, :S].contiguous(), v.transpose(1, 2)[:, :, :S].contiguous()
-    ring_k = torch.zeros(B, G, W, D, dtype=torch.bfloat16, device=dev)
-    ring_v = torch.zeros_like(ring_k)
-    ring_pos = torch.full((W,), -1, dtype=torch.long, device=dev)
+    if cache is None:
+        sk, sv = kr[:, :, :S].contiguous(), v.transpose(1, 2)[:, :, :S].contiguous()
+        ring_k = torch.zeros(B, G, W, D, dtype=torch.bfloat16, device=dev)
+        ring_v = torch.zeros_like(ring_k)
+        ring_pos = torch.full((W,), -1, dtype=torch.long, device=dev)
+    else:
+        sk, sv = cache["sink_k"].contiguous(), cache["sink_v"].contiguous()
+        ring_k, ring_v, ring_pos = cache["ring_k"], cache["ring_v"], cache["ring_pos"]
     gen = torch.Generator(device=dev).manual_seed(9)
     o_mem = torch.randn(B, T, H, D, device=dev, generator=gen).bfloat16()
-    z = F.linear(x, m.mix.weight, m.mix.bias).contiguous()
+    from heimdall_amd import hibrit
+    z = hibrit._gate_logits(m, x)[1]
     mix_lse, mem_scale = m.mix_lse.detach().float().contiguous(), m.mem_scale.detach().float().contiguous()
     o = torch.empty(B, T, H, D, dtype=torch.float32, device=dev)
     lib = _lib.load()
     st = lambda t_, dims: tuple(int(t_.stride(i)) for i in dims)
-    wargs = (B, G, H // G, D, T, W, S, 0, _lib.DTYPE_BF16, qr.data_ptr(), *st(qr, (0, 1, 2)), kr.data_ptr(),
+    wargs = (B, G, H // G, D, T, W, S, start, _lib.DTYPE_BF16, qr.data_ptr(), *st(qr, (0, 1, 2)), kr.data_ptr(),
              *st(kr, (0, 1, 2)), v.data_ptr(), *st(v, (0, 2, 1)), ring_k.data_ptr(), ring_v.data_ptr(),
              ring_pos.data_ptr(), sk.data_ptr(), sv.data_ptr(), S, 1, o_mem.data_ptr(), _lib.DTYPE_BF16, z.data_ptr(),
              mix_lse.data_ptr(), mem_scale.data_ptr(), o.data_ptr(), _lib.DTYPE_F32, None, stream_ptr(dev))
@@ -735,9 +747,9 @@ def run_layer(steps, warmup, dev, T=32768, window_pass=True):
     from heimdall_amd import hibrit
 
     g_ = LAYER_GEOM
-    B, H, G, D, W, S = g_["B"], g_["H"], g_["G"], g_["D"], g_["W"], g_["S"]
-    m = layer_core(H, G, D, W, S, LIVES, dev)
-    args = layer_inputs(B, T, H, G, D, dev)
+    B, H, G, D, W, S, d = g_["B"], g_["H"], g_["G"], g_["D"], g_["W"], g_["S"], g_["d"]
+    m = layer_core(H, G, D, W, S, LIVES, dev, d)
+    args = layer_inputs(B, T, H, G, D, dev, d=d)
     with torch.no_grad():
         for _ in range(warmup):
             hibrit.student(m, *args, 0, {})
@@ -749,7 +761,8 @@ def run_layer(steps, warmup, dev, T=32768, window_pass=True):
         wall = time.perf_counter() - t0
     ms = wall * 1e3 / steps
     fl = layer_flops(T, H, G, D, W, S)
-    out = {"workload": f"layer prefill B={B} T={T} H={H} G={G} D={D} W={W}+{S} bf16 activations, fp32 state",
+    out = {"workload": f"layer prefill B={B} T={T} H={H} G={G} D={D} W={W}+{S} d_model={d} bf16 activations, "
+                       f"fp32 state",
            "T": T, "ms_per_step": ms, "tokens_per_s": T / (ms * 1e-3), "steps": steps, "flops": fl,
            "tflops": fl["total"] / (ms * 1e-3) / 1e12,
            "mfma_frac_whole_call": fl["total"] / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
@@ -792,6 +805,95 @@ def cpu_layer(m, args, budget_s=40.0):
                       f"{cpu_model()}"}
 
 
+def run_layer_chunked(dev, T=32768, chunk=2048, reps=3, window_pass=True):
+    """The layer driven the way the reference's HybridLM.prefill drives it (Heimdall/heimdall/hibrit.py:718-734): T
+    tokens as T / 2048 student calls through the cache, each at its own position (the headline's core and inputs,
+    d_model 5120, bf16). Timed: whole prefills (every chunk call) bracketed by device synchronisation, `reps` of them
+    after one warm-up. The dominant kernel is timed alone on a chunk in the steady state: 2048 queries at position
+    T - 2048 over a full ring, HIP events on the launch stream."""
+    from heimdall_amd import hibrit
+
+    g_ = LAYER_GEOM
+    B, H, G, D, W, S, d = g_["B"], g_["H"], g_["G"], g_["D"], g_["W"], g_["S"], g_["d"]
+    m = layer_core(H, G, D, W, S, LIVES, dev, d)
+    args = layer_inputs(B, T, H, G, D, dev, d=d)
+    sl = lambda a, e: (args[0][:, a:e], args[1][:, a:e], args[2][:, a:e], args[3][:, a:e], args[4][:, :, a:e],
+                       args[5][:, :, a:e])
+
+    def prefill(upto=T):
+        cache = {}
+        for a in range(0, upto, chunk):
+            hibrit.student(m, *sl(a, min(a + chunk, upto)), a, cache)
+        return cache
+
+    with torch.no_grad():
+        prefill()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            prefill()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / reps
+    fl = layer_flops(T, H, G, D, W, S)
+    out = {"workload": f"layer prefill as {T // chunk} calls of {chunk} tokens through the cache, B={B} T={T} H={H} "
+                       f"G={G} D={D} W={W}+{S} d_model={d} bf16",
+           "T": T, "chunk": chunk, "ms_per_prefill": ms, "tokens_per_s": T / (ms * 1e-3), "reps": reps,
+           "ms_per_chunk_call": ms / (T // chunk), "flops": fl["total"],
+           "mfma_frac_whole_prefill": fl["total"] / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
+    if window_pass:
+        with torch.no_grad():
+            p0 = T - chunk
+            cache = prefill(p0)
+            us = time_window_in_layer(m, sl(p0, T), 20, 3, dev, start=p0, cache=cache)
+        wfl = 4 * D * H * chunk * (W + S)
+        tf = wfl / (us * 1e-6) / 1e12
+        out["roofline"] = {"bound": "mfma", "kernel": "window_fa_kernel<256>, 2048 queries over a full ring",
+                           "achieved": tf, "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": tf / BF16_PEAK_TFLOPS,
+                           "launch_us": us, "flops_per_launch": wfl}
+    return out
+
+
+def run_mtp_verify(dev, P=32768, steps=200, warmup=20):
+    """The MTP verification step of the reference's generate (Heimdall/heimdall/hibrit.py:758-771): after a prefill of
+    P tokens, the layer's student call on t = 2 tokens (the last token and the draft) at the current position, B = 1,
+    each step two positions further (an accepted draft); next to it, the plain decode step t = 1. The headline's core
+    (H=24, G=4, D=256, W=2048 + 4, d_model 5120, bf16). Timed with HIP events over `steps` calls; the cache snapshot
+    the reference takes before each verify is not included."""
+    from heimdall_amd import hibrit
+
+    g_ = LAYER_GEOM
+    B, H, G, D, W, S, d = g_["B"], g_["H"], g_["G"], g_["D"], g_["W"], g_["S"], g_["d"]
+    m = layer_core(H, G, D, W, S, LIVES, dev, d)
+    n = P + 2 * (steps + warmup) + 2
+    args = layer_inputs(B, n, H, G, D, dev, d=d)
+    sl = lambda a, e: (args[0][:, a:e], args[1][:, a:e], args[2][:, a:e], args[3][:, a:e], args[4][:, :, a:e],
+                       args[5][:, :, a:e])
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+    with torch.no_grad():
+        for t in (2, 1):
+            cache = {}
+            for a in range(0, P, 2048):
+                hibrit.student(m, *sl(a, a + 2048), a, cache)
+            p = P
+            for _ in range(warmup):
+                hibrit.student(m, *sl(p, p + t), p, cache)
+                p += t
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(steps):
+                hibrit.student(m, *sl(p, p + t), p, cache)
+                p += t
+            e1.record(stream)
+            torch.cuda.synchronize()
+            res[t] = e0.elapsed_time(e1) * 1e3 / steps
+    return {"workload": f"MTP verify: layer student call with t=2 at position {P}+, B=1 H={H} G={G} D={D} W={W}+{S} "
+                        f"d_model={d} bf16 (decode t=1 beside it)",
+            "us_per_verify_step": res[2], "us_per_decode_step": res[1], "steps": steps,
+            "tokens_per_s_verify_accepted": 2 / (res[2] * 1e-6)}
+
+
 def gdn_leg(steps, warmup, dev, cpu):
     """Standalone chunked delta-rule prefill (B=1, T=32768, H=4, D=256, bf16 q/k/v, fp32 state and output), priced
     as an HBM-bound pass over its algorithmic bytes (bf16 q, k, v; fp32 g, beta, o, final state) and, for its
@@ -825,9 +927,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--no-extra", action="store_true", help="the headline only (no secondary legs)")
-    ap.add_argument("--copy-probe", action="store_true", help="run one 256 MiB device copy first (counter scaling)")
-    ap.add_argument("--only", choices=("layer", "layer131k", "gdn", "decode", "varlen", "gdn_layer", "teacher",
-                                       "teacher_decode", "teacher_decode_full", "gdn_bwd", "llama_state"),
+    ap.add_argument("--calib", action="store_true",
+                    help="first run a 1 GiB read-only pass (torch sum) and a 1 GiB write-only pass (torch fill), the "
+                         "known-size kernels that scale the FETCH_SIZE / WRITE_SIZE counters of a profiling run")
+    ap.add_argument("--only", choices=("layer", "layer131k", "layer_chunked", "layer_chunked131k", "mtp_verify", "gdn",
+                                       "decode", "varlen", "gdn_layer", "teacher", "teacher_decode",
+                                       "teacher_decode_full", "gdn_bwd", "llama_state"),
                     default=None,
                     help="run one secondary leg alone and print its JSON object (for per-workload profiling)")
     args = ap.parse_args()
@@ -837,17 +942,21 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    if args.copy_probe:
-        # a plain copy of known size, so HBM byte counters of a profiling run can be scaled (read and write 256 MiB)
-        src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
-        dst = torch.empty_like(src)
-        dst.copy_(src)
+    if args.calib:
+        # counter calibration: 1 GiB read once (a sum) and 1 GiB written once (a fill), four times the 256 MB
+        # last-level cache, so neither pass can be served from it; the first two GPU kernels of the run
+        buf = torch.empty(256 << 20, dtype=torch.float32, device=dev)
+        buf.sum()
+        buf.fill_(1.0)
         torch.cuda.synchronize()
-        del src, dst
+        del buf
 
     if args.only:
         leg = {"layer": lambda: run_layer(args.steps, args.warmup, dev)[0],
                "layer131k": lambda: run_layer(args.steps, args.warmup, dev, T=131072)[0],
+               "layer_chunked": lambda: run_layer_chunked(dev),
+               "layer_chunked131k": lambda: run_layer_chunked(dev, T=131072, reps=1),
+               "mtp_verify": lambda: run_mtp_verify(dev),
                "gdn": lambda: gdn_leg(args.steps, args.warmup, dev, not args.no_cpu),
                "decode": lambda: run_decode(args.steps, args.warmup, dev),
                "varlen": lambda: run_varlen(args.steps, args.warmup, dev),
@@ -876,7 +985,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "layer_prefill", "B": g_["B"], "T": r["T"], "H": g_["H"], "G": g_["G"],
-                   "D": g_["D"], "window": g_["W"], "sinks": g_["S"], "chunk": C,
+                   "D": g_["D"], "window": g_["W"], "sinks": g_["S"], "chunk": C, "d_model": g_["d"],
                    "inputs": "bf16 activations, fp32 delta-rule state, decay half-lives 2048/45255/1e6 + archival",
                    "parallelism": "single GPU"},
         "roofline": r["roofline"],
@@ -887,6 +996,9 @@ def main():
     if not args.no_extra:
         r131, _ = run_layer(3, 1, dev, T=131072, window_pass=False)
         line["layer_prefill_131k"] = r131
+        line["layer_chunked"] = run_layer_chunked(dev)
+        line["layer_chunked_131k"] = run_layer_chunked(dev, T=131072, reps=1, window_pass=False)
+        line["mtp_verify"] = run_mtp_verify(dev)
         line["gdn_prefill"] = gdn_leg(args.steps, args.warmup, dev, not args.no_cpu)
         line["decode"] = run_decode(200, 100, dev)
         line["varlen_gdn"] = run_varlen(10, 3, dev)

@@ -55,8 +55,10 @@ int gdn_output(const GdnArgs& a, hipStream_t stream);
 
 struct DecodeArgs {
     int B, G, R, D, W, sinks;
-    long pos;                 // absolute position of the new token (same for all sequences)
-    int mem_on;               // memory branch active: pos >= W and memory enabled
+    long pos;                 // absolute position of the new token (same for all sequences; pos_arr == null)
+    const int64_t* pos_arr;   // [B] positions of the sequences (device), or null: one position for all
+    int mem_on;               // shared position: memory branch active (pos >= W and memory enabled); with pos_arr:
+                              // memory enabled (sequence b's branch is active when pos_arr[b] >= W)
     int kv_dtype, q_dtype;
     const void* qr;           // [B][H][D] q_dtype
     const float* qm;          // [B][H][D]
@@ -68,25 +70,40 @@ struct DecodeArgs {
     const float* z;           // [B][H] mix logits
     const float* mix_lse;     // [H]
     const float* mem_scale;   // [H]
-    const void* sink_k;       // [B][G][n_sinks][D] kv_dtype
-    const void* sink_v;
-    int n_sinks;
+    void* sink_k;             // [B][G][n_sinks][D] kv_dtype; with pos_arr [B][G][sinks][D], the first
+    void* sink_v;             //   min(pos, sinks) rows valid and the new token written to row pos if pos < sinks
+    int n_sinks;              // sink rows per (sequence, KV head): present sinks, or the capacity `sinks` with pos_arr
     void* ring_k;             // [B][G][W][D] kv_dtype
     void* ring_v;
     float* ring_km;           // [B][W][G][D]
     float* ring_g;            // [B][W][G]
     float* ring_beta;         // [B][W][G]
-    int64_t* ring_pos;        // [W]
+    int64_t* ring_pos;        // [W]; with pos_arr [B][W], one per sequence
     float* state;             // [B][G][D][D]
     float* o;                 // [B][H][D]
     float* lse;               // [B][H] or null
-    int nsplit;               // window splits of DECODE_SLOTS ring slots
+    int nsplit, slots;        // window splits of `slots` ring slots (decode_split)
     float* ws_om;             // [B][H][D] memory read
     float* ws_part;           // [B][G][nsplit][R][D + 2] window partials
     float* ws_ev;             // [B][G][2 D + 4] the ring row leaving the window: v, km, g, beta, valid
 };
 
 int decode_dispatch(const DecodeArgs& a, hipStream_t stream);
+
+// Window splits of a decode step: at least two workgroups per CU over the B * G (sequence, KV head) pairs, splits of
+// at most DECODE_SLOTS and at least 16 ring slots (a multiple of 16), at most 64 splits (the merge keeps 64 in LDS).
+// B = 64, G = 4, W = 2048: 2 splits of 1024 slots; B = 1: 64 splits of 32.
+inline void decode_split(int B, int G, int W, int& nsplit, int& slots) {
+    const long bg = (long)B * G;
+    const long need = (W + DECODE_SLOTS - 1) / DECODE_SLOTS;
+    long n = (512 + bg - 1) / bg;
+    const long most = (W + 15) / 16 < 64 ? (W + 15) / 16 : 64;
+    if (n > most) n = most;
+    if (n < need) n = need;
+    slots = (int)(((W + n - 1) / n + 15) / 16 * 16);
+    if (slots > DECODE_SLOTS) slots = DECODE_SLOTS;
+    nsplit = (W + slots - 1) / slots;
+}
 
 struct StepArgs {
     int B, G, R, D;
@@ -170,6 +187,20 @@ struct MemGatesArgs {
     float *g, *beta;                // [n_tok][G]
 };
 int mem_gates_dispatch(const MemGatesArgs& a, hipStream_t stream);
+
+constexpr int GP_MAX_OUT = 64;      // gate projection: n0 + n1 output columns at most
+struct GateProjArgs {
+    const uint16_t* x;              // bf16 rows: token t at x + t * x_st, d contiguous (d a multiple of 8)
+    long n_tok, x_st;
+    int d;
+    const float *w0, *b0;           // [n0][d], [n0] (b0 may be null)
+    int n0;
+    float* out0;                    // [n_tok][n0]
+    const float *w1, *b1;           // [n1][d], [n1]
+    int n1;
+    float* out1;                    // [n_tok][n1]
+};
+int gate_project_dispatch(const GateProjArgs& a, hipStream_t stream);
 int mem_project_dispatch(const MemProjArgs& a, hipStream_t stream);
 int window_fa_dispatch(const WinArgs& a, hipStream_t stream);
 

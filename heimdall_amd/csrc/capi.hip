@@ -194,7 +194,8 @@ int bf_gdn_step(const float* q, const float* k, const float* v, const float* g, 
 int bf_decode_workspace_size(int B, int G, int R, int D, int W, size_t* bytes) {
     if (!bytes || B <= 0 || G <= 0 || R <= 0 || W <= 0) return BF_STATUS_INVALID;
     if (!supported_dim(D) || R > 8) return BF_STATUS_UNSUPPORTED;
-    const size_t nsplit = (size_t)(W + bf::DECODE_SLOTS - 1) / bf::DECODE_SLOTS;
+    int nsplit = 0, slots = 0;
+    bf::decode_split(B, G, W, nsplit, slots);
     *bytes = align256((size_t)B * G * R * D * sizeof(float)) +
              align256((size_t)B * G * nsplit * R * (D + 2) * sizeof(float)) +
              align256((size_t)B * G * (2 * D + 4) * sizeof(float));
@@ -226,10 +227,46 @@ int bf_decode_fwd(int B, int G, int R, int D, int W, int sinks, int64_t pos, int
     a.kv_dtype = kv_dtype; a.q_dtype = q_dtype;
     a.qr = qr; a.qm = qm; a.kr = kr; a.v = v; a.km = km; a.g_new = g_new; a.beta_new = beta_new;
     a.z = z; a.mix_lse = mix_lse; a.mem_scale = mem_scale;
-    a.sink_k = sink_k; a.sink_v = sink_v; a.n_sinks = n_sinks;
+    a.sink_k = const_cast<void*>(sink_k); a.sink_v = const_cast<void*>(sink_v); a.n_sinks = n_sinks;
     a.ring_k = ring_k; a.ring_v = ring_v; a.ring_km = ring_km; a.ring_g = ring_g; a.ring_beta = ring_beta;
     a.ring_pos = ring_pos; a.state = state; a.o = o; a.lse = lse;
-    a.nsplit = (W + bf::DECODE_SLOTS - 1) / bf::DECODE_SLOTS;
+    bf::decode_split(B, G, W, a.nsplit, a.slots);
+    char* ws = static_cast<char*>(workspace);
+    a.ws_om = reinterpret_cast<float*>(ws);
+    a.ws_part = reinterpret_cast<float*>(ws + align256((size_t)B * G * R * D * sizeof(float)));
+    a.ws_ev = reinterpret_cast<float*>(reinterpret_cast<char*>(a.ws_part) +
+                                       align256((size_t)B * G * a.nsplit * R * (D + 2) * sizeof(float)));
+    return bf::decode_dispatch(a, static_cast<hipStream_t>(stream));
+}
+
+int bf_decode_fwd_batch(int B, int G, int R, int D, int W, int sinks, const int64_t* pos, int memory, int kv_dtype,
+                        int q_dtype, const void* qr, const float* qm, const void* kr, const void* v, const float* km,
+                        const float* g_new, const float* beta_new, const float* z, const float* mix_lse,
+                        const float* mem_scale, void* sink_k, void* sink_v, void* ring_k, void* ring_v, float* ring_km,
+                        float* ring_g, float* ring_beta, int64_t* ring_pos, float* state, float* o, float* lse,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+    if (B <= 0 || G <= 0 || R <= 0 || W <= 0 || sinks < 0 || sinks > 63 || !pos) return BF_STATUS_INVALID;
+    if (!supported_dim(D) || R > 8 || !supported_dtype(kv_dtype) || !supported_dtype(q_dtype))
+        return BF_STATUS_UNSUPPORTED;
+    if (sinks > 0 && (!sink_k || !sink_v)) return BF_STATUS_INVALID;
+    if (!qr || !kr || !v || !km || !g_new || !beta_new || !ring_k || !ring_v || !ring_km || !ring_g || !ring_beta ||
+        !ring_pos || !o)
+        return BF_STATUS_INVALID;
+    // the positions live on the device: any sequence may read its memory, so its inputs must be given
+    if (memory && (!qm || !z || !mix_lse || !mem_scale || !state)) return BF_STATUS_INVALID;
+    size_t need = 0;
+    const int st = bf_decode_workspace_size(B, G, R, D, W, &need);
+    if (st) return st;
+    if (!workspace || workspace_bytes < need) return BF_STATUS_WORKSPACE;
+    bf::DecodeArgs a{};
+    a.B = B; a.G = G; a.R = R; a.D = D; a.W = W; a.sinks = sinks; a.pos = 0; a.pos_arr = pos; a.mem_on = memory != 0;
+    a.kv_dtype = kv_dtype; a.q_dtype = q_dtype;
+    a.qr = qr; a.qm = qm; a.kr = kr; a.v = v; a.km = km; a.g_new = g_new; a.beta_new = beta_new;
+    a.z = z; a.mix_lse = mix_lse; a.mem_scale = mem_scale;
+    a.sink_k = sink_k; a.sink_v = sink_v; a.n_sinks = sinks;
+    a.ring_k = ring_k; a.ring_v = ring_v; a.ring_km = ring_km; a.ring_g = ring_g; a.ring_beta = ring_beta;
+    a.ring_pos = ring_pos; a.state = state; a.o = o; a.lse = lse;
+    bf::decode_split(B, G, W, a.nsplit, a.slots);
     char* ws = static_cast<char*>(workspace);
     a.ws_om = reinterpret_cast<float*>(ws);
     a.ws_part = reinterpret_cast<float*>(ws + align256((size_t)B * G * R * D * sizeof(float)));
@@ -305,6 +342,21 @@ int bf_mem_gates(const float* ab, int64_t n_tok, int64_t T, int G, int64_t ab_st
     a.ab = ab; a.n_tok = n_tok; a.T = T; a.ab_st = ab_st; a.G = G; a.sinks = sinks; a.start = start;
     a.A_log = A_log; a.dt_bias = dt_bias; a.decay_mask = decay_mask; a.g = g; a.beta = beta;
     return bf::mem_gates_dispatch(a, static_cast<hipStream_t>(stream));
+}
+
+int bf_gate_project(const void* x, int64_t n_tok, int d, int64_t x_st, const float* w0, const float* b0, int n0,
+                    float* out0, const float* w1, const float* b1, int n1, float* out1, void* stream) {
+    if (n_tok < 0 || d <= 0 || d % 8 || x_st < d || x_st % 8 || n0 < 0 || n1 < 0 || n0 + n1 <= 0 ||
+        n0 + n1 > bf::GP_MAX_OUT)
+        return BF_STATUS_INVALID;
+    if (n_tok == 0) return BF_STATUS_OK;
+    if (!x || (n0 && (!w0 || !out0)) || (n1 && (!w1 || !out1))) return BF_STATUS_INVALID;
+    auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    if (!al16(x) || !al16(w0) || !al16(w1)) return BF_STATUS_INVALID;
+    bf::GateProjArgs a{};
+    a.x = static_cast<const uint16_t*>(x); a.n_tok = n_tok; a.x_st = x_st; a.d = d;
+    a.w0 = w0; a.b0 = b0; a.n0 = n0; a.out0 = out0; a.w1 = w1; a.b1 = b1; a.n1 = n1; a.out1 = out1;
+    return bf::gate_project_dispatch(a, static_cast<hipStream_t>(stream));
 }
 
 int bf_gdn_conv_inputs(const void* z, int64_t z_st, const void* prefix, int in_dtype, const float* conv_w, int K,

@@ -11,10 +11,14 @@
 //
 // Layout (row-major): state [B][G][D][D] f32; ring_k, ring_v [B][G][W][D]; ring_km [B][W][G][D] f32;
 // ring_g, ring_beta [B][W][G] f32; ring_pos [W] int64; sinks [B][G][ns][D]; qr, qm, o [B][H][D]; kr, v, km [B][G][D].
+// Per-sequence positions (pos_arr, the llama.cpp multi-sequence setting): sequence b at position pos_arr[b] with its
+// own ring_pos row [b][W] and a fixed sink block [b][g][S][D] whose first min(pos, S) rows are present; the new token
+// is written to sink row pos when pos < S, and the memory branch of b is active when pos >= W.
 //
 // Kernels (two launches per step):
-//   decode_main    grid (W/1024, G, B): window split x (1024 ring slots; split 0 also takes the sinks and the new
-//                  token, saves the ring row leaving the window and writes the new token's values into its slot)
+//   decode_main    grid (nsplit, G, B): window split x (a.slots ring slots, decode_split; split 0 also takes the
+//                  sinks and the new token, saves the ring row leaving the window and writes the new token's values
+//                  into its slot)
 //   decode_tail    grid (D/64, G, B): state slab x (64 columns): memory write of the saved row, memory read; then
 //                  the merge of the window splits, the gamma mix and o for the slab's 64 dims; the new ring_pos entry
 //   gdn_step       grid (D/64, G, B): the state slab pass alone (delta_rule_step)
@@ -24,7 +28,7 @@
 namespace bf {
 
 constexpr int NT_DEC = 256;
-constexpr int SLOTS = DECODE_SLOTS;   // ring slots per window split
+constexpr int SLOTS = DECODE_SLOTS;   // ring slots per window split at most (LDS sizing)
 constexpr int SCG = 16;          // 4-column groups per state slab (64 columns: 1024 slab workgroups at B = 64, G = 4
                                  // fit one round; 16 / 32 / 128 columns measured 150 / 133 / 134 us per step, 64 131)
 constexpr int SCOL = 4 * SCG;    // state columns per slab
@@ -157,13 +161,20 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const long bg = (long)b * G + g;
 
+    // ---- this sequence's position, ring positions and present sinks
+    const long pos = a.pos_arr ? a.pos_arr[b] : a.pos;
+    int64_t* RPOS = a.ring_pos + (a.pos_arr ? (long)b * W : 0L);
+    const int nsk = a.pos_arr ? (int)min((long)a.n_sinks, pos) : a.n_sinks;
+    // the new token: its own key (with pos_arr always; otherwise the caller appended it to the sinks while pos < S)
+    const bool new_vis = a.pos_arr ? true : pos >= a.sinks;
+
     // ---- window split x
-    const int s0 = x * SLOTS, s1 = min(W, s0 + SLOTS);
+    const int s0 = x * a.slots, s1 = min(W, s0 + a.slots);
     const int nring = s1 - s0;
-    const int nextra = x == 0 ? a.n_sinks + 1 : 0;      // sinks and the new token ride on split 0
+    const int nextra = x == 0 ? nsk + 1 : 0;            // sinks and the new token ride on split 0
     const int nkeys = nring + nextra;
     const float scale = rsqrtf((float)D);
-    const long lo = max((long)a.sinks, a.pos - W + 1);  // oldest visible window position
+    const long lo = max((long)a.sinks, pos - W + 1);    // oldest visible window position
 
     const int sl = lane / LPS, dl = (lane % LPS) * 16;  // slot within the wave step, dims dl..dl+15
     const T* RK = reinterpret_cast<const T*>(a.ring_k) + bg * W * D;
@@ -176,7 +187,7 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
     // key index k in [0, nkeys): ring slot s0 + k, then sinks, then the new token
     auto key_row = [&](int k, const T* ring, const T* sink, const T* nw) -> const T* {
         if (k < nring) return ring + (long)(s0 + k) * D;
-        if (k < nring + a.n_sinks) return sink + (long)(k - nring) * D;
+        if (k < nring + nsk) return sink + (long)(k - nring) * D;
         return nw;
     };
     // visibility of every key of the split, read once into LDS (its ring_pos loads overlap the first K loads). The
@@ -186,13 +197,12 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
         constexpr int VI = (SLOTS + 64 + NT_DEC - 1) / NT_DEC;
         long rpv[VI];
 #pragma unroll
-        for (int u = 0; u < VI; ++u) rpv[u] = a.ring_pos[s0 + min(tid + u * NT_DEC, nring - 1)];
+        for (int u = 0; u < VI; ++u) rpv[u] = RPOS[s0 + min(tid + u * NT_DEC, nring - 1)];
 #pragma unroll
         for (int u = 0; u < VI; ++u) {
             const int k = tid + u * NT_DEC;
             if (k < nkeys) {
-                const bool v_ = k < nring ? rpv[u] >= lo && rpv[u] <= a.pos - 1
-                                          : (k < nring + a.n_sinks ? true : a.pos >= a.sinks);
+                const bool v_ = k < nring ? rpv[u] >= lo && rpv[u] <= pos - 1 : (k < nring + nsk ? true : new_vis);
                 vis[k] = v_;
             }
         }
@@ -440,8 +450,8 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
     // Split 0: the ring row of slot pos mod W (position pos - W, leaving the window) into ws_ev for the state update
     // of decode_tail_kernel, then the new token into that slot. No split reads the slot's values: its ring_pos
     // (pos - W or older, rewritten by the tail) keeps it out of every window, so its scores are masked.
-    const int slot = (int)(a.pos % W);
-    const long pe = a.pos - W, rg = ((long)b * W + slot) * G + g;
+    const int slot = (int)(pos % W);
+    const long pe = pos - W, rg = ((long)b * W + slot) * G + g;
     T* RKs = reinterpret_cast<T*>(a.ring_k) + (bg * W + slot) * D;
     T* RVs = reinterpret_cast<T*>(a.ring_v) + (bg * W + slot) * D;
     float* KM = a.ring_km + rg * D;
@@ -454,8 +464,16 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
         RVs[d] = NV[d];
         KM[d] = a.km[bg * D + d];
     }
+    if (a.pos_arr && pos < a.n_sinks) {                 // the new token becomes sink row pos (no split reads it)
+        T* sk = reinterpret_cast<T*>(a.sink_k) + (bg * a.n_sinks + pos) * D;
+        T* sv = reinterpret_cast<T*>(a.sink_v) + (bg * a.n_sinks + pos) * D;
+        for (int d = tid; d < D; d += NT_DEC) {
+            sk[d] = NK[d];
+            sv[d] = NV[d];
+        }
+    }
     if (tid == 0) {
-        const bool valid = pe >= 0 && a.ring_pos[slot] == pe;
+        const bool valid = pe >= 0 && RPOS[slot] == pe;
         ev[2 * D] = a.ring_g[rg];
         ev[2 * D + 1] = a.ring_beta[rg];
         ev[2 * D + 2] = valid ? 1.f : 0.f;
@@ -480,8 +498,10 @@ __global__ __launch_bounds__(NT_DEC) void decode_tail_kernel(DecodeArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const long bg = (long)b * G + g;
     const int j0 = x * SCOL;
+    const long pos = a.pos_arr ? a.pos_arr[b] : a.pos;
+    const bool mem_on = a.mem_on && (!a.pos_arr || pos >= W);
     float* om = a.ws_om + ((long)b * H + g * R) * D;
-    if (a.mem_on) {
+    if (mem_on) {
         const float* ev = a.ws_ev + bg * (2 * D + 4);
         const bool valid = ev[2 * D + 2] != 0.f;
         const float wg = valid ? ev[2 * D] : 0.f, wb = valid ? ev[2 * D + 1] : 0.f;
@@ -513,14 +533,14 @@ __global__ __launch_bounds__(NT_DEC) void decode_tail_kernel(DecodeArgs a) {
         ow /= L;
         const float lse = M + logf(L);
         float o = ow;
-        if (a.mem_on) {
+        if (mem_on) {
             const float gam = 1.f / (1.f + __expf(-(a.z[(long)b * H + h] + a.mix_lse[h] * (lse - lnW))));
             o = ow + gam * (a.mem_scale[h] * om[r * D + d] - ow);
         }
         a.o[((long)b * H + h) * D + d] = o;
         if (x == 0 && i % SCOL == 0 && a.lse) a.lse[(long)b * H + h] = lse;
     }
-    if (x == 0 && b == 0 && g == 0 && tid == 0) a.ring_pos[(int)(a.pos % W)] = a.pos;
+    if (x == 0 && g == 0 && tid == 0 && (a.pos_arr || b == 0)) a.ring_pos[(a.pos_arr ? (long)b * W : 0L) + pos % W] = pos;
 }
 
 // ----------------------------------------------------------------------------------------------- single-token GDN

@@ -154,4 +154,138 @@ int mem_gates_dispatch(const MemGatesArgs& a, hipStream_t stream) {
     return (int)hipGetLastError();
 }
 
+// Gate projections of the converted layer for bf16 activations (reference: HybridAttention._mem_inputs' ab(x),
+// Heimdall/heimdall/hibrit.py:330, and the gamma logit mix(x), :409): y = x W^T + b for the two small Linear layers
+// at once, out0 = x W0^T + b0 ([n_tok][n0], the ab columns [a | b]) and out1 = x W1^T + b1 ([n_tok][n1], mix), fp32.
+//
+// One workgroup = 8 waves x 16 tokens; d is walked in steps of 128 with v_mfma_f32_16x16x32_bf16: A = the tokens' x
+// rows (bf16, exact), B = W^T split into bf16 high and low parts (W = hi + lo + r, |r| <= 2^-18 |W|), so the sum over
+// d is the fp32 product to ~4e-6 relative, without a cast of x to fp32 in HBM. Within a step lane group lg takes the
+// 32 consecutive elements 32 lg .. + 31 of the step (four 16-byte loads: each row read as whole 256-byte pieces) and
+// MFMA j sums elements 8 j .. + 7 of each group, the same permutation of d on both operands. Each step's W tile (up
+// to 64 rows x 128 fp32) is read once per workgroup (each thread 8 or 16 consecutive floats of a row), split, and
+// stored in LDS as the B fragments (1 KB each, contiguous per fragment), double-buffered with one barrier per step;
+// x of the next step is loaded while the current one is multiplied. Bound by reading x once: 2 d bytes per token.
+constexpr int GP_WAVES = 8;
+
+__global__ __launch_bounds__(64 * GP_WAVES) void gate_project_kernel(GateProjArgs a) {
+    constexpr int MAXT = GP_MAX_OUT / 16;
+    constexpr int FRAG = 64 * 16;                              // bytes of one B fragment
+    constexpr int TILE = MAXT * 4 * 2 * FRAG;                  // (nt, j, hi / lo) fragments of one step
+    __shared__ __align__(16) char wt[2][TILE];
+    const int lane = lane_id(), wv = wave_id(), l16 = lane & 15, lg = lane >> 4;
+    const int tid = threadIdx.x;
+    const long tok0 = ((long)blockIdx.x * GP_WAVES + wv) * 16;
+    const int nout = a.n0 + a.n1, nt_used = (nout + 15) / 16;
+    const long tok = tok0 + l16;
+    const bool tok_ok = tok < a.n_tok;
+    const uint16_t* xrow = a.x + (tok_ok ? tok : 0) * a.x_st + 32 * lg;
+    f32x4 acc[MAXT];
+#pragma unroll
+    for (int nt = 0; nt < MAXT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // W tile of a step: thread tid covers rows r = tid / 16 and r + 32, elements 8 (tid % 16) .. + 7 of the step;
+    // element 8 c of a row is lane group lg = c / 4, MFMA j = c % 4 of B fragment (r / 16, j).
+    const int wr = tid >> 4, wc = tid & 15;
+    auto wsrc = [&](int r) -> const float* {
+        return r < a.n0 ? a.w0 + (long)r * a.d : (r < nout ? a.w1 + (long)(r - a.n0) * a.d : nullptr);
+    };
+    const float* wp[2] = {wsrc(wr), wsrc(wr + 32)};
+    auto load_w = [&](int k0, float (&w)[2][8]) {
+        const int k = k0 + 8 * wc;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            if (wp[h] && k < a.d) {
+                const float4 u = *reinterpret_cast<const float4*>(wp[h] + k);
+                const float4 v = *reinterpret_cast<const float4*>(wp[h] + k + 4);
+                w[h][0] = u.x; w[h][1] = u.y; w[h][2] = u.z; w[h][3] = u.w;
+                w[h][4] = v.x; w[h][5] = v.y; w[h][6] = v.z; w[h][7] = v.w;
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) w[h][e] = 0.f;
+            }
+        }
+    };
+    auto store_w = [&](char* t, const float (&w)[2][8]) {
+        const int flg = wc >> 2, fj = wc & 3;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int r = wr + 32 * h, nt = r >> 4;
+            if (nt >= MAXT) continue;
+            uint32_t hi[4], lo[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                hi[e] = pack_bf16x2(w[h][2 * e], w[h][2 * e + 1]);
+                lo[e] = pack_bf16x2(w[h][2 * e] - __uint_as_float(hi[e] << 16),
+                                    w[h][2 * e + 1] - __uint_as_float(hi[e] & 0xffff0000u));
+            }
+            const int ln = 16 * flg + (r & 15);
+            char* f = t + ((nt * 4 + fj) * 2) * FRAG + 16 * ln;
+            st16(f, make_uint4(hi[0], hi[1], hi[2], hi[3]));
+            st16(f + FRAG, make_uint4(lo[0], lo[1], lo[2], lo[3]));
+        }
+    };
+    auto load_x = [&](int k0, uint4 (&xa)[4]) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            xa[j] = tok_ok && k0 + 32 * lg + 8 * j < a.d ? ld16(xrow + k0 + 8 * j) : zero16();
+    };
+
+    float w[2][8];
+    uint4 xc[4], xn[4];
+    load_w(0, w);
+    load_x(0, xc);
+    store_w(wt[0], w);
+    __syncthreads();
+    int buf = 0;
+    for (int k0 = 0; k0 < a.d; k0 += 128) {
+        const bool more = k0 + 128 < a.d;
+        if (more) {
+            load_w(k0 + 128, w);
+            load_x(k0 + 128, xn);
+        }
+        const char* t = wt[buf];
+#pragma unroll
+        for (int nt = 0; nt < MAXT; ++nt) {
+            if (nt >= nt_used) break;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const char* f = t + ((nt * 4 + j) * 2) * FRAG + 16 * lane;
+                mma<BF16>(acc[nt], xc[j], lds16(f, 0));
+                mma<BF16>(acc[nt], xc[j], lds16(f, FRAG));
+            }
+        }
+        if (more) {
+            store_w(wt[buf ^ 1], w);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) xc[j] = xn[j];
+        }
+        __syncthreads();                                        // tile buf read by every wave, tile buf ^ 1 written
+        buf ^= 1;
+    }
+    // accumulator: lane holds output column 16 nt + l16, tokens tok0 + 4 lg .. + 3
+    if (tok0 >= a.n_tok) return;
+#pragma unroll
+    for (int nt = 0; nt < MAXT; ++nt) {
+        if (nt >= nt_used) break;
+        const int c = 16 * nt + l16;
+        if (c >= nout) continue;
+        float* out = c < a.n0 ? a.out0 : a.out1;
+        const int n = c < a.n0 ? a.n0 : a.n1, cc = c < a.n0 ? c : c - a.n0;
+        const float bias = c < a.n0 ? (a.b0 ? a.b0[cc] : 0.f) : (a.b1 ? a.b1[cc] : 0.f);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const long t = tok0 + 4 * lg + e;
+            if (t < a.n_tok) out[t * n + cc] = acc[nt][e] + bias;
+        }
+    }
+}
+
+int gate_project_dispatch(const GateProjArgs& a, hipStream_t stream) {
+    const long waves = (a.n_tok + 15) / 16;
+    hipLaunchKernelGGL(gate_project_kernel, dim3((unsigned)((waves + GP_WAVES - 1) / GP_WAVES)), dim3(64 * GP_WAVES),
+                       0, stream, a);
+    return (int)hipGetLastError();
+}
+
 }  // namespace bf

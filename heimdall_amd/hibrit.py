@@ -65,16 +65,10 @@ def mem_inputs(self, x, q, k, pos):
 
 
 def _ft_bf16(self, name: str) -> torch.Tensor:
-    """The projection ``name`` (fq or fk, [nh, D, D]) transposed in bf16, as bf_mem_project reads it; kept between
-    calls and rebuilt when the parameter changes (its storage or its version counter)."""
-    f = getattr(self, name)
-    cache = self.__dict__.setdefault("_ft_cache", {})
-    key = (f.data_ptr(), f._version, f.dtype, f.shape)
-    hit = cache.get(name)
-    if hit is None or hit[0] != key:
-        hit = (key, f.detach().transpose(1, 2).to(torch.bfloat16).contiguous())
-        cache[name] = hit
-    return hit[1]
+    """The projection ``name`` (fq or fk, [nh, D, D]) transposed in bf16, as bf_mem_project reads it. Built on every
+    call (one small cast of H D^2 elements): a copy kept between calls would go stale on parameter writes that leave
+    no trace on the Parameter, such as ``p.data.copy_`` (the reference's apply_conversion, hibrit.py:798)."""
+    return getattr(self, name).detach().transpose(1, 2).to(torch.bfloat16).contiguous()
 
 
 def _project_bf16(x: torch.Tensor, ft: torch.Tensor, scale: float) -> torch.Tensor:
@@ -89,36 +83,59 @@ def _project_bf16(x: torch.Tensor, ft: torch.Tensor, scale: float) -> torch.Tens
     return out
 
 
-def _mem_inputs_bf16(self, xf, q, k, start: int):
+def _gate_logits(self, x):
+    """The two gate projections of a chunk, fp32: ab = ab(x) [B, t, 2G] (``hibrit.py:330``) and z = mix(x) [B, t, H]
+    (the gamma logit, ``:409``). bf16 x with a row length that is a multiple of 8: one bf_gate_project pass over x (x
+    exact, the weights as bf16 high + low parts, fp32 accumulation); otherwise fp32 PyTorch products."""
+    G, H = self.c.hkv, self.c.h
+    b, t, d = x.shape
+    f32 = lambda p: p if p.dtype == torch.float32 and p.is_contiguous() else p.float().contiguous()
+    if (x.dtype == torch.bfloat16 and d % 8 == 0 and x.stride(-1) == 1 and x.stride(1) % 8 == 0
+            and (b == 1 or x.stride(0) == t * x.stride(1)) and x.data_ptr() % 16 == 0):
+        ab = torch.empty(b, t, 2 * G, dtype=torch.float32, device=x.device)
+        z = torch.empty(b, t, H, dtype=torch.float32, device=x.device)
+        w0, b0 = f32(self.ab.weight.detach()), f32(self.ab.bias.detach())
+        w1, b1 = f32(self.mix.weight.detach()), f32(self.mix.bias.detach())
+        check(_lib.load().bf_gate_project(x.data_ptr(), b * t, d, x.stride(1), w0.data_ptr(), b0.data_ptr(), 2 * G,
+                                          ab.data_ptr(), w1.data_ptr(), b1.data_ptr(), H, z.data_ptr(),
+                                          stream_ptr(x.device)), "bf_gate_project")
+        return ab, z
+    xf = x.float()
+    ab = F.linear(xf, self.ab.weight.float(), self.ab.bias.float()).contiguous()
+    z = F.linear(xf, self.mix.weight.float(), self.mix.bias.float()).contiguous()
+    return ab, z
+
+
+def _mem_inputs_bf16(self, ab, q, k, start: int):
     """mem_inputs for bf16 activations (no autograd): qm, km from the fused projection kernel (bf16 out, fp32
-    accumulation and norm), the gates g, beta in fp32 from xf = x in fp32 by bf_mem_gates (``hibrit.py:327-334``)."""
+    accumulation and norm), the gates g, beta in fp32 from the ab projection ``ab`` [B, t, 2G] by bf_mem_gates
+    (``hibrit.py:327-334``)."""
     dh, G = self.c.dh, self.c.hkv
     qm = _project_bf16(q, _ft_bf16(self, "fq"), dh ** -0.5)
     km = _project_bf16(k, _ft_bf16(self, "fk"), 1.0)
-    ab = F.linear(xf, self.ab.weight.float(), self.ab.bias.float())
-    if not ab.is_contiguous():
-        ab = ab.contiguous()
     b, t = ab.shape[:2]
-    g = torch.empty(b, t, G, dtype=torch.float32, device=xf.device)
+    g = torch.empty(b, t, G, dtype=torch.float32, device=ab.device)
     beta = torch.empty_like(g)
     f32 = lambda p: p if p.dtype == torch.float32 and p.is_contiguous() else p.float().contiguous()
     A_log, dt_bias, mask = f32(self.A_log.detach()), f32(self.dt_bias.detach()), f32(self.decay_mask)
     check(_lib.load().bf_mem_gates(ab.data_ptr(), b * t, t, G, 2 * G, A_log.data_ptr(), dt_bias.data_ptr(),
                                    mask.data_ptr(), start, self.sinks, g.data_ptr(), beta.data_ptr(),
-                                   stream_ptr(xf.device)), "bf_mem_gates")
+                                   stream_ptr(ab.device)), "bf_mem_gates")
     return qm, km, g, beta
 
 
 def _new_ring(b, G, w, D, kdt, vdt, dev, overwritten: bool = False):
     """An empty ring (no valid slot). ``overwritten``: the caller's next write fills every slot before anything reads
-    the ring (a prefill of at least W tokens from position 0), so the tensors are left uninitialised."""
+    the ring (a prefill of at least W tokens from position 0), so the row tensors are left uninitialised; ring_pos
+    still starts at -1 (no valid slot), so a call that fails before its write-back leaves a cache whose garbage
+    rows are never read."""
     if overwritten:
         return dict(ring_k=torch.empty(b, G, w, D, dtype=kdt, device=dev),
                     ring_v=torch.empty(b, G, w, D, dtype=vdt, device=dev),
                     ring_km=torch.empty(b, w, G, D, dtype=torch.float32, device=dev),
                     ring_g=torch.empty(b, w, G, dtype=torch.float32, device=dev),
                     ring_beta=torch.empty(b, w, G, dtype=torch.float32, device=dev),
-                    ring_pos=torch.empty(w, dtype=torch.long, device=dev))
+                    ring_pos=torch.full((w,), -1, dtype=torch.long, device=dev))
     return dict(ring_k=torch.zeros(b, G, w, D, dtype=kdt, device=dev),
                 ring_v=torch.zeros(b, G, w, D, dtype=vdt, device=dev),
                 ring_km=torch.zeros(b, w, G, D, dtype=torch.float32, device=dev),
@@ -182,6 +199,95 @@ def _decode(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memo
     return o.view(b, 1, H, D)
 
 
+BATCH_KEYS = ("sink_k", "sink_v", "ring_k", "ring_v", "ring_km", "ring_g", "ring_beta", "ring_pos", "S")
+
+
+def new_batch_cache(self, b: int, dtype: torch.dtype, device) -> dict:
+    """An empty per-sequence cache for ``student_batch``: the _student cache keys with one row per sequence and fixed
+    sizes (the llama.cpp state-row model, ``bifrost.patch:221-239``): sink_k / sink_v [B, G, S, D] (rows 0 ..
+    min(pos, S) - 1 present), ring_* as _student's, ring_pos [B, W] (-1 empty), S [B, G, D, D] zero."""
+    c = self.c
+    G, D, w, s = c.hkv, c.dh, self.window, self.sinks
+    bc = _new_ring(b, G, w, D, dtype, dtype, device)
+    bc["ring_pos"] = torch.full((b, w), -1, dtype=torch.long, device=device)
+    bc["sink_k"] = torch.zeros(b, G, s, D, dtype=dtype, device=device)
+    bc["sink_v"] = torch.zeros(b, G, s, D, dtype=dtype, device=device)
+    bc["S"] = torch.zeros(b, G, D, D, dtype=torch.float32, device=device)
+    return bc
+
+
+def batch_cache_set(self, bc: dict, i: int, cache: Optional[dict]) -> None:
+    """Row i of a batch cache := a single-sequence _student cache (B = 1; None or {} for an empty sequence)."""
+    cache = cache or {}
+    for key in BATCH_KEYS:
+        bc[key][i].zero_() if key != "ring_pos" else bc[key][i].fill_(-1)
+    if "ring_k" in cache:
+        for key in ("ring_k", "ring_v", "ring_km", "ring_g", "ring_beta"):
+            bc[key][i].copy_(cache[key][0].to(bc[key].dtype))
+        bc["ring_pos"][i].copy_(cache["ring_pos"])
+    if cache.get("sink_k") is not None:
+        n = cache["sink_k"].size(2)
+        bc["sink_k"][i, :, :n].copy_(cache["sink_k"][0].to(bc["sink_k"].dtype))
+        bc["sink_v"][i, :, :n].copy_(cache["sink_v"][0].to(bc["sink_v"].dtype))
+    if cache.get("S") is not None:
+        bc["S"][i].copy_(cache["S"][0])
+
+
+def batch_cache_get(self, bc: dict, i: int, pos: int) -> dict:
+    """Row i of a batch cache at position ``pos`` as a single-sequence _student cache (B = 1), the reverse of
+    ``batch_cache_set``: sinks cut to the min(pos, S) present rows; S only once the memory has been written."""
+    out = {key: bc[key][i:i + 1].clone() for key in ("ring_k", "ring_v", "ring_km", "ring_g", "ring_beta")}
+    out["ring_pos"] = bc["ring_pos"][i].clone()
+    n = min(pos, self.sinks)
+    out["sink_k"] = bc["sink_k"][i:i + 1, :, :n].clone() if n else None
+    out["sink_v"] = bc["sink_v"][i:i + 1, :, :n].clone() if n else None
+    if pos > self.window:
+        out["S"] = bc["S"][i:i + 1].clone()
+    return out
+
+
+def student_batch(self, x, q, k, v, qr, kr, pos: torch.Tensor, cache: dict, memory: bool = True):
+    """One token for each of B sequences at its own position (continuous batching; llama.cpp's multi-sequence ubatch,
+    ``bifrost.patch:841-884``): per sequence the result and the cache update of ``_student`` with t == 1
+    (``hibrit.py:363-424``) on that sequence's own cache, in one bf_decode_fwd_batch call.
+
+    x [B, 1, d]; q [B, 1, H, D]; k, v [B, 1, G, D]; qr [B, H, 1, D], kr [B, G, 1, D]; pos [B] int64 on the device;
+    cache: a batch cache (``new_batch_cache``), mutated in place. Returns o [B, 1, H, D] fp32."""
+    require_device(x, q, k, v, qr, kr, pos)
+    require_no_grad(x, q, k, v, qr, kr)
+    c = self.c
+    b = x.shape[0]
+    if x.shape[1] != 1:
+        raise BifrostError("student_batch takes one token per sequence")
+    H, G, D, w, r = c.h, c.hkv, c.dh, self.window, c.h // c.hkv
+    dev = x.device
+    kvdt = cache["ring_k"].dtype
+    pos = pos.to(device=dev, dtype=torch.long).contiguous()
+    # memory inputs without the sink mask of beta (position S passed), then the mask per sequence
+    qm, km, g, beta = self._mem_inputs(x, q, k, torch.full((1,), self.sinks, device=dev))
+    beta = beta * (pos >= self.sinks).float()[:, None, None]
+    z = F.linear(x.float(), self.mix.weight.float(), self.mix.bias.float()).contiguous()
+    f32 = lambda t_: t_.float().contiguous()
+    qm_, km_, g_, b_ = f32(qm[:, 0]), f32(km[:, 0]), f32(g[:, 0]), f32(beta[:, 0])
+    qrd = qr[:, :, 0].to(torch.bfloat16 if qr.dtype == torch.bfloat16 else torch.float32).contiguous()
+    kr_, v_ = kr[:, :, 0].to(kvdt).contiguous(), v[:, 0].to(kvdt).contiguous()
+    mix_lse, mem_scale = self.mix_lse.float().contiguous(), self.mem_scale.float().contiguous()
+    o = torch.empty(b, H, D, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    nbytes = _lib.ctypes.c_size_t(0)
+    check(lib.bf_decode_workspace_size(b, G, r, D, w, _lib.ctypes.byref(nbytes)), "bf_decode_workspace_size")
+    ws = workspace(nbytes.value, dev)
+    ptr = lambda t_: t_.data_ptr()
+    check(lib.bf_decode_fwd_batch(b, G, r, D, w, self.sinks, ptr(pos), int(memory), dtype_code(kvdt),
+                                  dtype_code(qrd.dtype), ptr(qrd), ptr(qm_), ptr(kr_), ptr(v_), ptr(km_), ptr(g_),
+                                  ptr(b_), ptr(z), ptr(mix_lse), ptr(mem_scale), ptr(cache["sink_k"]),
+                                  ptr(cache["sink_v"]), ptr(cache["ring_k"]), ptr(cache["ring_v"]),
+                                  ptr(cache["ring_km"]), ptr(cache["ring_g"]), ptr(cache["ring_beta"]),
+                                  ptr(cache["ring_pos"]), ptr(cache["S"]), ptr(o), None, ptr(ws), ws.numel(),
+                                  stream_ptr(dev)), "bf_decode_fwd_batch")
+    return o.view(b, 1, H, D)
+
+
 def student(self, x, q, k, v, qr, kr, start: int, cache: Optional[dict], memory: bool = True):
     """Window + sinks attention, delta-rule memory written on window exit, gamma mix (``hibrit.py:363-424``).
 
@@ -207,10 +313,10 @@ def student(self, x, q, k, v, qr, kr, start: int, cache: Optional[dict], memory:
     if n_new:
         sink_k = kr[:, :, :n_new] if sink_k is None else torch.cat((sink_k, kr[:, :, :n_new]), 2)
         sink_v = vt[:, :, :n_new] if sink_v is None else torch.cat((sink_v, vt[:, :, :n_new]), 2)
-    xf = None
+    zmix = None
     if t > 1 and all(z.dtype == torch.bfloat16 for z in (q, k, qr, kr)):
-        xf = x.float()
-        qm, km, g, beta = _mem_inputs_bf16(self, xf, q, k, start)
+        ab, zmix = _gate_logits(self, x)
+        qm, km, g, beta = _mem_inputs_bf16(self, ab, q, k, start)
     else:
         qm, km, g, beta = self._mem_inputs(x, q, k, pos)
     if "ring_k" not in st:
@@ -222,7 +328,7 @@ def student(self, x, q, k, v, qr, kr, start: int, cache: Optional[dict], memory:
         o = _decode(self, x, qr, kr[:, :, 0], v[:, 0], qm[:, 0], km[:, 0], g[:, 0], beta[:, 0], start, st, sink_k,
                     sink_v, memory)
     else:
-        o = _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memory, xf)
+        o = _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memory, zmix)
     st["sink_k"], st["sink_v"] = sink_k, sink_v
     return o
 
@@ -378,12 +484,12 @@ def _strides(t: torch.Tensor, dims):
     return tuple(int(t.stride(d)) for d in dims)
 
 
-def _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memory, xf=None):
+def _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memory, zmix=None):
     """A chunk of t > 1 tokens in one bf_layer_prefill_fwd call: the delta-rule memory on the write stream (ring rows
     leaving the window, then the chunk's own rows, hibrit.py:391-408), the window + sinks + LSE with the gamma mix
     (hibrit.py:385-411), then the ring / state write-back (hibrit.py:412-423). From an empty cache (start 0, no
     state) the queries before W never read the memory, so the library runs the memory on queries W..t-1 against the
-    writes of tokens 0..t-W-1 only."""
+    writes of tokens 0..t-W-1 only. ``zmix``: the gamma logit mix(x) [B, t, H] fp32 if already computed."""
     c = self.c
     b, t = x.shape[:2]
     H, G, D, w, r = c.h, c.hkv, c.dh, self.window, c.h // c.hkv
@@ -399,7 +505,8 @@ def _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, mem
         S = S.float().contiguous()
     z = mix_lse = mem_scale = None
     if use_mem:
-        z = F.linear(xf if xf is not None else x.float(), self.mix.weight.float(), self.mix.bias.float()).contiguous()
+        z = zmix if zmix is not None else F.linear(x.float(), self.mix.weight.float(), self.mix.bias.float())
+        z = z.contiguous()
         mix_lse = self.mix_lse.float().contiguous()
         mem_scale = self.mem_scale.float().contiguous()
     mdt = lambda t_: t_.contiguous() if t_.dtype in (torch.float32, torch.bfloat16) else t_.to(cdt).contiguous()

@@ -130,6 +130,27 @@ int bf_decode_fwd(int B, int G, int R, int D, int W, int sinks, int64_t pos, int
                   void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * One decode step for B sequences each at its own position (continuous batching): the step of bf_decode_fwd for
+ * sequence b at position pos[b], with a per-sequence cache. Replaces the batched-ubatch form of llama.cpp's
+ * build_layer_bifrost, whose set_input takes each sequence's own positions and state row
+ * (Heimdall/llamacpp/bifrost.patch:841-884; multi-sequence check llamacpp/bifrost_multiseq.cpp:48-98); per
+ * sequence the result equals the reference's _student with t == 1 (Heimdall/heimdall/hibrit.py:363-424) on that
+ * sequence's own cache.
+ *   pos [B] int64 on the device; sequence b: ring rows [b] as in bf_decode_fwd, ring_pos [B][W] (its own slot
+ *   positions, -1 empty), sink_k / sink_v [B][G][sinks][D] kv_dtype with rows 0 .. min(pos[b], sinks) - 1 present:
+ *   the new token is written to sink row pos[b] when pos[b] < sinks (and to ring slot pos[b] mod W as always);
+ *   state [B][G][D][D] f32, updated when memory and pos[b] >= W. The memory inputs (qm, z, mix_lse, mem_scale,
+ *   state) are required when memory is set, since the positions are not read on the host.
+ * Workspace: bf_decode_workspace_size bytes. sinks <= 63, R <= 8.
+ */
+int bf_decode_fwd_batch(int B, int G, int R, int D, int W, int sinks, const int64_t* pos, int memory, int kv_dtype,
+                        int q_dtype, const void* qr, const float* qm, const void* kr, const void* v, const float* km,
+                        const float* g_new, const float* beta_new, const float* z, const float* mix_lse,
+                        const float* mem_scale, void* sink_k, void* sink_v, void* ring_k, void* ring_v, float* ring_km,
+                        float* ring_g, float* ring_beta, int64_t* ring_pos, float* state, float* o, float* lse,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * bf_decode_fwd without a workspace argument: the same kernels and results, with their scratch (the memory read and
  * the window-split partials, bf_decode_workspace_size bytes) in a static device buffer of
  * BF_DECODE_STATIC_SCRATCH_BYTES that the library holds on each GPU it runs on until the process ends. No counterpart
@@ -198,6 +219,20 @@ int bf_mem_project(const void* x, int64_t n_tok, int nh, int D, int64_t x_st, in
 int bf_mem_gates(const float* ab, int64_t n_tok, int64_t T, int G, int64_t ab_st, const float* A_log,
                  const float* dt_bias, const float* decay_mask, int64_t start, int sinks, float* g, float* beta,
                  void* stream);
+
+/*
+ * Gate projections of the converted layer for bf16 activations: the two small Linear layers applied to x,
+ *     out0[t] = x_t W0^T + b0   (ab(x), HybridAttention._mem_inputs, Heimdall/heimdall/hibrit.py:330)
+ *     out1[t] = x_t W1^T + b1   (mix(x), the gamma logit, hibrit.py:409)
+ * in one pass over x.
+ *   x: bf16 rows, token t at x + t * x_st elements, d contiguous, d a multiple of 8, 16-byte aligned rows
+ *   w0 [n0][d], w1 [n1][d] f32; b0 [n0], b1 [n1] f32 or null; out0 [n_tok][n0], out1 [n_tok][n1] f32;
+ *   n0 + n1 <= 64 (n1 may be 0)
+ * Arithmetic: x exact (bf16), W as bf16 high + low parts (relative residual <= 2^-18), fp32 accumulation: the fp32
+ * product to ~4e-6 relative (the reference runs these layers under bf16 autocast, i.e. with W rounded to bf16).
+ */
+int bf_gate_project(const void* x, int64_t n_tok, int d, int64_t x_st, const float* w0, const float* b0, int n0,
+                    float* out0, const float* w1, const float* b1, int n1, float* out1, void* stream);
 
 /*
  * Native Gated DeltaNet layer, the pass before the delta rule: GatedDeltaNet.forward up to delta_rule

@@ -34,3 +34,27 @@ def dev():
 
 
 os.environ.setdefault("PYTHONHASHSEED", "0")
+
+_MARGINS = []
+
+
+@pytest.fixture
+def margin(request):
+    """margin(name, err, tol): assert a parity error is below its tolerance and keep the measurement, so every
+    full-size check's margin appears in the run's log (the table printed at the end of the session, also under -q,
+    and the test's user_properties for junit-xml)."""
+    def rec(name, err, tol):
+        err, tol = float(err), float(tol)
+        _MARGINS.append((request.node.name, name, err, tol))
+        request.node.user_properties.append((name, err))
+        assert err < tol, f"{name}: {err:.3e} is not below {tol:.1e}"
+    return rec
+
+
+def pytest_terminal_summary(terminalreporter):
+    if not _MARGINS:
+        return
+    tr = terminalreporter
+    tr.section("parity margins: relative L2 error against the oracle / tolerance")
+    for test, name, err, tol in _MARGINS:
+        tr.write_line(f"{test} | {name}: {err:.3e} / {tol:.0e} = {err / tol:.3f} of the tolerance")

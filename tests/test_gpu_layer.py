@@ -87,7 +87,8 @@ def test_mem_inputs_bf16_fused_projection(dev, d):
     pos = torch.arange(t)
     qm_ref, km_ref, g_ref, b_ref = olayer.mem_inputs(m, x, q.float(), k.float(), pos)
     with torch.no_grad():
-        qm, km, g, beta = hibrit._mem_inputs_bf16(mg, x.to(dev), q.to(dev), k.to(dev), 0)
+        ab, _ = hibrit._gate_logits(mg, x.to(dev))
+        qm, km, g, beta = hibrit._mem_inputs_bf16(mg, ab, q.to(dev), k.to(dev), 0)
     assert qm.dtype == km.dtype == torch.bfloat16
     for got, ref in ((qm, qm_ref), (km, km_ref), (g, g_ref), (beta, b_ref)):
         assert rel(got, ref) < TOL_BF16, rel(got, ref)
@@ -99,8 +100,9 @@ def test_mem_inputs_bf16_fused_projection(dev, d):
 
 def test_mem_gates_and_projection_cache(dev):
     """bf_mem_gates (the gates of _mem_inputs for bf16 activations) against the oracle's fp32 gates for B = 2
-    sequences starting at position 1 with 2 sinks (beta is zero at position 1), relative error <= 1e-5; then an
-    in-place change of fq (as an optimizer step makes) reaches the next projection through the cached bf16 F^T."""
+    sequences starting at position 1 with 2 sinks (beta is zero at position 1), relative error <= 1e-5; then changes
+    of fq reach the next projection: an in-place step on the Parameter (as an optimizer step makes) and a write
+    through ``.data`` (as the reference's apply_conversion makes, hibrit.py:798), which leaves no version bump."""
     from heimdall_amd import hibrit
     print("mem_inputs bf16 gates and F^T cache, D=64", flush=True)
     m = make_core(6, 2, 64, 32, window=16, sinks=2)
@@ -119,16 +121,71 @@ def test_mem_gates_and_projection_cache(dev):
     pos = torch.arange(start, start + t)
     _, _, g_ref, b_ref = olayer.mem_inputs(m, x, q.float(), k.float(), pos)
     with torch.no_grad():
-        qm0, _, g, beta = hibrit._mem_inputs_bf16(mg, x.to(dev), q.to(dev), k.to(dev), start)
+        ab, _ = hibrit._gate_logits(mg, x.to(dev))
+        qm0, _, g, beta = hibrit._mem_inputs_bf16(mg, ab, q.to(dev), k.to(dev), start)
     assert rel(g, g_ref) < 1e-5 and rel(beta, b_ref) < 1e-5, (rel(g, g_ref), rel(beta, b_ref))
     assert beta[:, 0].abs().max().item() == 0.0
     noise = torch.randn(m.fq.shape, generator=gen) * 0.3
     with torch.no_grad():
         m.fq.add_(noise)
         mg.fq.add_(noise.to(dev))
-        qm1, _, _, _ = hibrit._mem_inputs_bf16(mg, x.to(dev), q.to(dev), k.to(dev), start)
+        qm1, _, _, _ = hibrit._mem_inputs_bf16(mg, ab, q.to(dev), k.to(dev), start)
     qm_ref, _, _, _ = olayer.mem_inputs(m, x, q.float(), k.float(), pos)
     assert rel(qm1, qm_ref) < TOL_BF16 and rel(qm1, qm0) > 10 * TOL_BF16, (rel(qm1, qm_ref), rel(qm1, qm0))
+    new_fq = torch.eye(64).repeat(6, 1, 1) + torch.randn(m.fq.shape, generator=gen) * 0.3
+    with torch.no_grad():
+        m.fq.data.copy_(new_fq)
+        mg.fq.data.copy_(new_fq.to(dev))
+        qm2, _, _, _ = hibrit._mem_inputs_bf16(mg, ab, q.to(dev), k.to(dev), start)
+    qm_ref2, _, _, _ = olayer.mem_inputs(m, x, q.float(), k.float(), pos)
+    assert rel(qm2, qm_ref2) < TOL_BF16 and rel(qm2, qm1) > 10 * TOL_BF16, (rel(qm2, qm_ref2), rel(qm2, qm1))
+
+
+@pytest.mark.parametrize("b,t,d,n1", [(1, 1000, 5120, 24), (2, 37, 40, 24), (1, 130, 1024, 0), (3, 16, 256, 56)])
+def test_gate_project(dev, b, t, d, n1):
+    """bf_gate_project (the ab and mix projections of a bf16 chunk in one pass) against fp32 products of the same
+    bf16 x: relative error <= 1e-5 per output (W split into bf16 high and low parts); d = 40 ends on a partial
+    32-wide step, n1 = 0 has one output, n0 + n1 = 64 is the widest; a strided x view (every other token row of a
+    wider tensor) goes through _gate_logits."""
+    from heimdall_amd import _lib
+    from heimdall_amd._device import stream_ptr
+    print(f"gate projection B={b} t={t} d={d} n0=8 n1={n1}", flush=True)
+    gen = torch.Generator().manual_seed(31 + d)
+    x = torch.randn(b * t, d, generator=gen).bfloat16()
+    w0, b0 = torch.randn(8, d, generator=gen) * d ** -0.5, torch.randn(8, generator=gen)
+    w1, b1 = torch.randn(max(n1, 1), d, generator=gen) * d ** -0.5, torch.randn(max(n1, 1), generator=gen)
+    ref0 = x.double() @ w0.double().T + b0.double()
+    ref1 = x.double() @ w1.double().T + b1.double()
+    xd, w0d, b0d, w1d, b1d = (z.to(dev).contiguous() for z in (x, w0, b0, w1, b1))
+    o0 = torch.empty(b * t, 8, device=dev)
+    o1 = torch.empty(b * t, max(n1, 1), device=dev)
+    rc = _lib.load().bf_gate_project(xd.data_ptr(), b * t, d, d, w0d.data_ptr(), b0d.data_ptr(), 8, o0.data_ptr(),
+                                     w1d.data_ptr() if n1 else None, b1d.data_ptr() if n1 else None, n1,
+                                     o1.data_ptr() if n1 else None, stream_ptr(dev))
+    assert rc == 0, rc
+    e0 = rel(o0, ref0)
+    assert e0 < 1e-5, e0
+    if n1:
+        e1 = rel(o1, ref1)
+        assert e1 < 1e-5, e1
+    # the host helper on a strided view (token stride 2 d): the kernel path, equal to the fp32 torch path
+    if d % 8 == 0 and n1 == 24:
+        from heimdall_amd import hibrit
+        G, H = 4, 24
+        core = make_core(H, G, 64, d, window=16, sinks=2)
+        with torch.no_grad():
+            core.ab.weight.copy_(w0)
+            core.ab.bias.copy_(b0)
+            core.mix.weight.copy_(w1)
+            core.mix.bias.copy_(b1)
+        core = core.to(dev)
+        wide = torch.randn(b, 2 * t, d, generator=gen).bfloat16().to(dev)
+        xv = wide[:, ::2]
+        with torch.no_grad():
+            ab, z = hibrit._gate_logits(core, xv)
+            ab_ref = torch.nn.functional.linear(xv.double(), core.ab.weight.double(), core.ab.bias.double())
+            z_ref = torch.nn.functional.linear(xv.double(), core.mix.weight.double(), core.mix.bias.double())
+        assert rel(ab, ab_ref) < 1e-5 and rel(z, z_ref) < 1e-5, (rel(ab, ab_ref), rel(z, z_ref))
 
 
 @pytest.mark.parametrize("b", [1, 3])

@@ -309,10 +309,35 @@ def run_decode(steps, warmup, dev):
     nbytes = (B * G * D * D * 4 * 2 + B * G * (W + S + 1) * D * 2 * 2 + B * H * D * (2 + 4 + 4)
               + B * G * D * (4 + 2 + 2 + 4))
     gbs = nbytes / (us * 1e-6) / 1e9
+    # the same step with the 64 sequences at their own positions (bf_decode_fwd_batch): positions 100000 + 37 b
+    # (every sequence's ring full, memory active), per-sequence ring_pos rows and sink blocks
+    pos_b = torch.tensor([p + 37 * i for i in range(B)], device=dev, dtype=torch.long)
+    rp_b = torch.stack([torch.tensor([pp for pp in range(int(q_) - W, int(q_))], device=dev)[
+        torch.argsort(torch.arange(int(q_) - W, int(q_), device=dev) % W)] for q_ in pos_b]).contiguous()
+    sk_b, sv_b = sink_k.clone(), sink_v.clone()
+    bargs = (B, G, R, D, W, S, pos_b.data_ptr(), 1, _lib.DTYPE_BF16, _lib.DTYPE_BF16, qr.data_ptr(), qm.data_ptr(),
+             kr.data_ptr(), v.data_ptr(), km.data_ptr(), g_new.data_ptr(), b_new.data_ptr(), z.data_ptr(),
+             mix_lse.data_ptr(), mem_scale.data_ptr(), sk_b.data_ptr(), sv_b.data_ptr(), ring_k.data_ptr(),
+             ring_v.data_ptr(), ring_km.data_ptr(), ring_g.data_ptr(), ring_beta.data_ptr(), rp_b.data_ptr(),
+             state.data_ptr(), o.data_ptr(), None, ws.data_ptr(), ws.numel(), st)
+    for _ in range(warmup):
+        _lib.check(lib.bf_decode_fwd_batch(*bargs), "bf_decode_fwd_batch")
+    torch.cuda.synchronize()
+    e0.record(torch.cuda.current_stream(dev))
+    rcs = [lib.bf_decode_fwd_batch(*bargs) for _ in range(steps)]
+    e1.record(torch.cuda.current_stream(dev))
+    torch.cuda.synchronize()
+    for rc in rcs:
+        _lib.check(rc, "bf_decode_fwd_batch")
+    us_b = e0.elapsed_time(e1) * 1e3 / steps
+    gbs_b = nbytes / (us_b * 1e-6) / 1e9
     return {"workload": "decode B=64 H=16 G=4 D=256 W=2048+4 bf16 ring, fp32 state", "us_per_step": us,
             "steps": steps, "roofline": {"bound": "hbm", "kernel": "decode_main_kernel+decode_tail_kernel",
                                          "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                         "frac": gbs / HBM_PEAK_GBS, "bytes_per_step": nbytes}}
+                                         "frac": gbs / HBM_PEAK_GBS, "bytes_per_step": nbytes},
+            "mixed_positions": {"workload": "the same step, the 64 sequences at positions 100000 + 37 b "
+                                            "(bf_decode_fwd_batch, per-sequence ring_pos and sinks)",
+                                "us_per_step": us_b, "GBs": gbs_b, "frac": gbs_b / HBM_PEAK_GBS}}
 
 
 def run_varlen(steps, warmup, dev):

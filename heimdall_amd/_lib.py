@@ -30,7 +30,7 @@ SIGNATURES = {
     "bf_decode_fwd_noalloc": (_c_int, [_c_int] * 6 + [_c_i64] + [_c_int] * 3 + [_vp] * 12 + [_c_int] + [_vp] * 9 + [_vp]),
     "bf_window_fwd": (_c_int, [_c_int] * 7 + [_c_i64, _c_int] + ([_vp] + [_c_i64] * 3) * 3 + [_vp] * 5 + [_c_int] * 2
                       + [_vp, _c_int] + [_vp] * 4 + [_c_int, _vp, _vp]),
-    "bf_mem_project": (_c_int, [_vp, _c_i64, _c_int, _c_int, _c_i64, _c_i64, _vp, _fp, _vp, _c_int, _vp]),
+    "bf_mem_project": (_c_int, [_vp, _c_i64, _c_int, _c_int, _c_i64, _c_i64, _vp, _fp, _vp, _c_int, _c_int, _vp]),
     "bf_mem_gates": (_c_int, [_vp, _c_i64, _c_i64, _c_int, _c_i64, _vp, _vp, _vp, _c_i64, _c_int, _vp, _vp, _vp]),
     "bf_gate_project": (_c_int, [_vp, _c_i64, _c_int, _c_i64, _vp, _vp, _c_int, _vp, _vp, _vp, _c_int, _vp, _vp]),
     "bf_gdn_conv_inputs": (_c_int, [_vp, _c_i64, _vp, _c_int, _vp, _c_int] + [_vp] * 5 + [_c_int, _c_i64]

@@ -173,9 +173,10 @@ struct MemProjArgs {
     long n_tok;
     int nh, D;
     long x_st, x_sh;
-    const void* ft;           // [nh][D][D] bf16, F_h transposed: ft[h][j][i] = F_h[i][j]
+    const float* f;           // [nh][D][D] fp32, the projections as the module holds them: f[h][i][j] = F_h[i][j]
     float scale;
-    void* out;                // [n_tok][nh][D] bf16
+    void* out;                // [n_tok][nh][D] in out_dtype
+    int out_dtype;            // DT_BF16 or DT_F32
 };
 
 struct MemGatesArgs {

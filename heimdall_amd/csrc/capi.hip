@@ -319,16 +319,16 @@ int bf_window_fwd(int B, int G, int R, int D, int T, int W, int sinks, int64_t s
     return bf::window_dispatch(a, static_cast<hipStream_t>(stream));
 }
 
-int bf_mem_project(const void* x, int64_t n_tok, int nh, int D, int64_t x_st, int64_t x_sh, const void* ft,
-                   float scale, void* out, int in_dtype, void* stream) {
+int bf_mem_project(const void* x, int64_t n_tok, int nh, int D, int64_t x_st, int64_t x_sh, const float* f,
+                   float scale, void* out, int in_dtype, int out_dtype, void* stream) {
     if (n_tok < 0 || nh <= 0 || x_st <= 0 || x_sh < 0) return BF_STATUS_INVALID;
-    if (!supported_dim(D) || in_dtype != BF_DTYPE_BF16) return BF_STATUS_UNSUPPORTED;
+    if (!supported_dim(D) || in_dtype != BF_DTYPE_BF16 || !supported_dtype(out_dtype)) return BF_STATUS_UNSUPPORTED;
     if (n_tok == 0) return BF_STATUS_OK;
-    if (!x || !ft || !out) return BF_STATUS_INVALID;
+    if (!x || !f || !out) return BF_STATUS_INVALID;
     if (x_st * 16 * 2 > 0xffffffffLL) return BF_STATUS_INVALID;     // 16 token rows per 32-bit buffer range
     bf::MemProjArgs a{};
     a.x = x; a.n_tok = n_tok; a.nh = nh; a.D = D; a.x_st = x_st; a.x_sh = x_sh;
-    a.ft = ft; a.scale = scale; a.out = out;
+    a.f = f; a.scale = scale; a.out = out; a.out_dtype = out_dtype;
     return bf::mem_project_dispatch(a, static_cast<hipStream_t>(stream));
 }
 

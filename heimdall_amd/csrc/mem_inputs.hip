@@ -4,11 +4,13 @@
 // used for qm (x = q, F = fq, scale = D^-1/2) and km (x = k, F = fk, scale = 1), for bf16 activations.
 //
 // One workgroup owns one head h and a strided set of 64-token tiles (one round of workgroups over the CUs). F_h^T
-// (D x D bf16, 128 KB at D = 256) is staged in LDS once; each of the 4 waves computes 16 tokens x D outputs per tile
+// (D x D bf16, 128 KB at D = 256) is built in LDS once from the module's fp32 F_h (each thread assembles one 16-byte
+// row block of F_h^T from 8 loads down a column of F_h, coalesced across lanes, rounded to bf16 to nearest even);
+// each of the 4 waves computes 16 tokens x D outputs per tile
 // as Y^T = F_h^T X^T with v_mfma_f32_16x16x32_bf16 (A = rows of F_h^T from LDS, read 8 MFMAs ahead; B = the token
 // rows of x from global memory, loaded two tiles ahead), so every lane holds 4 consecutive outputs of one token: the
-// row norm is a sum over the lane's values and two cross-lane steps, and the bf16 result is stored 8 bytes at a
-// time. The pass reads x and writes y once (806 MB at T = 32768, 24 heads, D = 256).
+// row norm is a sum over the lane's values and two cross-lane steps, and the result is stored 8 (bf16) or 16 (fp32)
+// bytes at a time. The pass reads x and writes y once (806 MB at T = 32768, 24 heads, D = 256, bf16 out).
 #include "bf_common.h"
 #include "bf_internal.h"
 
@@ -35,10 +37,30 @@ __global__ __launch_bounds__(64 * MP_WAVES, 1) void mem_project_kernel(MemProjAr
     const int h = blockIdx.x % a.nh, tg = blockIdx.x / a.nh, ntg = gridDim.x / a.nh;
     const int lane = lane_id(), wv = wave_id(), l16 = lane & 15, lg = lane >> 4;
 
-    // stage F_h^T: LDS row j holds row j of F_h^T with its 16-byte blocks permuted by mp_sw(j)
-    const rsrc_t rf = make_rsrc(reinterpret_cast<const uint16_t*>(a.ft) + (long)h * D * D, (uint32_t)(D * ROWB));
-    stage_tile(rf, (uint32_t)ROWB, ROWB, ft, D * ROWB, wv, MP_WAVES, lane, [](int row) { return mp_sw<NBLK>(row); },
-               NBLK);
+    // F_h^T into LDS: row j holds column j of F_h in bf16, its 16-byte blocks permuted by mp_sw(j). Block c of row j
+    // (elements F_h[8 c .. 8 c + 7][j]) is one thread's: consecutive threads take consecutive j, so each of the 8 loads
+    // reads 4 bytes per lane from one row of F_h, contiguous across the lanes.
+    {
+        const float* F = a.f + (long)h * D * D;
+        constexpr int NB = D * D / 8, UN = NB / (64 * MP_WAVES) < 4 ? NB / (64 * MP_WAVES) : 4;
+        static_assert(NB % (64 * MP_WAVES * UN) == 0, "F staging split");
+        for (int i0 = threadIdx.x; i0 < NB; i0 += 64 * MP_WAVES * UN) {
+            float v[UN][8];
+#pragma unroll
+            for (int u = 0; u < UN; ++u) {
+                const int idx = i0 + u * 64 * MP_WAVES, j = idx % D, c = idx / D;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[u][e] = F[(long)(8 * c + e) * D + j];
+            }
+#pragma unroll
+            for (int u = 0; u < UN; ++u) {
+                const int idx = i0 + u * 64 * MP_WAVES, j = idx % D, c = idx / D;
+                st16(reinterpret_cast<char*>(ft) + j * ROWB + 16 * (c ^ mp_sw<NBLK>(j)),
+                     make_uint4(pack_bf16x2(v[u][0], v[u][1]), pack_bf16x2(v[u][2], v[u][3]),
+                                pack_bf16x2(v[u][4], v[u][5]), pack_bf16x2(v[u][6], v[u][7])));
+            }
+        }
+    }
 
     int abase[NKB];
     {
@@ -48,7 +70,6 @@ __global__ __launch_bounds__(64 * MP_WAVES, 1) void mem_project_kernel(MemProjAr
     }
     const char* Fb = reinterpret_cast<const char*>(ft);
     const uint16_t* X = reinterpret_cast<const uint16_t*>(a.x) + (long)h * a.x_sh;
-    uint16_t* Out = reinterpret_cast<uint16_t*>(a.out);
 
     const long ntiles = (a.n_tok + MP_TILE - 1) / MP_TILE;
     // B fragments of token 16 wv + l16 of tile t: x[token][32 ks + 8 lg .. +7]
@@ -100,13 +121,21 @@ __global__ __launch_bounds__(64 * MP_WAVES, 1) void mem_project_kernel(MemProjAr
         const float inv = a.scale / fmaxf(sqrtf(ss), 1e-12f);
         const long tok = t * MP_TILE + 16 * wv + l16;
         if (tok < a.n_tok) {
-            uint16_t* orow = Out + (tok * a.nh + h) * D;
+            if (a.out_dtype == DT_BF16) {
+                uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + (tok * a.nh + h) * D;
 #pragma unroll
-            for (int jt = 0; jt < NDT; ++jt) {
-                uint2 v;
-                v.x = pack_bf16x2(acc[jt][0] * inv, acc[jt][1] * inv);
-                v.y = pack_bf16x2(acc[jt][2] * inv, acc[jt][3] * inv);
-                *reinterpret_cast<uint2*>(orow + 16 * jt + 4 * lg) = v;
+                for (int jt = 0; jt < NDT; ++jt) {
+                    uint2 v;
+                    v.x = pack_bf16x2(acc[jt][0] * inv, acc[jt][1] * inv);
+                    v.y = pack_bf16x2(acc[jt][2] * inv, acc[jt][3] * inv);
+                    *reinterpret_cast<uint2*>(orow + 16 * jt + 4 * lg) = v;
+                }
+            } else {
+                float* orow = reinterpret_cast<float*>(a.out) + (tok * a.nh + h) * D;
+#pragma unroll
+                for (int jt = 0; jt < NDT; ++jt)
+                    *reinterpret_cast<float4*>(orow + 16 * jt + 4 * lg) =
+                        make_float4(acc[jt][0] * inv, acc[jt][1] * inv, acc[jt][2] * inv, acc[jt][3] * inv);
             }
         }
 #pragma unroll
@@ -281,10 +310,92 @@ __global__ __launch_bounds__(64 * GP_WAVES) void gate_project_kernel(GateProjArg
     }
 }
 
+// The same projections for a few tokens (a decode step, a short chunk): one workgroup per 16 tokens whose 8 waves
+// take every 8th 128-wide step of d each (the same lane / MFMA mapping as gate_project_kernel), reading their own
+// part of W straight from memory (each weight once per workgroup), then the 8 partial sums through LDS.
+__global__ __launch_bounds__(64 * GP_WAVES) void gate_project_small_kernel(GateProjArgs a) {
+    constexpr int MAXT = GP_MAX_OUT / 16;
+    __shared__ f32x4 red[GP_WAVES][MAXT][64];
+    const int lane = lane_id(), wv = wave_id(), l16 = lane & 15, lg = lane >> 4;
+    const long tok0 = (long)blockIdx.x * 16;
+    const int nout = a.n0 + a.n1, nt_used = (nout + 15) / 16;
+    const long tok = tok0 + l16;
+    const bool tok_ok = tok < a.n_tok;
+    const uint16_t* xrow = a.x + (tok_ok ? tok : 0) * a.x_st + 32 * lg;
+    const float* wrow[MAXT];
+#pragma unroll
+    for (int nt = 0; nt < MAXT; ++nt) {
+        const int c = 16 * nt + l16;
+        wrow[nt] = c < a.n0 ? a.w0 + (long)c * a.d : (c < nout ? a.w1 + (long)(c - a.n0) * a.d : nullptr);
+        if (wrow[nt]) wrow[nt] += 32 * lg;
+    }
+    f32x4 acc[MAXT];
+#pragma unroll
+    for (int nt = 0; nt < MAXT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 128 * wv; k0 < a.d; k0 += 128 * GP_WAVES) {
+        uint4 xa[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            xa[j] = tok_ok && k0 + 32 * lg + 8 * j < a.d ? ld16(xrow + k0 + 8 * j) : zero16();
+#pragma unroll
+        for (int nt = 0; nt < MAXT; ++nt) {
+            if (nt >= nt_used) break;
+            float4 w4[4][2];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bool ok = wrow[nt] && k0 + 32 * lg + 8 * j < a.d;
+                w4[j][0] = ok ? *reinterpret_cast<const float4*>(wrow[nt] + k0 + 8 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
+                w4[j][1] = ok ? *reinterpret_cast<const float4*>(wrow[nt] + k0 + 8 * j + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float w[8] = {w4[j][0].x, w4[j][0].y, w4[j][0].z, w4[j][0].w,
+                                    w4[j][1].x, w4[j][1].y, w4[j][1].z, w4[j][1].w};
+                uint32_t hi[4], lo[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    hi[e] = pack_bf16x2(w[2 * e], w[2 * e + 1]);
+                    lo[e] = pack_bf16x2(w[2 * e] - __uint_as_float(hi[e] << 16),
+                                        w[2 * e + 1] - __uint_as_float(hi[e] & 0xffff0000u));
+                }
+                mma<BF16>(acc[nt], xa[j], make_uint4(hi[0], hi[1], hi[2], hi[3]));
+                mma<BF16>(acc[nt], xa[j], make_uint4(lo[0], lo[1], lo[2], lo[3]));
+            }
+        }
+    }
+#pragma unroll
+    for (int nt = 0; nt < MAXT; ++nt)
+        if (nt < nt_used) red[wv][nt][lane] = acc[nt];
+    __syncthreads();
+    // wave nt sums output tile nt over the 8 waves and stores it
+    if (wv >= nt_used) return;
+    f32x4 t = red[0][wv][lane];
+#pragma unroll
+    for (int w = 1; w < GP_WAVES; ++w) {
+        const f32x4 u = red[w][wv][lane];
+        t[0] += u[0]; t[1] += u[1]; t[2] += u[2]; t[3] += u[3];
+    }
+    const int c = 16 * wv + l16;
+    if (c >= nout) return;
+    float* out = c < a.n0 ? a.out0 : a.out1;
+    const int n = c < a.n0 ? a.n0 : a.n1, cc = c < a.n0 ? c : c - a.n0;
+    const float bias = c < a.n0 ? (a.b0 ? a.b0[cc] : 0.f) : (a.b1 ? a.b1[cc] : 0.f);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const long tt = tok0 + 4 * lg + e;
+        if (tt < a.n_tok) out[tt * n + cc] = t[e] + bias;
+    }
+}
+
 int gate_project_dispatch(const GateProjArgs& a, hipStream_t stream) {
-    const long waves = (a.n_tok + 15) / 16;
-    hipLaunchKernelGGL(gate_project_kernel, dim3((unsigned)((waves + GP_WAVES - 1) / GP_WAVES)), dim3(64 * GP_WAVES),
-                       0, stream, a);
+    const long tiles = (a.n_tok + 15) / 16;
+    // up to 2048 tokens (128 workgroups of 8 waves) the chip is filled by splitting d; beyond, W is shared through
+    // LDS by the 8 token tiles of a workgroup, so its L2 traffic stays below that of x
+    if (a.n_tok <= 2048)
+        hipLaunchKernelGGL(gate_project_small_kernel, dim3((unsigned)tiles), dim3(64 * GP_WAVES), 0, stream, a);
+    else
+        hipLaunchKernelGGL(gate_project_kernel, dim3((unsigned)((tiles + GP_WAVES - 1) / GP_WAVES)),
+                           dim3(64 * GP_WAVES), 0, stream, a);
     return (int)hipGetLastError();
 }
 

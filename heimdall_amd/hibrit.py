@@ -64,22 +64,25 @@ def mem_inputs(self, x, q, k, pos):
     return qm, km, g, beta
 
 
-def _ft_bf16(self, name: str) -> torch.Tensor:
-    """The projection ``name`` (fq or fk, [nh, D, D]) transposed in bf16, as bf_mem_project reads it. Built on every
-    call (one small cast of H D^2 elements): a copy kept between calls would go stale on parameter writes that leave
-    no trace on the Parameter, such as ``p.data.copy_`` (the reference's apply_conversion, hibrit.py:798)."""
-    return getattr(self, name).detach().transpose(1, 2).to(torch.bfloat16).contiguous()
+def _f32(p: torch.Tensor) -> torch.Tensor:
+    """A parameter as a contiguous fp32 tensor (itself when it already is one: no copy, read where it lies)."""
+    p = p.detach()
+    return p if p.dtype == torch.float32 and p.is_contiguous() else p.float().contiguous()
 
 
-def _project_bf16(x: torch.Tensor, ft: torch.Tensor, scale: float) -> torch.Tensor:
-    """bf16 x [B, t, nh, D] -> scale * normalize(x_h f_h) as bf16 [B, t, nh, D] on bf_mem_project (ft = f_h^T in
-    bf16, [nh, D, D])."""
+def _project_bf16(x: torch.Tensor, f: torch.Tensor, scale: float, out_dtype=torch.bfloat16) -> torch.Tensor:
+    """bf16 x [B, t, nh, D] -> scale * normalize(x_h f_h) [B, t, nh, D] in out_dtype on bf_mem_project, which reads
+    the projection f [nh, D, D] as the module holds it (fp32) on every call: nothing is cached between calls, so
+    parameter writes of any kind (an optimizer step, ``p.data.copy_`` as the reference's apply_conversion makes,
+    hibrit.py:798) reach the next call."""
     b, t, nh, d = x.shape
     if x.stride(-1) != 1 or (b > 1 and x.stride(0) != t * x.stride(1)):
         x = x.contiguous()
-    out = torch.empty(b, t, nh, d, dtype=torch.bfloat16, device=x.device)
-    check(_lib.load().bf_mem_project(x.data_ptr(), b * t, nh, d, x.stride(1), x.stride(2), ft.data_ptr(), float(scale),
-                                     out.data_ptr(), _lib.DTYPE_BF16, stream_ptr(x.device)), "bf_mem_project")
+    out = torch.empty(b, t, nh, d, dtype=out_dtype, device=x.device)
+    f = _f32(f)
+    check(_lib.load().bf_mem_project(x.data_ptr(), b * t, nh, d, x.stride(1), x.stride(2), f.data_ptr(), float(scale),
+                                     out.data_ptr(), _lib.DTYPE_BF16, dtype_code(out_dtype), stream_ptr(x.device)),
+          "bf_mem_project")
     return out
 
 
@@ -106,13 +109,13 @@ def _gate_logits(self, x):
     return ab, z
 
 
-def _mem_inputs_bf16(self, ab, q, k, start: int):
-    """mem_inputs for bf16 activations (no autograd): qm, km from the fused projection kernel (bf16 out, fp32
+def _mem_inputs_bf16(self, ab, q, k, start: int, out_dtype=torch.bfloat16):
+    """mem_inputs for bf16 activations (no autograd): qm, km from the fused projection kernel (out_dtype out, fp32
     accumulation and norm), the gates g, beta in fp32 from the ab projection ``ab`` [B, t, 2G] by bf_mem_gates
     (``hibrit.py:327-334``)."""
     dh, G = self.c.dh, self.c.hkv
-    qm = _project_bf16(q, _ft_bf16(self, "fq"), dh ** -0.5)
-    km = _project_bf16(k, _ft_bf16(self, "fk"), 1.0)
+    qm = _project_bf16(q, self.fq, dh ** -0.5, out_dtype)
+    km = _project_bf16(k, self.fk, 1.0, out_dtype)
     b, t = ab.shape[:2]
     g = torch.empty(b, t, G, dtype=torch.float32, device=ab.device)
     beta = torch.empty_like(g)
@@ -158,8 +161,9 @@ def _ring_to(st: dict, kvdt: torch.dtype) -> None:
         st["ring_pos"] = st["ring_pos"].long().contiguous()
 
 
-def _decode(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memory):
-    """One token for every sequence: bf_decode_fwd (window, memory write on exit, read, mix, ring write)."""
+def _decode(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memory, zmix=None):
+    """One token for every sequence: bf_decode_fwd (window, memory write on exit, read, mix, ring write). ``zmix``:
+    the gamma logit mix(x) [B, H] fp32 if already computed."""
     c = self.c
     b = x.shape[0]
     H, G, D, w, r = c.h, c.hkv, c.dh, self.window, c.h // c.hkv
@@ -179,7 +183,10 @@ def _decode(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memo
     sv = sink_v.to(kvdt).contiguous() if ns else None
     _ring_to(st, kvdt)
     qrd = qr.to(torch.bfloat16 if qr.dtype == torch.bfloat16 else torch.float32).contiguous()
-    z = F.linear(x.float(), self.mix.weight.float(), self.mix.bias.float()).contiguous() if use_mem else None
+    z = None
+    if use_mem:
+        z = (zmix if zmix is not None else F.linear(x.float(), self.mix.weight.float(), self.mix.bias.float()))
+        z = z.reshape(b, -1).contiguous()
     mix_lse = self.mix_lse.float().contiguous() if use_mem else None
     mem_scale = self.mem_scale.float().contiguous() if use_mem else None
     qm_ = qm.contiguous() if use_mem else None
@@ -199,6 +206,10 @@ def _decode(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memo
     return o.view(b, 1, H, D)
 
 
+# Chunks of up to this many tokens over a cache run as consecutive decode steps. 1 (off): measured at B = 1, H = 24,
+# G = 4, D = 256, W = 2048 + 4, a t = 2 chunk costs 207 us through the chunk kernels and 261 us as two decode steps,
+# whose time is mostly host launch gaps between their six library calls.
+SMALL_CHUNK = 1
 BATCH_KEYS = ("sink_k", "sink_v", "ring_k", "ring_v", "ring_km", "ring_g", "ring_beta", "ring_pos", "S")
 
 
@@ -264,9 +275,14 @@ def student_batch(self, x, q, k, v, qr, kr, pos: torch.Tensor, cache: dict, memo
     kvdt = cache["ring_k"].dtype
     pos = pos.to(device=dev, dtype=torch.long).contiguous()
     # memory inputs without the sink mask of beta (position S passed), then the mask per sequence
-    qm, km, g, beta = self._mem_inputs(x, q, k, torch.full((1,), self.sinks, device=dev))
+    if all(z_.dtype == torch.bfloat16 for z_ in (q, k, qr, kr)):
+        ab, z = _gate_logits(self, x)
+        qm, km, g, beta = _mem_inputs_bf16(self, ab, q, k, self.sinks, torch.float32)
+    else:
+        qm, km, g, beta = self._mem_inputs(x, q, k, torch.full((1,), self.sinks, device=dev))
+        z = F.linear(x.float(), self.mix.weight.float(), self.mix.bias.float())
     beta = beta * (pos >= self.sinks).float()[:, None, None]
-    z = F.linear(x.float(), self.mix.weight.float(), self.mix.bias.float()).contiguous()
+    z = z.reshape(b, H).contiguous()
     f32 = lambda t_: t_.float().contiguous()
     qm_, km_, g_, b_ = f32(qm[:, 0]), f32(km[:, 0]), f32(g[:, 0]), f32(beta[:, 0])
     qrd = qr[:, :, 0].to(torch.bfloat16 if qr.dtype == torch.bfloat16 else torch.float32).contiguous()
@@ -306,7 +322,12 @@ def student(self, x, q, k, v, qr, kr, start: int, cache: Optional[dict], memory:
     w, s = self.window, self.sinks
     dev = x.device
     st = cache if cache is not None else {}
-    pos = torch.arange(start, start + t, device=dev)
+    if 1 < t <= SMALL_CHUNK and "ring_k" in st:
+        # a few tokens over a cache (an MTP verification, hibrit.py:758): one decode step each, the reference's
+        # chunking invariance (a chunk equals its tokens one at a time); a decode step splits the window over
+        # the chip, where the chunk kernels would run one workgroup per query head
+        return torch.cat([student(self, *(z[:, i:i + 1] for z in (x, q, k, v)), qr[:, :, i:i + 1], kr[:, :, i:i + 1],
+                                  start + i, st, memory) for i in range(t)], 1)
     vt = v.transpose(1, 2)
     sink_k, sink_v = st.get("sink_k"), st.get("sink_v")
     n_new = max(0, min(t, s - start))
@@ -314,11 +335,12 @@ def student(self, x, q, k, v, qr, kr, start: int, cache: Optional[dict], memory:
         sink_k = kr[:, :, :n_new] if sink_k is None else torch.cat((sink_k, kr[:, :, :n_new]), 2)
         sink_v = vt[:, :, :n_new] if sink_v is None else torch.cat((sink_v, vt[:, :, :n_new]), 2)
     zmix = None
-    if t > 1 and all(z.dtype == torch.bfloat16 for z in (q, k, qr, kr)):
+    if all(z.dtype == torch.bfloat16 for z in (q, k, qr, kr)):
+        # fused: the gate projections, qm / km (bf16 for a chunk's memory branch, fp32 for the decode step), gates
         ab, zmix = _gate_logits(self, x)
-        qm, km, g, beta = _mem_inputs_bf16(self, ab, q, k, start)
+        qm, km, g, beta = _mem_inputs_bf16(self, ab, q, k, start, torch.bfloat16 if t > 1 else torch.float32)
     else:
-        qm, km, g, beta = self._mem_inputs(x, q, k, pos)
+        qm, km, g, beta = self._mem_inputs(x, q, k, torch.arange(start, start + t, device=dev))
     if "ring_k" not in st:
         # a prefill of t >= W tokens from position 0 writes every ring slot (bf_layer_prefill_fwd's write-back) and
         # reads none before that
@@ -326,7 +348,7 @@ def student(self, x, q, k, v, qr, kr, start: int, cache: Optional[dict], memory:
         st.update(_new_ring(b, c.hkv, w, c.dh, kr.dtype, vt.dtype, dev, overwritten=full))
     if t == 1:
         o = _decode(self, x, qr, kr[:, :, 0], v[:, 0], qm[:, 0], km[:, 0], g[:, 0], beta[:, 0], start, st, sink_k,
-                    sink_v, memory)
+                    sink_v, memory, zmix)
     else:
         o = _prefill(self, x, qr, kr, v, qm, km, g, beta, start, st, sink_k, sink_v, memory, zmix)
     st["sink_k"], st["sink_v"] = sink_k, sink_v

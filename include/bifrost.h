@@ -200,13 +200,13 @@ int bf_window_fwd(int B, int G, int R, int D, int T, int W, int sinks, int64_t s
  * qm = normalize(q_h fq_h) * D^-1/2 (x = q, scale = D^-1/2) and km = normalize(k_g fk_g) (x = k, scale = 1).
  *
  *   x: bf16, token t / head h at x + t * x_st + h * x_sh elements, D contiguous; n_tok tokens, nh heads
- *   ft [nh][D][D] bf16: the projections transposed, ft[h][j][i] = F_h[i][j]
- *   out [n_tok][nh][D] bf16
- * Arithmetic: bf16 MFMA with fp32 accumulation, norm and scale in fp32. in_dtype must be BF_DTYPE_BF16 (fp32 runs
- * keep the reference's fp32 projections).
+ *   f [nh][D][D] f32: the projections as the module holds them (fq, fk), f[h][i][j] = F_h[i][j]
+ *   out [n_tok][nh][D] in out_dtype (bf16 or f32)
+ * Arithmetic: F_h rounded to bf16 (nearest even), bf16 MFMA with fp32 accumulation, norm and scale in fp32.
+ * in_dtype must be BF_DTYPE_BF16 (fp32 runs keep the reference's fp32 projections).
  */
-int bf_mem_project(const void* x, int64_t n_tok, int nh, int D, int64_t x_st, int64_t x_sh, const void* ft,
-                   float scale, void* out, int in_dtype, void* stream);
+int bf_mem_project(const void* x, int64_t n_tok, int nh, int D, int64_t x_st, int64_t x_sh, const float* f,
+                   float scale, void* out, int in_dtype, int out_dtype, void* stream);
 
 /*
  * Memory-branch gates of the converted layer, replacing the gate lines of HybridAttention._mem_inputs

@@ -215,3 +215,19 @@ def test_window_attention_and_window_binding(dev):
                              pos.to(dev))
     o2_ref, lse2_ref = owin.window_attention_lse(q2, ext_k, ext_v, ext_pos, sk, sv, pos, 16, 3)
     assert rel(o2, o2_ref) < 1e-4 and (lse2.cpu() - lse2_ref).abs().max() < 1e-4
+
+
+def test_window_inputs_requiring_grad_raise(dev):
+    """The conversion's stage B (Heimdall/heimdall/donustur_hibrit.py:441-470) trains every converted layer end to end
+    through HybridLM.hidden, so a layer's qr, kr and v require grad there; the window branch has no backward in this
+    library, and the student refuses such inputs with BifrostError (it does not return a result whose window gradient
+    would be missing). Stage A's case, the memory inputs and new parameters only, is differentiable (the tests above)."""
+    from heimdall_amd import hibrit
+    from heimdall_amd._device import BifrostError
+    m = make_core(4, 2, 64, 32, window=8, sinks=2).to(dev)
+    args = [z.to(dev) for z in make_inputs(m, 1, 20)]
+    for i in (3, 4, 5):                                  # v, qr, kr
+        a = [z.detach().clone() for z in args]
+        a[i].requires_grad_(True)
+        with pytest.raises(BifrostError, match="window branch has no backward"):
+            hibrit.student(m, *a, 0, {})

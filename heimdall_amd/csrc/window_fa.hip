@@ -5,18 +5,21 @@
 // p = start + i and sees the sinks j < n_sinks with j <= p and the keys kp with S <= kp <= p, p - kp < W (the ring
 // for kp < start, slot kp mod W valid iff ring_pos[slot] == kp; the chunk for kp >= start).
 //
-// Work split. One workgroup = 128 consecutive queries of one query head, 4 waves x 32 queries. A wave holds its 32
-// queries as two 16-query MFMA tiles, so every K / V fragment it reads from LDS feeds two v_mfma_f32_16x16x32_bf16:
-// 32 FLOP per LDS byte, above the ~21 FLOP/B at which gfx950's LDS read rate (~165 B/clk/CU) and MFMA rate meet.
+// Work split. One workgroup = 128 consecutive queries of one query head. D <= 128: 4 waves x 32 queries, held as two
+// 16-query MFMA tiles, so every K / V fragment a wave reads from LDS feeds two v_mfma_f32_16x16x32_bf16. D = 256:
+// 8 waves x 16 queries, so that two waves fit each SIMD's registers.
 //   S^T = K Q^T      A = K rows (LDS),             B = Q (registers, loaded once)
 //   O^T += V^T P^T   A = V^T via ds_read_b64_tr_b16 of the row-major V tile,  B = P straight from the S registers
-// Scores are transposed so that a query's softmax statistics live in its own lane column (max: two cross-lane
-// steps per block; sum: per-lane partials reduced once at the end). The running max is raised only when a block's
-// max exceeds it by more than 8 (log2 units), so O is rescaled rarely and P stays <= 2^8.
+// Scores are transposed so that a query's softmax statistics live in its own lane column (max: two lane swaps per
+// block; sum: per-lane partials reduced once at the end). The scale D^-1/2 log2(e) is applied inside the exponent
+// (one FMA per score). The running max is raised only when a block's max exceeds it by more than 8 (log2 units), so
+// O is rescaled rarely and P stays <= 2^8.
 //
 // Keys come in blocks of 64 rows from one contiguous source (sinks, ring before / after its wrap point, chunk). A
 // block's K and V tiles are copied global -> LDS with buffer_load ... lds (no registers; one buffer descriptor per
 // source, lanes of other sources masked off), double-buffered: block i+1 is in flight while block i is computed.
+// When block i+1 is all chunk rows, a wave issues its copies one per step of its S product (a base offset and a
+// scalar step per copy), so no wave stalls on a burst of copies before its first MFMA.
 // Buffer rather than global loads: the compiler counts a global load into LDS as a flat access that may touch LDS
 // and then drains every LDS wait to zero while one is in flight, which serialised the fragment reads. Per wave, blocks no query of the wave can see are skipped and blocks every
 // query sees skip the mask. Workgroups are mapped XCD-aware: consecutive workgroups of one XCD take the R query
@@ -67,6 +70,20 @@ __device__ __forceinline__ uint2 fa_tr16(const char* p) {
     return make_uint2((uint16_t)v[0] | ((uint32_t)(uint16_t)v[1] << 16), (uint16_t)v[2] | ((uint32_t)(uint16_t)v[3] << 16));
 }
 
+
+// max / sum of a value over lanes l, l ^ 16, l ^ 32, l ^ 48 by lane swaps (v_permlane16_swap, v_permlane32_swap)
+__device__ __forceinline__ float fa_max4(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float fa_sum4(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 
 }  // namespace
 
@@ -151,8 +168,9 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
     const rsrc_t rcv = make_rsrc(cv, (uint32_t)(((long)(a.T - 1) * a.v_st + D) * 2));
     const uint32_t kst_b = (uint32_t)(a.k_st * 2), vst_b = (uint32_t)(a.v_st * 2);
     const uint32_t crow_max = (uint32_t)(p_last - start);          // chunk row of the last query
-    auto dma = [](rsrc_t r, void* dst, uint32_t off) {   // 16 bytes at byte offset off (per lane) -> dst + 16 lane
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, off, 0, 0, 0);
+    // 16 bytes at byte offset off + soff (per lane; soff wave-uniform) -> dst + 16 lane
+    auto dma = [](rsrc_t r, void* dst, uint32_t off, uint32_t soff = 0u) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, off, soff, 0, 0);
     };
     auto stage = [&](FaTile<D>& t, int i) {
         char* tk = reinterpret_cast<char*>(t.k) + wv * 1024;
@@ -239,6 +257,12 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
         for (int dt = 0; dt < NDT; ++dt) o[dt][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     const float cs = FA_LOG2E * rsqrtf((float)D);             // score scale in log2 units
+    // the next block's copy plan when it is spread over the S product (set per block by step)
+    bool spread = false;
+    uint32_t off_k = 0, off_v = 0;
+    char* tk_next = nullptr;
+    char* tv_next = nullptr;
+    const uint32_t step_k = (uint32_t)RPI * kst_b, step_v = (uint32_t)RPI * vst_b;
 
     auto compute = [&](const FaTile<D>& t, int i, uint64_t vmask) {
         const bool sink = has_sink && i == 0;
@@ -273,6 +297,15 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
             for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
                 for (int qt = 0; qt < QT; ++qt) mma<BF16>(s[kt][qt], ak[kt], fq[qt][kf]);
+            if (spread) {                                    // copies j: K rows row0 + RPI j, then V rows
+                constexpr int CPS = (2 * NLD + NKD - 1) / NKD;
+#pragma unroll
+                for (int c = 0; c < CPS; ++c) {
+                    const int j = kf * CPS + c;
+                    if (j < NLD) dma(rck, tk_next + NW * j * 1024, off_k, j * step_k);
+                    else if (j < 2 * NLD) dma(rcv, tv_next + NW * (j - NLD) * 1024, off_v, (j - NLD) * step_v);
+                }
+            }
             if (kf + 1 < NKD) {
 #pragma unroll
                 for (int kt = 0; kt < 4; ++kt) ak[kt] = an[kt];
@@ -280,15 +313,8 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
             __builtin_amdgcn_sched_barrier(0);
         }
 
-        // scale (+ mask): element (kt, qt, e) is key row 16 kt + 4 lg + e, query 16 qt + l16 of the wave
-        if (full) {
-#pragma unroll
-            for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-                for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) s[kt][qt][e] *= cs;
-        } else {
+        // mask: element (kt, qt, e) is key row 16 kt + 4 lg + e, query 16 qt + l16 of the wave
+        if (!full) {
             const long dq = qw0 - kp0;
             const int base = (int)max(min(dq, (long)(1 << 30)), -(long)(1 << 30)) + l16 - 4 * lg;
             const uint64_t vm = vmask >> (4 * lg);
@@ -300,7 +326,7 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
                     for (int e = 0; e < 4; ++e) {
                         const int rel = base + 16 * (qt - kt) - e;
                         const bool vis = ((vm >> (16 * kt + e)) & 1ull) && rel >= 0 && (sink || rel < a.W);
-                        s[kt][qt][e] = vis ? s[kt][qt][e] * cs : -INFINITY;
+                        s[kt][qt][e] = vis ? s[kt][qt][e] : -INFINITY;
                     }
         }
 
@@ -312,8 +338,7 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
             for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) bm = fmaxf(bm, s[kt][qt][e]);
-            bm = fmaxf(bm, __shfl_xor(bm, 16));
-            bm = fmaxf(bm, __shfl_xor(bm, 32));
+            bm = fa_max4(bm) * cs;
             const bool up = bm > m[qt] + FA_SLACK;
             if (__builtin_amdgcn_ballot_w64(up)) {
                 const float mn = up ? bm : m[qt];
@@ -331,7 +356,7 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
             for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float p = __builtin_amdgcn_exp2f(s[kt][qt][e] - msub);
+                    const float p = __builtin_amdgcn_exp2f(fmaf(s[kt][qt][e], cs, -msub));
                     s[kt][qt][e] = p;
                     ls += p;
                 }
@@ -370,6 +395,8 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
 
     // ---- main loop over key blocks, two tiles in turn. The next block is staged unconditionally (the last block
     // re-stages itself into the idle tile), so the compiler's wait counts never drain it before the current compute.
+    // Its copies are spread over the S product when they need no clamping (all rows chunk rows up to the last query)
+    // and the wave computes block i; a wave that sees nothing of block i skips its S product and copies at once.
     uint2 rp = load_rp(0);
     stage(t0, 0);
     auto step = [&](FaTile<D>& tc, FaTile<D>& tn, int i) {
@@ -378,7 +405,24 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
         const uint64_t vmask = __builtin_amdgcn_ballot_w64(valid_row(i, rp));
         const int inext = i + 1 < nblk ? i + 1 : i;
         rp = load_rp(inext);
-        stage(tn, inext);
+        {
+            const bool sink = has_sink && i == 0;
+            const long kp0 = sink ? 0 : kp_lo + (long)(i - has_sink) * FA_KB;
+            const long kp1 = kp0 + (64 - __builtin_clzll(vmask | 1ull)) - 1;
+            const bool none = nqw == 0 || vmask == 0 || kp0 > qw1 || (!sink && qw0 - kp1 >= a.W);   // as in compute
+            const long kpb = kp_lo + (long)(inext - has_sink) * FA_KB;
+            spread = !none && !(has_sink && inext == 0) && (kpb >= start || !rk) &&
+                     kpb + FA_KB - 1 - start <= (long)crow_max;
+            if (spread) {
+                const uint32_t rb = (uint32_t)(kpb - start) + (uint32_t)row0;
+                off_k = __umul24(rb, kst_b) + kb0;
+                off_v = __umul24(rb, vst_b) + vb0;
+                tk_next = reinterpret_cast<char*>(tn.k) + wv * 1024;
+                tv_next = reinterpret_cast<char*>(tn.v) + wv * 1024;
+            } else {
+                stage(tn, inext);
+            }
+        }
         compute(tc, i, vmask);
     };
     for (int i = 0;;) {
@@ -393,9 +437,7 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
     const float lnW = logf((float)a.W);
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-        float lt = l[qt];
-        lt += __shfl_xor(lt, 16);
-        lt += __shfl_xor(lt, 32);
+        const float lt = fa_sum4(l[qt]);
         const int qi = QW * wv + 16 * qt + l16;
         if (qi >= nq) continue;
         const long tq = qi0 + qi;

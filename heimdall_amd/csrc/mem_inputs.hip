@@ -9,8 +9,11 @@
 // each of the 4 waves computes 16 tokens x D outputs per tile
 // as Y^T = F_h^T X^T with v_mfma_f32_16x16x32_bf16 (A = rows of F_h^T from LDS, read 8 MFMAs ahead; B = the token
 // rows of x from global memory, loaded two tiles ahead), so every lane holds 4 consecutive outputs of one token: the
-// row norm is a sum over the lane's values and two cross-lane steps, and the result is stored 8 (bf16) or 16 (fp32)
-// bytes at a time. The pass reads x and writes y once (806 MB at T = 32768, 24 heads, D = 256, bf16 out).
+// row norm is a sum over the lane's values and two cross-lane steps. bf16 results go through a per-wave LDS
+// buffer so that every store writes whole output rows (512 bytes at D = 256; stored straight from the fragments,
+// 32-byte pieces of 16 rows per instruction, the qm pass took 240 us instead of 180); fp32 results are stored
+// 16 bytes per lane from the fragments. The pass reads x and writes y once (806 MB at T = 32768, 24 heads,
+// D = 256, bf16 out).
 #include "bf_common.h"
 #include "bf_internal.h"
 
@@ -33,6 +36,8 @@ __global__ __launch_bounds__(64 * MP_WAVES, 1) void mem_project_kernel(MemProjAr
     constexpr int NKD = D / 32, NDT = D / 16;
     constexpr int NKB = NKD < 4 ? NKD : 4;
     __shared__ __align__(16) uint16_t ft[D * D];
+    // each wave's 16 output rows (bf16), 16-byte blocks permuted by the row (r & 15), for whole-row stores
+    __shared__ __align__(16) uint16_t ot[MP_WAVES][16 * D];
 
     const int h = blockIdx.x % a.nh, tg = blockIdx.x / a.nh, ntg = gridDim.x / a.nh;
     const int lane = lane_id(), wv = wave_id(), l16 = lane & 15, lg = lane >> 4;
@@ -122,20 +127,33 @@ __global__ __launch_bounds__(64 * MP_WAVES, 1) void mem_project_kernel(MemProjAr
         const long tok = t * MP_TILE + 16 * wv + l16;
         if (tok < a.n_tok) {
             if (a.out_dtype == DT_BF16) {
-                uint16_t* orow = reinterpret_cast<uint16_t*>(a.out) + (tok * a.nh + h) * D;
-#pragma unroll
-                for (int jt = 0; jt < NDT; ++jt) {
-                    uint2 v;
-                    v.x = pack_bf16x2(acc[jt][0] * inv, acc[jt][1] * inv);
-                    v.y = pack_bf16x2(acc[jt][2] * inv, acc[jt][3] * inv);
-                    *reinterpret_cast<uint2*>(orow + 16 * jt + 4 * lg) = v;
-                }
             } else {
                 float* orow = reinterpret_cast<float*>(a.out) + (tok * a.nh + h) * D;
 #pragma unroll
                 for (int jt = 0; jt < NDT; ++jt)
                     *reinterpret_cast<float4*>(orow + 16 * jt + 4 * lg) =
                         make_float4(acc[jt][0] * inv, acc[jt][1] * inv, acc[jt][2] * inv, acc[jt][3] * inv);
+            }
+        }
+        if (a.out_dtype == DT_BF16) {
+            char* ow = reinterpret_cast<char*>(ot[wv]);
+            constexpr int RB = D * 2, NB = RB / 16;
+#pragma unroll
+            for (int jt = 0; jt < NDT; ++jt) {
+                uint2 v;
+                v.x = pack_bf16x2(acc[jt][0] * inv, acc[jt][1] * inv);
+                v.y = pack_bf16x2(acc[jt][2] * inv, acc[jt][3] * inv);
+                const int blk = (2 * jt + (lg >> 1)) ^ (l16 & 15 & (NB - 1));
+                *reinterpret_cast<uint2*>(ow + l16 * RB + 16 * blk + 8 * (lg & 1)) = v;
+            }
+            constexpr int RPI = 64 / NB;                     // rows per 64-lane pass
+#pragma unroll
+            for (int p = 0; p < 16 / RPI; ++p) {
+                const int r = p * RPI + lane / NB, bk = lane % NB;
+                const long tk = t * MP_TILE + 16 * wv + r;
+                const uint4 v = *reinterpret_cast<const uint4*>(ow + r * RB + 16 * (bk ^ (r & 15 & (NB - 1))));
+                if (tk < a.n_tok)
+                    *reinterpret_cast<uint4*>(reinterpret_cast<uint16_t*>(a.out) + (tk * a.nh + h) * D + 8 * bk) = v;
             }
         }
 #pragma unroll
@@ -149,7 +167,7 @@ __global__ __launch_bounds__(64 * MP_WAVES, 1) void mem_project_kernel(MemProjAr
 int mem_project_dispatch(const MemProjArgs& a, hipStream_t stream) {
     const long ntiles = (a.n_tok + MP_TILE - 1) / MP_TILE;
     // one round of workgroups over the 256 CUs (F_h^T takes D * D * 2 bytes of LDS per workgroup)
-    const long per_cu = (long)(160 * 1024) / ((long)a.D * a.D * 2);
+    const long per_cu = (long)(160 * 1024) / ((long)a.D * a.D * 2 + (long)MP_WAVES * 16 * a.D * 2);
     const long want = (256 * (per_cu > 0 ? per_cu : 1)) / a.nh;
     const int ntg = (int)(ntiles < want ? ntiles : (want > 0 ? want : 1));
     const dim3 grid((unsigned)(a.nh * (ntg > 0 ? ntg : 1))), block(64 * MP_WAVES);

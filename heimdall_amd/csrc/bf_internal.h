@@ -184,6 +184,7 @@ struct MemGatesArgs {
     long n_tok, T, ab_st;           // tokens, tokens per sequence, row stride
     int G, sinks;
     long start;                     // position of each sequence's first token
+    const int64_t* pos_arr;         // or null: sequence b's first token at pos_arr[b] (device memory)
     const float *A_log, *dt_bias, *decay_mask;
     float *g, *beta;                // [n_tok][G]
 };

@@ -275,6 +275,98 @@ int bf_decode_fwd_batch(int B, int G, int R, int D, int W, int sinks, const int6
     return bf::decode_dispatch(a, static_cast<hipStream_t>(stream));
 }
 
+// One decode step of the converted layer from the layer's own inputs (bf16 activations): the gate projections, the
+// memory projections and gates, then the decode kernels, on one stream and one workspace. Intermediates (ab, z, qm,
+// km, g, beta: the same values the separate entry points produce) sit at the head of the workspace, the decode
+// workspace after them.
+namespace {
+struct StudentDecodeWs {
+    size_t ab, z, qm, km, g, beta, dec, total;
+};
+int student_decode_layout(int B, int H, int G, int D, int W, StudentDecodeWs& l) {
+    if (B <= 0 || G <= 0 || H <= 0 || H % G || W <= 0) return BF_STATUS_INVALID;
+    size_t dec = 0;
+    const int st = bf_decode_workspace_size(B, G, H / G, D, W, &dec);
+    if (st) return st;
+    size_t o = 0;
+    auto take = [&](size_t n) { const size_t at = o; o += align256(n); return at; };
+    l.ab = take((size_t)B * 2 * G * sizeof(float));
+    l.z = take((size_t)B * H * sizeof(float));
+    l.qm = take((size_t)B * H * D * sizeof(float));
+    l.km = take((size_t)B * G * D * sizeof(float));
+    l.g = take((size_t)B * G * sizeof(float));
+    l.beta = take((size_t)B * G * sizeof(float));
+    l.dec = take(dec);
+    l.total = o;
+    return BF_STATUS_OK;
+}
+}  // namespace
+
+int bf_student_decode_workspace_size(int B, int H, int G, int D, int W, size_t* bytes) {
+    if (!bytes) return BF_STATUS_INVALID;
+    StudentDecodeWs l{};
+    const int st = student_decode_layout(B, H, G, D, W, l);
+    if (st) return st;
+    *bytes = l.total;
+    return BF_STATUS_OK;
+}
+
+int bf_student_decode(int B, int H, int G, int D, int W, int sinks, int64_t pos, const int64_t* pos_arr, int memory,
+                      int d_model, const void* x, const void* q, const void* k, const void* v, const void* qr,
+                      const void* kr, const float* fq, const float* fk, const float* w_ab, const float* b_ab,
+                      const float* w_mix, const float* b_mix, const float* A_log, const float* dt_bias,
+                      const float* decay_mask, const float* mix_lse, const float* mem_scale, void* sink_k,
+                      void* sink_v, int n_sinks, void* ring_k, void* ring_v, float* ring_km, float* ring_g,
+                      float* ring_beta, int64_t* ring_pos, float* state, float* o, void* workspace,
+                      size_t workspace_bytes, void* stream) {
+    StudentDecodeWs l{};
+    int st = student_decode_layout(B, H, G, D, W, l);
+    if (st) return st;
+    if (!supported_dim(D)) return BF_STATUS_UNSUPPORTED;
+    if (d_model <= 0 || d_model % 8 || 2 * G + H > bf::GP_MAX_OUT || sinks < 0 || sinks > 63 || (!pos_arr && pos < 0))
+        return BF_STATUS_INVALID;
+    if (!x || !q || !k || !v || !qr || !kr || !fq || !fk || !w_ab || !w_mix || !A_log || !dt_bias || !decay_mask ||
+        !mix_lse || !mem_scale || !ring_k || !ring_v || !ring_km || !ring_g || !ring_beta || !ring_pos || !o)
+        return BF_STATUS_INVALID;
+    auto al16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+    if (!al16(x) || !al16(w_ab) || !al16(w_mix)) return BF_STATUS_INVALID;
+    if (!workspace || workspace_bytes < l.total) return BF_STATUS_WORKSPACE;
+    char* ws = static_cast<char*>(workspace);
+    float *ab = reinterpret_cast<float*>(ws + l.ab), *z = reinterpret_cast<float*>(ws + l.z);
+    float *qm = reinterpret_cast<float*>(ws + l.qm), *km = reinterpret_cast<float*>(ws + l.km);
+    float *g = reinterpret_cast<float*>(ws + l.g), *beta = reinterpret_cast<float*>(ws + l.beta);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    {
+        bf::GateProjArgs a{};
+        a.x = static_cast<const uint16_t*>(x); a.n_tok = B; a.x_st = d_model; a.d = d_model;
+        a.w0 = w_ab; a.b0 = b_ab; a.n0 = 2 * G; a.out0 = ab; a.w1 = w_mix; a.b1 = b_mix; a.n1 = H; a.out1 = z;
+        if ((st = bf::gate_project_dispatch(a, s))) return st;
+    }
+    {
+        bf::MemProjArgs a{};
+        a.x = q; a.n_tok = B; a.nh = H; a.D = D; a.x_st = (long)H * D; a.x_sh = D;
+        a.f = fq; a.scale = 1.f / sqrtf((float)D); a.out = qm; a.out_dtype = BF_DTYPE_F32;
+        if ((st = bf::mem_project_dispatch(a, s))) return st;
+        a.x = k; a.nh = G; a.x_st = (long)G * D; a.f = fk; a.scale = 1.f; a.out = km;
+        if ((st = bf::mem_project_dispatch(a, s))) return st;
+    }
+    {
+        bf::MemGatesArgs a{};
+        a.ab = ab; a.n_tok = B; a.T = 1; a.ab_st = 2 * G; a.G = G; a.sinks = sinks; a.start = pos_arr ? 0 : pos;
+        a.pos_arr = pos_arr; a.A_log = A_log; a.dt_bias = dt_bias; a.decay_mask = decay_mask; a.g = g; a.beta = beta;
+        if ((st = bf::mem_gates_dispatch(a, s))) return st;
+    }
+    void* dws = ws + l.dec;
+    const size_t dn = workspace_bytes - l.dec;
+    if (pos_arr)
+        return bf_decode_fwd_batch(B, G, H / G, D, W, sinks, pos_arr, memory, BF_DTYPE_BF16, BF_DTYPE_BF16, qr, qm,
+                                   kr, v, km, g, beta, z, mix_lse, mem_scale, sink_k, sink_v, ring_k, ring_v, ring_km,
+                                   ring_g, ring_beta, ring_pos, state, o, nullptr, dws, dn, stream);
+    return bf_decode_fwd(B, G, H / G, D, W, sinks, pos, memory, BF_DTYPE_BF16, BF_DTYPE_BF16, qr, qm, kr, v, km, g,
+                         beta, z, mix_lse, mem_scale, sink_k, sink_v, n_sinks, ring_k, ring_v, ring_km, ring_g,
+                         ring_beta, ring_pos, state, o, nullptr, dws, dn, stream);
+}
+
 int bf_decode_fwd_noalloc(int B, int G, int R, int D, int W, int sinks, int64_t pos, int memory, int kv_dtype,
                           int q_dtype, const void* qr, const float* qm, const void* kr, const void* v, const float* km,
                           const float* g_new, const float* beta_new, const float* z, const float* mix_lse,

@@ -191,7 +191,7 @@ __global__ __launch_bounds__(256) void mem_gates_kernel(MemGatesArgs a) {
     const float x = row[j] + a.dt_bias[j];
     const float sp = x > 20.f ? x : log1pf(expf(x));            // softplus, torch's default threshold
     a.g[e] = -expf(a.A_log[j]) * sp * a.decay_mask[j];
-    const long pos = a.start + t % a.T;
+    const long pos = (a.pos_arr ? a.pos_arr[t / a.T] : a.start) + t % a.T;
     a.beta[e] = pos >= a.sinks ? 1.f / (1.f + expf(-row[a.G + j])) : 0.f;
 }
 

@@ -257,6 +257,47 @@ def batch_cache_get(self, bc: dict, i: int, pos: int) -> dict:
     return out
 
 
+def _fused_decode_ok(self, x, q, k, v, qr, kr) -> bool:
+    """bf_student_decode covers this step: bf16 activations, a d_model the gate projection kernel takes, and the
+    kernels' head limits."""
+    c = self.c
+    return (all(z_.dtype == torch.bfloat16 for z_ in (x, q, k, v, qr, kr)) and x.shape[-1] % 8 == 0
+            and 2 * c.hkv + c.h <= 64 and c.h % c.hkv == 0 and c.h // c.hkv <= 8 and c.dh in (64, 128, 256))
+
+
+def _student_decode(self, x, q, k, v, qr, kr, pos, pos_arr, st, sink_k, sink_v, ns, S, memory):
+    """One bf_student_decode call (gate and memory projections, gates, decode step) for one token per sequence.
+    pos_arr None: every sequence at ``pos`` with the cache of ``_student``; otherwise the batch cache of
+    ``student_batch``. Returns o [B, 1, H, D] fp32."""
+    c = self.c
+    b = x.shape[0]
+    H, G, D, w = c.h, c.hkv, c.dh, self.window
+    dev = x.device
+    xs = x.reshape(b, -1)
+    if not xs.is_contiguous() or xs.data_ptr() % 16:
+        xs = xs.contiguous()
+    q_, k_, v_ = q.reshape(b, H, D).contiguous(), k.reshape(b, G, D).contiguous(), v.reshape(b, G, D).contiguous()
+    qr_, kr_ = qr[:, :, 0].contiguous(), kr[:, :, 0].contiguous()
+    f32 = lambda p_: p_.detach() if p_.dtype == torch.float32 and p_.is_contiguous() else p_.detach().float().contiguous()
+    ab_b = None if self.ab.bias is None else f32(self.ab.bias)
+    mix_b = None if self.mix.bias is None else f32(self.mix.bias)
+    prm = (f32(self.fq), f32(self.fk), f32(self.ab.weight), ab_b, f32(self.mix.weight), mix_b, f32(self.A_log),
+           f32(self.dt_bias), f32(self.decay_mask), f32(self.mix_lse), f32(self.mem_scale))
+    o = torch.empty(b, H, D, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    nbytes = _lib.ctypes.c_size_t(0)
+    check(lib.bf_student_decode_workspace_size(b, H, G, D, w, _lib.ctypes.byref(nbytes)),
+          "bf_student_decode_workspace_size")
+    ws = workspace(nbytes.value, dev)
+    ptr = lambda t_: t_.data_ptr() if t_ is not None else None
+    check(lib.bf_student_decode(b, H, G, D, w, self.sinks, pos, ptr(pos_arr), int(memory), xs.shape[1], ptr(xs),
+                                ptr(q_), ptr(k_), ptr(v_), ptr(qr_), ptr(kr_), *(ptr(t_) for t_ in prm),
+                                ptr(sink_k), ptr(sink_v), ns, ptr(st["ring_k"]), ptr(st["ring_v"]), ptr(st["ring_km"]),
+                                ptr(st["ring_g"]), ptr(st["ring_beta"]), ptr(st["ring_pos"]), ptr(S), ptr(o), ptr(ws),
+                                ws.numel(), stream_ptr(dev)), "bf_student_decode")
+    return o.view(b, 1, H, D)
+
+
 def student_batch(self, x, q, k, v, qr, kr, pos: torch.Tensor, cache: dict, memory: bool = True):
     """One token for each of B sequences at its own position (continuous batching; llama.cpp's multi-sequence ubatch,
     ``bifrost.patch:841-884``): per sequence the result and the cache update of ``_student`` with t == 1
@@ -274,6 +315,9 @@ def student_batch(self, x, q, k, v, qr, kr, pos: torch.Tensor, cache: dict, memo
     dev = x.device
     kvdt = cache["ring_k"].dtype
     pos = pos.to(device=dev, dtype=torch.long).contiguous()
+    if kvdt == torch.bfloat16 and _fused_decode_ok(self, x, q, k, v, qr, kr):
+        return _student_decode(self, x, q, k, v, qr, kr, 0, pos, cache, cache["sink_k"], cache["sink_v"],
+                               self.sinks, cache["S"], memory)
     # memory inputs without the sink mask of beta (position S passed), then the mask per sequence
     if all(z_.dtype == torch.bfloat16 for z_ in (q, k, qr, kr)):
         ab, z = _gate_logits(self, x)
@@ -334,6 +378,24 @@ def student(self, x, q, k, v, qr, kr, start: int, cache: Optional[dict], memory:
     if n_new:
         sink_k = kr[:, :, :n_new] if sink_k is None else torch.cat((sink_k, kr[:, :, :n_new]), 2)
         sink_v = vt[:, :, :n_new] if sink_v is None else torch.cat((sink_v, vt[:, :, :n_new]), 2)
+    if t == 1 and _fused_decode_ok(self, x, q, k, v, qr, kr):
+        if "ring_k" not in st:
+            st.update(_new_ring(b, c.hkv, w, c.dh, torch.bfloat16, torch.bfloat16, dev))
+        _ring_to(st, torch.bfloat16)
+        S = None
+        if memory and start + 1 > w:
+            S = st.get("S")
+            if S is None:
+                S = torch.zeros(b, c.hkv, c.dh, c.dh, dtype=torch.float32, device=dev)
+            elif not (S.dtype == torch.float32 and S.is_contiguous()):
+                S = S.float().contiguous()
+            st["S"] = S
+        ns = 0 if sink_k is None else sink_k.size(2)
+        sk = sink_k.to(torch.bfloat16).contiguous() if ns else None
+        sv = sink_v.to(torch.bfloat16).contiguous() if ns else None
+        o = _student_decode(self, x, q, k, v, qr, kr, start, None, st, sk, sv, ns, S, memory)
+        st["sink_k"], st["sink_v"] = sink_k, sink_v
+        return o
     zmix = None
     if all(z.dtype == torch.bfloat16 for z in (q, k, qr, kr)):
         # fused: the gate projections, qm / km (bf16 for a chunk's memory branch, fp32 for the decode step), gates

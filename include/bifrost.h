@@ -151,6 +151,33 @@ int bf_decode_fwd_batch(int B, int G, int R, int D, int W, int sinks, const int6
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * One decode step of the converted layer from the layer's own inputs, for bf16 activations: _student with t == 1
+ * (Heimdall/heimdall/hibrit.py:363-424) including its _mem_inputs (:327-334) and the gamma logit mix(x) (:409), in
+ * one call. It runs the kernels of bf_gate_project (ab and mix), bf_mem_project (qm with scale D^-1/2 and km, fp32),
+ * bf_mem_gates and then bf_decode_fwd (pos_arr null: all sequences at pos) or bf_decode_fwd_batch (pos_arr [B]
+ * int64 on the device: sequence b at pos_arr[b]) on `stream`, so results equal those entry points' chained (bit for
+ * bit). The caller keeps the cache bookkeeping of those entry points: with one position, the new token appended to
+ * the sinks while pos < sinks (n_sinks counts it) and a zero state before the memory is first written; with
+ * pos_arr, the fixed per-sequence sink blocks and ring_pos rows of bf_decode_fwd_batch.
+ *   x [B][d_model] bf16 (d_model a multiple of 8, 16-byte aligned); q [B][H][D], k, v [B][G][D], qr [B][H][D],
+ *   kr [B][G][D] bf16, dense; fq [H][D][D], fk [G][D][D] f32 (the module's projections); w_ab [2G][d_model], w_mix
+ *   [H][d_model] f32 (16-byte aligned), b_ab [2G], b_mix [H] f32 or null; A_log, dt_bias, decay_mask [G],
+ *   mix_lse, mem_scale [H] f32; the cache and o as in bf_decode_fwd / bf_decode_fwd_batch (bf16 ring and sinks).
+ *   2G + H <= 64, H = G * R with R <= 8, sinks <= 63.
+ * Workspace: bf_student_decode_workspace_size bytes.
+ */
+int bf_student_decode_workspace_size(int B, int H, int G, int D, int W, size_t* bytes);
+
+int bf_student_decode(int B, int H, int G, int D, int W, int sinks, int64_t pos, const int64_t* pos_arr, int memory,
+                      int d_model, const void* x, const void* q, const void* k, const void* v, const void* qr,
+                      const void* kr, const float* fq, const float* fk, const float* w_ab, const float* b_ab,
+                      const float* w_mix, const float* b_mix, const float* A_log, const float* dt_bias,
+                      const float* decay_mask, const float* mix_lse, const float* mem_scale, void* sink_k,
+                      void* sink_v, int n_sinks, void* ring_k, void* ring_v, float* ring_km, float* ring_g,
+                      float* ring_beta, int64_t* ring_pos, float* state, float* o, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/*
  * bf_decode_fwd without a workspace argument: the same kernels and results, with their scratch (the memory read and
  * the window-split partials, bf_decode_workspace_size bytes) in a static device buffer of
  * BF_DECODE_STATIC_SCRATCH_BYTES that the library holds on each GPU it runs on until the process ends. No counterpart

@@ -177,6 +177,10 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
     const long lo = max((long)a.sinks, pos - W + 1);    // oldest visible window position
 
     const int sl = lane / LPS, dl = (lane % LPS) * 16;  // slot within the wave step, dims dl..dl+15
+    // bf16 V rows: a lane takes dims 8 lq .. + 7 and D / 2 + 8 lq .. + 7 (each load instruction reads whole 256-byte
+    // halves of SPW rows)
+    const int lq = lane % LPS;
+    auto vdim = [&](int i) { return sizeof(T) == 2 ? (i < 8 ? 8 * lq + i : D / 2 + 8 * lq + i - 8) : dl + i; };
     const T* RK = reinterpret_cast<const T*>(a.ring_k) + bg * W * D;
     const T* RV = reinterpret_cast<const T*>(a.ring_v) + bg * W * D;
     const T* SK = reinterpret_cast<const T*>(a.sink_k) + bg * a.n_sinks * D;
@@ -246,21 +250,26 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
         // ring keys: two 16-key groups per wave iteration (addresses past the last ring key clamped to it)
         const int ngrp = (nring + 15) / 16;
         const uint16_t* rk16 = reinterpret_cast<const uint16_t*>(RK) + (long)s0 * D + 8 * lg;
-        constexpr int KG = D <= 128 ? 8 : 4;              // 16-key groups per wave iteration, loaded together
-        for (int t0 = wv; t0 < ngrp; t0 += 4 * KG) {
-            uint4 ka[KG][NKD];
+        constexpr int KG = D <= 128 ? 4 : 2;              // 16-key groups per wave iteration; the next KG loaded ahead
+        auto ldk = [&](int t0, uint4 (&ka)[KG][NKD]) {
 #pragma unroll
             for (int u = 0; u < KG; ++u) {
                 const int key = min(16 * (t0 + 4 * u) + l16, nring - 1);
 #pragma unroll
                 for (int ks = 0; ks < NKD; ++ks) ka[u][ks] = ld16(rk16 + (long)key * D + 32 * ks);
             }
+        };
+        uint4 kc[KG][NKD];
+        ldk(wv, kc);
+        for (int t0 = wv; t0 < ngrp; t0 += 4 * KG) {
+            uint4 kn[KG][NKD];
+            ldk(t0 + 4 * KG, kn);
 #pragma unroll
             for (int u = 0; u < KG; ++u) {
                 const int t = t0 + 4 * u;
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int ks = 0; ks < NKD; ++ks) mma<BF16>(acc, ka[u][ks], qf[ks]);
+                for (int ks = 0; ks < NKD; ++ks) mma<BF16>(acc, kc[u][ks], qf[ks]);
                 if (t < ngrp && l16 < R) {
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
@@ -269,6 +278,10 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
                     }
                 }
             }
+#pragma unroll
+            for (int u = 0; u < KG; ++u)
+#pragma unroll
+                for (int ks = 0; ks < NKD; ++ks) kc[u][ks] = kn[u][ks];
         }
         // extra keys of split 0 (sinks, new token), wave 0, 16 at a time
         if (nextra > 0 && wv == 0) {
@@ -327,6 +340,20 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
             }
         }
     }
+    // bf16: this wave's first V rows are loaded before the softmax barrier, so the V stream starts while the scores
+    // finish
+    constexpr int U = RM <= 4 ? 4 : 2;
+    const uint16_t* rv16 = reinterpret_cast<const uint16_t*>(RV) + (long)s0 * D + 8 * lq;
+    auto ldv = [&](int k0, uint4 (&vr)[U][2]) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int k = min(k0 + u * SPW + sl, nring - 1);
+            vr[u][0] = ld16(rv16 + (long)k * D);
+            vr[u][1] = ld16(rv16 + (long)k * D + D / 2);
+        }
+    };
+    uint4 cur[U][2];
+    if constexpr (sizeof(T) == 2) ldv(wv * SPW * U, cur);
     __syncthreads();
     // max and exp-sum per head (wave r handles head r, r + 4, ...)
     for (int r = wv; r < R; r += 4) {
@@ -354,20 +381,8 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
     // ring keys: U slot steps per wave iteration, every lane's U rows loaded before use (addresses past the last
     // ring key are clamped to it and their probabilities taken as zero). bf16: the rows stay packed in registers and
     // the next iteration's rows are loaded while the current ones are accumulated.
-    constexpr int U = RM <= 4 ? 4 : 2;
     if constexpr (sizeof(T) == 2) {
-        const uint16_t* rv16 = reinterpret_cast<const uint16_t*>(RV) + (long)s0 * D + dl;
-        auto ldv = [&](int k0, uint4 (&vr)[U][2]) {
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int k = min(k0 + u * SPW + sl, nring - 1);
-                vr[u][0] = ld16(rv16 + (long)k * D);
-                vr[u][1] = ld16(rv16 + (long)k * D + 8);
-            }
-        };
-        uint4 cur[U][2];
         int k0 = wv * SPW * U;
-        ldv(k0, cur);
         for (; k0 < nring; k0 += 4 * SPW * U) {
             uint4 nxt[U][2];
             ldv(min(k0 + 4 * SPW * U, nring - 1), nxt);
@@ -412,7 +427,18 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
     for (int k0 = nring + wv * SPW; k0 < nkeys; k0 += 4 * SPW) {
         const int k = k0 + sl;
         float vv[16];
-        ld16f<KV>(key_row(min(k, nkeys - 1), RV, SV, NV) + dl, vv);
+        if constexpr (sizeof(T) == 2) {
+            const T* row = key_row(min(k, nkeys - 1), RV, SV, NV);
+            const uint4 h0 = ld16(row + 8 * lq), h1 = ld16(row + D / 2 + 8 * lq);
+            const uint32_t w[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                vv[2 * i] = __uint_as_float(w[i] << 16);
+                vv[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+            }
+        } else {
+            ld16f<KV>(key_row(min(k, nkeys - 1), RV, SV, NV) + dl, vv);
+        }
 #pragma unroll
         for (int r = 0; r < RMAX; ++r) {
             const float p = (r < R && k < nkeys) ? sc[r][k < nkeys ? k : 0] : 0.f;
@@ -432,7 +458,7 @@ __global__ __launch_bounds__(NT_DEC) void decode_main_kernel(DecodeArgs a) {
         for (int r = 0; r < RMAX; ++r)
             if (r < R) {
 #pragma unroll
-                for (int i = 0; i < 16; ++i) part[wv][r][dl + i] = acc[r][i];
+                for (int i = 0; i < 16; ++i) part[wv][r][vdim(i)] = acc[r][i];
             }
     }
     __syncthreads();

@@ -27,7 +27,7 @@ SIGNATURES = {
     "bf_decode_workspace_size": (_c_int, [_c_int] * 5 + [ctypes.POINTER(_c_sz)]),
     "bf_decode_fwd": (_c_int, [_c_int] * 6 + [_c_i64] + [_c_int] * 3 + [_vp] * 12 + [_c_int] + [_vp] * 10 + [_c_sz, _vp]),
     "bf_decode_fwd_batch": (_c_int, [_c_int] * 6 + [_vp, _c_int, _c_int, _c_int] + [_vp] * 22 + [_c_sz, _vp]),
-    "bf_student_decode_workspace_size": (_c_int, [_c_int] * 5 + [ctypes.POINTER(_c_sz)]),
+    "bf_student_decode_workspace_size": (_c_int, [_c_int] * 6 + [ctypes.POINTER(_c_sz)]),
     "bf_student_decode": (_c_int, [_c_int] * 6 + [_c_i64, _vp, _c_int, _c_int] + [_vp] * 19 + [_c_int]
                           + [_vp] * 9 + [_c_sz, _vp]),
     "bf_decode_fwd_noalloc": (_c_int, [_c_int] * 6 + [_c_i64] + [_c_int] * 3 + [_vp] * 12 + [_c_int] + [_vp] * 9 + [_vp]),
@@ -35,7 +35,9 @@ SIGNATURES = {
                       + [_vp, _c_int] + [_vp] * 4 + [_c_int, _vp, _vp]),
     "bf_mem_project": (_c_int, [_vp, _c_i64, _c_int, _c_int, _c_i64, _c_i64, _vp, _fp, _vp, _c_int, _c_int, _vp]),
     "bf_mem_gates": (_c_int, [_vp, _c_i64, _c_i64, _c_int, _c_i64, _vp, _vp, _vp, _c_i64, _c_int, _vp, _vp, _vp]),
-    "bf_gate_project": (_c_int, [_vp, _c_i64, _c_int, _c_i64, _vp, _vp, _c_int, _vp, _vp, _vp, _c_int, _vp, _vp]),
+    "bf_gate_project_workspace_size": (_c_int, [_c_i64, _c_int, _c_int, ctypes.POINTER(_c_sz)]),
+    "bf_gate_project": (_c_int, [_vp, _c_i64, _c_int, _c_i64, _vp, _vp, _c_int, _vp, _vp, _vp, _c_int, _vp, _vp,
+                                 _c_sz, _vp]),
     "bf_gdn_conv_inputs": (_c_int, [_vp, _c_i64, _vp, _c_int, _vp, _c_int] + [_vp] * 5 + [_c_int, _c_i64]
                            + [_c_int] * 3 + [_fp, _fp] + [_vp] * 5 + [_c_int, _vp]),
     "bf_gated_norm": (_c_int, [_vp, _c_int, _vp, _vp, _c_i64, _c_int, _fp, _vp, _c_int, _vp]),

@@ -201,7 +201,19 @@ struct GateProjArgs {
     const float *w1, *b1;           // [n1][d], [n1]
     int n1;
     float* out1;                    // [n_tok][n1]
+    float* part;                    // split-d partial sums [nsplit][n_tok][n0 + n1] (gate_project_split)
 };
+// Split-d form of the gate projection for up to GP_SPLIT_MAX_TOK tokens: its d splits and workspace bytes.
+constexpr long GP_SPLIT_MAX_TOK = 4096;
+inline int gate_project_nsplit(long n_tok, int d) {
+    if (n_tok > GP_SPLIT_MAX_TOK) return 0;
+    const long tiles = (n_tok + 15) / 16, steps = (d + 127) / 128;
+    long ns = 1024 / (tiles > 0 ? tiles : 1);
+    return (int)(ns < 1 ? 1 : (ns > steps ? steps : ns));
+}
+inline size_t gate_project_workspace(long n_tok, int d, int nout) {
+    return (size_t)gate_project_nsplit(n_tok, d) * (size_t)n_tok * (size_t)nout * sizeof(float);
+}
 int gate_project_dispatch(const GateProjArgs& a, hipStream_t stream);
 int mem_project_dispatch(const MemProjArgs& a, hipStream_t stream);
 int window_fa_dispatch(const WinArgs& a, hipStream_t stream);

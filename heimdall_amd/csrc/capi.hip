@@ -281,10 +281,10 @@ int bf_decode_fwd_batch(int B, int G, int R, int D, int W, int sinks, const int6
 // workspace after them.
 namespace {
 struct StudentDecodeWs {
-    size_t ab, z, qm, km, g, beta, dec, total;
+    size_t ab, z, qm, km, g, beta, gp, dec, total;
 };
-int student_decode_layout(int B, int H, int G, int D, int W, StudentDecodeWs& l) {
-    if (B <= 0 || G <= 0 || H <= 0 || H % G || W <= 0) return BF_STATUS_INVALID;
+int student_decode_layout(int B, int H, int G, int D, int W, int d_model, StudentDecodeWs& l) {
+    if (B <= 0 || G <= 0 || H <= 0 || H % G || W <= 0 || d_model <= 0) return BF_STATUS_INVALID;
     size_t dec = 0;
     const int st = bf_decode_workspace_size(B, G, H / G, D, W, &dec);
     if (st) return st;
@@ -296,16 +296,17 @@ int student_decode_layout(int B, int H, int G, int D, int W, StudentDecodeWs& l)
     l.km = take((size_t)B * G * D * sizeof(float));
     l.g = take((size_t)B * G * sizeof(float));
     l.beta = take((size_t)B * G * sizeof(float));
+    l.gp = take(bf::gate_project_workspace(B, d_model, 2 * G + H));
     l.dec = take(dec);
     l.total = o;
     return BF_STATUS_OK;
 }
 }  // namespace
 
-int bf_student_decode_workspace_size(int B, int H, int G, int D, int W, size_t* bytes) {
+int bf_student_decode_workspace_size(int B, int H, int G, int D, int W, int d_model, size_t* bytes) {
     if (!bytes) return BF_STATUS_INVALID;
     StudentDecodeWs l{};
-    const int st = student_decode_layout(B, H, G, D, W, l);
+    const int st = student_decode_layout(B, H, G, D, W, d_model, l);
     if (st) return st;
     *bytes = l.total;
     return BF_STATUS_OK;
@@ -320,7 +321,7 @@ int bf_student_decode(int B, int H, int G, int D, int W, int sinks, int64_t pos,
                       float* ring_beta, int64_t* ring_pos, float* state, float* o, void* workspace,
                       size_t workspace_bytes, void* stream) {
     StudentDecodeWs l{};
-    int st = student_decode_layout(B, H, G, D, W, l);
+    int st = student_decode_layout(B, H, G, D, W, d_model, l);
     if (st) return st;
     if (!supported_dim(D)) return BF_STATUS_UNSUPPORTED;
     if (d_model <= 0 || d_model % 8 || 2 * G + H > bf::GP_MAX_OUT || sinks < 0 || sinks > 63 || (!pos_arr && pos < 0))
@@ -340,6 +341,7 @@ int bf_student_decode(int B, int H, int G, int D, int W, int sinks, int64_t pos,
         bf::GateProjArgs a{};
         a.x = static_cast<const uint16_t*>(x); a.n_tok = B; a.x_st = d_model; a.d = d_model;
         a.w0 = w_ab; a.b0 = b_ab; a.n0 = 2 * G; a.out0 = ab; a.w1 = w_mix; a.b1 = b_mix; a.n1 = H; a.out1 = z;
+        a.part = reinterpret_cast<float*>(ws + l.gp);
         if ((st = bf::gate_project_dispatch(a, s))) return st;
     }
     {
@@ -436,8 +438,15 @@ int bf_mem_gates(const float* ab, int64_t n_tok, int64_t T, int G, int64_t ab_st
     return bf::mem_gates_dispatch(a, static_cast<hipStream_t>(stream));
 }
 
+int bf_gate_project_workspace_size(int64_t n_tok, int d, int nout, size_t* bytes) {
+    if (!bytes || n_tok < 0 || d <= 0 || nout <= 0 || nout > bf::GP_MAX_OUT) return BF_STATUS_INVALID;
+    *bytes = bf::gate_project_workspace(n_tok, d, nout);
+    return BF_STATUS_OK;
+}
+
 int bf_gate_project(const void* x, int64_t n_tok, int d, int64_t x_st, const float* w0, const float* b0, int n0,
-                    float* out0, const float* w1, const float* b1, int n1, float* out1, void* stream) {
+                    float* out0, const float* w1, const float* b1, int n1, float* out1, void* workspace,
+                    size_t workspace_bytes, void* stream) {
     if (n_tok < 0 || d <= 0 || d % 8 || x_st < d || x_st % 8 || n0 < 0 || n1 < 0 || n0 + n1 <= 0 ||
         n0 + n1 > bf::GP_MAX_OUT)
         return BF_STATUS_INVALID;
@@ -448,6 +457,9 @@ int bf_gate_project(const void* x, int64_t n_tok, int d, int64_t x_st, const flo
     bf::GateProjArgs a{};
     a.x = static_cast<const uint16_t*>(x); a.n_tok = n_tok; a.x_st = x_st; a.d = d;
     a.w0 = w0; a.b0 = b0; a.n0 = n0; a.out0 = out0; a.w1 = w1; a.b1 = b1; a.n1 = n1; a.out1 = out1;
+    const size_t need = bf::gate_project_workspace(n_tok, d, n0 + n1);
+    if (need && (!workspace || workspace_bytes < need)) return BF_STATUS_WORKSPACE;
+    a.part = static_cast<float*>(workspace);
     return bf::gate_project_dispatch(a, static_cast<hipStream_t>(stream));
 }
 

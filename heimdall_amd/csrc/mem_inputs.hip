@@ -328,47 +328,63 @@ __global__ __launch_bounds__(64 * GP_WAVES) void gate_project_kernel(GateProjArg
     }
 }
 
-// The same projections for a few tokens (a decode step, a short chunk): one workgroup per 16 tokens whose 8 waves
-// take every 8th 128-wide step of d each (the same lane / MFMA mapping as gate_project_kernel), reading their own
-// part of W straight from memory (each weight once per workgroup), then the 8 partial sums through LDS.
-__global__ __launch_bounds__(64 * GP_WAVES) void gate_project_small_kernel(GateProjArgs a) {
-    constexpr int MAXT = GP_MAX_OUT / 16;
-    __shared__ f32x4 red[GP_WAVES][MAXT][64];
-    const int lane = lane_id(), wv = wave_id(), l16 = lane & 15, lg = lane >> 4;
-    const long tok0 = (long)blockIdx.x * 16;
-    const int nout = a.n0 + a.n1, nt_used = (nout + 15) / 16;
+// The same projections for up to GP_SPLIT_MAX_TOK tokens (decode steps, a prompt's 2048-token chunks), where one
+// workgroup per token tile would read all of W (n0 + n1 rows of d fp32) on one CU: workgroup (s, tile) = one wave, 16
+// tokens, the d range of split s (whole 128-wide steps). It reads its W rows straight from memory (L2-resident: every
+// tile reads the same rows), splits them into bf16 high and low parts in registers, loads the next step's x and W
+// while the current one multiplies (the lane / MFMA mapping of gate_project_kernel), and writes its partial sums to
+// part[s][token][n0 + n1]; gate_project_reduce_kernel adds the splits in a fixed order (s = 0, 1, ..) and the bias.
+template <int NT>
+__global__ __launch_bounds__(64) void gate_project_split_kernel(GateProjArgs a, int steps_per) {
+    const int lane = lane_id(), l16 = lane & 15, lg = lane >> 4;
+    const int sp = blockIdx.x;
+    const long tok0 = (long)blockIdx.y * 16;
+    const int nout = a.n0 + a.n1;
     const long tok = tok0 + l16;
     const bool tok_ok = tok < a.n_tok;
     const uint16_t* xrow = a.x + (tok_ok ? tok : 0) * a.x_st + 32 * lg;
-    const float* wrow[MAXT];
+    const float* wrow[NT];
 #pragma unroll
-    for (int nt = 0; nt < MAXT; ++nt) {
+    for (int nt = 0; nt < NT; ++nt) {
         const int c = 16 * nt + l16;
         wrow[nt] = c < a.n0 ? a.w0 + (long)c * a.d : (c < nout ? a.w1 + (long)(c - a.n0) * a.d : nullptr);
         if (wrow[nt]) wrow[nt] += 32 * lg;
     }
-    f32x4 acc[MAXT];
-#pragma unroll
-    for (int nt = 0; nt < MAXT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 128 * wv; k0 < a.d; k0 += 128 * GP_WAVES) {
-        uint4 xa[4];
+    const int kb = sp * steps_per * 128, ke = min(a.d, kb + steps_per * 128);
+    auto ldx = [&](int k0, uint4 (&xa)[4]) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            xa[j] = tok_ok && k0 + 32 * lg + 8 * j < a.d ? ld16(xrow + k0 + 8 * j) : zero16();
+            xa[j] = tok_ok && k0 + 32 * lg + 8 * j < ke ? ld16(xrow + k0 + 8 * j) : zero16();
+    };
+    auto ldw = [&](int k0, float4 (&w4)[NT][4][2]) {
 #pragma unroll
-        for (int nt = 0; nt < MAXT; ++nt) {
-            if (nt >= nt_used) break;
-            float4 w4[4][2];
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const bool ok = wrow[nt] && k0 + 32 * lg + 8 * j < a.d;
-                w4[j][0] = ok ? *reinterpret_cast<const float4*>(wrow[nt] + k0 + 8 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
-                w4[j][1] = ok ? *reinterpret_cast<const float4*>(wrow[nt] + k0 + 8 * j + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+                const bool ok = wrow[nt] && k0 + 32 * lg + 8 * j < ke;
+                w4[nt][j][0] = ok ? *reinterpret_cast<const float4*>(wrow[nt] + k0 + 8 * j) : make_float4(0.f, 0.f, 0.f, 0.f);
+                w4[nt][j][1] = ok ? *reinterpret_cast<const float4*>(wrow[nt] + k0 + 8 * j + 4)
+                                  : make_float4(0.f, 0.f, 0.f, 0.f);
             }
+    };
+    f32x4 acc[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    uint4 xc[4];
+    float4 wc[NT][4][2];
+    ldx(kb, xc);
+    ldw(kb, wc);
+    for (int k0 = kb; k0 < ke; k0 += 128) {
+        uint4 xn[4];
+        float4 wn[NT][4][2];
+        ldx(k0 + 128, xn);                                     // past the split: zeros
+        ldw(k0 + 128, wn);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float w[8] = {w4[j][0].x, w4[j][0].y, w4[j][0].z, w4[j][0].w,
-                                    w4[j][1].x, w4[j][1].y, w4[j][1].z, w4[j][1].w};
+                const float w[8] = {wc[nt][j][0].x, wc[nt][j][0].y, wc[nt][j][0].z, wc[nt][j][0].w,
+                                    wc[nt][j][1].x, wc[nt][j][1].y, wc[nt][j][1].z, wc[nt][j][1].w};
                 uint32_t hi[4], lo[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -376,44 +392,61 @@ __global__ __launch_bounds__(64 * GP_WAVES) void gate_project_small_kernel(GateP
                     lo[e] = pack_bf16x2(w[2 * e] - __uint_as_float(hi[e] << 16),
                                         w[2 * e + 1] - __uint_as_float(hi[e] & 0xffff0000u));
                 }
-                mma<BF16>(acc[nt], xa[j], make_uint4(hi[0], hi[1], hi[2], hi[3]));
-                mma<BF16>(acc[nt], xa[j], make_uint4(lo[0], lo[1], lo[2], lo[3]));
+                mma<BF16>(acc[nt], xc[j], make_uint4(hi[0], hi[1], hi[2], hi[3]));
+                mma<BF16>(acc[nt], xc[j], make_uint4(lo[0], lo[1], lo[2], lo[3]));
             }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xc[j] = xn[j];
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                wc[nt][j][0] = wn[nt][j][0];
+                wc[nt][j][1] = wn[nt][j][1];
+            }
+    }
+    // accumulator: lane holds output column 16 nt + l16, tokens tok0 + 4 lg .. + 3
+    float* part = a.part + (long)sp * a.n_tok * nout;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+        const int c = 16 * nt + l16;
+        if (c >= nout) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const long t = tok0 + 4 * lg + e;
+            if (t < a.n_tok) part[t * nout + c] = acc[nt][e];
         }
-    }
-#pragma unroll
-    for (int nt = 0; nt < MAXT; ++nt)
-        if (nt < nt_used) red[wv][nt][lane] = acc[nt];
-    __syncthreads();
-    // wave nt sums output tile nt over the 8 waves and stores it
-    if (wv >= nt_used) return;
-    f32x4 t = red[0][wv][lane];
-#pragma unroll
-    for (int w = 1; w < GP_WAVES; ++w) {
-        const f32x4 u = red[w][wv][lane];
-        t[0] += u[0]; t[1] += u[1]; t[2] += u[2]; t[3] += u[3];
-    }
-    const int c = 16 * wv + l16;
-    if (c >= nout) return;
-    float* out = c < a.n0 ? a.out0 : a.out1;
-    const int n = c < a.n0 ? a.n0 : a.n1, cc = c < a.n0 ? c : c - a.n0;
-    const float bias = c < a.n0 ? (a.b0 ? a.b0[cc] : 0.f) : (a.b1 ? a.b1[cc] : 0.f);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const long tt = tok0 + 4 * lg + e;
-        if (tt < a.n_tok) out[tt * n + cc] = t[e] + bias;
     }
 }
 
+__global__ __launch_bounds__(256) void gate_project_reduce_kernel(GateProjArgs a, int nsplit) {
+    const int nout = a.n0 + a.n1;
+    const long e = (long)blockIdx.x * 256 + threadIdx.x;
+    if (e >= a.n_tok * nout) return;
+    const long t = e / nout;
+    const int c = (int)(e % nout);
+    float s = 0.f;
+    for (int sp = 0; sp < nsplit; ++sp) s += a.part[(long)sp * a.n_tok * nout + e];
+    if (c < a.n0) a.out0[t * a.n0 + c] = s + (a.b0 ? a.b0[c] : 0.f);
+    else a.out1[t * a.n1 + (c - a.n0)] = s + (a.b1 ? a.b1[c - a.n0] : 0.f);
+}
+
 int gate_project_dispatch(const GateProjArgs& a, hipStream_t stream) {
+    const int nsplit = gate_project_nsplit(a.n_tok, a.d);
+    if (nsplit > 0) {
+        if (!a.part) return BF_STATUS_WORKSPACE;
+        const int steps = (a.d + 127) / 128, per = (steps + nsplit - 1) / nsplit;
+        const int ns = (steps + per - 1) / per;               // splits that hold at least one step
+        const dim3 grid((unsigned)ns, (unsigned)((a.n_tok + 15) / 16));
+        if (a.n0 + a.n1 <= 32) hipLaunchKernelGGL(gate_project_split_kernel<2>, grid, dim3(64), 0, stream, a, per);
+        else hipLaunchKernelGGL(gate_project_split_kernel<GP_MAX_OUT / 16>, grid, dim3(64), 0, stream, a, per);
+        const long n = a.n_tok * (a.n0 + a.n1);
+        hipLaunchKernelGGL(gate_project_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a, ns);
+        return (int)hipGetLastError();
+    }
     const long tiles = (a.n_tok + 15) / 16;
-    // up to 2048 tokens (128 workgroups of 8 waves) the chip is filled by splitting d; beyond, W is shared through
-    // LDS by the 8 token tiles of a workgroup, so its L2 traffic stays below that of x
-    if (a.n_tok <= 2048)
-        hipLaunchKernelGGL(gate_project_small_kernel, dim3((unsigned)tiles), dim3(64 * GP_WAVES), 0, stream, a);
-    else
-        hipLaunchKernelGGL(gate_project_kernel, dim3((unsigned)((tiles + GP_WAVES - 1) / GP_WAVES)),
-                           dim3(64 * GP_WAVES), 0, stream, a);
+    hipLaunchKernelGGL(gate_project_kernel, dim3((unsigned)((tiles + GP_WAVES - 1) / GP_WAVES)),
+                       dim3(64 * GP_WAVES), 0, stream, a);
     return (int)hipGetLastError();
 }
 

@@ -99,9 +99,15 @@ def _gate_logits(self, x):
         z = torch.empty(b, t, H, dtype=torch.float32, device=x.device)
         w0, b0 = f32(self.ab.weight.detach()), f32(self.ab.bias.detach())
         w1, b1 = f32(self.mix.weight.detach()), f32(self.mix.bias.detach())
-        check(_lib.load().bf_gate_project(x.data_ptr(), b * t, d, x.stride(1), w0.data_ptr(), b0.data_ptr(), 2 * G,
-                                          ab.data_ptr(), w1.data_ptr(), b1.data_ptr(), H, z.data_ptr(),
-                                          stream_ptr(x.device)), "bf_gate_project")
+        lib = _lib.load()
+        nb = _lib.ctypes.c_size_t(0)
+        check(lib.bf_gate_project_workspace_size(b * t, d, 2 * G + H, _lib.ctypes.byref(nb)),
+              "bf_gate_project_workspace_size")
+        ws = workspace(nb.value, x.device) if nb.value else None
+        check(lib.bf_gate_project(x.data_ptr(), b * t, d, x.stride(1), w0.data_ptr(), b0.data_ptr(), 2 * G,
+                                  ab.data_ptr(), w1.data_ptr(), b1.data_ptr(), H, z.data_ptr(),
+                                  None if ws is None else ws.data_ptr(), nb.value, stream_ptr(x.device)),
+              "bf_gate_project")
         return ab, z
     xf = x.float()
     ab = F.linear(xf, self.ab.weight.float(), self.ab.bias.float()).contiguous()
@@ -286,7 +292,7 @@ def _student_decode(self, x, q, k, v, qr, kr, pos, pos_arr, st, sink_k, sink_v, 
     o = torch.empty(b, H, D, dtype=torch.float32, device=dev)
     lib = _lib.load()
     nbytes = _lib.ctypes.c_size_t(0)
-    check(lib.bf_student_decode_workspace_size(b, H, G, D, w, _lib.ctypes.byref(nbytes)),
+    check(lib.bf_student_decode_workspace_size(b, H, G, D, w, xs.shape[1], _lib.ctypes.byref(nbytes)),
           "bf_student_decode_workspace_size")
     ws = workspace(nbytes.value, dev)
     ptr = lambda t_: t_.data_ptr() if t_ is not None else None

@@ -166,7 +166,7 @@ int bf_decode_fwd_batch(int B, int G, int R, int D, int W, int sinks, const int6
  *   2G + H <= 64, H = G * R with R <= 8, sinks <= 63.
  * Workspace: bf_student_decode_workspace_size bytes.
  */
-int bf_student_decode_workspace_size(int B, int H, int G, int D, int W, size_t* bytes);
+int bf_student_decode_workspace_size(int B, int H, int G, int D, int W, int d_model, size_t* bytes);
 
 int bf_student_decode(int B, int H, int G, int D, int W, int sinks, int64_t pos, const int64_t* pos_arr, int memory,
                       int d_model, const void* x, const void* q, const void* k, const void* v, const void* qr,
@@ -257,9 +257,14 @@ int bf_mem_gates(const float* ab, int64_t n_tok, int64_t T, int G, int64_t ab_st
  *   n0 + n1 <= 64 (n1 may be 0)
  * Arithmetic: x exact (bf16), W as bf16 high + low parts (relative residual <= 2^-18), fp32 accumulation: the fp32
  * product to ~4e-6 relative (the reference runs these layers under bf16 autocast, i.e. with W rounded to bf16).
+ * Workspace: bf_gate_project_workspace_size(n_tok, d, n0 + n1) bytes (0 above 4096 tokens; up to that the d range
+ * is split over workgroups and the partial sums are added in a fixed order, so results are reproducible).
  */
+int bf_gate_project_workspace_size(int64_t n_tok, int d, int nout, size_t* bytes);
+
 int bf_gate_project(const void* x, int64_t n_tok, int d, int64_t x_st, const float* w0, const float* b0, int n0,
-                    float* out0, const float* w1, const float* b1, int n1, float* out1, void* stream);
+                    float* out0, const float* w1, const float* b1, int n1, float* out1, void* workspace,
+                    size_t workspace_bytes, void* stream);
 
 /*
  * Native Gated DeltaNet layer, the pass before the delta rule: GatedDeltaNet.forward up to delta_rule

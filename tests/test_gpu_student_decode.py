@@ -78,8 +78,8 @@ def test_fused_decode_rejects_bad_arguments(dev):
     from heimdall_amd import _lib
     lib = _lib.load()
     n = _lib.ctypes.c_size_t(0)
-    assert lib.bf_student_decode_workspace_size(1, 6, 4, 64, 16, _lib.ctypes.byref(n)) != 0     # H % G != 0
-    assert lib.bf_student_decode_workspace_size(1, 8, 4, 64, 16, _lib.ctypes.byref(n)) == 0
+    assert lib.bf_student_decode_workspace_size(1, 6, 4, 64, 16, 32, _lib.ctypes.byref(n)) != 0  # H % G != 0
+    assert lib.bf_student_decode_workspace_size(1, 8, 4, 64, 16, 32, _lib.ctypes.byref(n)) == 0
     assert n.value > 0
     args = [1, 8, 4, 64, 16, 2, 5, None, 1, 30] + [None] * 19 + [0] + [None] * 9 + [n.value, None]
     assert lib.bf_student_decode(*args) != 0                       # d_model not a multiple of 8, null pointers

@@ -601,18 +601,22 @@ def run_gdn_bwd(steps, warmup, dev, T=8192, cpu=False):
            "steps": steps, "flops": fl, "workspace_bytes": nbytes.value,
            "roofline": {"bound": "mfma", "achieved": tf, "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
                         "frac": tf / FP32_PEAK_TFLOPS}}
-    if cpu:
+    host = [x.cpu() for x in (q, k, v, g, beta, do, s0, dsf)]
+
+    def cpu_run():
         # the oracle's gradients (autograd of the restated reference, fp32) on the host, on the same segment
         from oracle import gdn as ogdn
         torch.set_num_threads(len(os.sched_getaffinity(0)))
-        n = T
-        xs = [x[:, :n].cpu() for x in (q, k, v, g, beta, do)]
         t0 = time.perf_counter()
-        ogdn.delta_rule_gqa_grads(xs[0], xs[1], xs[2], xs[3], xs[4], s0.cpu(), xs[5], dsf.cpu(), dtype=torch.float32)
+        ogdn.delta_rule_gqa_grads(*host[:5], host[6], host[5], host[7], dtype=torch.float32)
         dt = time.perf_counter() - t0
-        out["cpu_baseline"] = {"value": n / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-                               "sample": f"oracle delta_rule_gqa_grads fp32 (autograd), T={n} G={G} R={R} D={D}, "
-                                         f"one run, {cpu_model()}"}
+        return {"value": T / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+                "sample": f"oracle delta_rule_gqa_grads fp32 (autograd), T={T} G={G} R={R} D={D}, "
+                          f"one run, {cpu_model()}"}
+    if cpu == "later":
+        return out, cpu_run
+    if cpu:
+        out["cpu_baseline"] = cpu_run()
     return out
 
 
@@ -940,6 +944,8 @@ def gdn_leg(steps, warmup, dev, cpu):
            "phases_ms": pm, "phased_step_ms": sum(pm.values()),
            "kernel_tflops_own_flops": {k_: kf[k_] / (pm[k_] * 1e-3) / 1e12 for k_ in PHASES},
            "traffic": {k_: traffic_from_profile("gdn_" + k_) for k_ in PHASES}}
+    if cpu == "later":
+        return out, (lambda: cpu_baseline(r["inputs"]))
     if cpu:
         out["cpu_baseline"] = cpu_baseline(r["inputs"])
     return out
@@ -1024,16 +1030,18 @@ def main():
         line["layer_chunked"] = run_layer_chunked(dev)
         line["layer_chunked_131k"] = run_layer_chunked(dev, T=131072, reps=1, window_pass=False)
         line["mtp_verify"] = run_mtp_verify(dev)
-        line["gdn_prefill"] = gdn_leg(args.steps, args.warmup, dev, not args.no_cpu)
+        # every GPU leg runs before any CPU baseline: the oracle's host threads must not compete with the launches
+        line["gdn_prefill"], cpu_gdn = gdn_leg(args.steps, args.warmup, dev, "later")
         line["decode"] = run_decode(200, 100, dev)
         line["varlen_gdn"] = run_varlen(10, 3, dev)
         line["gdn_layer"] = run_gdn_layer(10, 3, dev)
         line["teacher_decode"] = run_teacher_decode(50, 10, dev)
-        line["gdn_bwd"] = run_gdn_bwd(10, 2, dev, cpu=not args.no_cpu)
+        line["gdn_bwd"], cpu_bwd = run_gdn_bwd(10, 2, dev, cpu="later")
         line["llama_state"] = run_llama_state(5, 2, dev)
         if not args.no_cpu:
-            for leg, fn in (("decode", cpu_decode), ("varlen_gdn", cpu_varlen), ("gdn_layer", cpu_gdn_layer),
-                            ("teacher_decode", cpu_teacher_decode), ("llama_state", cpu_llama_state)):
+            for leg, fn in (("gdn_prefill", cpu_gdn), ("decode", cpu_decode), ("varlen_gdn", cpu_varlen),
+                            ("gdn_layer", cpu_gdn_layer), ("teacher_decode", cpu_teacher_decode),
+                            ("gdn_bwd", cpu_bwd), ("llama_state", cpu_llama_state)):
                 line[leg]["cpu_baseline"] = fn()
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_layer(m, inputs)

@@ -143,7 +143,20 @@ struct WinArgs {
     const float* mem_scale;   // [H]
     void* o;                  // [B][T][H][D] o_dtype
     float* lse;               // [B][H][T] or null
+    int split_x;              // bf16 kernel: items per XCD split into two key halves (window_split_x), 0: none
+    float* part;              // their partial rows [8 split_x][2][128][D + 4] (m, l, -, -, unnormalised o)
 };
+
+// Window work items past the last full round of an XCD (32 CUs) are split into two key halves when they fill at
+// most half a round: the XCD then runs one full round and a round of halves instead of two full rounds. Items of
+// 128 queries x one query head, mapped to the 8 XCDs in contiguous ranges.
+inline int window_split_x(long nwork) {
+    const long per = (nwork + 7) / 8, rem = per % 32;
+    return rem > 0 && rem <= 16 ? (int)rem : 0;
+}
+inline size_t window_split_bytes(long nwork, int D) {
+    return (size_t)8 * window_split_x(nwork) * 2 * 128 * (D + 4) * sizeof(float);
+}
 
 int window_dispatch(const WinArgs& a, hipStream_t stream);
 

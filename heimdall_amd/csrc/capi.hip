@@ -388,12 +388,14 @@ int bf_decode_fwd_noalloc(int B, int G, int R, int D, int W, int sinks, int64_t 
                          ring_pos, state, o, lse, ws, sizeof(scratch), stream);
 }
 
-int bf_window_fwd(int B, int G, int R, int D, int T, int W, int sinks, int64_t start, int in_dtype, const void* q,
-                  int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
-                  const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, const void* ring_k, const void* ring_v,
-                  const int64_t* ring_pos, const void* sink_k, const void* sink_v, int n_sinks, int mix,
-                  const void* o_mem, int o_mem_dtype, const float* z, const float* mix_lse, const float* mem_scale, void* o,
-                  int o_dtype, float* lse, void* stream) {
+// bf_window_fwd with an optional partial-row buffer of window_split_bytes(B G ceil(T / 128) R, D) bytes: with it,
+// bf16 inputs run the work items of a last, at most half-full round on each XCD as two key halves (merged after).
+static int window_fwd(int B, int G, int R, int D, int T, int W, int sinks, int64_t start, int in_dtype, const void* q,
+                      int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                      const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, const void* ring_k, const void* ring_v,
+                      const int64_t* ring_pos, const void* sink_k, const void* sink_v, int n_sinks, int mix,
+                      const void* o_mem, int o_mem_dtype, const float* z, const float* mix_lse, const float* mem_scale,
+                      void* o, int o_dtype, float* lse, float* part, void* stream) {
     if (B <= 0 || G <= 0 || R <= 0 || T <= 0 || W <= 0 || sinks < 0 || start < 0) return BF_STATUS_INVALID;
     if (!supported_dim(D) || !supported_dtype(in_dtype) || !supported_dtype(o_dtype)) return BF_STATUS_UNSUPPORTED;
     if (!q || !k || !v || !o) return BF_STATUS_INVALID;
@@ -411,7 +413,22 @@ int bf_window_fwd(int B, int G, int R, int D, int T, int W, int sinks, int64_t s
     a.sink_k = sink_k; a.sink_v = sink_v; a.n_sinks = n_sinks;
     a.mix_on = mix; a.o_mem = o_mem; a.o_mem_dtype = o_mem_dtype; a.z = z; a.mix_lse = mix_lse; a.mem_scale = mem_scale;
     a.o = o; a.lse = lse;
+    if (part && in_dtype == BF_DTYPE_BF16) {
+        a.split_x = bf::window_split_x((long)B * G * ((T + 127) / 128) * R);
+        a.part = part;
+    }
     return bf::window_dispatch(a, static_cast<hipStream_t>(stream));
+}
+
+int bf_window_fwd(int B, int G, int R, int D, int T, int W, int sinks, int64_t start, int in_dtype, const void* q,
+                  int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
+                  const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, const void* ring_k, const void* ring_v,
+                  const int64_t* ring_pos, const void* sink_k, const void* sink_v, int n_sinks, int mix,
+                  const void* o_mem, int o_mem_dtype, const float* z, const float* mix_lse, const float* mem_scale, void* o,
+                  int o_dtype, float* lse, void* stream) {
+    return window_fwd(B, G, R, D, T, W, sinks, start, in_dtype, q, q_sb, q_sh, q_st, k, k_sb, k_sh, k_st, v, v_sb,
+                      v_sh, v_st, ring_k, ring_v, ring_pos, sink_k, sink_v, n_sinks, mix, o_mem, o_mem_dtype, z,
+                      mix_lse, mem_scale, o, o_dtype, lse, nullptr, stream);
 }
 
 int bf_mem_project(const void* x, int64_t n_tok, int nh, int D, int64_t x_st, int64_t x_sh, const float* f,
@@ -509,7 +526,7 @@ static bool kv_aligned(const void* p, int64_t s1, int64_t s2) {
 // inner call runs on at most B T tokens with that same segment length, and every buffer of the GDN layout grows
 // monotonically with the token count at a fixed segment length, so the reservation always suffices.
 struct LayerWs {
-    size_t wq, wk, wv, wg, wb, om, o_mem, s_new, gdn, total;
+    size_t wq, wk, wv, wg, wb, om, o_mem, s_new, part, gdn, total;
     int seg_chunks;
 };
 static LayerWs layer_ws(int B, int G, int R, int D, int T, int in_dtype) {
@@ -525,6 +542,7 @@ static LayerWs layer_ws(int B, int G, int R, int D, int T, int in_dtype) {
     put(w.om, BT * H * D * esz);
     put(w.o_mem, BT * H * D * esz);
     put(w.s_new, (size_t)B * G * D * D * 4);
+    put(w.part, in_dtype == BF_DTYPE_BF16 ? bf::window_split_bytes((long)B * G * ((T + 127) / 128) * R, D) : 0);
     const GdnLayout gl = gdn_layout((int64_t)B * T, B, G, R, D, in_dtype, 0);
     w.seg_chunks = gl.seg_chunks;
     put(w.gdn, gl.total);
@@ -603,10 +621,10 @@ int bf_layer_prefill_fwd(int B, int G, int R, int D, int T, int W, int sinks, in
         if (!rows && (rc = bf::layer_launch(a, 1, st))) return rc;
         o_mem = a.o_mem;
     }
-    rc = bf_window_fwd(B, G, R, D, T, W, sinks, start, in_dtype, qr, q_sb, q_sh, q_st, kr, k_sb, k_sh, k_st, v, v_sb,
-                       v_sh, v_st, ring_k, ring_v, ring_pos, sink_k, sink_v, n_sinks, use_mem ? 1 : 0, o_mem,
-                       in_dtype, use_mem ? z : nullptr, use_mem ? mix_lse : nullptr, use_mem ? mem_scale : nullptr, o,
-                       BF_DTYPE_F32, lse, stream);
+    rc = window_fwd(B, G, R, D, T, W, sinks, start, in_dtype, qr, q_sb, q_sh, q_st, kr, k_sb, k_sh, k_st, v, v_sb,
+                    v_sh, v_st, ring_k, ring_v, ring_pos, sink_k, sink_v, n_sinks, use_mem ? 1 : 0, o_mem,
+                    in_dtype, use_mem ? z : nullptr, use_mem ? mix_lse : nullptr, use_mem ? mem_scale : nullptr, o,
+                    BF_DTYPE_F32, lse, reinterpret_cast<float*>(ws + L.part), stream);
     if (rc) return rc;
     if ((rc = bf::layer_launch(a, 2, st))) return rc;         // ring write-back after every read of the ring
     if (use_mem && (rc = bf::layer_launch(a, 3, st))) return rc;

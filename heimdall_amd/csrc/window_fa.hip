@@ -87,7 +87,7 @@ __device__ __forceinline__ float fa_sum4(float v) {
 
 }  // namespace
 
-template <int D, bool BO>
+template <int D, bool BO, bool SPLIT>
 __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a) {
     constexpr int QT = FaShape<D>::QT, NW = FaShape<D>::NW, QW = 16 * QT;
     constexpr int ROWB = D * 2, NBLK = ROWB / 16;
@@ -100,12 +100,22 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
     __shared__ FaTile<D> t0;
     __shared__ FaTile<D> t1;
 
-    // ---- work item (XCD-aware)
+    // ---- work item (XCD-aware: workgroup x runs on XCD x mod 8, which takes a contiguous range of items). SPLIT:
+    // the last split_x items of each XCD run as two workgroups each, one per half of the item's key blocks, and
+    // write partial rows that window_merge_kernel combines.
     const int R = a.R, G = a.G, H = G * R;
     const int nqb = (a.T + FA_BQ - 1) / FA_BQ;
     const long nwork = (long)a.B * G * nqb * R;
     const long per = (nwork + FA_NXCD - 1) / FA_NXCD;
-    const long wi = (long)(blockIdx.x % FA_NXCD) * per + blockIdx.x / FA_NXCD;
+    const int xcd = (int)(blockIdx.x % FA_NXCD), sx = SPLIT ? a.split_x : 0;
+    long idx = blockIdx.x / FA_NXCD;
+    int half = -1;                                      // -1: the whole item, else its first (0) or second key half
+    if (SPLIT && idx >= per - sx) {
+        const long k = idx - (per - sx);
+        idx = per - sx + (k >> 1);
+        half = (int)(k & 1);
+    }
+    const long wi = (long)xcd * per + idx;
     if (wi >= nwork) return;
     const int r = (int)(wi % R);
     long rest = wi / R;
@@ -147,6 +157,8 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
     const int has_sink = ns > 0 ? 1 : 0;
     const int nwin = kp_lo <= p_last ? (int)((p_last - kp_lo) / FA_KB) + 1 : 0;
     const int nblk = has_sink + nwin;
+    const int nh = (nblk + 1) >> 1;                                // blocks of a split item's first half
+    const int i_beg = SPLIT && half == 1 ? nh : 0, i_end = SPLIT && half == 0 ? nh : nblk;
     const int slot_lo = rk ? (int)(kp_lo % a.W) : 0;               // ring slot of kp_lo (one division)
     const long start = a.start;
 
@@ -342,7 +354,8 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
             const bool up = bm > m[qt] + FA_SLACK;
             if (__builtin_amdgcn_ballot_w64(up)) {
                 const float mn = up ? bm : m[qt];
-                const float corr = __builtin_amdgcn_exp2f(m[qt] - mn);   // 0 when m was -inf, 1 without update
+                // 0 when m was -inf, 1 without update (also for a row that has seen no key yet while others update)
+                const float corr = up ? __builtin_amdgcn_exp2f(m[qt] - mn) : 1.f;
                 m[qt] = mn;
                 l[qt] *= corr;
 #pragma unroll
@@ -397,13 +410,18 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
     // re-stages itself into the idle tile), so the compiler's wait counts never drain it before the current compute.
     // Its copies are spread over the S product when they need no clamping (all rows chunk rows up to the last query)
     // and the wave computes block i; a wave that sees nothing of block i skips its S product and copies at once.
-    uint2 rp = load_rp(0);
-    stage(t0, 0);
+    // (an unsplit item always runs its first block, masked out when the item has none)
+    const bool run = !SPLIT || i_beg < i_end;
+    uint2 rp = make_uint2(0u, 0u);
+    if (run) {
+        rp = load_rp(i_beg);
+        stage(t0, i_beg);
+    }
     auto step = [&](FaTile<D>& tc, FaTile<D>& tn, int i) {
         wait_vmem_all();
         __syncthreads();                                   // block i is in tc; every wave is done with tn
         const uint64_t vmask = __builtin_amdgcn_ballot_w64(valid_row(i, rp));
-        const int inext = i + 1 < nblk ? i + 1 : i;
+        const int inext = i + 1 < i_end ? i + 1 : i;
         rp = load_rp(inext);
         {
             const bool sink = has_sink && i == 0;
@@ -425,13 +443,33 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
         }
         compute(tc, i, vmask);
     };
-    for (int i = 0;;) {
-        step(t0, t1, i);
-        if (++i >= nblk) break;
-        step(t1, t0, i);
-        if (++i >= nblk) break;
+    if (run) {                                             // uniform over the workgroup
+        for (int i = i_beg;;) {
+            step(t0, t1, i);
+            if (++i >= i_end) break;
+            step(t1, t0, i);
+            if (++i >= i_end) break;
+        }
+        wait_vmem_all();                                   // the last (redundant) stage has landed before exit
     }
-    wait_vmem_all();                                       // the last (redundant) stage has landed before exit
+
+    if (SPLIT && half >= 0) {
+        // partial rows of the key half, query qi at row qi: m (running max, log2 units), l, 2 unused, o unnormalised
+        float* pp = a.part + (((long)xcd * sx + (idx - (per - sx))) * 2 + half) * FA_BQ * (D + 4);
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            const float lt = fa_sum4(l[qt]);
+            const int qi = QW * wv + 16 * qt + l16;
+            if (qi >= nq) continue;
+            float* row = pp + (long)qi * (D + 4);
+            if (lg == 0) *reinterpret_cast<float2*>(row) = make_float2(m[qt], lt);
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt)
+                *reinterpret_cast<float4*>(row + 4 + 16 * dt + 4 * lg) =
+                    make_float4(o[dt][qt][0], o[dt][qt][1], o[dt][qt][2], o[dt][qt][3]);
+        }
+        return;
+    }
 
     // ---- epilogue: row sums, normalise, lse (natural log), gamma mix, store o [B][T][H][D]
     const float lnW = logf((float)a.W);
@@ -471,23 +509,92 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
     }
 }
 
+// The two key halves of each split item: rows m0, l0, o0 and m1, l1, o1 (each relative to its own running max)
+// combine as L = c0 l0 + c1 l1, O = c0 o0 + c1 o1 with c = exp2(m - max(m0, m1)); then the window epilogue of
+// window_fa_kernel: o = O / L, lse, gamma mix, store. D / 4 threads per query row, 4 consecutive d each.
+template <int D, bool BO>
+__global__ __launch_bounds__(256) void window_merge_kernel(WinArgs a) {
+    constexpr int LPR = D / 4;
+    const long t = (long)blockIdx.x * 256 + threadIdx.x;
+    const long row = t / LPR;
+    const int c = (int)(t % LPR), sx = a.split_x;
+    if (row >= (long)FA_NXCD * sx * FA_BQ) return;
+    const int s = (int)(row / FA_BQ), qi = (int)(row % FA_BQ);
+    const int R = a.R, G = a.G, H = G * R;
+    const int nqb = (a.T + FA_BQ - 1) / FA_BQ;
+    const long nwork = (long)a.B * G * nqb * R;
+    const long per = (nwork + FA_NXCD - 1) / FA_NXCD;
+    const long wi = (long)(s / sx) * per + (per - sx) + s % sx;
+    if (wi >= nwork) return;
+    const int r = (int)(wi % R);
+    long rest = wi / R;
+    const int qb = nqb - 1 - (int)(rest % nqb);
+    rest /= nqb;
+    const int g = (int)(rest % G), b = (int)(rest / G), h = g * R + r;
+    const long tq = (long)qb * FA_BQ + qi;
+    if (tq >= a.T) return;
+    const float* p0 = a.part + ((long)s * 2 * FA_BQ + qi) * (D + 4);
+    const float* p1 = p0 + (long)FA_BQ * (D + 4);
+    const float2 ml0 = *reinterpret_cast<const float2*>(p0), ml1 = *reinterpret_cast<const float2*>(p1);
+    const float4 o0 = *reinterpret_cast<const float4*>(p0 + 4 + 4 * c);
+    const float4 o1 = *reinterpret_cast<const float4*>(p1 + 4 + 4 * c);
+    const float mx = fmaxf(ml0.x, ml1.x);
+    const float c0 = ml0.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml0.x - mx);
+    const float c1 = ml1.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml1.x - mx);
+    const float lt = c0 * ml0.y + c1 * ml1.y;
+    const float inv = 1.f / lt;
+    const float lse = (mx + __log2f(lt)) * FA_LN2;
+    if (a.lse && c == 0) a.lse[((long)b * H + h) * a.T + tq] = lse;
+    float r4[4] = {(c0 * o0.x + c1 * o1.x) * inv, (c0 * o0.y + c1 * o1.y) * inv, (c0 * o0.z + c1 * o1.z) * inv,
+                   (c0 * o0.w + c1 * o1.w) * inv};
+    const long orow = (((long)b * a.T + tq) * H + h) * D;
+    if (a.mix_on && a.start + tq >= a.W) {
+        const float gam =
+            1.f / (1.f + __expf(-(a.z[((long)b * a.T + tq) * H + h] + a.mix_lse[h] * (lse - logf((float)a.W)))));
+        if (gam != 0.f) {                                  // rows the delta rule never wrote stay out, as in the kernel
+            const float ms = a.mem_scale[h];
+            float4 om[1];
+            load_om<1>(a, orow + 4 * c, om);
+            const float mv[4] = {om[0].x, om[0].y, om[0].z, om[0].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) r4[e] = r4[e] + gam * (ms * mv[e] - r4[e]);
+        }
+    }
+    if constexpr (BO) store4<BF16>(reinterpret_cast<uint16_t*>(a.o) + orow + 4 * c, r4[0], r4[1], r4[2], r4[3]);
+    else store4<F32>(reinterpret_cast<float*>(a.o) + orow + 4 * c, r4[0], r4[1], r4[2], r4[3]);
+}
+
 namespace {
 
 template <int D>
 int launch_window_fa(const WinArgs& a, hipStream_t stream) {
+    static_assert(FA_BQ == 128 && FA_NXCD == 8, "window_split_x assumes 128-query items over 8 XCDs");
     const long nqb = (a.T + FA_BQ - 1) / FA_BQ;
     const long nwork = (long)a.B * a.G * nqb * a.R;
     const long per = (nwork + FA_NXCD - 1) / FA_NXCD;
-    if (FA_NXCD * per > 0x7fffffffL) return BF_STATUS_INVALID;
+    const int sx = a.split_x;
+    if (sx < 0 || sx > per || (sx && !a.part)) return BF_STATUS_INVALID;
+    if (FA_NXCD * (per + sx) > 0x7fffffffL) return BF_STATUS_INVALID;
     // chunk K / V rows are addressed by 32-bit buffer offsets
     if (((long)(a.T - 1) * a.k_st + D) * 2 > 0xffffffffL || ((long)(a.T - 1) * a.v_st + D) * 2 > 0xffffffffL)
         return BF_ERR_UNSUPPORTED;
     // the tile copy forms row offsets with 24-bit multiplies: chunk rows and row strides in bytes below 2^24
     if (a.T >= (1L << 24) || a.k_st * 2 >= (1L << 24) || a.v_st * 2 >= (1L << 24)) return BF_ERR_UNSUPPORTED;
-    const dim3 grid((unsigned)(FA_NXCD * per)), block(FaShape<D>::NT);
-    if (a.o_dtype == DT_BF16) hipLaunchKernelGGL((window_fa_kernel<D, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((window_fa_kernel<D, false>), grid, block, 0, stream, a);
-    const hipError_t e = hipGetLastError();
+    const dim3 grid((unsigned)(FA_NXCD * (per + sx))), block(FaShape<D>::NT);
+    const bool bo = a.o_dtype == DT_BF16;
+    if (sx) {
+        if (bo) hipLaunchKernelGGL((window_fa_kernel<D, true, true>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((window_fa_kernel<D, false, true>), grid, block, 0, stream, a);
+    } else {
+        if (bo) hipLaunchKernelGGL((window_fa_kernel<D, true, false>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((window_fa_kernel<D, false, false>), grid, block, 0, stream, a);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !sx) return e == hipSuccess ? 0 : (int)e;
+    const dim3 mgrid((unsigned)(((long)FA_NXCD * sx * FA_BQ * (D / 4) + 255) / 256));
+    if (bo) hipLaunchKernelGGL((window_merge_kernel<D, true>), mgrid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL((window_merge_kernel<D, false>), mgrid, dim3(256), 0, stream, a);
+    e = hipGetLastError();
     return e == hipSuccess ? 0 : (int)e;
 }
 

@@ -50,18 +50,20 @@ def test_chunked_cache_equals_oracle_fp32(dev, d):
 
 
 def test_production_geometry_bf16(dev):
-    """H=24, G=4, D=256, W=2048 + 4 sinks, bf16 activations: a 3000-token prefill then a 1200-token chunk (the
-    memory branch becomes active mid-chunk, the window reads across the ring), against the fp32 oracle on the same
-    bf16 values."""
+    """H=24, G=4, D=256, W=2048 + 4 sinks, bf16 activations: a 3000-token prefill, a 1200-token chunk (the memory
+    branch becomes active mid-chunk, the window reads across the ring) and a 2048-token chunk over a full ring,
+    against the fp32 oracle on the same bf16 values. The window's work items of 128 queries x 1 head are 576, 240
+    and 384: the first and last leave a last round of at most 16 items on each XCD, which run as two key halves
+    each (merged afterwards), the middle one does not."""
     from heimdall_amd import hibrit
-    print("layer bf16 H=24 G=4 D=256 W=2048 T=3000+1200", flush=True)
+    print("layer bf16 H=24 G=4 D=256 W=2048 T=3000+1200+2048", flush=True)
     m = make_core(24, 4, 256, 64, window=2048, sinks=4)
     mg = make_core(24, 4, 256, 64, window=2048, sinks=4).to(dev)
-    args = make_inputs(m, 1, 4200, seed=13, dtype=torch.bfloat16)
+    args = make_inputs(m, 1, 6248, seed=13, dtype=torch.bfloat16)
     argsf = tuple(z.float() for z in args)
     c_ref, c_gpu = {}, {}
     with torch.no_grad():
-        for a, e in ((0, 3000), (3000, 4200)):
+        for a, e in ((0, 3000), (3000, 4200), (4200, 6248)):
             o_ref = olayer.student(m, *split(argsf, a, e), a, c_ref)
             o = hibrit.student(mg, *to_dev(split(args, a, e), dev), a, c_gpu)
             print(f"  chunk {a}:{e} rel err {rel(o, o_ref):.2e}", flush=True)

@@ -119,6 +119,39 @@ struct StepArgs {
 
 int step_dispatch(const StepArgs& a, hipStream_t stream);
 
+// Work items of the bf16 window kernel: 128 consecutive queries x one query head. Row u = (b G + g) nqb + j holds
+// the R heads of query block nqb - 1 - j (later blocks first within each (b, g)); item u R + r is head r of row u.
+// The 8 XCDs form 8 / f groups of f XCDs: group q takes the contiguous rows [q rpg, (q + 1) rpg), and XCD e of the
+// group every f-th row of them from row q rpg + e. The XCDs of a group read about the same key range (each into its
+// own L2), and query blocks of unequal length (causal attention, the first W positions) spread evenly over them.
+// Each XCD takes its items in order, its last rot items first; workgroup x runs on XCD x mod 8 as dispatch slot
+// x / 8 of per.
+struct WinMap {
+    long nrow, rpg, per;
+    int R, f, rot;
+};
+__host__ __device__ inline WinMap window_map_make(int B, int G, int R, int T, int f, int rot) {
+    WinMap m{};
+    m.nrow = (long)B * G * ((T + 127) / 128);
+    m.R = R;
+    m.f = f;
+    m.rot = rot;
+    m.rpg = (m.nrow + 8 / f - 1) / (8 / f);
+    m.per = (m.rpg + f - 1) / f * R;
+    return m;
+}
+// item u R + r of dispatch slot k on XCD x, -1 past the XCD's items
+__host__ __device__ inline long window_item(const WinMap& m, int x, long k) {
+    const int q = x / m.f, e = x % m.f;
+    const long u0 = q * m.rpg + e, u1 = m.nrow < (q + 1) * m.rpg ? m.nrow : (q + 1) * m.rpg;
+    if (u0 >= u1) return -1;
+    const long n = (u1 - u0 + m.f - 1) / m.f * m.R;
+    if (k >= n) return -1;
+    const long rot = m.rot < n ? m.rot : n;
+    const long pos = k < rot ? n - rot + k : k - rot;
+    return (u0 + m.f * (pos / m.R)) * m.R + pos % m.R;
+}
+
 struct WinArgs {
     int B, G, R, D, T, W, sinks;
     long start;               // absolute position of the chunk's first token
@@ -143,19 +176,33 @@ struct WinArgs {
     const float* mem_scale;   // [H]
     void* o;                  // [B][T][H][D] o_dtype
     float* lse;               // [B][H][T] or null
-    int split_x;              // bf16 kernel: items per XCD split into two key halves (window_split_x), 0: none
+    int split_x;              // bf16 kernel: slots per XCD split into two key halves (window_split_x), 0: none
     float* part;              // their partial rows [8 split_x][2][128][D + 4] (m, l, -, -, unnormalised o)
+    WinMap map;               // bf16 kernel: set by its launcher from window_map
 };
 
-// Window work items past the last full round of an XCD (32 CUs) are split into two key halves when they fill at
-// most half a round: the XCD then runs one full round and a round of halves instead of two full rounds. Items of
-// 128 queries x one query head, mapped to the 8 XCDs in contiguous ranges.
-inline int window_split_x(long nwork) {
-    const long per = (nwork + 7) / 8, rem = per % 32;
+// The bf16 window kernel's item map for B sequences of T queries, G KV heads of R query heads each, window W from
+// position start. The slot count per XCD, ceil(ceil(rows / (8 / f)) / f) R = ceil(rows / 8) R, does not depend on f.
+// When queries before position W see fewer keys (start < W: a prefill's first chunk, causal attention), XCDs are
+// paired (f = 2) so that both take long and short query blocks: causal attention over 32768 queries (H = 24, G = 4,
+// D = 256) 12.6 ms against 18.8 ms with contiguous ranges per XCD (f = 1), which gave one XCD of each pair the 128
+// longest query blocks of its KV head and the other the 128 shortest; f = 4 12.7 ms, f = 8 13.1 ms. With rot = 32
+// each XCD starts with its shortest items, so its workgroups do not reach their epilogues (the o stores) in
+// lockstep: sliding window 2048 over 32768 queries 1955-1965 us against 1975-1990 us without the rotation. Chunks
+// past the first W positions (every item as long) keep contiguous ranges (f = 1), whose concurrent items share
+// one L2's keys: 16 chunks of 2048 at 5.61-5.66 ms against 5.68-5.72 ms paired.
+inline WinMap window_map(int B, int G, int R, int T, int W, long start) {
+    return start < W ? window_map_make(B, G, R, T, 2, 32) : window_map_make(B, G, R, T, 1, 0);
+}
+
+// Dispatch slots past the last full round of an XCD (32 CUs) are split into two key halves when they fill at most
+// half a round: the XCD then runs one full round and a round of halves instead of two full rounds.
+inline int window_split_x(const WinMap& m) {
+    const long rem = m.per % 32;
     return rem > 0 && rem <= 16 ? (int)rem : 0;
 }
-inline size_t window_split_bytes(long nwork, int D) {
-    return (size_t)8 * window_split_x(nwork) * 2 * 128 * (D + 4) * sizeof(float);
+inline size_t window_split_bytes(const WinMap& m, int D) {
+    return (size_t)8 * window_split_x(m) * 2 * 128 * (D + 4) * sizeof(float);
 }
 
 int window_dispatch(const WinArgs& a, hipStream_t stream);

@@ -388,8 +388,8 @@ int bf_decode_fwd_noalloc(int B, int G, int R, int D, int W, int sinks, int64_t 
                          ring_pos, state, o, lse, ws, sizeof(scratch), stream);
 }
 
-// bf_window_fwd with an optional partial-row buffer of window_split_bytes(B G ceil(T / 128) R, D) bytes: with it,
-// bf16 inputs run the work items of a last, at most half-full round on each XCD as two key halves (merged after).
+// bf_window_fwd with an optional partial-row buffer of window_split_bytes(window_map(...), D) bytes: with it, bf16
+// inputs run the work items of a last, at most half-full round on each XCD as two key halves (merged after).
 static int window_fwd(int B, int G, int R, int D, int T, int W, int sinks, int64_t start, int in_dtype, const void* q,
                       int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
                       const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, const void* ring_k, const void* ring_v,
@@ -414,7 +414,7 @@ static int window_fwd(int B, int G, int R, int D, int T, int W, int sinks, int64
     a.mix_on = mix; a.o_mem = o_mem; a.o_mem_dtype = o_mem_dtype; a.z = z; a.mix_lse = mix_lse; a.mem_scale = mem_scale;
     a.o = o; a.lse = lse;
     if (part && in_dtype == BF_DTYPE_BF16) {
-        a.split_x = bf::window_split_x((long)B * G * ((T + 127) / 128) * R);
+        a.split_x = bf::window_split_x(bf::window_map(B, G, R, T, W, start));
         a.part = part;
     }
     return bf::window_dispatch(a, static_cast<hipStream_t>(stream));
@@ -542,7 +542,8 @@ static LayerWs layer_ws(int B, int G, int R, int D, int T, int in_dtype) {
     put(w.om, BT * H * D * esz);
     put(w.o_mem, BT * H * D * esz);
     put(w.s_new, (size_t)B * G * D * D * 4);
-    put(w.part, in_dtype == BF_DTYPE_BF16 ? bf::window_split_bytes((long)B * G * ((T + 127) / 128) * R, D) : 0);
+    // the item map's slot count does not depend on the window or the position
+    put(w.part, in_dtype == BF_DTYPE_BF16 ? bf::window_split_bytes(bf::window_map(B, G, R, T, 1, 0), D) : 0);
     const GdnLayout gl = gdn_layout((int64_t)B * T, B, G, R, D, in_dtype, 0);
     w.seg_chunks = gl.seg_chunks;
     put(w.gdn, gl.total);

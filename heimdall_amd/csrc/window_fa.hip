@@ -22,10 +22,10 @@
 // scalar step per copy), so no wave stalls on a burst of copies before its first MFMA.
 // Buffer rather than global loads: the compiler counts a global load into LDS as a flat access that may touch LDS
 // and then drains every LDS wait to zero while one is in flight, which serialised the fragment reads. Per wave, blocks no query of the wave can see are skipped and blocks every
-// query sees skip the mask. Workgroups are mapped XCD-aware: consecutive workgroups of one XCD take the R query
-// heads of one query block, then the previous query block of the same KV head, so one L2 serves their K / V
-// re-reads; query blocks go from last to first, so with a window as long as the chunk (causal attention, the
-// teacher's blockwise attention) the longest workgroups start first.
+// query sees skip the mask. Workgroups are mapped XCD-aware (WinMap): consecutive workgroups of one XCD take the R
+// query heads of one query block, then an earlier query block of the same KV head, so one L2 serves their K / V
+// re-reads; when query blocks differ in length (causal attention, a prefill's first W positions) pairs of XCDs
+// share the blocks of a KV head alternately, so both get long and short ones.
 #include "bf_common.h"
 #include "bf_internal.h"
 
@@ -100,13 +100,12 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
     __shared__ FaTile<D> t0;
     __shared__ FaTile<D> t1;
 
-    // ---- work item (XCD-aware: workgroup x runs on XCD x mod 8, which takes a contiguous range of items). SPLIT:
-    // the last split_x items of each XCD run as two workgroups each, one per half of the item's key blocks, and
-    // write partial rows that window_merge_kernel combines.
+    // ---- work item (the map of WinMap: workgroup x is dispatch slot x / 8 of XCD x mod 8). SPLIT: the last split_x
+    // slots of each XCD run as two workgroups each, one per half of the item's key blocks, and write partial rows
+    // that window_merge_kernel combines.
     const int R = a.R, G = a.G, H = G * R;
     const int nqb = (a.T + FA_BQ - 1) / FA_BQ;
-    const long nwork = (long)a.B * G * nqb * R;
-    const long per = (nwork + FA_NXCD - 1) / FA_NXCD;
+    const long per = a.map.per;
     const int xcd = (int)(blockIdx.x % FA_NXCD), sx = SPLIT ? a.split_x : 0;
     long idx = blockIdx.x / FA_NXCD;
     int half = -1;                                      // -1: the whole item, else its first (0) or second key half
@@ -115,8 +114,8 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
         idx = per - sx + (k >> 1);
         half = (int)(k & 1);
     }
-    const long wi = (long)xcd * per + idx;
-    if (wi >= nwork) return;
+    const long wi = window_item(a.map, xcd, idx);
+    if (wi < 0) return;
     const int r = (int)(wi % R);
     long rest = wi / R;
     const int qb = nqb - 1 - (int)(rest % nqb);        // later query blocks (the most keys) are dispatched first
@@ -522,10 +521,8 @@ __global__ __launch_bounds__(256) void window_merge_kernel(WinArgs a) {
     const int s = (int)(row / FA_BQ), qi = (int)(row % FA_BQ);
     const int R = a.R, G = a.G, H = G * R;
     const int nqb = (a.T + FA_BQ - 1) / FA_BQ;
-    const long nwork = (long)a.B * G * nqb * R;
-    const long per = (nwork + FA_NXCD - 1) / FA_NXCD;
-    const long wi = (long)(s / sx) * per + (per - sx) + s % sx;
-    if (wi >= nwork) return;
+    const long wi = window_item(a.map, s / sx, a.map.per - sx + s % sx);
+    if (wi < 0) return;
     const int r = (int)(wi % R);
     long rest = wi / R;
     const int qb = nqb - 1 - (int)(rest % nqb);
@@ -567,11 +564,11 @@ __global__ __launch_bounds__(256) void window_merge_kernel(WinArgs a) {
 namespace {
 
 template <int D>
-int launch_window_fa(const WinArgs& a, hipStream_t stream) {
-    static_assert(FA_BQ == 128 && FA_NXCD == 8, "window_split_x assumes 128-query items over 8 XCDs");
-    const long nqb = (a.T + FA_BQ - 1) / FA_BQ;
-    const long nwork = (long)a.B * a.G * nqb * a.R;
-    const long per = (nwork + FA_NXCD - 1) / FA_NXCD;
+int launch_window_fa(const WinArgs& args, hipStream_t stream) {
+    static_assert(FA_BQ == 128 && FA_NXCD == 8, "WinMap assumes 128-query items over 8 XCDs");
+    WinArgs a = args;
+    a.map = window_map(a.B, a.G, a.R, a.T, a.W, a.start);
+    const long per = a.map.per;
     const int sx = a.split_x;
     if (sx < 0 || sx > per || (sx && !a.part)) return BF_STATUS_INVALID;
     if (FA_NXCD * (per + sx) > 0x7fffffffL) return BF_STATUS_INVALID;

@@ -1,6 +1,7 @@
 """CPU checks of the host side of the product (no GPU): the layer's workspace reservation against the inner delta
-rule's needs, the cache-ring normalisation before a kernel writes into it, the compute-dtype rule, and the product
-core's conversion init against the closed form of ``HybridAttention.convert`` (``hibrit.py:211-240``)."""
+rule's needs, the cache-ring normalisation before a kernel writes into it, the compute-dtype rule, the product
+core's conversion init against the closed form of ``HybridAttention.convert`` (``hibrit.py:211-240``), and the window
+kernel's XCD item map."""
 import ctypes
 import math
 
@@ -105,3 +106,53 @@ def test_noalloc_decode_size_limit_without_gpu(cpu_lib):
     assert cpu_lib.bf_decode_workspace_size(256, 4, 8, 256, 8192, ctypes.byref(n)) == 0 and n.value > 16 << 20
     assert cpu_lib.bf_decode_fwd_noalloc(256, 4, 8, 256, 8192, 4, 100000, 1, 1, 1, *([256] * 12), 0, *([256] * 9),
                                          None) == -4
+
+
+_WINMAP_CHECK = r"""
+#include "bf_internal.h"
+#include <cstdio>
+#include <vector>
+// Every work item of the bf16 window kernel comes from exactly one (XCD, dispatch slot), for every interleave f and
+// rotation, and the slot count per XCD does not depend on f (the layer sizes its partial-row buffer without it).
+int main() {
+    long bad = 0, cases = 0;
+    for (int B : {1, 2, 3, 5}) for (int G : {1, 2, 3, 4, 8}) for (int R : {1, 2, 6, 7})
+    for (int T : {1, 100, 128, 129, 1000, 2048, 3000, 32768}) {
+        const long per1 = bf::window_map_make(B, G, R, T, 1, 0).per;
+        for (int f : {1, 2, 4, 8}) for (int rot : {0, 1, 31, 32, 1000}) {
+            const bf::WinMap m = bf::window_map_make(B, G, R, T, f, rot);
+            bad += m.per != per1;
+            std::vector<int> seen(m.nrow * R, 0);
+            for (int x = 0; x < 8; ++x)
+                for (long k = 0; k < m.per; ++k) {
+                    const long w = bf::window_item(m, x, k);
+                    if (w < -1 || w >= m.nrow * R) ++bad;
+                    else if (w >= 0) ++seen[w];
+                }
+            for (int c : seen) bad += c != 1;
+            ++cases;
+        }
+    }
+    printf("%ld %ld\n", cases, bad);
+    return bad != 0;
+}
+"""
+
+
+def test_window_item_map_is_a_bijection(tmp_path):
+    """The window kernel's XCD item map (bf_internal.h window_item), compiled for the host with g++."""
+    import shutil
+    import subprocess
+    from pathlib import Path
+    gxx = shutil.which("g++")
+    if gxx is None or not Path("/opt/rocm/include/hip/hip_runtime.h").exists():
+        pytest.skip("g++ or the HIP headers are not available")
+    src = tmp_path / "winmap.cpp"
+    src.write_text(_WINMAP_CHECK)
+    csrc = Path(__file__).resolve().parents[1] / "heimdall_amd" / "csrc"
+    exe = tmp_path / "winmap"
+    subprocess.run([gxx, "-std=c++17", "-O1", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include", f"-I{csrc}",
+                    str(src), "-o", str(exe)], check=True, capture_output=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True)
+    cases, bad = map(int, out.stdout.split())
+    assert out.returncode == 0 and bad == 0 and cases == 12800, out.stdout

@@ -67,12 +67,17 @@ __device__ __forceinline__ void mma<F32>(f32x4& acc, const uint4& a, const uint4
 __device__ __forceinline__ uint4 ld16(const void* p) { return *reinterpret_cast<const uint4*>(p); }
 __device__ __forceinline__ void st16(void* p, const uint4& v) { *reinterpret_cast<uint4*>(p) = v; }
 __device__ __forceinline__ uint4 zero16() { return make_uint4(0u, 0u, 0u, 0u); }
-// Streaming (non-temporal) 16-byte accesses, for data touched once per kernel (the decode step's state slabs): the
-// loads and stores skip cache retention, which measured 4 % faster on the state read + write of a decode step.
+// Streaming (non-temporal) 16-byte accesses, for data touched once per kernel (the decode step's state slabs, the
+// window kernel's queries): the loads and stores skip cache retention, which measured 4 % faster on the state read +
+// write of a decode step.
 typedef unsigned int nt_u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float4 nt_ldf4(const float* p) {
     const nt_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4*>(p));
     return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+__device__ __forceinline__ uint4 nt_ld16(const void* p) {
+    const nt_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const nt_u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ void nt_stf4(float* p, const float4& s) {
     __builtin_nontemporal_store(nt_u32x4{__float_as_uint(s.x), __float_as_uint(s.y), __float_as_uint(s.z),

@@ -89,14 +89,9 @@ __device__ __forceinline__ float fa_sum4(float v) {
 // so they should not displace the K / V tiles other workgroups re-read from L2 (the sliding window over 32768
 // queries ran 1909-1927 us against 1938-1963 us with ordinary accesses).
 typedef unsigned int fa_u2 __attribute__((ext_vector_type(2)));
-typedef float fa_f4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint2 fa_ld8_nt(const void* p) {
     const fa_u2 v = __builtin_nontemporal_load(reinterpret_cast<const fa_u2*>(p));
     return make_uint2(v[0], v[1]);
-}
-__device__ __forceinline__ float4 fa_ld16_nt(const void* p) {
-    const fa_f4 v = __builtin_nontemporal_load(reinterpret_cast<const fa_f4*>(p));
-    return make_float4(v[0], v[1], v[2], v[3]);
 }
 template <bool BO>
 __device__ __forceinline__ void fa_st4_nt(void* o, long i, const float (&r)[4]) {
@@ -105,8 +100,7 @@ __device__ __forceinline__ void fa_st4_nt(void* o, long i, const float (&r)[4]) 
                          (uint32_t)f2bf(r[2]) | ((uint32_t)f2bf(r[3]) << 16)};
         __builtin_nontemporal_store(v, reinterpret_cast<fa_u2*>(reinterpret_cast<uint16_t*>(o) + i));
     } else {
-        const fa_f4 v = {r[0], r[1], r[2], r[3]};
-        __builtin_nontemporal_store(v, reinterpret_cast<fa_f4*>(reinterpret_cast<float*>(o) + i));
+        nt_stf4(reinterpret_cast<float*>(o) + i, make_float4(r[0], r[1], r[2], r[3]));
     }
 }
 
@@ -155,7 +149,8 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
     const int nqw = max(0, min(QW, nq - QW * wv));                // queries of this wave
     const long qw0 = p_first + QW * wv, qw1 = qw0 + nqw - 1;
 
-    // ---- Q fragments (B operand of S^T = K Q^T): query tile qt, column l16, d range 32 kf + 8 lg
+    // ---- Q fragments (B operand of S^T = K Q^T): query tile qt, column l16, d range 32 kf + 8 lg. Each query row is
+    // read by this workgroup only: streaming loads leave L2 to the K / V tiles (1.5 % on the sliding window).
     const uint16_t* Qb = reinterpret_cast<const uint16_t*>(a.q) + b * a.q_sb + h * a.q_sh;
     uint4 fq[QT][NKD];
 #pragma unroll
@@ -163,7 +158,7 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
         const int qi = QW * wv + 16 * qt + l16;
         const uint16_t* qrow = Qb + (qi0 + qi) * a.q_st;
 #pragma unroll
-        for (int kf = 0; kf < NKD; ++kf) fq[qt][kf] = qi < nq ? ld16(qrow + 32 * kf + 8 * lg) : zero16();
+        for (int kf = 0; kf < NKD; ++kf) fq[qt][kf] = qi < nq ? nt_ld16(qrow + 32 * kf + 8 * lg) : zero16();
     }
 
     // ---- key blocks: [the sink block] then 64 consecutive positions each from kp_lo (window start of the first
@@ -489,8 +484,7 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
             if (lg == 0) *reinterpret_cast<float2*>(row) = make_float2(m[qt], lt);
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt)
-                *reinterpret_cast<float4*>(row + 4 + 16 * dt + 4 * lg) =
-                    make_float4(o[dt][qt][0], o[dt][qt][1], o[dt][qt][2], o[dt][qt][3]);
+                nt_stf4(row + 4 + 16 * dt + 4 * lg, make_float4(o[dt][qt][0], o[dt][qt][1], o[dt][qt][2], o[dt][qt][3]));
         }
         return;
     }
@@ -558,7 +552,7 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
                 mv[0] = __uint_as_float(omr[i].x << 16); mv[1] = __uint_as_float(omr[i].x & 0xffff0000u);
                 mv[2] = __uint_as_float(omr[i].y << 16); mv[3] = __uint_as_float(omr[i].y & 0xffff0000u);
             } else {
-                const float4 f4 = fa_ld16_nt(reinterpret_cast<const float*>(a.o_mem) + orow);
+                const float4 f4 = nt_ldf4(reinterpret_cast<const float*>(a.o_mem) + orow);
                 mv[0] = f4.x; mv[1] = f4.y; mv[2] = f4.z; mv[3] = f4.w;
             }
 #pragma unroll

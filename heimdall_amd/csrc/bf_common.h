@@ -297,10 +297,14 @@ __device__ __forceinline__ uint4 lds16(const void* base, int byte_off) {
     return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base) + byte_off);
 }
 
+// Cache policy of a buffer access: streaming (non-temporal), for data read or written once per kernel.
+constexpr int kCpolStream = 2;
+
 // Copy a tile of SC rows into LDS with buffer_load ... lds: LDS row r (rowb bytes) holds global row r (pitch bytes)
 // with its 16-byte blocks permuted by sw(r). One instruction moves 64 x 16 bytes; `nbytes` = SC * rowb is a multiple
-// of 1 KB. Blocks at or beyond `valid_blk` of a row read as zero, as do rows past the descriptor's range.
-template <class Swz>
+// of 1 KB. Blocks at or beyond `valid_blk` of a row read as zero, as do rows past the descriptor's range. `cpol`:
+// the loads' cache policy (0, or kCpolStream for rows no other workgroup reads).
+template <int cpol = 0, class Swz>
 __device__ __forceinline__ void stage_tile(rsrc_t src, uint32_t pitch, int rowb, void* lds, int nbytes, int wv,
                                            int nw, int lane, Swz sw, int valid_blk) {
     const int nblk = rowb / 16;
@@ -311,7 +315,7 @@ __device__ __forceinline__ void stage_tile(rsrc_t src, uint32_t pitch, int rowb,
         const uint32_t off = lb < valid_blk ? (uint32_t)r * pitch + (uint32_t)(lb * 16) : 0xFFFFFFF0u;
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             src, (__attribute__((address_space(3))) void*)(reinterpret_cast<char*>(lds) + i * 1024), 16, off, 0, 0,
-            0);
+            cpol);
     }
 }
 

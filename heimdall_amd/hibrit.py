@@ -382,8 +382,10 @@ def student(self, x, q, k, v, qr, kr, start: int, cache: Optional[dict], memory:
     sink_k, sink_v = st.get("sink_k"), st.get("sink_v")
     n_new = max(0, min(t, s - start))
     if n_new:
-        sink_k = kr[:, :, :n_new] if sink_k is None else torch.cat((sink_k, kr[:, :, :n_new]), 2)
-        sink_v = vt[:, :, :n_new] if sink_v is None else torch.cat((sink_v, vt[:, :, :n_new]), 2)
+        # stored dense: a view of the chunk would keep the whole chunk alive in the cache and be copied to a dense
+        # operand by every later call (two small copy launches per chunk call)
+        sink_k = kr[:, :, :n_new].contiguous() if sink_k is None else torch.cat((sink_k, kr[:, :, :n_new]), 2)
+        sink_v = vt[:, :, :n_new].contiguous() if sink_v is None else torch.cat((sink_v, vt[:, :, :n_new]), 2)
     if t == 1 and _fused_decode_ok(self, x, q, k, v, qr, kr):
         if "ring_k" not in st:
             st.update(_new_ring(b, c.hkv, w, c.dh, torch.bfloat16, torch.bfloat16, dev))

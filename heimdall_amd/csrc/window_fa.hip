@@ -469,7 +469,8 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
             step(t1, t0, i);
             if (++i >= i_end) break;
         }
-        wait_vmem_all();                                   // the last (redundant) stage has landed before exit
+        wait_vmem_all();                                   // the last (redundant) stage has landed: the epilogue
+                                                           // reuses the tiles
     }
 
     if (SPLIT && half >= 0) {

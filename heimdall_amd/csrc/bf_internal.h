@@ -263,7 +263,9 @@ struct GateProjArgs {
     float* out1;                    // [n_tok][n1]
     float* part;                    // split-d partial sums [nsplit][n_tok][n0 + n1] (gate_project_split)
 };
-// Split-d form of the gate projection for up to GP_SPLIT_MAX_TOK tokens: its d splits and workspace bytes.
+// Split-d form of the gate projection for up to GP_SPLIT_MAX_TOK tokens: its d splits, whose partial sums
+// [nsplit][n_tok][nout] fp32 are the workspace. Above that the workspace holds W^T split into bf16 high and low parts
+// in MFMA B-fragment order: 2 ceil(d / 256) sub-steps of 128 elements, 8 KB per 16 outputs each.
 constexpr long GP_SPLIT_MAX_TOK = 4096;
 inline int gate_project_nsplit(long n_tok, int d) {
     if (n_tok > GP_SPLIT_MAX_TOK) return 0;
@@ -271,7 +273,10 @@ inline int gate_project_nsplit(long n_tok, int d) {
     long ns = 1024 / (tiles > 0 ? tiles : 1);
     return (int)(ns < 1 ? 1 : (ns > steps ? steps : ns));
 }
+inline int gate_project_wsplit_substeps(int d) { return 2 * ((d + 255) / 256); }
 inline size_t gate_project_workspace(long n_tok, int d, int nout) {
+    if (n_tok > GP_SPLIT_MAX_TOK)
+        return (size_t)gate_project_wsplit_substeps(d) * (size_t)((nout + 15) / 16) * 8 * 1024;
     return (size_t)gate_project_nsplit(n_tok, d) * (size_t)n_tok * (size_t)nout * sizeof(float);
 }
 int gate_project_dispatch(const GateProjArgs& a, hipStream_t stream);

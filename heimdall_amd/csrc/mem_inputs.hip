@@ -205,109 +205,124 @@ int mem_gates_dispatch(const MemGatesArgs& a, hipStream_t stream) {
 // Heimdall/heimdall/hibrit.py:330, and the gamma logit mix(x), :409): y = x W^T + b for the two small Linear layers
 // at once, out0 = x W0^T + b0 ([n_tok][n0], the ab columns [a | b]) and out1 = x W1^T + b1 ([n_tok][n1], mix), fp32.
 //
-// One workgroup = 8 waves x 16 tokens; d is walked in steps of 128 with v_mfma_f32_16x16x32_bf16: A = the tokens' x
-// rows (bf16, exact), B = W^T split into bf16 high and low parts (W = hi + lo + r, |r| <= 2^-18 |W|), so the sum over
-// d is the fp32 product to ~4e-6 relative, without a cast of x to fp32 in HBM. Within a step lane group lg takes the
-// 32 consecutive elements 32 lg .. + 31 of the step (four 16-byte loads: each row read as whole 256-byte pieces) and
-// MFMA j sums elements 8 j .. + 7 of each group, the same permutation of d on both operands. Each step's W tile (up
-// to 64 rows x 128 fp32) is read once per workgroup (each thread 8 or 16 consecutive floats of a row), split, and
-// stored in LDS as the B fragments (1 KB each, contiguous per fragment), double-buffered with one barrier per step;
-// x of the next step is loaded while the current one is multiplied. Bound by reading x once: 2 d bytes per token.
-constexpr int GP_WAVES = 8;
+// d is walked in 128-wide sub-steps with v_mfma_f32_16x16x32_bf16: A = the tokens' x rows (bf16, exact), B = W^T split
+// into bf16 high and low parts (W = hi + lo + r, |r| <= 2^-18 |W|), so the sum over d is the fp32 product to ~4e-6
+// relative, without a cast of x to fp32 in HBM. Within a sub-step lane group lg takes the 32 consecutive elements
+// 32 lg .. + 31 (four 16-byte loads: each row read as whole 256-byte pieces) and MFMA j sums elements 8 j .. + 7 of
+// each group, the same permutation of d on both operands.
+//
+// Above GP_SPLIT_MAX_TOK tokens: gate_split_w_kernel first writes W^T, split, into the workspace in B-fragment order
+// (1 KB per fragment). gate_project_kernel then runs 4 waves x 16 tokens per workgroup, two workgroups per CU. Each
+// step (SUB sub-steps) copies its fragments from L2 into LDS by DMA (buffer_load ... lds, no registers, no VALU work),
+// double-buffered with one barrier per step, while the x rows of the next step load. Two independent workgroups per
+// CU and 256-wide steps keep the x stream going across the barriers: 89 us at 32768 tokens, d = 5120, 32 outputs,
+// against 113 us for 8-wave workgroups that split their 128-wide W tile on the VALU each step (100 us with the
+// split W, 8 waves and 256-wide steps; 92 us with 4 waves and 128-wide steps; streaming x loads 135 us). The bits are
+// the same: the products are added in the same order. Bound by reading x once: 2 d bytes per token.
+constexpr int GP_WAVES = 4;
+constexpr int GP_FRAG = 64 * 16;                               // bytes of one B fragment
 
-__global__ __launch_bounds__(64 * GP_WAVES) void gate_project_kernel(GateProjArgs a) {
-    constexpr int MAXT = GP_MAX_OUT / 16;
-    constexpr int FRAG = 64 * 16;                              // bytes of one B fragment
-    constexpr int TILE = MAXT * 4 * 2 * FRAG;                  // (nt, j, hi / lo) fragments of one step
+// W^T of both projections split into bf16 high and low parts, in the B-fragment order of gate_project_kernel's LDS
+// tile: sub-step s (elements 128 s .. 128 s + 127 of d), then fragment (nt * 4 + j) * 2 + hl (output tile nt, MFMA j,
+// high / low part) of 64 lanes x 16 bytes. Thread (s, r, c) splits elements 8 c .. 8 c + 7 of sub-step s of output
+// row r (zero past d and past n0 + n1 rows); lane 16 (c / 4) + r % 16 of fragment (r / 16 * 4 + c % 4) holds them.
+__global__ __launch_bounds__(256) void gate_split_w_kernel(GateProjArgs a, char* ws, int nsub) {
+    const int nout = a.n0 + a.n1, ntu = (nout + 15) / 16, rows = 16 * ntu;
+    const long e = (long)blockIdx.x * 256 + threadIdx.x;
+    if (e >= (long)nsub * rows * 16) return;
+    const int c = (int)(e & 15), r = (int)((e >> 4) % rows), s = (int)((e >> 4) / rows);
+    const int k = 128 * s + 8 * c;
+    const float* src = r < a.n0 ? a.w0 + (long)r * a.d : (r < nout ? a.w1 + (long)(r - a.n0) * a.d : nullptr);
+    float w[8];
+    if (src && k < a.d) {                                      // d is a multiple of 8: the 8 floats are in the row
+        const float4 u = *reinterpret_cast<const float4*>(src + k), v = *reinterpret_cast<const float4*>(src + k + 4);
+        w[0] = u.x; w[1] = u.y; w[2] = u.z; w[3] = u.w; w[4] = v.x; w[5] = v.y; w[6] = v.z; w[7] = v.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = 0.f;
+    }
+    uint32_t hi[4], lo[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        hi[i] = pack_bf16x2(w[2 * i], w[2 * i + 1]);
+        lo[i] = pack_bf16x2(w[2 * i] - __uint_as_float(hi[i] << 16),
+                            w[2 * i + 1] - __uint_as_float(hi[i] & 0xffff0000u));
+    }
+    const int ln = 16 * (c >> 2) + (r & 15);
+    char* f = ws + ((long)s * ntu * 8 + ((r >> 4) * 4 + (c & 3)) * 2) * GP_FRAG + 16 * ln;
+    st16(f, make_uint4(hi[0], hi[1], hi[2], hi[3]));
+    st16(f + GP_FRAG, make_uint4(lo[0], lo[1], lo[2], lo[3]));
+}
+
+// MAXT: output tiles of 16 columns the LDS tile holds (n0 + n1 <= 16 MAXT); SUB: 128-wide sub-steps per step. ws:
+// the split W^T of gate_split_w_kernel, at least SUB * ceil(d / (128 SUB)) sub-steps.
+template <int MAXT, int SUB>
+__global__ __launch_bounds__(64 * GP_WAVES) void gate_project_kernel(GateProjArgs a, const char* ws) {
+    constexpr int TILE = SUB * MAXT * 4 * 2 * GP_FRAG;        // (sub-step, nt, j, hi / lo) fragments of one step
+    constexpr int KSTEP = 128 * SUB;
     __shared__ __align__(16) char wt[2][TILE];
     const int lane = lane_id(), wv = wave_id(), l16 = lane & 15, lg = lane >> 4;
-    const int tid = threadIdx.x;
     const long tok0 = ((long)blockIdx.x * GP_WAVES + wv) * 16;
-    const int nout = a.n0 + a.n1, nt_used = (nout + 15) / 16;
+    const int nout = a.n0 + a.n1, nt_used = (nout + 15) / 16, nfr = nt_used * 8;
+    const int nstep = (a.d + KSTEP - 1) / KSTEP;
     const long tok = tok0 + l16;
     const bool tok_ok = tok < a.n_tok;
     const uint16_t* xrow = a.x + (tok_ok ? tok : 0) * a.x_st + 32 * lg;
+    const rsrc_t wsrc = make_rsrc(ws, (uint32_t)(nstep * SUB * nfr * GP_FRAG));
     f32x4 acc[MAXT];
 #pragma unroll
     for (int nt = 0; nt < MAXT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // W tile of a step: thread tid covers rows r = tid / 16 and r + 32, elements 8 (tid % 16) .. + 7 of the step;
-    // element 8 c of a row is lane group lg = c / 4, MFMA j = c % 4 of B fragment (r / 16, j).
-    const int wr = tid >> 4, wc = tid & 15;
-    auto wsrc = [&](int r) -> const float* {
-        return r < a.n0 ? a.w0 + (long)r * a.d : (r < nout ? a.w1 + (long)(r - a.n0) * a.d : nullptr);
-    };
-    const float* wp[2] = {wsrc(wr), wsrc(wr + 32)};
-    auto load_w = [&](int k0, float (&w)[2][8]) {
-        const int k = k0 + 8 * wc;
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            if (wp[h] && k < a.d) {
-                const float4 u = *reinterpret_cast<const float4*>(wp[h] + k);
-                const float4 v = *reinterpret_cast<const float4*>(wp[h] + k + 4);
-                w[h][0] = u.x; w[h][1] = u.y; w[h][2] = u.z; w[h][3] = u.w;
-                w[h][4] = v.x; w[h][5] = v.y; w[h][6] = v.z; w[h][7] = v.w;
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) w[h][e] = 0.f;
-            }
+    // the step's SUB * nfr fragments (contiguous in ws) into LDS: fragment f of sub-step h at (h * MAXT * 8 + f) KB
+    auto dma_w = [&](int st, char* t) {
+        for (int i = wv; i < SUB * nfr; i += GP_WAVES) {
+            const int h = i / nfr, f = i % nfr;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                wsrc, (__attribute__((address_space(3))) void*)(t + (h * MAXT * 8 + f) * GP_FRAG), 16,
+                (uint32_t)(((st * SUB + h) * nfr + f) * GP_FRAG + 16 * lane), 0, 0, 0);
         }
     };
-    auto store_w = [&](char* t, const float (&w)[2][8]) {
-        const int flg = wc >> 2, fj = wc & 3;
+    auto load_x = [&](int k0, uint4 (&xa)[4 * SUB]) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int r = wr + 32 * h, nt = r >> 4;
-            if (nt >= MAXT) continue;
-            uint32_t hi[4], lo[4];
+        for (int h = 0; h < SUB; ++h)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                hi[e] = pack_bf16x2(w[h][2 * e], w[h][2 * e + 1]);
-                lo[e] = pack_bf16x2(w[h][2 * e] - __uint_as_float(hi[e] << 16),
-                                    w[h][2 * e + 1] - __uint_as_float(hi[e] & 0xffff0000u));
-            }
-            const int ln = 16 * flg + (r & 15);
-            char* f = t + ((nt * 4 + fj) * 2) * FRAG + 16 * ln;
-            st16(f, make_uint4(hi[0], hi[1], hi[2], hi[3]));
-            st16(f + FRAG, make_uint4(lo[0], lo[1], lo[2], lo[3]));
-        }
-    };
-    auto load_x = [&](int k0, uint4 (&xa)[4]) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            xa[j] = tok_ok && k0 + 32 * lg + 8 * j < a.d ? ld16(xrow + k0 + 8 * j) : zero16();
+            for (int j = 0; j < 4; ++j)
+                xa[4 * h + j] = tok_ok && k0 + 128 * h + 32 * lg + 8 * j < a.d ? ld16(xrow + k0 + 128 * h + 8 * j)
+                                                                              : zero16();
     };
 
-    float w[2][8];
-    uint4 xc[4], xn[4];
-    load_w(0, w);
+    uint4 xc[4 * SUB], xn[4 * SUB];
+    dma_w(0, wt[0]);
     load_x(0, xc);
-    store_w(wt[0], w);
+    wait_vmem_all();                                            // this wave's copies have landed
     __syncthreads();
     int buf = 0;
-    for (int k0 = 0; k0 < a.d; k0 += 128) {
-        const bool more = k0 + 128 < a.d;
+    for (int st = 0; st < nstep; ++st) {
+        const bool more = st + 1 < nstep;
         if (more) {
-            load_w(k0 + 128, w);
-            load_x(k0 + 128, xn);
+            dma_w(st + 1, wt[buf ^ 1]);
+            load_x((st + 1) * KSTEP, xn);
         }
         const char* t = wt[buf];
 #pragma unroll
-        for (int nt = 0; nt < MAXT; ++nt) {
-            if (nt >= nt_used) break;
+        for (int h = 0; h < SUB; ++h)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const char* f = t + ((nt * 4 + j) * 2) * FRAG + 16 * lane;
-                mma<BF16>(acc[nt], xc[j], lds16(f, 0));
-                mma<BF16>(acc[nt], xc[j], lds16(f, FRAG));
+            for (int nt = 0; nt < MAXT; ++nt) {
+                if (nt >= nt_used) break;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const char* f = t + ((h * MAXT + nt) * 4 + j) * 2 * GP_FRAG + 16 * lane;
+                    mma<BF16>(acc[nt], xc[4 * h + j], lds16(f, 0));
+                    mma<BF16>(acc[nt], xc[4 * h + j], lds16(f, GP_FRAG));
+                }
             }
-        }
         if (more) {
-            store_w(wt[buf ^ 1], w);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) xc[j] = xn[j];
+            for (int j = 0; j < 4 * SUB; ++j) xc[j] = xn[j];
         }
-        __syncthreads();                                        // tile buf read by every wave, tile buf ^ 1 written
+        // every wave has read tile buf, and (the barrier's wait for all memory operations) every wave's copies into
+        // tile buf ^ 1 have landed
+        __syncthreads();
         buf ^= 1;
     }
     // accumulator: lane holds output column 16 nt + l16, tokens tok0 + 4 lg .. + 3
@@ -444,9 +459,17 @@ int gate_project_dispatch(const GateProjArgs& a, hipStream_t stream) {
         hipLaunchKernelGGL(gate_project_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, a, ns);
         return (int)hipGetLastError();
     }
+    // split W^T, then the projection: 256-wide steps (64 KB of LDS) up to 32 outputs, else 128-wide (64 KB)
+    if (!a.part) return BF_STATUS_WORKSPACE;
+    const int nsub = gate_project_wsplit_substeps(a.d);
+    const long nthr = (long)nsub * 16 * ((a.n0 + a.n1 + 15) / 16) * 16;
+    hipLaunchKernelGGL(gate_split_w_kernel, dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, stream, a,
+                       reinterpret_cast<char*>(a.part), nsub);
     const long tiles = (a.n_tok + 15) / 16;
-    hipLaunchKernelGGL(gate_project_kernel, dim3((unsigned)((tiles + GP_WAVES - 1) / GP_WAVES)),
-                       dim3(64 * GP_WAVES), 0, stream, a);
+    const dim3 grid((unsigned)((tiles + GP_WAVES - 1) / GP_WAVES)), block(64 * GP_WAVES);
+    const char* ws = reinterpret_cast<const char*>(a.part);
+    if (a.n0 + a.n1 <= 32) hipLaunchKernelGGL((gate_project_kernel<2, 2>), grid, block, 0, stream, a, ws);
+    else hipLaunchKernelGGL((gate_project_kernel<GP_MAX_OUT / 16, 1>), grid, block, 0, stream, a, ws);
     return (int)hipGetLastError();
 }
 

@@ -257,8 +257,10 @@ int bf_mem_gates(const float* ab, int64_t n_tok, int64_t T, int G, int64_t ab_st
  *   n0 + n1 <= 64 (n1 may be 0)
  * Arithmetic: x exact (bf16), W as bf16 high + low parts (relative residual <= 2^-18), fp32 accumulation: the fp32
  * product to ~4e-6 relative (the reference runs these layers under bf16 autocast, i.e. with W rounded to bf16).
- * Workspace: bf_gate_project_workspace_size(n_tok, d, n0 + n1) bytes (0 above 4096 tokens; up to that the d range
- * is split over workgroups and the partial sums are added in a fixed order, so results are reproducible).
+ * Workspace: bf_gate_project_workspace_size(n_tok, d, n0 + n1) bytes, always required. Up to 4096 tokens the d range
+ * is split over workgroups and the partial sums are added in a fixed order, so results are reproducible. Above that
+ * it holds W split into bf16 high and low parts (4 bytes per weight, with d rounded up to a multiple of 256 and
+ * n0 + n1 to a multiple of 16), which the call writes before it reads x.
  */
 int bf_gate_project_workspace_size(int64_t n_tok, int d, int nout, size_t* bytes);
 

@@ -144,13 +144,15 @@ def test_mem_gates_and_projection_cache(dev):
 
 
 @pytest.mark.parametrize("b,t,d,n1", [(1, 1000, 5120, 24), (2, 37, 40, 24), (1, 130, 1024, 0), (3, 16, 256, 56),
-                                      (1, 1, 5120, 24), (1, 4100, 512, 24)])
+                                      (1, 1, 5120, 24), (1, 4100, 512, 24), (1, 4200, 1000, 56), (2, 2600, 264, 0)])
 def test_gate_project(dev, b, t, d, n1):
     """bf_gate_project (the ab and mix projections of a bf16 chunk in one pass) against fp32 products of the same
     bf16 x: relative error <= 1e-5 per output (W split into bf16 high and low parts); d = 40 ends on a partial
-    32-wide step, n1 = 0 has one output, n0 + n1 = 64 is the widest; one token (a decode step) and 4100 tokens (above
-    the split-d range: the LDS-tiled kernel, no workspace); a strided x view (every other token row of a wider
-    tensor) goes through _gate_logits. The split-d path is run twice and must reproduce its bits."""
+    32-wide step, n1 = 0 has one output, n0 + n1 = 64 is the widest; one token (a decode step). Above 4096 tokens the
+    LDS-tiled kernel runs on W split into the workspace: 256-wide steps up to 32 outputs (4100 tokens; 5200 tokens
+    with d = 264 ending on a partial step), 128-wide steps for 64 outputs with d = 1000 ending inside a step. A
+    strided x view (every other token row of a wider tensor) goes through _gate_logits. Both paths need their
+    workspace, and each is run twice and must reproduce its bits."""
     from heimdall_amd import _lib
     from heimdall_amd._device import stream_ptr
     print(f"gate projection B={b} t={t} d={d} n0=8 n1={n1}", flush=True)
@@ -166,15 +168,16 @@ def test_gate_project(dev, b, t, d, n1):
     lib = _lib.load()
     nb = _lib.ctypes.c_size_t(0)
     assert lib.bf_gate_project_workspace_size(b * t, d, 8 + n1, _lib.ctypes.byref(nb)) == 0
-    assert (nb.value == 0) == (b * t > 4096)
-    ws = torch.empty(max(nb.value, 1), dtype=torch.uint8, device=dev)
+    assert nb.value > 0
+    if b * t > 4096:                       # W^T split: 2 ceil(d / 256) sub-steps x 8 KB per 16 outputs
+        assert nb.value == 2 * ((d + 255) // 256) * ((8 + n1 + 15) // 16) * 8192
+    ws = torch.empty(nb.value, dtype=torch.uint8, device=dev)
     run = lambda: lib.bf_gate_project(xd.data_ptr(), b * t, d, d, w0d.data_ptr(), b0d.data_ptr(), 8, o0.data_ptr(),
                                       w1d.data_ptr() if n1 else None, b1d.data_ptr() if n1 else None, n1,
                                       o1.data_ptr() if n1 else None, ws.data_ptr(), nb.value, stream_ptr(dev))
-    if nb.value:
-        assert lib.bf_gate_project(xd.data_ptr(), b * t, d, d, w0d.data_ptr(), b0d.data_ptr(), 8, o0.data_ptr(),
-                                   w1d.data_ptr() if n1 else None, b1d.data_ptr() if n1 else None, n1,
-                                   o1.data_ptr() if n1 else None, None, 0, stream_ptr(dev)) != 0   # no workspace
+    assert lib.bf_gate_project(xd.data_ptr(), b * t, d, d, w0d.data_ptr(), b0d.data_ptr(), 8, o0.data_ptr(),
+                               w1d.data_ptr() if n1 else None, b1d.data_ptr() if n1 else None, n1,
+                               o1.data_ptr() if n1 else None, None, 0, stream_ptr(dev)) != 0   # no workspace
     rc = run()
     assert rc == 0, rc
     first = (o0.clone(), o1.clone())

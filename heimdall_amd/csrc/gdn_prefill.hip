@@ -21,17 +21,14 @@ namespace bf {
 constexpr int CH = 64;     // chunk length
 constexpr int NT = 256;    // threads per workgroup (4 waves)
 
-// LDS: the chunk's K tile (swizzled rows, staged by buffer_load ... lds) and A.
+// LDS: the chunk's K tile (swizzled rows, staged by buffer_load ... lds) and A. The inverse's diagonal blocks X_bb are
+// written over A's diagonal blocks once forward substitution has read them (the block products read A only below the
+// diagonal), so no LDS is set aside for X: 34 KB at D = 128 (four workgroups per CU, three with a separate X; the
+// prep phase of 4 packed sequences {8192, 16384, 24576, 16384}, H = 32, went from 279-307 to 236-269 us).
 template <class E, int D>
 struct __align__(16) PrepLds {
-    // the inverse X overlays K once A is built, where K is large enough
-    static constexpr bool XK = CH * D * sizeof(typename E::T) >= CH * (CH + 4) * sizeof(float);
-    union {
-        typename E::T K[CH * D];
-        float XoK[XK ? CH : 1][CH + 4];
-    };
+    typename E::T K[CH * D];
     float A[CH][CH + 4];
-    float Xs[XK ? 1 : CH][CH + 4];
     float gc[CH];
     float beta[CH];
 };
@@ -102,11 +99,12 @@ __global__ __launch_bounds__(NT) void gdn_prep_kernel(GdnArgs a) {
     __syncthreads();
 
     // (I + A)^-1, blocked over 16 x 16 blocks (L = I + A unit lower triangular, X = L^-1):
-    //   X_bb = L_bb^-1 for the 4 diagonal blocks: forward substitution, one column per lane (wave 0, lane 16 b + c);
+    //   X_bb = L_bb^-1 for the 4 diagonal blocks: forward substitution, one column per lane (wave 0, lane 16 b + c),
+    //   written over A's diagonal block b after all of its reads (one wave: its LDS accesses run in order);
     //   X_ij = -X_ii sum_{k=j}^{i-1} A_ik X_kj for i > j: wave j walks i = j+1 .. 3 with fp32 MFMAs; every 16 x 16
     //   accumulator (lane: column l16, rows 4 lg ..) is already laid out as the B operand of the next product.
     // T'[i][j] = X[i][j] beta_j (rows of tokens past the end are zero because their A rows and beta are).
-    float (*X)[CH + 4] = PrepLds<E, D>::XK ? sm.XoK : sm.Xs;
+    float (*X)[CH + 4] = sm.A;
     if (wv == 0) {
         const int bb = lane >> 4, c = lane & 15, o = 16 * bb;
         float x[16];

@@ -1,5 +1,5 @@
 """Device-side plumbing shared by the operator wrappers: dtype codes, workspace, stream, the GDN launcher."""
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 
@@ -62,12 +62,17 @@ def gdn_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tens
                 num_seqs: int, cu_seqlens: Optional[torch.Tensor] = None, initial_state: Optional[torch.Tensor] = None,
                 scale: float = 1.0, out_dtype: torch.dtype = torch.float32, phases: int = _lib.PHASE_ALL,
                 out: Optional[torch.Tensor] = None, final_state: Optional[torch.Tensor] = None,
-                ws: Optional[torch.Tensor] = None, segment_chunks: int = 0):
+                ws: Optional[torch.Tensor] = None, segment_chunks: int = 0,
+                gated_norm: Optional[Tuple[torch.Tensor, torch.Tensor, float]] = None):
     """Packed GQA gated delta rule on the GPU.
 
     q [N, G*R, D], k [N, G, D], v [N, G, D], g/beta [N, G]; cu_seqlens int32 [num_seqs + 1] on the device or None
     (equal sequences). ``segment_chunks``: 64-token chunks per independently scanned segment (0 = chosen from the
     problem size). Returns (o [N, G*R, D] out_dtype, final_state [num_seqs, G, D, D] fp32).
+
+    ``gated_norm`` = (z [N, G*R, D] bf16, w [D], eps): bf16 inputs, D <= 128; the output rows go through the
+    native layer's GatedNorm inside the output scan (``bf_gdn_fwd_gated``), the same bits as ``gated_norm`` applied
+    to the bf16 output, and the bf16 result is returned in place of o.
     """
     dev = require_device(q, k, v, g, beta, cu_seqlens, initial_state)
     N, H, D = q.shape
@@ -98,9 +103,26 @@ def gdn_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, g: torch.Tens
                                     _lib.ctypes.byref(nbytes)), "bf_gdn_workspace_size")
     if ws is None or ws.numel() < nbytes.value:
         ws = workspace(nbytes.value, dev)
+    if gated_norm is not None:
+        gz, gw, geps = gated_norm
+        if cdt != torch.bfloat16 or D > 128 or gz.dtype != torch.bfloat16 or gz.numel() != N * H * D:
+            raise BifrostError("the fused GatedNorm takes bf16 inputs and z rows [N, H, D] with D <= 128")
+        gz = gz.reshape(N, H, D).contiguous()
+        gw = gw.detach().float().contiguous()
+        if gw.numel() != D or (out is not None and out.dtype != torch.bfloat16):
+            raise BifrostError("the fused GatedNorm takes w [D] and writes a bf16 output")
+        out_dtype = torch.bfloat16
     o = out if out is not None else torch.empty(N, H, D, dtype=out_dtype, device=dev)
     s_out = final_state if final_state is not None else torch.empty(num_seqs, G, D, D, dtype=torch.float32,
                                                                      device=dev)
+    if gated_norm is not None:
+        check(lib.bf_gdn_fwd_gated(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
+                                   cu_seqlens.data_ptr() if cu_seqlens is not None else None, num_seqs, N, G, R, D,
+                                   float(scale), s0.data_ptr() if s0 is not None else None, gz.data_ptr(),
+                                   gw.data_ptr(), float(geps), o.data_ptr(), s_out.data_ptr(), int(segment_chunks),
+                                   ws.data_ptr(), ws.numel(), phases, stream_ptr(dev)),
+              "bf_gdn_fwd_gated")
+        return o, s_out
     check(lib.bf_gdn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
                          cu_seqlens.data_ptr() if cu_seqlens is not None else None, num_seqs, N, G, R, D,
                          dtype_code(cdt), float(scale), s0.data_ptr() if s0 is not None else None, o.data_ptr(),

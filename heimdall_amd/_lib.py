@@ -41,6 +41,8 @@ SIGNATURES = {
     "bf_gdn_conv_inputs": (_c_int, [_vp, _c_i64, _vp, _c_int, _vp, _c_int] + [_vp] * 5 + [_c_int, _c_i64]
                            + [_c_int] * 3 + [_fp, _fp] + [_vp] * 5 + [_c_int, _vp]),
     "bf_gated_norm": (_c_int, [_vp, _c_int, _vp, _vp, _c_i64, _c_int, _fp, _vp, _c_int, _vp]),
+    "bf_gdn_fwd_gated": (_c_int, [_vp] * 6 + [_c_int, _c_i64, _c_int, _c_int, _c_int, _fp, _vp, _vp, _vp, _fp, _vp, _vp,
+                                       _c_int, _vp, _c_sz, _c_int, _vp]),
     "bf_gdn_bwd_workspace_size": (_c_int, [_c_int, _c_i64, _c_int, _c_int, _c_int, ctypes.POINTER(_c_sz)]),
     "bf_gdn_bwd": (_c_int, [_vp] * 6 + [_fp, _vp, _vp, _c_int, _c_i64, _c_int, _c_int, _c_int] + [_vp] * 7
                    + [_c_sz, _vp]),

@@ -46,6 +46,10 @@ struct GdnArgs {
     float* ws_c;             // [sid][G]           c = e^{sum of g over the segment}
     float* ws_n;             // [sid][G][D*D]      segment state from a zero entry state (fp32, accumulator-fragment order)
     float* ws_sin;           // [sid][G][D*D]      entry state of each segment (fp32, accumulator-fragment order; segments > 0)
+    // the output scan's fused GatedNorm (null: o is stored as computed): z rows [N_tok][G*R][D] bf16, w [D] f32
+    const void* gn_z;
+    const float* gn_w;
+    float gn_eps;
 };
 
 int gdn_prep(const GdnArgs& a, hipStream_t stream);

@@ -134,10 +134,15 @@ int bf_gdn_workspace_size(int64_t total_tokens, int num_seqs, int G, int R, int 
     return BF_STATUS_OK;
 }
 
-int bf_gdn_fwd(const void* q, const void* k, const void* v, const float* g, const float* beta,
-               const int32_t* cu_seqlens, int num_seqs, int64_t total_tokens, int G, int R, int D, int in_dtype,
-               float scale, const float* initial_state, void* o, int o_dtype, float* final_state,
-               int segment_chunks, void* workspace, size_t workspace_bytes, int phases, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// bf_gdn_fwd, with the output scan's fused GatedNorm when gn_z is set (bf_gdn_fwd_gated)
+int gdn_fwd(const void* q, const void* k, const void* v, const float* g, const float* beta, const int32_t* cu_seqlens,
+            int num_seqs, int64_t total_tokens, int G, int R, int D, int in_dtype, float scale,
+            const float* initial_state, void* o, int o_dtype, float* final_state, int segment_chunks, void* workspace,
+            size_t workspace_bytes, int phases, const void* gn_z, const float* gn_w, float gn_eps, void* stream) {
     if (num_seqs <= 0 || total_tokens < 0 || G <= 0 || R <= 0 || segment_chunks < 0 ||
         (phases & ~BF_GDN_PHASE_ALL) || !phases)
         return BF_STATUS_INVALID;
@@ -169,6 +174,7 @@ int bf_gdn_fwd(const void* q, const void* k, const void* v, const float* g, cons
     a.ws_c = reinterpret_cast<float*>(ws + L.c);
     a.ws_n = reinterpret_cast<float*>(ws + L.n);
     a.ws_sin = reinterpret_cast<float*>(ws + L.sin);
+    a.gn_z = gn_z; a.gn_w = gn_w; a.gn_eps = gn_eps;
     if (total_tokens == 0 && !final_state) return BF_STATUS_OK;
     const hipStream_t st = static_cast<hipStream_t>(stream);
     int rc = 0;
@@ -178,6 +184,33 @@ int bf_gdn_fwd(const void* q, const void* k, const void* v, const float* g, cons
         return rc;
     if (phases & BF_GDN_PHASE_OUTPUT) return bf::gdn_output(a, st);
     return BF_STATUS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int bf_gdn_fwd(const void* q, const void* k, const void* v, const float* g, const float* beta,
+               const int32_t* cu_seqlens, int num_seqs, int64_t total_tokens, int G, int R, int D, int in_dtype,
+               float scale, const float* initial_state, void* o, int o_dtype, float* final_state,
+               int segment_chunks, void* workspace, size_t workspace_bytes, int phases, void* stream) {
+    return gdn_fwd(q, k, v, g, beta, cu_seqlens, num_seqs, total_tokens, G, R, D, in_dtype, scale, initial_state, o,
+                   o_dtype, final_state, segment_chunks, workspace, workspace_bytes, phases, nullptr, nullptr, 0.f,
+                   stream);
+}
+
+int bf_gdn_fwd_gated(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                     const int32_t* cu_seqlens, int num_seqs, int64_t total_tokens, int G, int R, int D,
+                     float scale, const float* initial_state, const void* norm_z, const float* norm_w,
+                     float norm_eps, void* out, float* final_state, int segment_chunks, void* workspace,
+                     size_t workspace_bytes, int phases, void* stream) {
+    if (D > 128) return BF_STATUS_UNSUPPORTED;
+    if (total_tokens > 0 && (phases & BF_GDN_PHASE_OUTPUT) &&
+        (!norm_z || !norm_w || ((uintptr_t)norm_z & 15) || ((uintptr_t)out & 15)))
+        return BF_STATUS_INVALID;
+    return gdn_fwd(q, k, v, g, beta, cu_seqlens, num_seqs, total_tokens, G, R, D, BF_DTYPE_BF16, scale,
+                   initial_state, out, BF_DTYPE_BF16, final_state, segment_chunks, workspace, workspace_bytes, phases,
+                   norm_z, norm_w, norm_eps, stream);
 }
 
 int bf_gdn_step(const float* q, const float* k, const float* v, const float* g, const float* beta,

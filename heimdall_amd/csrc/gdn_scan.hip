@@ -205,6 +205,39 @@ struct SegCfg {
 // prow(tile, l16) = tp(tile) + lt and an accumulator row is prow(tile, 4lg + i) = tp(tile) + VEC*lg + i. Every LDS and
 // global offset below is split into a per-lane part (computed once) and a part that depends only on unrolled loop
 // indices (an instruction immediate or a scalar offset), so the chunk loop keeps a handful of address registers.
+// GatedNorm of one bf16 row held by LPR consecutive lanes, 8 channels each (the arithmetic of gated_norm_kernel with
+// bf16 rows, Heimdall/heimdall/hibrit.py:118-129): out = bf16(bf16(w bf16(o rsqrt(mean(o^2) + eps))) SiLU(z)).
+template <int LPR>
+__device__ __forceinline__ uint4 gated_norm_row(const uint4& ov, const uint4& zv, const float (&w)[8], float eps,
+                                                int D) {
+    auto unpack = [](const uint4& u, float (&x)[8]) {
+        const uint32_t q[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x[2 * i] = __uint_as_float(q[i] << 16);
+            x[2 * i + 1] = __uint_as_float(q[i] & 0xffff0000u);
+        }
+    };
+    float o[8], z[8];
+    unpack(ov, o);
+    unpack(zv, z);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += o[e] * o[e];
+#pragma unroll
+    for (int m = LPR / 2; m >= 1; m >>= 1) ss += __shfl_xor(ss, m);
+    const float inv = rsqrtf(ss / (float)D + eps);
+    float r[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float h = bf2f(f2bf(o[e] * inv));
+        const float wh = bf2f(f2bf(w[e] * h));
+        r[e] = wh * (z[e] / (1.f + __expf(-z[e])));
+    }
+    return make_uint4(pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3]), pack_bf16x2(r[4], r[5]),
+                      pack_bf16x2(r[6], r[7]));
+}
+
 template <class E>
 __device__ __forceinline__ constexpr int tpart(int tile) {
     return E::KF * (tile / (E::VEC / 4)) + 4 * (tile % (E::VEC / 4));
@@ -219,7 +252,9 @@ __device__ __forceinline__ uint2 lds_tr16(const char* p) {
                       (uint16_t)v[2] | ((uint32_t)(uint16_t)v[3] << 16));
 }
 
-template <class E, int D, bool OUT, bool BO>
+// GN (output scan, bf16, whole rows per workgroup): each o row goes through the GatedNorm of the native layer before
+// it is stored, with the arithmetic of gated_norm_kernel (gdn_layer.hip), so the bits equal the two separate passes.
+template <class E, int D, bool OUT, bool BO, bool GN = false>
 __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(GdnArgs a) {
     using T = typename E::T;
     using Cfg = SegCfg<E, D, OUT>;
@@ -422,6 +457,13 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
     using OPk = typename std::conditional<BO, uint2, uint4>::type;   // one lane's 4 columns of one row
     // bf16 output scans whose o block (64 rows x the workgroup's columns) fits a q buffer stage o through it
     constexpr bool STG = OUT && DBUF && SC * VW * OS <= SC * D * ES;
+    static_assert(!GN || (STG && BO && VW == D), "the fused GatedNorm needs staged whole bf16 rows");
+    // GN: the norm weights of the lane's 8 channels (lane % (D / 8) of a row's D / 8 lanes, as in gated_norm_kernel)
+    float gnw[8];
+    if constexpr (GN) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gnw[e] = a.gn_w[8 * (lane % (D / 8)) + e];
+    }
     auto pack_o = [&](const f32x4 (&O)[NTC][NJ], OPk (&P)[NTC][NJ]) {
         const int qb4 = l16 & 3;
         auto pick = [&](const float (&x)[4], int idx) {
@@ -573,6 +615,23 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
     // come first and the copy then overlaps phases 1 to 3 instead of phase 1 only.
     auto compute = [&](const CL& cl, int c, bool prefetch, CL* next) {
         const int cn = c + 1 < count ? c + 1 : c;
+        // GN: the z rows of query head r of this chunk for the fused GatedNorm (rows past the chunk's end read as
+        // zero through the descriptor's range). Head 0's go out after the V fragment reads (the compiler drains every
+        // outstanding load before a transposing LDS read) and the next stage's copy, so they arrive under phases 1-3
+        constexpr int GRB = VW * 2, GLPR = GRB / 16, GRPI = 64 / GLPR, GNK = GN ? SC / NW / GRPI : 1;
+        uint4 zgv[GNK];
+        auto load_zg = [&](int r) {
+            if constexpr (GN) {
+                const rsrc_t rz = make_rsrc(reinterpret_cast<const char*>(a.gn_z) +
+                                                (chunk_tok0(c) * H + (long)g * R + r) * (long)D * 2,
+                                            (uint32_t)((long)chunk_len(c) * H * D * 2));
+#pragma unroll
+                for (int kk = 0; kk < GNK; ++kk) {
+                    const int row = (SC / NW) * wv + GRPI * kk + lane / GLPR;
+                    zgv[kk] = buf_ld16(rz, (uint32_t)(row * H * D * 2 + 16 * (lane % GLPR)));
+                }
+            }
+        };
         const char* Kb = reinterpret_cast<const char*>(cl.K);
         const char* Tb = reinterpret_cast<const char*>(TPS ? cl.Tp : ol.Tp);
         const char* Vb = reinterpret_cast<const char*>(ol.V);
@@ -602,6 +661,7 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
         };
         if constexpr (DBUF) read_vf();                  // single-buffered runs read V in phase 2 (fewer live registers)
         if (next) load_chunk(*next, cn);
+        load_zg(0);
         const float glast = cl.gc[SC - 1];
         const float decay = __expf(glast);
         float egc[NTC][4];                        // sc e^{gc} of the accumulator rows
@@ -675,6 +735,7 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
                 for (int jt = 0; jt < NJ; ++jt) vb[ks][jt] = pack_b<E>(Vn[ks * HP][jt], Vn[ks * HP + HP - 1][jt]);
             for (int r = 0; r < R; ++r) {
                 const int h = g * R + r;
+                if (r > 0) load_zg(r);                   // head 0's rows were loaded at the chunk's start
                 const char* Qb = reinterpret_cast<const char*>(ol.Q[QL ? qb : 0]);
                 const rsrc_t rq = make_rsrc(reinterpret_cast<const char*>(a.q) + (t0 * H + h) * D * ES,
                                             (uint32_t)(QL ? 0 : (long)len * H * D * ES));
@@ -744,7 +805,11 @@ __global__ __launch_bounds__(SEG_THREADS, SEG_WAVES_PER_EU) void gdn_seg_kernel(
 #pragma unroll
                     for (int k = 0; k < SC / NW / RPI; ++k) {
                         const int row = (SC / NW) * wv + RPI * k + lane / LPR, ch = lane % LPR;
-                        const uint4 v4 = lds16(stg, row * RB + 16 * ch);
+                        uint4 v4 = lds16(stg, row * RB + 16 * ch);
+                        if constexpr (GN) {
+                            static_assert(!GN || (BO && VW == D && LPR == GLPR), "GatedNorm needs whole bf16 rows");
+                            v4 = gated_norm_row<LPR>(v4, zgv[k], gnw, a.gn_eps, D);
+                        }
                         typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
                         const u32x4 w4 = {v4.x, v4.y, v4.z, v4.w};
                         __builtin_amdgcn_raw_buffer_store_b128(
@@ -1123,6 +1188,15 @@ int launch_states(const GdnArgs& a, hipStream_t stream, bool summary, bool combi
 template <class E, int D>
 int launch_output(const GdnArgs& a, hipStream_t stream) {
     const dim3 grid = seg_grid<E, D, true>(a), block(SegCfg<E, D, true>::NW * 64);
+    if (a.gn_z) {                                        // the fused GatedNorm: bf16 rows of D <= 128
+        if constexpr (std::is_same<E, BF16>::value && D <= 128) {
+            if (a.o_dtype != DT_BF16) return BF_ERR_UNSUPPORTED;
+            hipLaunchKernelGGL((gdn_seg_kernel<E, D, true, true, true>), grid, block, 0, stream, a);
+            return (int)hipGetLastError();
+        } else {
+            return BF_ERR_UNSUPPORTED;
+        }
+    }
     if (a.o_dtype == DT_BF16)
         hipLaunchKernelGGL((gdn_seg_kernel<E, D, true, true>), grid, block, 0, stream, a);
     else

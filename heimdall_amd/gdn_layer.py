@@ -78,6 +78,11 @@ def conv_inputs(z: torch.Tensor, conv_w: torch.Tensor, prefix: Optional[torch.Te
     return q, k, v, g, beta
 
 
+def _fused_norm(dtype: torch.dtype, d: int) -> bool:
+    """A bf16 layer with head dim <= 128 runs the GatedNorm inside the delta rule's output scan (bf_gdn_fwd_gated)."""
+    return dtype == torch.bfloat16 and d <= 128
+
+
 def gated_norm(o: torch.Tensor, z: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
     """weight * RMSNorm(o) * SiLU(z) over the last dim (``GatedNorm``, ``hibrit.py:118-129``). The result has z's
     dtype (the layer's dtype); a bf16 layer rounds where the reference does."""
@@ -149,14 +154,20 @@ class GatedDeltaNet(nn.Module):
         if cache is not None:
             full = z if prefix is None else torch.cat((prefix.to(z.dtype), z), 1)
             cache["conv"] = F.pad(full, (0, 0, max(0, k1 - full.size(1)), 0))[:, -k1:]
+        zg = self.in_proj_z(x).view(b, t, c.lin_hv, c.lin_dv)
+        fused = not step and _fused_norm(q.dtype, c.lin_dv)
         if step:
             o, s = gdn_step(q, k, v, g, beta, s0)
             o = o.to(x.dtype)
+        elif fused:                       # the output scan applies the GatedNorm to its rows (same bits)
+            o, s = gdn_forward(q, k, v, g, beta, num_seqs=b, initial_state=s0,
+                               gated_norm=(zg, self.norm.weight, self.norm.eps))
         else:
             o, s = gdn_forward(q, k, v, g, beta, num_seqs=b, initial_state=s0, out_dtype=x.dtype)
         if cache is not None:
             cache["S"] = s
-        o = self.norm(o.view(b, t, c.lin_hv, c.lin_dv), self.in_proj_z(x).view(b, t, c.lin_hv, c.lin_dv))
+        if not fused:
+            o = self.norm(o.view(b, t, c.lin_hv, c.lin_dv), zg)
         return self.out_proj(o.reshape(b, t, self.vd))
 
 
@@ -171,7 +182,11 @@ def gdn_layer_packed(m: GatedDeltaNet, z: torch.Tensor, a: torch.Tensor, b: torc
     num_seqs = cu_seqlens.numel() - 1
     q, k, v, g, beta = conv_inputs(z, m.conv1d.weight[:, 0], prefix, a, b, m.A_log, m.dt_bias, c.lin_hk, c.lin_hv,
                                    c.lin_dk, cu_seqlens=cu_seqlens, eps=1e-6)
-    o, s = gdn_forward(q, k, v, g, beta, num_seqs=num_seqs, cu_seqlens=cu_seqlens, initial_state=initial_state,
-                       out_dtype=z.dtype, segment_chunks=segment_chunks)
-    out = gated_norm(o, zg.view(o.shape), m.norm.weight, m.norm.eps)
+    if _fused_norm(q.dtype, c.lin_dv):
+        out, s = gdn_forward(q, k, v, g, beta, num_seqs=num_seqs, cu_seqlens=cu_seqlens, initial_state=initial_state,
+                             segment_chunks=segment_chunks, gated_norm=(zg.view(q.shape), m.norm.weight, m.norm.eps))
+    else:
+        o, s = gdn_forward(q, k, v, g, beta, num_seqs=num_seqs, cu_seqlens=cu_seqlens, initial_state=initial_state,
+                           out_dtype=z.dtype, segment_chunks=segment_chunks)
+        out = gated_norm(o, zg.view(o.shape), m.norm.weight, m.norm.eps)
     return out.view(z.shape[0], c.lin_hv * c.lin_dv), s

@@ -300,6 +300,21 @@ int bf_gated_norm(const void* o, int o_dtype, const void* z, const float* w, int
                   void* out, int io_dtype, void* stream);
 
 /*
+ * The native layer's delta rule and GatedNorm in one call (Heimdall/heimdall/hibrit.py:180-183: delta_rule, then
+ * self.norm(o, z)), for a bf16 layer with D <= 128: bf_gdn_fwd with in_dtype = o_dtype = bf16, whose output row of
+ * each (token, head) goes through bf_gated_norm's bf16 arithmetic before it is stored, so out holds the same bits as
+ * bf_gdn_fwd into o followed by bf_gated_norm(o, BF16, norm_z, norm_w, ..., out, BF16); o itself is never written.
+ *   norm_z [N_tok][G*R][D] bf16 (the z_g rows), norm_w [D] f32, out [N_tok][G*R][D] bf16 (norm_z, out 16-byte aligned);
+ *   the other arguments, the workspace (bf_gdn_workspace_size with in_dtype bf16) and the phases as for bf_gdn_fwd.
+ * BF_STATUS_UNSUPPORTED for D = 256 (a head's row spans two of the output scan's workgroups there).
+ */
+int bf_gdn_fwd_gated(const void* q, const void* k, const void* v, const float* g, const float* beta,
+                     const int32_t* cu_seqlens, int num_seqs, int64_t total_tokens, int G, int R, int D,
+                     float scale, const float* initial_state, const void* norm_z, const float* norm_w,
+                     float norm_eps, void* out, float* final_state, int segment_chunks, void* workspace,
+                     size_t workspace_bytes, int phases, void* stream);
+
+/*
  * One prefill chunk of the converted layer: HybridAttention._student with t > 1 (Heimdall/heimdall/hibrit.py:363-424)
  * on the student cache, in one call: the delta-rule write stream (the ring rows leaving the window, then the chunk's
  * own rows; from an empty cache the chunk shifted by W), bf_gdn_fwd on it from the cached state, bf_window_fwd with

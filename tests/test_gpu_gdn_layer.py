@@ -158,3 +158,41 @@ def test_packed_core_matches_per_sequence(dev):
                             c.lin_dk, c.eps, cache=cache, bf16_points=True)
         assert rel(out[lo:hi], ref[0]) < TOL16, i
         assert rel(s[i], cache["S"][0]) < TOL16, i
+
+
+@pytest.mark.parametrize("d,G,R", [(128, 4, 1), (64, 2, 2), (128, 1, 3)])
+def test_fused_gated_norm_equals_two_passes(dev, d, G, R):
+    """bf_gdn_fwd_gated (the GatedNorm applied by the output scan) against bf_gdn_fwd into o followed by
+    bf_gated_norm: the same bits, over packed sequences of 70, 1, 200 and 129 tokens (a partial chunk, a one-token
+    sequence) with an initial state, in single-segment and 2-chunk-segment scans; D = 256 and fp32 inputs are
+    refused."""
+    from heimdall_amd import _lib
+    from heimdall_amd._device import gdn_forward
+    from heimdall_amd.gdn_layer import gated_norm
+    print(f"fused GatedNorm d={d} G={G} R={R}", flush=True)
+    lens = [70, 1, 200, 129]
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32, device=dev)
+    N, H = sum(lens), G * R
+    gen = torch.Generator(device=dev).manual_seed(3 + d + R)
+    q = torch.randn(N, H, d, device=dev, generator=gen).bfloat16()
+    k = torch.nn.functional.normalize(torch.randn(N, G, d, device=dev, generator=gen), dim=-1).bfloat16()
+    v = torch.randn(N, G, d, device=dev, generator=gen).bfloat16()
+    g = -torch.rand(N, G, device=dev, generator=gen) * 0.1
+    beta = torch.sigmoid(torch.randn(N, G, device=dev, generator=gen))
+    s0 = torch.randn(4, G, d, d, device=dev, generator=gen) * 0.1
+    zg = torch.randn(N, H, d, device=dev, generator=gen).bfloat16()
+    w = torch.rand(d, device=dev, generator=gen) + 0.5
+    for L in (0, 2):
+        o, s = gdn_forward(q, k, v, g, beta, num_seqs=4, cu_seqlens=cu, initial_state=s0, scale=d ** -0.5,
+                           out_dtype=torch.bfloat16, segment_chunks=L)
+        ref = gated_norm(o, zg, w, 1e-6)
+        out, sf = gdn_forward(q, k, v, g, beta, num_seqs=4, cu_seqlens=cu, initial_state=s0, scale=d ** -0.5,
+                              segment_chunks=L, gated_norm=(zg, w, 1e-6))
+        assert out.dtype == torch.bfloat16 and torch.isfinite(out.float()).all()
+        assert torch.equal(out, ref), (L, (out.float() - ref.float()).abs().max().item())
+        assert torch.equal(sf, s), L
+    with pytest.raises(_lib.BifrostError):
+        gdn_forward(q.float(), k.float(), v.float(), g, beta, num_seqs=4, cu_seqlens=cu, gated_norm=(zg, w, 1e-6))
+    lib = _lib.load()
+    assert lib.bf_gdn_fwd_gated(*([None] * 6), 1, 64, 1, 1, 256, 1.0, None, None, None, 1e-6, None, None, 0,
+                                None, 0, _lib.PHASE_ALL, None) == -2          # BF_STATUS_UNSUPPORTED

@@ -882,9 +882,9 @@ def run_mtp_verify(dev, P=32768, steps=200, warmup=20):
     P tokens, the layer's student call on t = 2 tokens (the last token and the draft) at the current position, B = 1,
     each step two positions further (an accepted draft); next to it, the plain decode step t = 1. The headline's core
     (H=24, G=4, D=256, W=2048 + 4, d_model 5120, bf16). Timed with HIP events over `steps` calls; the cache snapshot
-    the reference takes before each verify is not included. The step is bound by the host (Python and ~11 launches),
-    so the garbage left by the earlier legs is collected before the timed loops: without that, the loop's own
-    allocations triggered collections over ~170 K objects of those legs, 279 instead of 115 us per step."""
+    the reference takes before each verify is not included. The step is ~11 small launches from Python, so the
+    garbage left by the earlier legs is collected before the timed loops: without that, the loop's own allocations
+    triggered collections over ~170 K objects of those legs, 279 instead of 115 us per step."""
     import gc
     from heimdall_amd import hibrit
 

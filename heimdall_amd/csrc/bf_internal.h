@@ -180,8 +180,9 @@ struct WinArgs {
     const float* mem_scale;   // [H]
     void* o;                  // [B][T][H][D] o_dtype
     float* lse;               // [B][H][T] or null
-    int split_x;              // bf16 kernel: slots per XCD split into two key halves (window_split_x), 0: none
-    float* part;              // their partial rows [8 split_x][2][128][D + 4] (m, l, -, -, unnormalised o)
+    int split_x;              // bf16 kernel: slots per XCD split into key parts (window_split_x), 0: none
+    int split_p;              // key parts per split slot (window_split_p)
+    float* part;              // their partial rows [8 split_x][split_p][128][D + 4] (m, l, -, -, unnormalised o)
     WinMap map;               // bf16 kernel: set by its launcher from window_map
 };
 
@@ -205,8 +206,15 @@ inline int window_split_x(const WinMap& m) {
     const long rem = m.per % 32;
     return rem > 0 && rem <= 16 ? (int)rem : 0;
 }
+// Key parts per split slot: two, unless every slot of an XCD is split and there are few (a chunk of a few tokens,
+// such as an MTP verification step), then as many as keep the XCD's parts within one round on its 32 CUs.
+inline int window_split_p(const WinMap& m) {
+    if (m.per > 16) return 2;
+    const long p = 32 / (m.per > 0 ? m.per : 1);
+    return (int)(p < 2 ? 2 : (p > 8 ? 8 : p));
+}
 inline size_t window_split_bytes(const WinMap& m, int D) {
-    return (size_t)8 * window_split_x(m) * 2 * 128 * (D + 4) * sizeof(float);
+    return (size_t)8 * window_split_x(m) * window_split_p(m) * 128 * (D + 4) * sizeof(float);
 }
 
 int window_dispatch(const WinArgs& a, hipStream_t stream);

@@ -447,7 +447,9 @@ static int window_fwd(int B, int G, int R, int D, int T, int W, int sinks, int64
     a.mix_on = mix; a.o_mem = o_mem; a.o_mem_dtype = o_mem_dtype; a.z = z; a.mix_lse = mix_lse; a.mem_scale = mem_scale;
     a.o = o; a.lse = lse;
     if (part && in_dtype == BF_DTYPE_BF16) {
-        a.split_x = bf::window_split_x(bf::window_map(B, G, R, T, W, start));
+        const bf::WinMap wm = bf::window_map(B, G, R, T, W, start);
+        a.split_x = bf::window_split_x(wm);
+        a.split_p = bf::window_split_p(wm);
         a.part = part;
     }
     return bf::window_dispatch(a, static_cast<hipStream_t>(stream));

@@ -120,18 +120,19 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
     __shared__ FaTile<D> t1;
 
     // ---- work item (the map of WinMap: workgroup x is dispatch slot x / 8 of XCD x mod 8). SPLIT: the last split_x
-    // slots of each XCD run as two workgroups each, one per half of the item's key blocks, and write partial rows
-    // that window_merge_kernel combines.
+    // slots of each XCD run as split_p workgroups each, one per part of the item's key blocks (two halves, or more
+    // parts for a grid of a few items), and write partial rows that window_merge_kernel combines.
     const int R = a.R, G = a.G, H = G * R;
     const int nqb = (a.T + FA_BQ - 1) / FA_BQ;
     const long per = a.map.per;
     const int xcd = (int)(blockIdx.x % FA_NXCD), sx = SPLIT ? a.split_x : 0;
     long idx = blockIdx.x / FA_NXCD;
-    int half = -1;                                      // -1: the whole item, else its first (0) or second key half
+    const int P = SPLIT ? a.split_p : 1;
+    int half = -1;                                      // -1: the whole item, else its key part 0 .. P - 1
     if (SPLIT && idx >= per - sx) {
         const long k = idx - (per - sx);
-        idx = per - sx + (k >> 1);
-        half = (int)(k & 1);
+        idx = per - sx + k / P;
+        half = (int)(k % P);
     }
     const long wi = window_item(a.map, xcd, idx);
     if (wi < 0) return;
@@ -176,8 +177,9 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
     const int has_sink = ns > 0 ? 1 : 0;
     const int nwin = kp_lo <= p_last ? (int)((p_last - kp_lo) / FA_KB) + 1 : 0;
     const int nblk = has_sink + nwin;
-    const int nh = (nblk + 1) >> 1;                                // blocks of a split item's first half
-    const int i_beg = SPLIT && half == 1 ? nh : 0, i_end = SPLIT && half == 0 ? nh : nblk;
+    // key part p of a split item: blocks ceil(nblk p / P) .. ceil(nblk (p + 1) / P) - 1 (P = 2: the two halves)
+    const int i_beg = SPLIT && half >= 0 ? (nblk * half + P - 1) / P : 0;
+    const int i_end = SPLIT && half >= 0 ? (nblk * (half + 1) + P - 1) / P : nblk;
     const int slot_lo = rk ? (int)(kp_lo % a.W) : 0;               // ring slot of kp_lo (one division)
     const long start = a.start;
 
@@ -475,7 +477,7 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
 
     if (SPLIT && half >= 0) {
         // partial rows of the key half, query qi at row qi: m (running max, log2 units), l, 2 unused, o unnormalised
-        float* pp = a.part + (((long)xcd * sx + (idx - (per - sx))) * 2 + half) * FA_BQ * (D + 4);
+        float* pp = a.part + (((long)xcd * sx + (idx - (per - sx))) * P + half) * FA_BQ * (D + 4);
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
             const float lt = fa_sum4(l[qt]);
@@ -563,9 +565,9 @@ __global__ __launch_bounds__(FaShape<D>::NT, 1) void window_fa_kernel(WinArgs a)
     }
 }
 
-// The two key halves of each split item: rows m0, l0, o0 and m1, l1, o1 (each relative to its own running max)
-// combine as L = c0 l0 + c1 l1, O = c0 o0 + c1 o1 with c = exp2(m - max(m0, m1)); then the window epilogue of
-// window_fa_kernel: o = O / L, lse, gamma mix, store. D / 4 threads per query row, 4 consecutive d each.
+// The P key parts of each split item: rows m_p, l_p, o_p (each relative to its own running max) combine as
+// L = sum c_p l_p, O = sum c_p o_p with c_p = exp2(m_p - max m); then the window epilogue of window_fa_kernel:
+// o = O / L, lse, gamma mix, store. D / 4 threads per query row, 4 consecutive d each.
 template <int D, bool BO>
 __global__ __launch_bounds__(256) void window_merge_kernel(WinArgs a) {
     constexpr int LPR = D / 4;
@@ -585,20 +587,28 @@ __global__ __launch_bounds__(256) void window_merge_kernel(WinArgs a) {
     const int g = (int)(rest % G), b = (int)(rest / G), h = g * R + r;
     const long tq = (long)qb * FA_BQ + qi;
     if (tq >= a.T) return;
-    const float* p0 = a.part + ((long)s * 2 * FA_BQ + qi) * (D + 4);
-    const float* p1 = p0 + (long)FA_BQ * (D + 4);
-    const float2 ml0 = *reinterpret_cast<const float2*>(p0), ml1 = *reinterpret_cast<const float2*>(p1);
-    const float4 o0 = *reinterpret_cast<const float4*>(p0 + 4 + 4 * c);
-    const float4 o1 = *reinterpret_cast<const float4*>(p1 + 4 + 4 * c);
-    const float mx = fmaxf(ml0.x, ml1.x);
-    const float c0 = ml0.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml0.x - mx);
-    const float c1 = ml1.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml1.x - mx);
-    const float lt = c0 * ml0.y + c1 * ml1.y;
+    // parts p = 0 .. P - 1 of the slot, added in order (P = 2: c0 x0 + c1 x1)
+    const int P = a.split_p;
+    const float* p0 = a.part + ((long)s * P * FA_BQ + qi) * (D + 4);
+    constexpr long PS = (long)FA_BQ * (D + 4);           // floats between consecutive parts of a row
+    float mx = -INFINITY;
+    for (int p = 0; p < P; ++p) mx = fmaxf(mx, p0[p * PS]);
+    float lt = 0.f, ox = 0.f, oy = 0.f, oz = 0.f, ow = 0.f;
+    for (int p = 0; p < P; ++p) {
+        const float* pp = p0 + p * PS;
+        const float2 ml = *reinterpret_cast<const float2*>(pp);
+        const float4 op = *reinterpret_cast<const float4*>(pp + 4 + 4 * c);
+        const float cp = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - mx);
+        if (p == 0) {
+            lt = cp * ml.y; ox = cp * op.x; oy = cp * op.y; oz = cp * op.z; ow = cp * op.w;
+        } else {
+            lt += cp * ml.y; ox += cp * op.x; oy += cp * op.y; oz += cp * op.z; ow += cp * op.w;
+        }
+    }
     const float inv = 1.f / lt;
     const float lse = (mx + __log2f(lt)) * FA_LN2;
     if (a.lse && c == 0) a.lse[((long)b * H + h) * a.T + tq] = lse;
-    float r4[4] = {(c0 * o0.x + c1 * o1.x) * inv, (c0 * o0.y + c1 * o1.y) * inv, (c0 * o0.z + c1 * o1.z) * inv,
-                   (c0 * o0.w + c1 * o1.w) * inv};
+    float r4[4] = {ox * inv, oy * inv, oz * inv, ow * inv};
     const long orow = (((long)b * a.T + tq) * H + h) * D;
     if (a.mix_on && a.start + tq >= a.W) {
         const float gam =
@@ -624,15 +634,15 @@ int launch_window_fa(const WinArgs& args, hipStream_t stream) {
     WinArgs a = args;
     a.map = window_map(a.B, a.G, a.R, a.T, a.W, a.start);
     const long per = a.map.per;
-    const int sx = a.split_x;
-    if (sx < 0 || sx > per || (sx && !a.part)) return BF_STATUS_INVALID;
-    if (FA_NXCD * (per + sx) > 0x7fffffffL) return BF_STATUS_INVALID;
+    const int sx = a.split_x, P = sx ? a.split_p : 1;
+    if (sx < 0 || sx > per || (sx && (!a.part || P < 2 || P > 8))) return BF_STATUS_INVALID;
+    if (FA_NXCD * (per + (long)sx * (P - 1)) > 0x7fffffffL) return BF_STATUS_INVALID;
     // chunk K / V rows are addressed by 32-bit buffer offsets
     if (((long)(a.T - 1) * a.k_st + D) * 2 > 0xffffffffL || ((long)(a.T - 1) * a.v_st + D) * 2 > 0xffffffffL)
         return BF_ERR_UNSUPPORTED;
     // the tile copy forms row offsets with 24-bit multiplies: chunk rows and row strides in bytes below 2^24
     if (a.T >= (1L << 24) || a.k_st * 2 >= (1L << 24) || a.v_st * 2 >= (1L << 24)) return BF_ERR_UNSUPPORTED;
-    const dim3 grid((unsigned)(FA_NXCD * (per + sx))), block(FaShape<D>::NT);
+    const dim3 grid((unsigned)(FA_NXCD * (per + (long)sx * (P - 1)))), block(FaShape<D>::NT);
     const bool bo = a.o_dtype == DT_BF16;
     if (sx) {
         if (bo) hipLaunchKernelGGL((window_fa_kernel<D, true, true>), grid, block, 0, stream, a);

@@ -51,19 +51,20 @@ def test_chunked_cache_equals_oracle_fp32(dev, d):
 
 def test_production_geometry_bf16(dev):
     """H=24, G=4, D=256, W=2048 + 4 sinks, bf16 activations: a 3000-token prefill, a 1200-token chunk (the memory
-    branch becomes active mid-chunk, the window reads across the ring) and a 2048-token chunk over a full ring,
-    against the fp32 oracle on the same bf16 values. The window's work items of 128 queries x 1 head are 576, 240
-    and 384: the first and last leave a last round of at most 16 items on each XCD, which run as two key halves
-    each (merged afterwards), the middle one does not."""
+    branch becomes active mid-chunk, the window reads across the ring), a 2048-token chunk over a full ring, then
+    chunks of 2 and 5 tokens (an MTP verification step), against the fp32 oracle on the same bf16 values. The
+    window's work items of 128 queries x 1 head are 576, 240, 384, 24 and 24: the first and third leave a last round
+    of at most 16 items on each XCD, which run as two key halves each (merged afterwards), the second does not, and
+    the last two run each item as 5 key parts of ~7 of the 35 key blocks."""
     from heimdall_amd import hibrit
-    print("layer bf16 H=24 G=4 D=256 W=2048 T=3000+1200+2048", flush=True)
+    print("layer bf16 H=24 G=4 D=256 W=2048 T=3000+1200+2048+2+5", flush=True)
     m = make_core(24, 4, 256, 64, window=2048, sinks=4)
     mg = make_core(24, 4, 256, 64, window=2048, sinks=4).to(dev)
-    args = make_inputs(m, 1, 6248, seed=13, dtype=torch.bfloat16)
+    args = make_inputs(m, 1, 6255, seed=13, dtype=torch.bfloat16)
     argsf = tuple(z.float() for z in args)
     c_ref, c_gpu = {}, {}
     with torch.no_grad():
-        for a, e in ((0, 3000), (3000, 4200), (4200, 6248)):
+        for a, e in ((0, 3000), (3000, 4200), (4200, 6248), (6248, 6250), (6250, 6255)):
             o_ref = olayer.student(m, *split(argsf, a, e), a, c_ref)
             o = hibrit.student(mg, *to_dev(split(args, a, e), dev), a, c_gpu)
             print(f"  chunk {a}:{e} rel err {rel(o, o_ref):.2e}", flush=True)

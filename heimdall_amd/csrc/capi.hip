@@ -422,7 +422,8 @@ int bf_decode_fwd_noalloc(int B, int G, int R, int D, int W, int sinks, int64_t 
 }
 
 // bf_window_fwd with an optional partial-row buffer of window_split_bytes(window_map(...), D) bytes: with it, bf16
-// inputs run the work items of a last, at most half-full round on each XCD as two key halves (merged after).
+// inputs run the work items of a last, at most half-full round on each XCD as two key halves, or a grid of a few
+// items as up to 8 key parts (merged after).
 static int window_fwd(int B, int G, int R, int D, int T, int W, int sinks, int64_t start, int in_dtype, const void* q,
                       int64_t q_sb, int64_t q_sh, int64_t q_st, const void* k, int64_t k_sb, int64_t k_sh, int64_t k_st,
                       const void* v, int64_t v_sb, int64_t v_sh, int64_t v_st, const void* ring_k, const void* ring_v,
